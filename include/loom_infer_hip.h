@@ -1,0 +1,489 @@
+/*
+ * loom_infer_hip.h — C ABI of libloom_infer_hip.so, the MI355X (gfx950)
+ * implementation of Loom Infer's paged-KV decode path:
+ *
+ *   fused NeoX RoPE + paged K/V append  ->  paged decode attention
+ *   (split over KV pages with an in-kernel log2-LSE merge)  ->  hipGraph
+ *   fixed-address capture and replay.
+ *
+ * The ABI mirrors the reference's Rust contract sequence
+ *   Spec::new -> Provider::plan_* -> queue.bindings(n) / bind_read /
+ *   bind_read_write -> queue.begin -> plan.enqueue_into(scope, args) ->
+ *   scope.finish() -> completion.wait() -> take_read_write
+ * (crates/loom-infer-cuda/src/attention/decode.rs:1067, :1199, :1452-1487;
+ *  crates/loom-infer-cuda/src/rope/mod.rs:628-682, :758, :846, :963-1047;
+ *  crates/loom-infer-cuda/src/command/{binding,submission,completion}.rs;
+ *  crates/loom-infer-cuda/src/graph/mod.rs).
+ *
+ * Conventions
+ *   - Every function returns a loom_status_t by value and never throws or
+ *     aborts across the ABI, except where the reference aborts: a failed
+ *     stream AND device synchronization while settling in-flight work
+ *     (command/completion.rs:165-182, graph/mod.rs:679-685).
+ *   - `err` may be NULL; when given it receives the variant payload and a
+ *     human-readable message equal to the reference's Display text.
+ *   - Buffers are raw device pointers with an element count and dtype.
+ *     Binding a buffer read-write transfers it to the binding set until the
+ *     command completion that used it is settled and the caller takes it back.
+ *   - No function here allocates device memory except *_new/_load and graph
+ *     instantiation; enqueue paths never allocate.
+ */
+#ifndef LOOM_INFER_HIP_H
+#define LOOM_INFER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LOOM_INFER_HIP_ABI_VERSION 1u
+#define LOOM_HEAD_DIM 128u                       /* single_decode/mod.rs:8 */
+#define LOOM_PAGE_SIZE 16u                       /* paged_decode/mod.rs:9 */
+#define LOOM_PARTIAL_STATE_WIDTH 130u            /* single_decode/mod.rs:13 */
+#define LOOM_APPEND_MAX_TOKENS 64u               /* paged_append/mod.rs:12 */
+/* Bulk explicit-token append (no reference counterpart: the reference caps the
+ * explicit contract at 64 tokens; this contract keeps its semantics and lifts
+ * the cap for batched multi-token appends). */
+#define LOOM_APPEND_MAX_TOKENS_EXTENDED 8192u
+
+/* ------------------------------------------------------------------------ */
+/* Status codes.                                                              */
+typedef int32_t loom_status_t;
+enum {
+  LOOM_OK = 0,
+  /* ContractError, crates/loom-infer/src/error.rs:6-109 (same order). */
+  LOOM_ZERO_DIMENSION = 1,
+  LOOM_ELEMENT_COUNT_OVERFLOW = 2,
+  LOOM_INVALID_EPSILON = 3,
+  LOOM_UNSUPPORTED_HEAD_DIMENSION = 4,
+  LOOM_UNSUPPORTED_PAGE_SIZE = 5,
+  LOOM_INVALID_HEAD_MAPPING = 6,
+  LOOM_INVALID_PARTITION_COUNT = 7,
+  LOOM_INVALID_INDPTR_START = 8,
+  LOOM_NON_MONOTONIC_INDPTR = 9,
+  LOOM_EMPTY_RAGGED_REQUEST = 10,
+  LOOM_RAGGED_QUERY_LONGER_THAN_KV = 11,
+  LOOM_INVALID_PAGE_INDPTR_START = 12,
+  LOOM_NON_MONOTONIC_PAGE_INDPTR = 13,
+  LOOM_EMPTY_PAGED_REQUEST = 14,
+  LOOM_PAGE_INDEX_OUT_OF_RANGE = 15,
+  LOOM_INVALID_LAST_PAGE_LENGTH = 16,
+  LOOM_INVALID_ROTARY_DIMENSION = 17,
+  LOOM_INVALID_ROPE_SCALE = 18,
+  LOOM_INVALID_ROPE_THETA = 19,
+  LOOM_NEGATIVE_POSITION_ID = 20,
+  LOOM_UNSUPPORTED_APPEND_TOKEN_COUNT = 21,
+  LOOM_APPEND_BATCH_INDEX_OUT_OF_RANGE = 22,
+  LOOM_APPEND_POSITION_OUT_OF_RANGE = 23,
+  LOOM_DUPLICATE_PAGE_APPEND_SLOT = 24,
+  LOOM_DUPLICATE_PAGE_APPEND_TOKEN_SLOT = 25,
+  LOOM_UNSUPPORTED_DTYPE = 26,
+  LOOM_LENGTH_MISMATCH = 27,
+
+  /* CommandError, crates/loom-infer-cuda/src/command/mod.rs:67-107. */
+  LOOM_CMD_ZERO_COMMAND_CAPACITY = 40,
+  LOOM_CMD_ZERO_BINDING_CAPACITY = 41,
+  LOOM_CMD_IDENTIFIER_SPACE_EXHAUSTED = 42,
+  LOOM_CMD_BINDINGS_QUEUE_MISMATCH = 43,
+  LOOM_CMD_QUEUE_POISONED = 44,
+  LOOM_CMD_SCOPE_POISONED = 45,
+  LOOM_CMD_BINDING_CAPACITY_EXCEEDED = 46,
+  LOOM_CMD_BUFFER_CONTEXT_MISMATCH = 47,
+  LOOM_CMD_BINDING_SET_MISMATCH = 48,
+  LOOM_CMD_BINDING_SLOT_OUT_OF_RANGE = 49,
+  LOOM_CMD_BINDING_IS_READ_ONLY = 50,
+  LOOM_CMD_BINDING_SLOT_VACANT = 51,
+  LOOM_CMD_BINDING_TYPE_MISMATCH = 52,
+  LOOM_CMD_DUPLICATE_BINDING_SLOT = 53,
+  LOOM_CMD_COMMAND_CAPACITY_EXCEEDED = 54,
+  LOOM_CMD_EXTERNAL = 55,
+  LOOM_CMD_DRIVER = 56,
+  /* C-ABI ownership checks that Rust's type system performs statically. */
+  LOOM_CMD_ALIASED_BINDING = 57,      /* a read-write range overlaps another lease */
+  LOOM_CMD_BINDINGS_IN_USE = 58,      /* bindings were moved into a live scope */
+  LOOM_NULL_ARGUMENT = 59,
+  LOOM_CMD_SCOPE_ACTIVE = 60,         /* the queue already has a live scope or unsettled completion */
+
+  /* Plan errors (decode.rs:1498-1513, rope/mod.rs:1049-1061). */
+  LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE = 70,
+  LOOM_PLAN_STATE_COUNT_OVERFLOW = 71,
+  LOOM_PLAN_UNSUPPORTED_HEAD_DIMENSION = 72,
+  LOOM_PLAN_UNSUPPORTED_ROTARY_DIMENSION = 73,
+  LOOM_PLAN_UNSUPPORTED_DEVICE = 74,   /* the provider only loads on gfx950 */
+  LOOM_PLAN_INVALID_OPTION = 75,
+
+  /* Enqueue errors (decode.rs:1515-1551, rope/mod.rs:1062-1077). */
+  LOOM_ENQ_LENGTH_MISMATCH = 90,
+  LOOM_ENQ_PAGE_INDICES_TOO_SHORT = 91,
+  LOOM_ENQ_MISALIGNED_BUFFER = 92,
+  LOOM_ENQ_PAGE_INDICES_TOO_LONG = 93, /* more pages than the plan's workspace covers */
+
+  /* GraphError, crates/loom-infer-cuda/src/graph/mod.rs:688-721. */
+  LOOM_GRAPH_DEFAULT_STREAM_UNSUPPORTED = 110,
+  LOOM_GRAPH_EMPTY_CAPTURE = 111,
+  LOOM_GRAPH_CAPTURE_INVALIDATED = 112,
+  LOOM_GRAPH_NULL_EXECUTABLE_HANDLE = 113,
+  LOOM_GRAPH_EXECUTION_POISONED = 114,
+  LOOM_GRAPH_REPLAY_IN_FLIGHT = 115,
+  LOOM_GRAPH_LAUNCH_COUNT_EXHAUSTED = 116,
+  LOOM_GRAPH_TIMING_EVENT_CONTEXT_MISMATCH = 117,
+  LOOM_GRAPH_DRIVER = 118,
+  LOOM_GRAPH_SETTLEMENT = 119
+};
+
+/* Variant payload: `fields` hold the variant's integer fields in declaration
+ * order (floats are stored as their f64 value in `value`), `operand` names the
+ * buffer for LengthMismatch-like variants, `hip_status` the HIP error for
+ * driver variants. */
+typedef struct loom_error {
+  int32_t code;
+  int32_t hip_status;
+  const char *operand;
+  int64_t fields[4];
+  double value;
+  char message[256];
+} loom_error_t;
+
+/* Returns the Display text for a status code without payload. */
+const char *loom_status_name(loom_status_t status);
+uint32_t loom_abi_version(void);
+
+typedef enum loom_dtype {
+  LOOM_DTYPE_F32 = 0, /* dtype.rs:2-20 */
+  LOOM_DTYPE_F16 = 1,
+  LOOM_DTYPE_BF16 = 2,
+  LOOM_DTYPE_I32 = 3, /* binding.rs:230-234 element types */
+  LOOM_DTYPE_U8 = 4
+} loom_dtype_t;
+
+/* ------------------------------------------------------------------------ */
+/* Paged batch-decode contract, crates/loom-infer/src/attention/paged_decode/mod.rs */
+typedef struct loom_paged_decode_spec {
+  uint64_t batch_size;
+  uint64_t max_num_pages;
+  uint64_t num_query_heads;
+  uint64_t num_kv_heads;
+  float softmax_scale;
+} loom_paged_decode_spec_t;
+
+/* Bf16PagedBatchDecodeSpec::new, paged_decode/mod.rs:28-82. */
+loom_status_t loom_paged_decode_spec_new(uint64_t batch_size, uint64_t max_num_pages,
+                                         uint64_t num_query_heads, uint64_t num_kv_heads,
+                                         uint64_t head_dim, uint64_t page_size,
+                                         loom_paged_decode_spec_t *out, loom_error_t *err);
+/* validate_page_table, paged_decode/mod.rs:152-213 (host metadata). */
+loom_status_t loom_paged_decode_validate_page_table(const loom_paged_decode_spec_t *spec,
+                                                    const int32_t *page_indptr, uint64_t n_indptr,
+                                                    const int32_t *page_indices,
+                                                    uint64_t n_indices,
+                                                    const int32_t *last_page_len,
+                                                    uint64_t n_last, loom_error_t *err);
+/* request_kv_len / physical_page_for_token, paged_decode/mod.rs:252-278, on a
+ * validated table.  Return LOOM_OK and fill the outputs (the reference's
+ * Some), or LOOM_PAGE_INDEX_OUT_OF_RANGE for the reference's None. */
+loom_status_t loom_paged_decode_request_kv_len(const loom_paged_decode_spec_t *spec,
+                                               const int32_t *page_indptr,
+                                               const int32_t *last_page_len, uint64_t request,
+                                               uint64_t *kv_len);
+loom_status_t loom_paged_decode_physical_page_for_token(
+    const loom_paged_decode_spec_t *spec, const int32_t *page_indptr,
+    const int32_t *page_indices, const int32_t *last_page_len, uint64_t request,
+    uint64_t logical_token, uint64_t *physical_page, uint64_t *page_offset);
+
+/* Fused RoPE + one-token append, paged_append/mod.rs:16-131. */
+typedef struct loom_rope_append_spec {
+  loom_paged_decode_spec_t paged;
+} loom_rope_append_spec_t;
+loom_status_t loom_rope_append_spec_new(uint64_t batch_size, uint64_t max_num_pages,
+                                        uint64_t num_query_heads, uint64_t num_kv_heads,
+                                        uint64_t head_dim, uint64_t page_size,
+                                        loom_rope_append_spec_t *out, loom_error_t *err);
+/* paged_append/mod.rs:95-131: page table + duplicate final slot rejection
+ * (reported for the first (first_request, second_request) pair in the
+ * reference's nested-loop order; computed in O(B) with a hash map). */
+loom_status_t loom_rope_append_validate_page_table(const loom_rope_append_spec_t *spec,
+                                                   const int32_t *page_indptr,
+                                                   uint64_t n_indptr,
+                                                   const int32_t *page_indices,
+                                                   uint64_t n_indices,
+                                                   const int32_t *last_page_len,
+                                                   uint64_t n_last, loom_error_t *err);
+
+/* Explicit-token append, paged_append/mod.rs:136-317. */
+typedef struct loom_rope_append_tokens_spec {
+  loom_paged_decode_spec_t paged;
+  uint64_t tokens;
+  uint64_t max_tokens; /* 64 (reference contract) or the extended bound */
+} loom_rope_append_tokens_spec_t;
+/* Bf16RopePagedKvAppendTokensSpec::new, paged_append/mod.rs:144-177 (T <= 64). */
+loom_status_t loom_rope_append_tokens_spec_new(uint64_t tokens, uint64_t batch_size,
+                                               uint64_t max_num_pages,
+                                               uint64_t num_query_heads,
+                                               uint64_t num_kv_heads, uint64_t head_dim,
+                                               uint64_t page_size,
+                                               loom_rope_append_tokens_spec_t *out,
+                                               loom_error_t *err);
+/* Same contract with T <= LOOM_APPEND_MAX_TOKENS_EXTENDED (no reference
+ * counterpart; for callers that append whole prefill chunks in one command). */
+loom_status_t loom_rope_append_tokens_spec_new_extended(
+    uint64_t tokens, uint64_t batch_size, uint64_t max_num_pages, uint64_t num_query_heads,
+    uint64_t num_kv_heads, uint64_t head_dim, uint64_t page_size,
+    loom_rope_append_tokens_spec_t *out, loom_error_t *err);
+/* validate_metadata, paged_append/mod.rs:244-317.  `slots` (optional, 2*T)
+ * receives (physical_page, offset) per token. Duplicates are found in O(T)
+ * and reported as the first (first_token, second_token) pair in token order. */
+loom_status_t loom_rope_append_tokens_validate_metadata(
+    const loom_rope_append_tokens_spec_t *spec, const int32_t *batch_indices, uint64_t n_batch,
+    const int32_t *positions, uint64_t n_positions, const int32_t *page_indptr,
+    uint64_t n_indptr, const int32_t *page_indices, uint64_t n_indices,
+    const int32_t *last_page_len, uint64_t n_last, uint64_t *slots, loom_error_t *err);
+
+/* ------------------------------------------------------------------------ */
+/* Command runtime, crates/loom-infer-cuda/src/command/.                       */
+typedef struct loom_command_queue loom_command_queue_t;
+typedef struct loom_bindings loom_bindings_t;
+typedef struct loom_command_scope loom_command_scope_t;
+typedef struct loom_command_completion loom_command_completion_t;
+
+/* Opaque binding handle (binding.rs:310-336 Read/ReadWrite/Write). */
+typedef struct loom_handle {
+  uint64_t set_id;
+  uint64_t slot;
+} loom_handle_t;
+
+/* CommandQueue::new(stream, max_commands), submission.rs:31-46.  `stream` is
+ * a hipStream_t owned by the caller (it must outlive the queue). */
+loom_status_t loom_command_queue_new(void *hip_stream, uint64_t max_commands,
+                                     loom_command_queue_t **out, loom_error_t *err);
+/* Drop: synchronizes the stream if commands are still retained. */
+void loom_command_queue_free(loom_command_queue_t *queue);
+uint64_t loom_command_queue_max_commands(const loom_command_queue_t *queue);
+int loom_command_queue_is_poisoned(const loom_command_queue_t *queue);
+
+/* CommandQueue::bindings(capacity), submission.rs:58-70. */
+loom_status_t loom_command_queue_bindings(loom_command_queue_t *queue, uint64_t capacity,
+                                          loom_bindings_t **out, loom_error_t *err);
+void loom_bindings_free(loom_bindings_t *bindings);
+uint64_t loom_bindings_len(const loom_bindings_t *bindings);
+uint64_t loom_bindings_capacity(const loom_bindings_t *bindings);
+/* bind_read / bind_read_write, binding.rs:38-91.  The device pointer must
+ * belong to the queue stream's device (BufferContextMismatch otherwise). */
+loom_status_t loom_bindings_bind_read(loom_bindings_t *bindings, const void *device_ptr,
+                                      uint64_t numel, loom_dtype_t dtype, loom_handle_t *out,
+                                      loom_error_t *err);
+loom_status_t loom_bindings_bind_read_write(loom_bindings_t *bindings, void *device_ptr,
+                                            uint64_t numel, loom_dtype_t dtype,
+                                            loom_handle_t *out, loom_error_t *err);
+/* take_read_write, binding.rs:93-107: returns the owned buffer and vacates
+ * the slot. */
+loom_status_t loom_bindings_take_read_write(loom_bindings_t *bindings, loom_handle_t handle,
+                                            void **device_ptr, uint64_t *numel,
+                                            loom_error_t *err);
+
+/* CommandQueue::begin, submission.rs:73-99.  On success the bindings move
+ * into the scope; the caller gets them back from completion_wait. */
+loom_status_t loom_command_queue_begin(loom_command_queue_t *queue, loom_bindings_t *bindings,
+                                       loom_command_scope_t **out, loom_error_t *err);
+/* CommandScope::finish, submission.rs:131-151: records the one completion
+ * event.  Consumes the scope. */
+loom_status_t loom_command_scope_finish(loom_command_scope_t *scope,
+                                        loom_command_completion_t **out, loom_error_t *err);
+/* Drop of an unfinished scope (synchronizes if anything was submitted). */
+void loom_command_scope_free(loom_command_scope_t *scope);
+uint64_t loom_command_scope_submitted(const loom_command_scope_t *scope);
+
+uint64_t loom_command_completion_submitted(const loom_command_completion_t *completion);
+/* is_complete / wait, completion.rs:37-83.  wait consumes the completion and
+ * returns the bindings (NULL and freed on failure, as the reference drops them). */
+loom_status_t loom_command_completion_is_complete(loom_command_completion_t *completion,
+                                                  int *complete, loom_error_t *err);
+loom_status_t loom_command_completion_wait(loom_command_completion_t *completion,
+                                           loom_bindings_t **bindings, loom_error_t *err);
+/* Drop: waits, poisons the queue on failure, frees the bindings. */
+void loom_command_completion_free(loom_command_completion_t *completion);
+
+/* ------------------------------------------------------------------------ */
+/* Paged decode provider and plan, crates/loom-infer-cuda/src/attention/decode.rs */
+typedef struct loom_decode_provider loom_decode_provider_t;
+typedef struct loom_paged_decode_plan loom_paged_decode_plan_t;
+
+/* DecodeProvider::load, decode.rs:1009-1014: binds the gfx950 kernels of this
+ * library on `device` (LOOM_PLAN_UNSUPPORTED_DEVICE on other targets). */
+loom_status_t loom_decode_provider_load(int device, loom_decode_provider_t **out,
+                                        loom_error_t *err);
+void loom_decode_provider_free(loom_decode_provider_t *provider);
+
+typedef enum loom_paged_decode_algorithm {
+  /* One workgroup per (request, kv-head, group tile, KV chunk of pages);
+   * the whole GQA group shares each K/V byte; chunks merge through a
+   * log2-LSE state workspace inside the same kernel. */
+  LOOM_PAGED_DECODE_SPLIT_KV_GROUP = 1
+} loom_paged_decode_algorithm_t;
+
+/* Planner inputs.  Zero means "choose for this device". */
+typedef struct loom_paged_decode_plan_options {
+  uint64_t max_total_pages; /* upper bound of page_indices length; 0 -> max_num_pages */
+  uint32_t chunk_pages;     /* pages per workgroup chunk (4..64, multiple of 4) */
+  uint32_t expected_kv_len; /* typical request length used to size chunks */
+} loom_paged_decode_plan_options_t;
+
+typedef struct loom_paged_decode_plan_info {
+  loom_paged_decode_spec_t spec;
+  int32_t algorithm;
+  uint32_t chunk_pages;
+  uint32_t group_tile;       /* query heads per workgroup column block */
+  uint32_t group_tiles;      /* ceil(group / group_tile) */
+  uint64_t max_total_pages;
+  uint64_t max_chunks;       /* state slots: ceil(max_total_pages/chunk_pages)+batch */
+  uint64_t workspace_bytes;  /* states + per-(request, kv-head, tile) counters */
+  uint32_t block_threads;
+  uint32_t device_cus;
+} loom_paged_decode_plan_info_t;
+
+/* DecodeProvider::plan_bf16_paged_batch, decode.rs:1067-1103.  The plan
+ * depends only on the spec and options, never on page-table contents. */
+loom_status_t loom_decode_provider_plan_bf16_paged_batch(
+    const loom_decode_provider_t *provider, const loom_paged_decode_spec_t *spec,
+    const loom_paged_decode_plan_options_t *options, loom_paged_decode_plan_t **out,
+    loom_error_t *err);
+void loom_paged_decode_plan_free(loom_paged_decode_plan_t *plan);
+void loom_paged_decode_plan_get_info(const loom_paged_decode_plan_t *plan,
+                                     loom_paged_decode_plan_info_t *info);
+
+/* Bf16PagedBatchDecodeArgs, decode.rs:1452-1487, plus the caller-owned
+ * workspace (u8, exactly plan.workspace_bytes, zero-filled once before its
+ * first use; every command leaves it zeroed again). */
+typedef struct loom_paged_decode_args {
+  loom_handle_t query;         /* Read<bf16>  [B, Hq, 128] */
+  loom_handle_t key_pages;     /* Read<bf16>  [pool, 16, Hkv, 128] */
+  loom_handle_t value_pages;   /* Read<bf16>  [pool, 16, Hkv, 128] */
+  loom_handle_t page_indptr;   /* Read<i32>   [B+1] */
+  loom_handle_t page_indices;  /* Read<i32>   [>= B] */
+  loom_handle_t last_page_len; /* Read<i32>   [B] */
+  loom_handle_t output;        /* Write<bf16> [B, Hq, 128] */
+  loom_handle_t lse;           /* Write<f32>  [B, Hq], log2 domain */
+  loom_handle_t workspace;     /* Write<u8>   [workspace_bytes] */
+} loom_paged_decode_args_t;
+
+/* Bf16PagedBatchDecodePlan::enqueue_into, decode.rs:1199-1296: one kernel. */
+loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
+                                        loom_command_scope_t *scope,
+                                        const loom_paged_decode_args_t *args,
+                                        loom_error_t *err);
+
+/* ------------------------------------------------------------------------ */
+/* Fused RoPE + paged append provider, crates/loom-infer-cuda/src/rope/mod.rs */
+typedef struct loom_rope_provider loom_rope_provider_t;
+typedef struct loom_rope_append_plan loom_rope_append_plan_t;
+
+loom_status_t loom_rope_provider_load(int device, loom_rope_provider_t **out,
+                                      loom_error_t *err);
+void loom_rope_provider_free(loom_rope_provider_t *provider);
+
+typedef struct loom_rope_append_plan_info {
+  uint64_t tokens;          /* B for the one-token form */
+  uint64_t batch_size;
+  uint64_t num_query_heads;
+  uint64_t num_kv_heads;
+  int32_t explicit_tokens;  /* 0: one token per request at kv_len-1 */
+  uint64_t workspace_bytes; /* validation flag words */
+  uint32_t validate_blocks;
+} loom_rope_append_plan_info_t;
+
+/* RopeProvider::plan_bf16_paged_append, rope/mod.rs:628-654. */
+loom_status_t loom_rope_provider_plan_bf16_paged_append(const loom_rope_provider_t *provider,
+                                                        const loom_rope_append_spec_t *spec,
+                                                        loom_rope_append_plan_t **out,
+                                                        loom_error_t *err);
+/* RopeProvider::plan_bf16_paged_append_tokens, rope/mod.rs:656-682. */
+loom_status_t loom_rope_provider_plan_bf16_paged_append_tokens(
+    const loom_rope_provider_t *provider, const loom_rope_append_tokens_spec_t *spec,
+    loom_rope_append_plan_t **out, loom_error_t *err);
+void loom_rope_append_plan_free(loom_rope_append_plan_t *plan);
+void loom_rope_append_plan_get_info(const loom_rope_append_plan_t *plan,
+                                    loom_rope_append_plan_info_t *info);
+
+/* Bf16RopePagedKvAppendArgs / ...TokensArgs, rope/mod.rs:963-1047, plus the
+ * caller-owned validation workspace (u8, plan.workspace_bytes, zero-filled
+ * once; every command leaves it zeroed).  batch_indices/positions are unused
+ * (pass {0,0}) for the one-token form. */
+typedef struct loom_rope_append_args {
+  loom_handle_t query;         /* Read<bf16> [T, Hq, 128] */
+  loom_handle_t key;           /* Read<bf16> [T, Hkv, 128] */
+  loom_handle_t value;         /* Read<bf16> [T, Hkv, 128] */
+  loom_handle_t batch_indices; /* Read<i32>  [T] (explicit form) */
+  loom_handle_t positions;     /* Read<i32>  [T] (explicit form) */
+  loom_handle_t page_indptr;   /* Read<i32>  [B+1] */
+  loom_handle_t page_indices;  /* Read<i32>  [>= B] */
+  loom_handle_t last_page_len; /* Read<i32>  [B] */
+  loom_handle_t query_output;  /* Write<bf16> [T, Hq, 128] */
+  loom_handle_t key_pages;     /* Write<bf16> [pool, 16, Hkv, 128] */
+  loom_handle_t value_pages;   /* Write<bf16> [pool, 16, Hkv, 128] */
+  loom_handle_t workspace;     /* Write<u8> */
+} loom_rope_append_args_t;
+
+/* enqueue_into, rope/mod.rs:758-830 / :846-934: a metadata-validation kernel
+ * (whole page table, batch indices, positions, duplicate physical slots) and
+ * the rotate+scatter kernel, stream ordered.  Invalid device metadata leaves
+ * every output untouched (the reference's sentinel guard). */
+loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
+                                       loom_command_scope_t *scope,
+                                       const loom_rope_append_args_t *args,
+                                       loom_error_t *err);
+
+/* ------------------------------------------------------------------------ */
+/* Graph capture and replay, crates/loom-infer-cuda/src/graph/mod.rs           */
+typedef struct loom_graph_queue loom_graph_queue_t;
+typedef struct loom_captured_graph loom_captured_graph_t;
+typedef struct loom_graph_exec loom_graph_exec_t;
+typedef struct loom_graph_completion loom_graph_completion_t;
+
+/* GraphQueue::new, graph/mod.rs:34-40: a private non-blocking stream. */
+loom_status_t loom_graph_queue_new(int device, uint64_t max_commands,
+                                   loom_graph_queue_t **out, loom_error_t *err);
+void loom_graph_queue_free(loom_graph_queue_t *queue);
+loom_status_t loom_graph_queue_bindings(loom_graph_queue_t *queue, uint64_t capacity,
+                                        loom_bindings_t **out, loom_error_t *err);
+/* GraphQueue::capture split in two C calls (graph/mod.rs:54-131): begin
+ * synchronizes the device, begins thread-local capture on the private stream
+ * and returns an ordinary scope to enqueue into; end_capture finishes the
+ * capture and consumes the queue and the scope. */
+loom_status_t loom_graph_queue_begin_capture(loom_graph_queue_t *queue,
+                                             loom_bindings_t *bindings,
+                                             loom_command_scope_t **scope, loom_error_t *err);
+loom_status_t loom_graph_queue_end_capture(loom_graph_queue_t *queue,
+                                           loom_command_scope_t *scope,
+                                           loom_captured_graph_t **out, loom_error_t *err);
+uint64_t loom_captured_graph_commands(const loom_captured_graph_t *graph);
+void loom_captured_graph_free(loom_captured_graph_t *graph);
+/* CapturedGraph::instantiate, graph/mod.rs:183-206. Consumes the graph. */
+loom_status_t loom_captured_graph_instantiate(loom_captured_graph_t *graph,
+                                              loom_graph_exec_t **out, loom_error_t *err);
+uint64_t loom_graph_exec_commands(const loom_graph_exec_t *exec);
+uint64_t loom_graph_exec_launches(const loom_graph_exec_t *exec);
+/* GraphExec::launch, graph/mod.rs:249-293. */
+loom_status_t loom_graph_exec_launch(loom_graph_exec_t *exec, loom_graph_completion_t **out,
+                                     loom_error_t *err);
+/* GraphExec::measure_launch_ms, graph/mod.rs:301-323 (events created on the
+ * exec's device by the caller, passed as hipEvent_t). */
+loom_status_t loom_graph_exec_measure_launch_ms(loom_graph_exec_t *exec, void *start_event,
+                                                void *end_event, float *ms, loom_error_t *err);
+/* GraphExec::into_bindings, graph/mod.rs:326-339. Consumes the exec. */
+loom_status_t loom_graph_exec_into_bindings(loom_graph_exec_t *exec, loom_bindings_t **out,
+                                            loom_error_t *err);
+void loom_graph_exec_free(loom_graph_exec_t *exec);
+uint64_t loom_graph_completion_launch_index(const loom_graph_completion_t *completion);
+loom_status_t loom_graph_completion_is_complete(loom_graph_completion_t *completion,
+                                                int *complete, loom_error_t *err);
+/* wait consumes the completion. */
+loom_status_t loom_graph_completion_wait(loom_graph_completion_t *completion,
+                                         loom_error_t *err);
+/* Drop: settles the replay. */
+void loom_graph_completion_free(loom_graph_completion_t *completion);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LOOM_INFER_HIP_H */

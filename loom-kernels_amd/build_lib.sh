@@ -1,0 +1,24 @@
+#!/usr/bin/env bash
+# Builds libloom_infer_hip.so (gfx950 only) in-tree:
+#   loom-kernels_amd/lib/libloom_infer_hip.so
+# Every HIP translation unit is compiled with packed FP32 ops disabled.
+set -euo pipefail
+here="$(cd "$(dirname "$0")" && pwd)"
+root="$(cd "$here/.." && pwd)"
+out="$here/lib"
+obj="$here/lib/obj"
+mkdir -p "$obj"
+HIPCC="${HIPCC:-/opt/rocm/bin/hipcc}"
+FLAGS=(--offload-arch=gfx950 -O3 -std=c++17 -fPIC -Wall -Wno-unused-function -Wno-unused-value -Wno-unused-result
+       -Xclang -target-feature -Xclang -packed-fp32-ops
+       -I"$root/include" -I"$here/csrc")
+srcs=(contract.cpp runtime.cpp paged_decode.hip rope_append.hip)
+pids=()
+for s in "${srcs[@]}"; do
+  "$HIPCC" -x hip "${FLAGS[@]}" -c "$here/csrc/$s" -o "$obj/${s%.*}.o" \
+      2> >(grep -v "packed-fp32-ops' is not a recognized feature" >&2) &
+  pids+=($!)
+done
+for p in "${pids[@]}"; do wait "$p"; done
+"$HIPCC" --offload-arch=gfx950 -shared -fPIC "$obj"/*.o -o "$out/libloom_infer_hip.so.tmp"
+mv "$out/libloom_infer_hip.so.tmp" "$out/libloom_infer_hip.so"

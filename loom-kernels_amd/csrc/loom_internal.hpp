@@ -1,0 +1,109 @@
+// Internal types shared by the host layer of libloom_infer_hip.so.
+// Not part of the ABI: include/loom_infer_hip.h is.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "loom_infer_hip.h"
+
+namespace loom {
+
+constexpr uint64_t kHeadDim = LOOM_HEAD_DIM;
+constexpr uint64_t kPageSize = LOOM_PAGE_SIZE;
+constexpr uint64_t kStateWidth = LOOM_PARTIAL_STATE_WIDTH;
+
+// ---- errors ---------------------------------------------------------------
+// Fills `err` (if any) with the variant payload and its Display text and
+// returns `code`.
+loom_status_t fail(loom_error_t *err, loom_status_t code, const char *operand = nullptr,
+                   int64_t f0 = 0, int64_t f1 = 0, int64_t f2 = 0, int64_t f3 = 0,
+                   double value = 0.0, int32_t hip_status = 0);
+inline loom_status_t ok(loom_error_t *err) {
+  if (err) {
+    err->code = LOOM_OK;
+    err->message[0] = 0;
+  }
+  return LOOM_OK;
+}
+
+uint64_t fresh_id();
+
+// ---- command runtime --------------------------------------------------------
+struct Lease {
+  uintptr_t ptr = 0;
+  uint64_t numel = 0;
+  loom_dtype_t dtype = LOOM_DTYPE_U8;
+  bool writable = false;
+  bool vacant = false;
+};
+
+}  // namespace loom
+
+struct loom_bindings {
+  uint64_t queue_id = 0;
+  uint64_t set_id = 0;
+  hipStream_t stream = nullptr;
+  int device = 0;
+  std::vector<loom::Lease> leases;
+  uint64_t capacity = 0;
+  bool moved = false;  // held by a live scope, completion or graph
+};
+
+struct loom_command_queue {
+  uint64_t id = 0;
+  hipStream_t stream = nullptr;
+  int device = 0;
+  hipEvent_t completion_event = nullptr;
+  uint64_t max_commands = 0;
+  uint64_t retained = 0;  // commands submitted and not yet settled
+  bool poisoned = false;
+  bool owns_stream = false;
+  bool active = false;  // a scope or completion borrows the queue (Rust's &mut)
+};
+
+struct loom_command_scope {
+  loom_command_queue *queue = nullptr;
+  loom_bindings *bindings = nullptr;
+  uint64_t scope_id = 0;
+  uint64_t submitted = 0;
+  int32_t submission_error = 0;  // hipError_t of a failed launch, 0 if none
+  bool finished = false;
+  bool capturing = false;
+};
+
+namespace loom {
+
+// Resolution of one command's operands (command/resolve.rs:843-885 plus the
+// element-type and access checks of binding.rs:257-304).
+struct OperandSpec {
+  const char *name;
+  loom_dtype_t dtype;
+  bool write;
+};
+
+// Checks scope health and capacity (submission.rs:154-184) and resolves the
+// handles; on success `out[i]` points at the leases in the scope's bindings.
+loom_status_t resolve_command(loom_command_scope *scope, const loom_handle_t *handles,
+                              const OperandSpec *specs, int count, const Lease **out,
+                              loom_error_t *err);
+// Records one kernel submission (or a failed one, which poisons the scope and
+// the queue: submission.rs:211-279).
+loom_status_t record_launch(loom_command_scope *scope, hipError_t launch_status,
+                            loom_error_t *err);
+
+// submission.rs / completion.rs:165-182: synchronize the stream, then the
+// device; abort when neither proves quiescence.
+hipError_t synchronize_stream_or_abort(hipStream_t stream);
+
+// Device facts used by providers.
+struct DeviceInfo {
+  int device = 0;
+  int cus = 0;
+  bool gfx950 = false;
+};
+loom_status_t query_device(int device, DeviceInfo *out, loom_error_t *err);
+
+}  // namespace loom

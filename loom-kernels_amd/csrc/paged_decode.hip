@@ -1,0 +1,573 @@
+// Paged decode attention for gfx950 (MI355X), BF16 NHD D128 page-16 caches.
+//
+// Semantics: crates/loom-infer/src/attention/paged_decode/mod.rs:287-366 (the
+// CPU reference), with the device metadata guards of
+// crates/loom-infer-cuda/src/attention/decode.rs:224-248 and :430-478 (an
+// invalid request keeps its output sentinels; valid requests complete).
+//
+// Work decomposition (MI355X-first, not the reference's warp-per-head):
+//   * one workgroup (4 wave64) per (KV chunk, kv-head, group tile); a chunk is
+//     `chunk_pages` consecutive pages of one request.  The whole GQA group of
+//     the kv-head (up to 8 query heads per tile) shares every K/V byte, so K/V
+//     is read from HBM once per kv-head instead of once per query head;
+//   * chunk slots are flattened over ragged requests with a workgroup-local
+//     prefix scan of the page table, so the grid depends only on buffer
+//     capacities (graph-replay safe) and every workgroup carries real work;
+//   * per page, S = K·Qᵀ runs on MFMA (v_mfma_f32_16x16x32_bf16: 16 tokens x
+//     16 query columns x 32 dims, 4 issues for D=128); K rows feed the A
+//     operand straight from 16-byte global loads;
+//   * online softmax in the log2 domain (v_exp_f32), P·V on the VALU in FP32
+//     with 16-byte V row loads (16 lanes cover one 256-byte row);
+//   * waves merge through LDS, chunks merge through an FP32 state workspace
+//     [chunk][Hq][130] = (max_log2, normalizer, acc[128]) (the split-K state
+//     layout of crates/loom-infer/src/attention/single_decode/mod.rs:10-13);
+//     the last chunk of a (request, kv-head, tile) to finish merges and writes
+//     O and LSE, then re-zeroes its arrival counter.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "loom_internal.hpp"
+
+using loom::fail;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kMaxChunkPages = 64;
+constexpr uint32_t kPoison = 0x80000000u;
+constexpr uint32_t kCountMask = 0x7fffffffu;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct DecodeArgs {
+  const uint16_t *q;
+  const uint16_t *k;
+  const uint16_t *v;
+  const int32_t *indptr;
+  const int32_t *indices;
+  const int32_t *last;
+  uint16_t *out;
+  float *lse;
+  float *states;       // [max_chunks][hq][130]
+  uint32_t *counters;  // [batch][hkv][group_tiles]
+  int32_t batch;
+  int32_t hq;
+  int32_t hkv;
+  int32_t group;
+  int32_t group_tiles;
+  int32_t chunk_pages;
+  int64_t pool;
+  int64_t n_indices;
+  int64_t grid_slots;  // chunk slots covered by the grid
+  float scale_log2;
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// half::bf16::from_f32 (round to nearest even, quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+
+__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int GT>
+struct Smem {
+  int pages[kMaxChunkPages];
+  float p[kWaves][GT][16];
+  float alpha[kWaves][GT];
+  float wm[kWaves][GT];
+  float wl[kWaves][GT];
+  float wacc[kWaves][GT][128];
+  int wave_tot[kWaves];
+  int req, split, nsplit;
+  long long prefix;
+  int last_flag;
+};
+
+// One page of K and V for one wave: K rows as MFMA A fragments, V rows for the
+// lane's 8-column slice.
+struct PageRegs {
+  u32x4 k[4];
+  u32x4 v[4];
+};
+
+__device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page, int lane,
+                                          int kvh) {
+  const int row = lane & 15, quad = lane >> 4;
+  const int64_t krow = ((int64_t)page * 16 + row) * a.hkv + kvh;
+  const uint16_t *kp = a.k + krow * 128 + quad * 32;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) r.k[c] = load16(kp + c * 8);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t vrow = ((int64_t)page * 16 + quad * 4 + j) * a.hkv + kvh;
+    r.v[j] = load16(a.v + vrow * 128 + row * 8);
+  }
+}
+
+template <int GT>
+__global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeArgs a) {
+  __shared__ Smem<GT> sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, quad = lane >> 4;
+
+  int w = blockIdx.x;
+  const int kvh = w % a.hkv;
+  w /= a.hkv;
+  const int gt = w % a.group_tiles;
+  const long long slot = w / a.group_tiles;
+
+  // ---- global metadata guard (decode.rs:233-246) --------------------------
+  const int32_t ip0 = a.indptr[0];
+  const int32_t ipB = a.indptr[a.batch];
+  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices) return;
+
+  // ---- flattened chunk schedule: prefix scan of chunks per request ---------
+  if (tid == 0) sm.req = -1;
+  long long carry = 0;
+  for (int base = 0; base < a.batch; base += kThreads) {
+    const int r = base + tid;
+    int c = 0;
+    if (r < a.batch) {
+      const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+      const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16;
+      c = valid ? (en - st + a.chunk_pages - 1) / a.chunk_pages : 0;
+    }
+    int x = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) sm.wave_tot[wave] = x;
+    __syncthreads();
+    int before = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      const int t = sm.wave_tot[i];
+      before += (i < wave) ? t : 0;
+      tot += t;
+    }
+    const long long incl = carry + before + x, excl = incl - c;
+    if (c > 0 && slot >= excl && slot < incl) {
+      sm.req = r;
+      sm.split = (int)(slot - excl);
+      sm.nsplit = c;
+      sm.prefix = excl;
+    }
+    carry += tot;
+    __syncthreads();
+  }
+  // More chunks than the grid covers only happens with overlapping request
+  // ranges; such metadata is rejected for the whole batch, consistently in
+  // every workgroup.
+  if (carry > a.grid_slots) return;
+  const int r = sm.req;
+  if (r < 0) return;
+  const int split = sm.split, nsplit = sm.nsplit;
+  const long long prefix = sm.prefix;
+
+  const int32_t req_start = a.indptr[r], req_end = a.indptr[r + 1];
+  const int tail = a.last[r];
+  const int p0 = req_start + split * a.chunk_pages;
+  const int npages = min(a.chunk_pages, req_end - p0);
+  uint32_t *counter = a.counters + ((int64_t)r * a.hkv + kvh) * a.group_tiles + gt;
+
+  // ---- page validation for this chunk (decode.rs:284-289 guard) -----------
+  int bad = 0;
+  if (tid < npages) {
+    const int32_t pg = a.indices[p0 + tid];
+    sm.pages[tid] = pg;
+    bad = (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
+  }
+  bad = __syncthreads_or(bad);
+  if (bad) {
+    if (nsplit > 1 && tid == 0) {
+      atomicOr(counter, kPoison);
+      const uint32_t old = atomicAdd(counter, 1u);
+      if ((old & kCountMask) + 1 == (uint32_t)nsplit) atomicExch(counter, 0u);
+    }
+    return;
+  }
+
+  // ---- Q fragment: column `col` is query head g of this tile -------------
+  const int g_base = gt * GT;
+  const int gcount = min(GT, a.group - g_base);
+  const bool col_valid = col < gcount;
+  u32x4 qf[4];
+  {
+    const int qh = kvh * a.group + g_base + col;
+    const uint16_t *qp = a.q + ((int64_t)r * a.hq + qh) * 128 + quad * 32;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qf[c] = col_valid ? load16(qp + c * 8) : u32x4{0, 0, 0, 0};
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  float acc[GT][8];
+#pragma unroll
+  for (int g = 0; g < GT; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
+
+  auto process = [&](const PageRegs &pr, int page_idx) {
+    const bool last_page = (p0 + page_idx == req_end - 1);
+    const int valid_tokens = last_page ? tail : 16;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pr.k[c]), as_bf16x8(qf[c]), s, 0,
+                                                  0, 0);
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      sv[i] = (quad * 4 + i < valid_tokens) ? s[i] * a.scale_log2 : -INFINITY;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_new);
+    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    m_run = m_new;
+    if (col < GT) {
+      *reinterpret_cast<f32x4 *>(&sm.p[wave][col][quad * 4]) = f32x4{p[0], p[1], p[2], p[3]};
+      if (quad == 0) sm.alpha[wave][col] = alpha;
+    }
+    wave_lds_fence();
+    // P·V: lane (col = 8-column slice, quad = rows 4*quad..4*quad+3)
+    float vf[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = quad * 4 + j < valid_tokens;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t wv = ok ? pr.v[j][e] : 0u;
+        vf[j][2 * e] = bf16_lo(wv);
+        vf[j][2 * e + 1] = bf16_hi(wv);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g < gcount) {
+        const float al = sm.alpha[wave][g];
+        const f32x4 pp = *reinterpret_cast<const f32x4 *>(&sm.p[wave][g][quad * 4]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float t = acc[g][e] * al;
+          t = fmaf(pp[0], vf[0][e], t);
+          t = fmaf(pp[1], vf[1][e], t);
+          t = fmaf(pp[2], vf[2][e], t);
+          t = fmaf(pp[3], vf[3][e], t);
+          acc[g][e] = t;
+        }
+      }
+    }
+    wave_lds_fence();
+  };
+
+  // ---- main loop: pages wave, wave+4, ... with one page of prefetch -------
+  {
+    int i = wave;
+    PageRegs ra, rb;
+    if (i < npages) load_page(ra, a, sm.pages[i], lane, kvh);
+    while (i < npages) {
+      const int inext = i + kWaves;
+      if (inext < npages) load_page(rb, a, sm.pages[inext], lane, kvh);
+      process(ra, i);
+      i = inext;
+      if (i >= npages) break;
+      const int inext2 = i + kWaves;
+      if (inext2 < npages) load_page(ra, a, sm.pages[inext2], lane, kvh);
+      process(rb, i);
+      i = inext2;
+    }
+  }
+
+  // ---- wave reduction over the 4 row quads ---------------------------------
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+#pragma unroll
+  for (int g = 0; g < GT; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = acc[g][e];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      acc[g][e] = x;
+    }
+  if (quad == 0) {
+    if (col < GT) {
+      sm.wm[wave][col] = m_run;
+      sm.wl[wave][col] = l_tot;
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.wacc[wave][g][col * 8 + e] = acc[g][e];
+  }
+  __syncthreads();
+
+  // ---- workgroup merge of the 4 wave states --------------------------------
+  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
+  float *chunk_states = a.states + ((prefix + split) * a.hq) * (int64_t)loom::kStateWidth;
+  for (int idx = tid; idx < GT * 128; idx += kThreads) {
+    const int g = idx >> 7, d = idx & 127;
+    if (g >= gcount) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) M = fmaxf(M, sm.wm[wv][g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const float f = fast_exp2(sm.wm[wv][g] - M);
+      L = fmaf(sm.wl[wv][g], f, L);
+      O = fmaf(sm.wacc[wv][g][d], f, O);
+    }
+    const int64_t qh = qh_base + g;
+    if (nsplit == 1) {
+      a.out[((int64_t)r * a.hq + qh) * 128 + d] = f32_to_bf16(O / L);
+      if (d == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(L);
+    } else {
+      float *st = chunk_states + qh * (int64_t)loom::kStateWidth;
+      if (d == 0) {
+        st[0] = M;
+        st[1] = L;
+      }
+      st[2 + d] = O;
+    }
+  }
+  if (nsplit == 1) return;
+
+  // ---- arrival: the last chunk merges all chunk states --------------------
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = atomicAdd(counter, 1u);
+    int flag = 0;
+    if ((old & kCountMask) + 1 == (uint32_t)nsplit) {
+      flag = (old & kPoison) ? 2 : 1;
+      atomicExch(counter, 0u);
+    }
+    sm.last_flag = flag;
+  }
+  __syncthreads();
+  if (sm.last_flag != 1) return;
+  __threadfence();
+
+  const float *req_states = a.states + (prefix * a.hq) * (int64_t)loom::kStateWidth;
+  const int64_t split_stride = (int64_t)a.hq * loom::kStateWidth;
+  for (int idx = tid; idx < GT * 128; idx += kThreads) {
+    const int g = idx >> 7, d = idx & 127;
+    if (g >= gcount) continue;
+    const int64_t qh = qh_base + g;
+    const float *st = req_states + qh * (int64_t)loom::kStateWidth;
+    float M = -INFINITY;
+    for (int sidx = 0; sidx < nsplit; ++sidx) M = fmaxf(M, st[sidx * split_stride]);
+    float L = 0.f, O = 0.f;
+    for (int sidx = 0; sidx < nsplit; ++sidx) {
+      const float *ss = st + sidx * split_stride;
+      const float f = fast_exp2(ss[0] - M);
+      L = fmaf(ss[1], f, L);
+      O = fmaf(ss[2 + d], f, O);
+    }
+    a.out[((int64_t)r * a.hq + qh) * 128 + d] = f32_to_bf16(O / L);
+    if (d == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(L);
+  }
+}
+
+}  // namespace
+
+// ---- provider / plan / enqueue -----------------------------------------------
+struct loom_decode_provider {
+  loom::DeviceInfo dev;
+};
+
+struct loom_paged_decode_plan {
+  loom_paged_decode_plan_info_t info;
+  int device = 0;
+};
+
+extern "C" {
+
+loom_status_t loom_decode_provider_load(int device, loom_decode_provider_t **out,
+                                        loom_error_t *err) {
+  if (!out) return fail(err, LOOM_NULL_ARGUMENT, "out");
+  loom::DeviceInfo dev;
+  loom_status_t rc = loom::query_device(device, &dev, err);
+  if (rc) return rc;
+  if (!dev.gfx950) return fail(err, LOOM_PLAN_UNSUPPORTED_DEVICE, nullptr, device);
+  auto *p = new loom_decode_provider;
+  p->dev = dev;
+  *out = p;
+  return loom::ok(err);
+}
+
+void loom_decode_provider_free(loom_decode_provider_t *p) { delete p; }
+
+loom_status_t loom_decode_provider_plan_bf16_paged_batch(
+    const loom_decode_provider_t *provider, const loom_paged_decode_spec_t *spec,
+    const loom_paged_decode_plan_options_t *options, loom_paged_decode_plan_t **out,
+    loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  loom_paged_decode_plan_options_t opt{};
+  if (options) opt = *options;
+  const uint64_t B = spec->batch_size, hq = spec->num_query_heads, hkv = spec->num_kv_heads;
+  const uint64_t group = hq / hkv;
+  const uint32_t gtile = group <= 4 ? 4u : 8u;
+  const uint64_t gtiles = (group + gtile - 1) / gtile;
+  const uint64_t max_pages = opt.max_total_pages ? opt.max_total_pages : spec->max_num_pages;
+  if (max_pages < B) return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
+  if (max_pages > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
+
+  // Chunk size: enough (request, kv-head, tile, chunk) workgroups to cover
+  // every CU several times at the expected length, and as long a chunk as
+  // that allows (fewer states to merge).
+  uint32_t chunk = opt.chunk_pages;
+  if (chunk == 0) {
+    const uint64_t expected = opt.expected_kv_len ? opt.expected_kv_len : 4096;
+    const uint64_t pages = (expected + loom::kPageSize - 1) / loom::kPageSize;
+    const uint64_t units = B * hkv * gtiles;
+    const uint64_t target_wgs = 8ull * (uint64_t)provider->dev.cus;
+    const uint64_t splits = std::max<uint64_t>(1, (target_wgs + units - 1) / units);
+    uint64_t c = (pages + splits - 1) / splits;
+    c = (c + 3) / 4 * 4;
+    chunk = (uint32_t)std::min<uint64_t>(kMaxChunkPages, std::max<uint64_t>(4, c));
+  }
+  if (chunk < 4 || chunk > (uint32_t)kMaxChunkPages || chunk % 4 != 0)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "chunk_pages", chunk);
+
+  const uint64_t max_chunks = (max_pages + chunk - 1) / chunk + B;
+  const uint64_t grid = max_chunks * hkv * gtiles;
+  if (grid > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged batch-decode", grid);
+  const uint64_t state_bytes = max_chunks * hq * loom::kStateWidth * 4;
+  const uint64_t counter_bytes = ((B * hkv * gtiles * 4) + 255) / 256 * 256;
+
+  auto *p = new loom_paged_decode_plan;
+  p->device = provider->dev.device;
+  loom_paged_decode_plan_info_t &i = p->info;
+  i.spec = *spec;
+  i.algorithm = LOOM_PAGED_DECODE_SPLIT_KV_GROUP;
+  i.chunk_pages = chunk;
+  i.group_tile = gtile;
+  i.group_tiles = (uint32_t)gtiles;
+  i.max_total_pages = max_pages;
+  i.max_chunks = max_chunks;
+  i.workspace_bytes = counter_bytes + state_bytes;
+  i.block_threads = kThreads;
+  i.device_cus = (uint32_t)provider->dev.cus;
+  *out = p;
+  return loom::ok(err);
+}
+
+void loom_paged_decode_plan_free(loom_paged_decode_plan_t *p) { delete p; }
+
+void loom_paged_decode_plan_get_info(const loom_paged_decode_plan_t *p,
+                                     loom_paged_decode_plan_info_t *info) {
+  if (p && info) *info = p->info;
+}
+
+loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
+                                        loom_command_scope_t *scope,
+                                        const loom_paged_decode_args_t *args,
+                                        loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_paged_decode_plan_info_t &pi = plan->info;
+  const loom_paged_decode_spec_t &s = pi.spec;
+  static const loom::OperandSpec ops[9] = {
+      {"Q", LOOM_DTYPE_BF16, false},           {"K_pages", LOOM_DTYPE_BF16, false},
+      {"V_pages", LOOM_DTYPE_BF16, false},     {"page_indptr", LOOM_DTYPE_I32, false},
+      {"page_indices", LOOM_DTYPE_I32, false}, {"last_page_len", LOOM_DTYPE_I32, false},
+      {"O", LOOM_DTYPE_BF16, true},            {"LSE", LOOM_DTYPE_F32, true},
+      {"workspace", LOOM_DTYPE_U8, true}};
+  const loom_handle_t hs[9] = {args->query,       args->key_pages,     args->value_pages,
+                               args->page_indptr, args->page_indices,  args->last_page_len,
+                               args->output,      args->lse,           args->workspace};
+  const loom::Lease *l[9];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, 9, l, err);
+  if (rc) return rc;
+  // decode.rs:1216-1242: exact lengths before submission.
+  const uint64_t qn = s.batch_size * s.num_query_heads * loom::kHeadDim;
+  const uint64_t kvn = s.max_num_pages * loom::kPageSize * s.num_kv_heads * loom::kHeadDim;
+  const uint64_t want[9] = {qn, kvn, kvn, s.batch_size + 1, 0, s.batch_size, qn,
+                            s.batch_size * s.num_query_heads, pi.workspace_bytes};
+  for (int i = 0; i < 9; ++i) {
+    if (i == 4) {
+      if (l[4]->numel < s.batch_size)
+        return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_SHORT, nullptr, s.batch_size, l[4]->numel);
+      if (l[4]->numel > pi.max_total_pages)
+        return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_LONG, nullptr, pi.max_total_pages,
+                    l[4]->numel);
+      continue;
+    }
+    if (l[i]->numel != want[i])
+      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
+  }
+  // 16-byte vector loads and stores (decode.rs:1243-1251 checks 4 bytes for its
+  // packed pairs; this kernel moves 16 bytes per lane).
+  const int align_ops[5] = {0, 1, 2, 6, 8};
+  for (int i : align_ops)
+    if (l[i]->ptr % 16 != 0)
+      return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, ops[i].name, (int64_t)l[i]->ptr, 16);
+
+  DecodeArgs a;
+  a.q = (const uint16_t *)l[0]->ptr;
+  a.k = (const uint16_t *)l[1]->ptr;
+  a.v = (const uint16_t *)l[2]->ptr;
+  a.indptr = (const int32_t *)l[3]->ptr;
+  a.indices = (const int32_t *)l[4]->ptr;
+  a.last = (const int32_t *)l[5]->ptr;
+  a.out = (uint16_t *)l[6]->ptr;
+  a.lse = (float *)l[7]->ptr;
+  const uint64_t counter_bytes =
+      ((s.batch_size * s.num_kv_heads * pi.group_tiles * 4) + 255) / 256 * 256;
+  a.counters = (uint32_t *)l[8]->ptr;
+  a.states = (float *)(l[8]->ptr + counter_bytes);
+  a.batch = (int32_t)s.batch_size;
+  a.hq = (int32_t)s.num_query_heads;
+  a.hkv = (int32_t)s.num_kv_heads;
+  a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
+  a.group_tiles = (int32_t)pi.group_tiles;
+  a.chunk_pages = (int32_t)pi.chunk_pages;
+  a.pool = (int64_t)s.max_num_pages;
+  a.n_indices = (int64_t)l[4]->numel;
+  a.grid_slots = (int64_t)((l[4]->numel + pi.chunk_pages - 1) / pi.chunk_pages + s.batch_size);
+  a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
+
+  const uint64_t grid = (uint64_t)a.grid_slots * s.num_kv_heads * pi.group_tiles;
+  hipStream_t stream = scope->queue->stream;
+  if (pi.group_tile == 4)
+    hipLaunchKernelGGL(paged_decode_split_kv_kernel<4>, dim3((unsigned)grid), dim3(kThreads), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL(paged_decode_split_kv_kernel<8>, dim3((unsigned)grid), dim3(kThreads), 0,
+                       stream, a);
+  return loom::record_launch(scope, hipGetLastError(), err);
+}
+
+}  // extern "C"

@@ -1,0 +1,412 @@
+// Fused NeoX RoPE + paged K/V append for gfx950, BF16 NHD D128 page-16.
+//
+// Semantics: crates/loom-infer/src/attention/paged_append/mod.rs:360-489 (the
+// CPU reference, one-token and explicit-token forms) via
+// crates/loom-infer/src/rope/mod.rs:136-161 (NeoX split-half rotation), with
+// the all-or-nothing device guard of crates/loom-infer-cuda/src/rope/mod.rs
+// (invalid metadata anywhere leaves every output untouched).
+//
+// MI355X design:
+//   * validation runs once per command, not once per workgroup: a small grid
+//     checks the whole page-index array in parallel; the last workgroup to
+//     arrive checks the request table, every token's (request, position,
+//     slot), sorts the T slot keys in LDS (bitonic) to find duplicate physical
+//     slots in O(T log^2 T), and publishes one validity word;
+//   * the apply kernel runs one workgroup per token: 64 lanes compute the
+//     token's 64 (sin, cos) pairs once into LDS, then 16 lanes per 256-byte
+//     head row rotate Q/K and scatter K/V rows into the page slot with 16-byte
+//     loads and stores;
+//   * inverse frequencies come from the host's powf (the reference's exact
+//     values); angle = pos * inv_freq in FP32; products are rounded separately
+//     (no FMA contraction) as in the Rust reference.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "loom_internal.hpp"
+
+using loom::fail;
+
+namespace {
+
+constexpr int kValidateThreads = 256;
+constexpr int kApplyThreads = 256;
+constexpr int kIndicesPerValidateBlock = 8192;
+constexpr int kMaxSortKeys = LOOM_APPEND_MAX_TOKENS_EXTENDED;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct AppendArgs {
+  const uint16_t *q;
+  const uint16_t *k;
+  const uint16_t *v;
+  const int32_t *batch_indices;  // null: one token per request at kv_len-1
+  const int32_t *positions;
+  const int32_t *indptr;
+  const int32_t *indices;
+  const int32_t *last;
+  uint16_t *q_out;
+  uint16_t *k_pages;
+  uint16_t *v_pages;
+  uint32_t *ws;  // [0] valid flag, [1] bad accumulator, [2] arrivals
+  int32_t tokens;
+  int32_t batch;
+  int32_t hq;
+  int32_t hkv;
+  int64_t pool;
+  int64_t n_indices;
+  float inv_freq[64];
+};
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+
+// Request and token geometry shared by both kernels.  Returns false for any
+// invalid mapping; on success fills the physical slot.
+__device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int *req, int *pos,
+                                           int64_t *page, int *off) {
+  const int r = a.batch_indices ? a.batch_indices[t] : t;
+  if (r < 0 || r >= a.batch) return false;
+  const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+  if (st < 0 || en <= st || (int64_t)en > a.n_indices || tl < 1 || tl > 16) return false;
+  const int kv_len = (en - st - 1) * 16 + tl;
+  const int p = a.batch_indices ? a.positions[t] : kv_len - 1;
+  if (p < 0 || p >= kv_len) return false;
+  const int32_t pg = a.indices[st + p / 16];
+  if (pg < 0 || (int64_t)pg >= a.pool) return false;
+  *req = r;
+  *pos = p;
+  *page = pg;
+  *off = p % 16;
+  return true;
+}
+
+__global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(AppendArgs a) {
+  __shared__ uint32_t keys[kMaxSortKeys];
+  __shared__ int s_last;
+  const int tid = threadIdx.x;
+  uint32_t *flag = a.ws, *bad_acc = a.ws + 1, *arrivals = a.ws + 2;
+
+  // Whole page-index array (rope/mod.rs:143-150): this block's range.
+  int bad = 0;
+  const int64_t lo = (int64_t)blockIdx.x * kIndicesPerValidateBlock;
+  const int64_t hi = min(lo + kIndicesPerValidateBlock, a.n_indices);
+  for (int64_t i = lo + tid; i < hi; i += kValidateThreads) {
+    const int32_t pg = a.indices[i];
+    bad |= (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
+  }
+  bad = __syncthreads_or(bad);
+  if (tid == 0) {
+    if (bad) atomicOr(bad_acc, 1u);
+    __threadfence();
+    const uint32_t old = atomicAdd(arrivals, 1u);
+    s_last = (old + 1 == gridDim.x) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  // Last block: request table (paged_decode/mod.rs:164-205).
+  bad = 0;
+  if (tid == 0) bad |= (a.indptr[0] != 0 || (int64_t)a.indptr[a.batch] != a.n_indices);
+  for (int r = tid; r < a.batch; r += kValidateThreads) {
+    const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+    bad |= (en <= st || tl < 1 || tl > 16) ? 1 : 0;
+  }
+  // Tokens (paged_append/mod.rs:262-309) and their slot keys.
+  int n = 1;
+  while (n < a.tokens) n <<= 1;
+  for (int t = tid; t < n; t += kValidateThreads) {
+    uint32_t key = 0xffffffffu;
+    if (t < a.tokens) {
+      int r, p, off;
+      int64_t pg;
+      if (token_slot(a, t, &r, &p, &pg, &off))
+        key = (uint32_t)(pg * 16 + off);
+      else
+        bad = 1;
+    }
+    keys[t] = key;
+  }
+  bad = __syncthreads_or(bad);
+  // Bitonic sort of the keys; equal neighbours are duplicate physical slots.
+  if (!bad) {
+    for (int size = 2; size <= n; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < n; i += kValidateThreads) {
+          const int j = i ^ stride;
+          if (j > i) {
+            const uint32_t x = keys[i], y = keys[j];
+            const bool up = (i & size) == 0;
+            if ((x > y) == up) {
+              keys[i] = y;
+              keys[j] = x;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    int dup = 0;
+    for (int i = tid; i + 1 < a.tokens; i += kValidateThreads)
+      dup |= (keys[i] == keys[i + 1]) ? 1 : 0;
+    bad = __syncthreads_or(dup);
+  }
+  if (tid == 0) {
+    const uint32_t prior_bad = atomicAdd(bad_acc, 0u);
+    *flag = (bad || prior_bad) ? 0u : 1u;
+    atomicExch(bad_acc, 0u);
+    atomicExch(arrivals, 0u);
+  }
+}
+
+__global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs a) {
+  __shared__ float s_cos[64], s_sin[64];
+  __shared__ int s_ok;
+  const int tid = threadIdx.x;
+  const int t = blockIdx.x;
+  if (tid == 0) s_ok = (__atomic_load_n(a.ws, __ATOMIC_RELAXED) == 1u) ? 1 : 0;
+  __syncthreads();
+  if (!s_ok) return;
+  int r, pos, off;
+  int64_t page;
+  if (!token_slot(a, t, &r, &pos, &page, &off)) return;  // unreachable after validation
+  if (tid < 64) {
+    const float angle = (float)pos * a.inv_freq[tid];
+    // sin/cos of the FP32 angle evaluated in FP64 and rounded once: the
+    // correctly rounded FP32 value, which is what the host C library's sinf /
+    // cosf return for all but rare near-tie inputs.  The reference's rotation
+    // cancels (x1*cos - x2*sin), so a 1-ulp FP32 difference here can move a
+    // small BF16 output by several ulps; matching the rounding avoids that.
+    const double ad = (double)angle;
+    s_sin[tid] = (float)sin(ad);
+    s_cos[tid] = (float)cos(ad);
+  }
+  __syncthreads();
+
+  const int c = tid & 15;
+  const int rows = a.hq + a.hkv;
+  for (int row = tid >> 4; row < rows; row += kApplyThreads / 16) {
+    const uint16_t *src;
+    uint16_t *dst;
+    const bool is_kv = row >= a.hq;
+    int64_t kv_dst = 0;
+    if (!is_kv) {
+      src = a.q + ((int64_t)t * a.hq + row) * 128;
+      dst = a.q_out + ((int64_t)t * a.hq + row) * 128;
+    } else {
+      const int kh = row - a.hq;
+      src = a.k + ((int64_t)t * a.hkv + kh) * 128;
+      kv_dst = ((page * 16 + off) * a.hkv + kh) * 128;
+      dst = a.k_pages + kv_dst;
+    }
+    const u32x4 x = *reinterpret_cast<const u32x4 *>(src + c * 8);
+    const u32x4 xp = *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
+    u32x4 o;
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int elem = c * 8 + e * 2 + h;
+          const int pair = elem & 63;
+          const float self = __uint_as_float(h ? (x[e] & 0xffff0000u) : (x[e] << 16));
+          const float other = __uint_as_float(h ? (xp[e] & 0xffff0000u) : (xp[e] << 16));
+          const float cs = s_cos[pair], sn = s_sin[pair];
+          // first half: first*cos - second*sin; second half: second*cos + first*sin
+          const float y = (c < 8) ? (self * cs - other * sn) : (self * cs + other * sn);
+          packed |= (uint32_t)f32_to_bf16(y) << (16 * h);
+        }
+        o[e] = packed;
+      }
+    }
+    *reinterpret_cast<u32x4 *>(dst + c * 8) = o;
+    if (is_kv) {
+      const int kh = row - a.hq;
+      const u32x4 vv =
+          *reinterpret_cast<const u32x4 *>(a.v + ((int64_t)t * a.hkv + kh) * 128 + c * 8);
+      *reinterpret_cast<u32x4 *>(a.v_pages + kv_dst + c * 8) = vv;
+    }
+  }
+}
+
+}  // namespace
+
+struct loom_rope_provider {
+  loom::DeviceInfo dev;
+};
+
+struct loom_rope_append_plan {
+  loom_rope_append_plan_info_t info;
+  uint64_t max_num_pages = 0;
+  float inv_freq[64];
+};
+
+extern "C" {
+
+loom_status_t loom_rope_provider_load(int device, loom_rope_provider_t **out, loom_error_t *err) {
+  if (!out) return fail(err, LOOM_NULL_ARGUMENT, "out");
+  loom::DeviceInfo dev;
+  loom_status_t rc = loom::query_device(device, &dev, err);
+  if (rc) return rc;
+  if (!dev.gfx950) return fail(err, LOOM_PLAN_UNSUPPORTED_DEVICE, nullptr, device);
+  auto *p = new loom_rope_provider;
+  p->dev = dev;
+  *out = p;
+  return loom::ok(err);
+}
+
+void loom_rope_provider_free(loom_rope_provider_t *p) { delete p; }
+
+static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t tokens,
+                               bool explicit_tokens, loom_rope_append_plan_t **out,
+                               loom_error_t *err) {
+  // rope/mod.rs:628-682: states = tokens * (Hq + Hkv) must fit the grid.
+  uint64_t rows = s.num_query_heads + s.num_kv_heads, states;
+  if (rows < s.num_query_heads || __builtin_mul_overflow(tokens, rows, &states))
+    return fail(err, LOOM_PLAN_STATE_COUNT_OVERFLOW, "RoPE");
+  if (states > (uint64_t)INT32_MAX || tokens > (uint64_t)kMaxSortKeys)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE", states);
+  // Slot keys are page*16+offset in 32 bits.
+  if (s.max_num_pages >= (1ull << 28))
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE page pool", s.max_num_pages);
+  auto *p = new loom_rope_append_plan;
+  p->info.tokens = tokens;
+  p->info.batch_size = s.batch_size;
+  p->info.num_query_heads = s.num_query_heads;
+  p->info.num_kv_heads = s.num_kv_heads;
+  p->info.explicit_tokens = explicit_tokens ? 1 : 0;
+  p->info.workspace_bytes = 256;
+  p->info.validate_blocks = 0;  // depends on the bound page_indices length
+  p->max_num_pages = s.max_num_pages;
+  // rope/mod.rs:148-149 with rope_scale = 1, rope_theta = 1e4, rotary_dim = 128
+  // (paged_append/mod.rs:395-403): the reference's exact FP32 inverse frequencies.
+  for (int i = 0; i < 64; ++i) {
+    const float exponent = 2.0f * (float)i / 128.0f;
+    p->inv_freq[i] = std::pow(10000.0f, -exponent) / 1.0f;
+  }
+  *out = p;
+  return loom::ok(err);
+}
+
+loom_status_t loom_rope_provider_plan_bf16_paged_append(const loom_rope_provider_t *provider,
+                                                        const loom_rope_append_spec_t *spec,
+                                                        loom_rope_append_plan_t **out,
+                                                        loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  return make_plan(spec->paged, spec->paged.batch_size, false, out, err);
+}
+
+loom_status_t loom_rope_provider_plan_bf16_paged_append_tokens(
+    const loom_rope_provider_t *provider, const loom_rope_append_tokens_spec_t *spec,
+    loom_rope_append_plan_t **out, loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  return make_plan(spec->paged, spec->tokens, true, out, err);
+}
+
+void loom_rope_append_plan_free(loom_rope_append_plan_t *p) { delete p; }
+
+void loom_rope_append_plan_get_info(const loom_rope_append_plan_t *p,
+                                    loom_rope_append_plan_info_t *info) {
+  if (p && info) *info = p->info;
+}
+
+loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
+                                       loom_command_scope_t *scope,
+                                       const loom_rope_append_args_t *args, loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_rope_append_plan_info_t &pi = plan->info;
+  const bool ex = pi.explicit_tokens != 0;
+  // Operand order of Bf16RopePagedKvAppend{,Tokens}Args (rope/mod.rs:963-1047).
+  loom::OperandSpec ops[12] = {
+      {"query", LOOM_DTYPE_BF16, false},        {"key", LOOM_DTYPE_BF16, false},
+      {"value", LOOM_DTYPE_BF16, false},        {"batch_indices", LOOM_DTYPE_I32, false},
+      {"positions", LOOM_DTYPE_I32, false},     {"page_indptr", LOOM_DTYPE_I32, false},
+      {"page_indices", LOOM_DTYPE_I32, false},  {"last_page_len", LOOM_DTYPE_I32, false},
+      {"query_output", LOOM_DTYPE_BF16, true},  {"key_pages", LOOM_DTYPE_BF16, true},
+      {"value_pages", LOOM_DTYPE_BF16, true},   {"workspace", LOOM_DTYPE_U8, true}};
+  loom_handle_t hs_all[12] = {args->query,        args->key,           args->value,
+                              args->batch_indices, args->positions,    args->page_indptr,
+                              args->page_indices, args->last_page_len, args->query_output,
+                              args->key_pages,    args->value_pages,   args->workspace};
+  // The one-token form has no batch_indices/positions operands.
+  loom::OperandSpec sel_ops[12];
+  loom_handle_t sel[12];
+  int map[12];
+  int n = 0;
+  for (int i = 0; i < 12; ++i) {
+    if (!ex && (i == 3 || i == 4)) continue;
+    sel_ops[n] = ops[i];
+    sel[n] = hs_all[i];
+    map[i] = n++;
+  }
+  const loom::Lease *l[12];
+  loom_status_t rc = loom::resolve_command(scope, sel, sel_ops, n, l, err);
+  if (rc) return rc;
+  auto L = [&](int i) { return l[map[i]]; };
+  const uint64_t T = pi.tokens, B = pi.batch_size, hq = pi.num_query_heads,
+                 hkv = pi.num_kv_heads;
+  const uint64_t kvn = plan->max_num_pages * loom::kPageSize * hkv * loom::kHeadDim;
+  struct Want {
+    int i;
+    uint64_t n;
+  };
+  const Want wants[] = {{0, T * hq * 128}, {1, T * hkv * 128}, {2, T * hkv * 128},
+                        {3, T},           {4, T},             {5, B + 1},
+                        {7, B},           {8, T * hq * 128},  {9, kvn},
+                        {10, kvn},        {11, pi.workspace_bytes}};
+  for (const Want &w : wants) {
+    if (!ex && (w.i == 3 || w.i == 4)) continue;
+    if (w.i == 7) {  // page_indices precedes last_page_len in the reference order
+      if (L(6)->numel < B)
+        return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_SHORT, nullptr, B, L(6)->numel);
+    }
+    if (L(w.i)->numel != w.n)
+      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[w.i].name, w.n, L(w.i)->numel);
+  }
+  for (int i : {0, 1, 2, 8, 9, 10})
+    if (L(i)->ptr % 16 != 0)
+      return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, ops[i].name, (int64_t)L(i)->ptr, 16);
+
+  AppendArgs a;
+  a.q = (const uint16_t *)L(0)->ptr;
+  a.k = (const uint16_t *)L(1)->ptr;
+  a.v = (const uint16_t *)L(2)->ptr;
+  a.batch_indices = ex ? (const int32_t *)L(3)->ptr : nullptr;
+  a.positions = ex ? (const int32_t *)L(4)->ptr : nullptr;
+  a.indptr = (const int32_t *)L(5)->ptr;
+  a.indices = (const int32_t *)L(6)->ptr;
+  a.last = (const int32_t *)L(7)->ptr;
+  a.q_out = (uint16_t *)L(8)->ptr;
+  a.k_pages = (uint16_t *)L(9)->ptr;
+  a.v_pages = (uint16_t *)L(10)->ptr;
+  a.ws = (uint32_t *)L(11)->ptr;
+  a.tokens = (int32_t)T;
+  a.batch = (int32_t)B;
+  a.hq = (int32_t)hq;
+  a.hkv = (int32_t)hkv;
+  a.pool = (int64_t)plan->max_num_pages;
+  a.n_indices = (int64_t)L(6)->numel;
+  for (int i = 0; i < 64; ++i) a.inv_freq[i] = plan->inv_freq[i];
+
+  const uint64_t vblocks =
+      std::max<uint64_t>(1, (L(6)->numel + kIndicesPerValidateBlock - 1) / kIndicesPerValidateBlock);
+  hipStream_t stream = scope->queue->stream;
+  // One command (one completion slot) of two stream-ordered kernels.
+  hipLaunchKernelGGL(append_validate_kernel, dim3((unsigned)vblocks), dim3(kValidateThreads), 0,
+                     stream, a);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(append_apply_kernel, dim3((unsigned)T), dim3(kApplyThreads), 0, stream, a);
+    e = hipGetLastError();
+  }
+  return loom::record_launch(scope, e, err);
+}
+
+}  // extern "C"

@@ -1,0 +1,157 @@
+"""ctypes declarations for include/loom_infer_hip.h (libloom_infer_hip.so)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libloom_infer_hip.so")
+
+u64, i32, u32, f32, vp = C.c_uint64, C.c_int32, C.c_uint32, C.c_float, C.c_void_p
+
+
+class Error(C.Structure):
+    _fields_ = [("code", i32), ("hip_status", i32), ("operand", C.c_char_p),
+                ("fields", C.c_int64 * 4), ("value", C.c_double), ("message", C.c_char * 256)]
+
+
+class PagedDecodeSpec(C.Structure):
+    _fields_ = [("batch_size", u64), ("max_num_pages", u64), ("num_query_heads", u64),
+                ("num_kv_heads", u64), ("softmax_scale", f32)]
+
+
+class RopeAppendSpec(C.Structure):
+    _fields_ = [("paged", PagedDecodeSpec)]
+
+
+class RopeAppendTokensSpec(C.Structure):
+    _fields_ = [("paged", PagedDecodeSpec), ("tokens", u64), ("max_tokens", u64)]
+
+
+class Handle(C.Structure):
+    _fields_ = [("set_id", u64), ("slot", u64)]
+
+
+class PagedDecodePlanOptions(C.Structure):
+    _fields_ = [("max_total_pages", u64), ("chunk_pages", u32), ("expected_kv_len", u32)]
+
+
+class PagedDecodePlanInfo(C.Structure):
+    _fields_ = [("spec", PagedDecodeSpec), ("algorithm", i32), ("chunk_pages", u32),
+                ("group_tile", u32), ("group_tiles", u32), ("max_total_pages", u64),
+                ("max_chunks", u64), ("workspace_bytes", u64), ("block_threads", u32),
+                ("device_cus", u32)]
+
+
+class PagedDecodeArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key_pages", "value_pages", "page_indptr",
+                                      "page_indices", "last_page_len", "output", "lse",
+                                      "workspace")]
+
+
+class RopeAppendPlanInfo(C.Structure):
+    _fields_ = [("tokens", u64), ("batch_size", u64), ("num_query_heads", u64),
+                ("num_kv_heads", u64), ("explicit_tokens", i32), ("workspace_bytes", u64),
+                ("validate_blocks", u32)]
+
+
+class RopeAppendArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key", "value", "batch_indices", "positions",
+                                      "page_indptr", "page_indices", "last_page_len",
+                                      "query_output", "key_pages", "value_pages", "workspace")]
+
+
+P = C.POINTER
+pi32 = P(i32)
+E = P(Error)
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "loom_abi_version": (u32, []),
+    "loom_status_name": (C.c_char_p, [i32]),
+    "loom_paged_decode_spec_new": (i32, [u64] * 6 + [P(PagedDecodeSpec), E]),
+    "loom_paged_decode_validate_page_table": (
+        i32, [P(PagedDecodeSpec), pi32, u64, pi32, u64, pi32, u64, E]),
+    "loom_paged_decode_request_kv_len": (i32, [P(PagedDecodeSpec), pi32, pi32, u64, P(u64)]),
+    "loom_paged_decode_physical_page_for_token": (
+        i32, [P(PagedDecodeSpec), pi32, pi32, pi32, u64, u64, P(u64), P(u64)]),
+    "loom_rope_append_spec_new": (i32, [u64] * 6 + [P(RopeAppendSpec), E]),
+    "loom_rope_append_validate_page_table": (
+        i32, [P(RopeAppendSpec), pi32, u64, pi32, u64, pi32, u64, E]),
+    "loom_rope_append_tokens_spec_new": (i32, [u64] * 7 + [P(RopeAppendTokensSpec), E]),
+    "loom_rope_append_tokens_spec_new_extended": (i32, [u64] * 7 + [P(RopeAppendTokensSpec), E]),
+    "loom_rope_append_tokens_validate_metadata": (
+        i32, [P(RopeAppendTokensSpec), pi32, u64, pi32, u64, pi32, u64, pi32, u64, pi32, u64,
+              P(u64), E]),
+    "loom_command_queue_new": (i32, [vp, u64, P(vp), E]),
+    "loom_command_queue_free": (None, [vp]),
+    "loom_command_queue_max_commands": (u64, [vp]),
+    "loom_command_queue_is_poisoned": (C.c_int, [vp]),
+    "loom_command_queue_bindings": (i32, [vp, u64, P(vp), E]),
+    "loom_bindings_free": (None, [vp]),
+    "loom_bindings_len": (u64, [vp]),
+    "loom_bindings_capacity": (u64, [vp]),
+    "loom_bindings_bind_read": (i32, [vp, vp, u64, C.c_int, P(Handle), E]),
+    "loom_bindings_bind_read_write": (i32, [vp, vp, u64, C.c_int, P(Handle), E]),
+    "loom_bindings_take_read_write": (i32, [vp, Handle, P(vp), P(u64), E]),
+    "loom_command_queue_begin": (i32, [vp, vp, P(vp), E]),
+    "loom_command_scope_finish": (i32, [vp, P(vp), E]),
+    "loom_command_scope_free": (None, [vp]),
+    "loom_command_scope_submitted": (u64, [vp]),
+    "loom_command_completion_submitted": (u64, [vp]),
+    "loom_command_completion_is_complete": (i32, [vp, P(C.c_int), E]),
+    "loom_command_completion_wait": (i32, [vp, P(vp), E]),
+    "loom_command_completion_free": (None, [vp]),
+    "loom_decode_provider_load": (i32, [C.c_int, P(vp), E]),
+    "loom_decode_provider_free": (None, [vp]),
+    "loom_decode_provider_plan_bf16_paged_batch": (
+        i32, [vp, P(PagedDecodeSpec), P(PagedDecodePlanOptions), P(vp), E]),
+    "loom_paged_decode_plan_free": (None, [vp]),
+    "loom_paged_decode_plan_get_info": (None, [vp, P(PagedDecodePlanInfo)]),
+    "loom_paged_decode_enqueue": (i32, [vp, vp, P(PagedDecodeArgs), E]),
+    "loom_rope_provider_load": (i32, [C.c_int, P(vp), E]),
+    "loom_rope_provider_free": (None, [vp]),
+    "loom_rope_provider_plan_bf16_paged_append": (i32, [vp, P(RopeAppendSpec), P(vp), E]),
+    "loom_rope_provider_plan_bf16_paged_append_tokens": (
+        i32, [vp, P(RopeAppendTokensSpec), P(vp), E]),
+    "loom_rope_append_plan_free": (None, [vp]),
+    "loom_rope_append_plan_get_info": (None, [vp, P(RopeAppendPlanInfo)]),
+    "loom_rope_append_enqueue": (i32, [vp, vp, P(RopeAppendArgs), E]),
+    "loom_graph_queue_new": (i32, [C.c_int, u64, P(vp), E]),
+    "loom_graph_queue_free": (None, [vp]),
+    "loom_graph_queue_bindings": (i32, [vp, u64, P(vp), E]),
+    "loom_graph_queue_begin_capture": (i32, [vp, vp, P(vp), E]),
+    "loom_graph_queue_end_capture": (i32, [vp, vp, P(vp), E]),
+    "loom_captured_graph_commands": (u64, [vp]),
+    "loom_captured_graph_free": (None, [vp]),
+    "loom_captured_graph_instantiate": (i32, [vp, P(vp), E]),
+    "loom_graph_exec_commands": (u64, [vp]),
+    "loom_graph_exec_launches": (u64, [vp]),
+    "loom_graph_exec_launch": (i32, [vp, P(vp), E]),
+    "loom_graph_exec_measure_launch_ms": (i32, [vp, vp, vp, P(f32), E]),
+    "loom_graph_exec_into_bindings": (i32, [vp, P(vp), E]),
+    "loom_graph_exec_free": (None, [vp]),
+    "loom_graph_completion_launch_index": (u64, [vp]),
+    "loom_graph_completion_is_complete": (i32, [vp, P(C.c_int), E]),
+    "loom_graph_completion_wait": (i32, [vp, E]),
+    "loom_graph_completion_free": (None, [vp]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Loads the HIP library; raises if it has not been built (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"libloom_infer_hip.so is not built at {path}; run "
+                "loom-kernels_amd/build_lib.sh (or __graft_entry__.build())")
+        lib = C.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib

@@ -1,0 +1,192 @@
+"""CPU tests of the product C ABI: exports and the host contract layer.
+
+No compute runs here (no GPU in this container): the library is loaded, every
+symbol declared in include/loom_infer_hip.h is resolved, and the host-side
+specifications and metadata validation are checked against the reference's
+unit-test tables and, on random metadata, against the pinned oracle.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "loom_infer_hip.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    import loom_infer_hip as L
+    L.lib()  # raises if the library has not been built
+    return L
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(loom_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(L):
+    import ctypes
+    lib = ctypes.CDLL(L._ffi.LIB_PATH)
+    names = declared_symbols()
+    assert len(names) > 60
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert missing == []
+    # and the Python mirror declares a signature for each of them
+    assert sorted(L._ffi.SIGNATURES) == names
+
+
+def test_abi_version_and_status_names(L):
+    assert L.lib().loom_abi_version() == 1
+    assert L.lib().loom_status_name(14) == b"paged decode request 0 has no KV pages"
+    assert b"capacity" in L.lib().loom_status_name(54)
+
+
+def test_spec_shapes_and_mapping(L):
+    # crates/loom-infer/src/attention/paged_decode/tests.rs:21-51
+    s = L.Bf16PagedBatchDecodeSpec(3, 7, 8, 2, 128, 16)
+    assert (s.batch_size, s.max_num_pages, s.num_query_heads, s.num_kv_heads) == (3, 7, 8, 2)
+    assert (s.head_dim, s.page_size, s.gqa_group_size) == (128, 16, 4)
+    assert [s.kv_head_for_query_head(i) for i in (0, 3, 4, 7, 8)] == [0, 0, 1, 1, None]
+    assert s.query_numel == 3 * 8 * 128 and s.kv_pages_numel == 7 * 16 * 2 * 128
+    assert s.lse_numel == 24 and s.page_indptr_numel == 4 and s.last_page_len_numel == 3
+    assert s.softmax_scale == np.float32(1.0) / np.sqrt(np.float32(128.0))
+
+
+def test_spec_rejections(L):
+    for dims in [(0, 1, 1, 1, 128, 16), (1, 0, 1, 1, 128, 16), (1, 1, 0, 1, 128, 16),
+                 (1, 1, 1, 0, 128, 16), (1, 1, 1, 1, 0, 16), (1, 1, 1, 1, 128, 0)]:
+        with pytest.raises(L.ContractError) as e:
+            L.Bf16PagedBatchDecodeSpec(*dims)
+        assert e.value.variant == "ZeroDimension"
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16PagedBatchDecodeSpec(1, 1, 1, 1, 64, 16)
+    assert (e.value.variant, e.value.fields[:2]) == ("UnsupportedHeadDimension", (128, 64))
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16PagedBatchDecodeSpec(1, 1, 1, 1, 128, 8)
+    assert (e.value.variant, e.value.fields[:2]) == ("UnsupportedPageSize", (16, 8))
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16PagedBatchDecodeSpec(1, 1, 6, 4)
+    assert (e.value.variant, e.value.fields[:2]) == ("InvalidHeadMapping", (6, 4))
+    assert str(e.value) == "query heads must be divisible by KV heads: query=6, KV=4"
+    for dims in [(2 ** 64 - 1, 1, 1, 1), (1, 2 ** 64 - 1, 1, 1)]:
+        with pytest.raises(L.ContractError) as e:
+            L.Bf16PagedBatchDecodeSpec(*dims)
+        assert e.value.variant == "ElementCountOverflow"
+
+
+def test_page_table_known_answers(L):
+    # crates/loom-infer/src/attention/paged_decode/tests.rs:106-133
+    s = L.Bf16PagedBatchDecodeSpec(3, 8, 4, 2)
+    t = s.validate_page_table([0, 2, 3, 6], [5, 1, 7, 2, 0, 6], [3, 16, 1])
+    assert [t.request_kv_len(r) for r in range(4)] == [19, 16, 33, None]
+    f = t.physical_page_for_token
+    assert f(0, 0) == (5, 0) and f(0, 15) == (5, 15) and f(0, 16) == (1, 0)
+    assert f(0, 18) == (1, 2) and f(0, 19) is None and f(1, 15) == (7, 15)
+    assert f(2, 32) == (6, 0) and f(3, 0) is None
+    assert t.request_page_range(1) == (2, 3) and t.request_page_range(3) is None
+
+
+MALFORMED = [
+    # crates/loom-infer/src/attention/paged_decode/tests.rs:135-217
+    (([0, 1], [0, 1], [16, 16]), ("LengthMismatch", "page_indptr", (3, 2, 0, 0))),
+    (([0, 1, 2], [0, 1], [16]), ("LengthMismatch", "last_page_len", (2, 1, 0, 0))),
+    (([1, 2, 3], [0, 1, 2], [16, 16]), ("InvalidPageIndptrStart", None, (1, 0, 0, 0))),
+    (([0, 2, 1], [0], [16, 16]), ("NonMonotonicPageIndptr", None, (1, 2, 1, 0))),
+    (([0, 0, 1], [0], [16, 16]), ("EmptyPagedRequest", None, (0, 0, 0, 0))),
+    (([0, 1, 2], [0, 1], [0, 16]), ("InvalidLastPageLength", None, (0, 0, 16, 0))),
+    (([0, 1, 2], [0, 1], [16, 17]), ("InvalidLastPageLength", None, (1, 17, 16, 0))),
+    (([0, 1, 2], [0], [16, 16]), ("LengthMismatch", "page_indices", (2, 1, 0, 0))),
+    (([0, 1, 2], [-1, 1], [16, 16]), ("PageIndexOutOfRange", None, (0, -1, 4, 0))),
+    (([0, 1, 2], [0, 4], [16, 16]), ("PageIndexOutOfRange", None, (1, 4, 4, 0))),
+]
+
+
+@pytest.mark.parametrize("args,expected", MALFORMED)
+def test_page_table_rejections(L, args, expected):
+    s = L.Bf16PagedBatchDecodeSpec(2, 4, 4, 2)
+    with pytest.raises(L.ContractError) as e:
+        s.validate_page_table(*args)
+    assert (e.value.variant, e.value.operand, e.value.fields) == expected
+
+
+def test_append_contracts_known_answers(L):
+    # crates/loom-infer/src/attention/paged_append/tests.rs:72-84, :185-247
+    s = L.Bf16RopePagedKvAppendSpec(2, 2, 2, 1, 128, 16)
+    with pytest.raises(L.ContractError) as e:
+        s.validate_page_table([0, 1, 2], [1, 1], [4, 4])
+    assert (e.value.variant, e.value.fields) == ("DuplicatePageAppendSlot", (0, 1, 1, 3))
+    ts = L.Bf16RopePagedKvAppendTokensSpec(6, 3, 8, 4, 2, 128, 16)
+    slots = ts.validate_metadata([2, 0, 1, 0, 2, 1], [17, 3, 20, 16, 16, 19], [0, 2, 4, 6],
+                                 [7, 3, 2, 6, 3, 1], [5, 8, 4])
+    assert slots == [(1, 1), (7, 3), (6, 4), (3, 0), (1, 0), (6, 3)]
+    ts = L.Bf16RopePagedKvAppendTokensSpec(2, 2, 4, 2, 1, 128, 16)
+    md = ([0, 2, 4], [3, 1, 3, 2], [4, 4])
+    for bi, pos, want in [([0, 2], [1, 17], ("AppendBatchIndexOutOfRange", (1, 2, 2, 0))),
+                          ([0, 1], [1, 20], ("AppendPositionOutOfRange", (1, 1, 20, 20))),
+                          ([0, 1], [2, 2], ("DuplicatePageAppendTokenSlot", (0, 1, 3, 2)))]:
+        with pytest.raises(L.ContractError) as e:
+            ts.validate_metadata(bi, pos, *md)
+        assert (e.value.variant, e.value.fields) == want
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16RopePagedKvAppendTokensSpec(65, 1, 1, 1, 1, 128, 16)
+    assert (e.value.variant, e.value.fields[:2]) == ("UnsupportedAppendTokenCount", (64, 65))
+    # the extended bulk contract admits the same shape
+    assert L.Bf16RopePagedKvAppendTokensSpec.extended(65, 1, 1, 1, 1).tokens == 65
+    with pytest.raises(L.ContractError):
+        L.Bf16RopePagedKvAppendTokensSpec.extended(8193, 1, 1, 1, 1)
+
+
+def test_duplicate_slot_reporting_matches_oracle_order(L, oracle):
+    """The product finds duplicates with hash maps in O(n); the reference scans
+    pairs.  Random tables with many collisions must report the same pair."""
+    rng = np.random.default_rng(11)
+    for trial in range(200):
+        B = int(rng.integers(2, 12))
+        pool = int(rng.integers(1, 6))
+        pages = rng.integers(1, 3, size=B)
+        indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+        indices = rng.integers(0, pool, size=int(indptr[-1])).astype(np.int32)
+        last = rng.integers(1, 4, size=B).astype(np.int32)
+        s = L.Bf16RopePagedKvAppendSpec(B, pool, 2, 1)
+        os_ = oracle.paged_spec(B, pool, 2, 1)
+        try:
+            oracle.append_validate(os_, indptr, indices, last)
+            want = None
+        except oracle.OracleError as e:
+            want = (e.name, e.fields)
+        try:
+            s.validate_page_table(indptr, indices, last)
+            got = None
+        except L.ContractError as e:
+            got = (e.variant, e.fields)
+        assert got == want, (trial, indptr, indices, last)
+        # explicit tokens: random requests/positions
+        T = int(rng.integers(1, 10))
+        bi = rng.integers(0, B, size=T).astype(np.int32)
+        kv = (pages - 1) * 16 + last
+        pos = np.array([rng.integers(0, kv[b]) for b in bi], np.int32)
+        ts = L.Bf16RopePagedKvAppendTokensSpec(T, B, pool, 2, 1)
+        try:
+            oracle.append_tokens_validate(os_, T, bi, pos, indptr, indices, last)
+            want = None
+        except oracle.OracleError as e:
+            want = (e.name, e.fields)
+        try:
+            ts.validate_metadata(bi, pos, indptr, indices, last)
+            got = None
+        except L.ContractError as e:
+            got = (e.variant, e.fields)
+        assert got == want, (trial, bi, pos)
+
+
+def test_command_errors_before_any_device_work(L):
+    # Queue construction needs a HIP stream; without a GPU the runtime reports a
+    # driver error rather than crashing.
+    with pytest.raises(L.CommandError) as e:
+        L.CommandQueue(0, 0)
+    assert e.value.variant == "ZeroCommandCapacity"

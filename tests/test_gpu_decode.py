@@ -1,0 +1,248 @@
+"""GPU parity of paged decode (libloom_infer_hip.so through the C ABI) against
+the pinned CPU oracle, on the reference's gate fixtures, seeded BASELINE-shaped
+workloads and the reference's negative cases."""
+import json
+import os
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+from gpu_util import (DecodeRunner, bf16_host, compare_decode, nan_bf16, ragged_table,
+                      seeded_normal_bf16, to_dev_bf16, to_dev_i32)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                     "reference_digests.json")))
+
+
+@pytest.fixture(scope="module")
+def L():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import loom_infer_hip as L
+    return L
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("case", GOLDEN["paged_decode"]["cases"], ids=lambda c: c["name"])
+def test_gate_fixtures(L, oracle, case):
+    # crates/loom-infer-validation/src/gates/paged_batch_decode.rs:316-358
+    log(f"decode gate fixture {case['name']}")
+    salt = int(case["salt"], 16)
+    B, pool, hq, hkv = case["batch"], case["pool"], case["hq"], case["hkv"]
+    q = oracle.deterministic_bf16(B * hq * 128, salt)
+    k = oracle.deterministic_bf16(pool * 16 * hkv * 128, salt ^ 0x4B455900)
+    v = oracle.deterministic_bf16(pool * 16 * hkv * 128, salt ^ 0x5641_4C55_4500)
+    s = oracle.paged_spec(B, pool, hq, hkv)
+    ref_out, ref_lse = oracle.paged_decode(s, q, k, v, case["indptr"], case["indices"],
+                                           case["last"])
+    for chunk in (0, 4):
+        r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=chunk)
+        out, lse = r.run(q, k, v, case["indptr"], case["indices"], case["last"])
+        stats = compare_decode(oracle, out, lse, ref_out, ref_lse)
+        log(f"  chunk={r.plan.info.chunk_pages} {stats}")
+
+
+SHAPES = [
+    # (name, B, hq, hkv, lens, chunk)
+    ("mha_c1_like", 1, 32, 32, [1024], 0),
+    ("gqa4_ragged", 6, 32, 8, [1, 15, 16, 17, 700, 2049], 0),
+    ("gqa4_ragged_chunk4", 6, 32, 8, [1, 15, 16, 17, 700, 2049], 4),
+    ("gqa4_ragged_chunk64", 5, 32, 8, [3000, 33, 4097, 1, 64], 64),
+    ("gqa8_long", 1, 64, 8, [8192], 0),
+    ("mqa_group8", 3, 8, 1, [16, 23, 48], 0),
+    ("group16_two_tiles", 2, 16, 1, [300, 77], 0),
+    ("group3", 3, 6, 2, [5, 40, 129], 4),
+    ("group2", 2, 4, 2, [33, 1000], 0),
+]
+
+
+@pytest.mark.parametrize("name,B,hq,hkv,lens,chunk", SHAPES, ids=[s[0] for s in SHAPES])
+def test_seeded_shapes(L, oracle, name, B, hq, hkv, lens, chunk):
+    log(f"decode seeded shape {name} B={B} hq={hq} hkv={hkv} lens={lens} chunk={chunk}")
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    pool = sum((x + 15) // 16 for x in lens) + 3
+    indptr, indices, last = ragged_table(rng, lens, pool)
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    s = oracle.paged_spec(B, pool, hq, hkv)
+    ref_out, ref_lse = oracle.paged_decode(s, q, k, v, indptr, indices, last)
+    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=chunk)
+    out, lse = r.run(q, k, v, indptr, indices, last)
+    log(f"  plan chunk={r.plan.info.chunk_pages} tile={r.plan.info.group_tile}x"
+        f"{r.plan.info.group_tiles} {compare_decode(oracle, out, lse, ref_out, ref_lse)}")
+    # the arrival counters are left at zero for the next call
+    ws = r.workspace.cpu().numpy()
+    ncnt = B * hkv * r.plan.info.group_tiles * 4
+    assert not ws[:ncnt].any()
+    out2, lse2 = r.run(q, k, v, indptr, indices, last)
+    assert np.array_equal(out2, out) and np.array_equal(lse2, lse)
+
+
+def test_closed_form_zero_query(L, oracle):
+    # Q = 0: O = mean(V) exactly representable inputs, LSE = log2(kv_len)
+    B, hq, hkv, pool = 2, 8, 2, 12
+    lens = [16, 160]
+    rng = np.random.default_rng(3)
+    indptr, indices, last = ragged_table(rng, lens, pool)
+    q = np.zeros(B * hq * 128, np.uint16)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = oracle.bf16_from_f32(rng.integers(-4, 5, pool * 16 * hkv * 128).astype(np.float32))
+    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=4)
+    out, lse = r.run(q, k, v, indptr, indices, last)
+    np.testing.assert_allclose(lse, np.repeat(np.log2(lens), hq), atol=2e-6)
+    ref_out, _ = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v, indptr,
+                                     indices, last)
+    assert np.array_equal(out, ref_out)
+
+
+def test_invalid_page_guard_preserves_sentinels(L):
+    # crates/loom-infer-validation/src/gates/paged_batch_decode.rs:224-308
+    torch = pytest.importorskip("torch")
+    r = DecodeRunner(L, 2, 2, 4, 2)
+    z = torch.zeros(r.spec.kv_pages_numel, dtype=torch.bfloat16, device="cuda")
+    q = torch.zeros(r.spec.query_numel, dtype=torch.bfloat16, device="cuda")
+    out, lse = r.run_dev(q, z, z.clone(), to_dev_i32([0, 1, 2]), to_dev_i32([0, 2]),
+                         to_dev_i32([16, 16]))
+    o = out.float().cpu().numpy()
+    l = lse.cpu().numpy()
+    assert np.all(o[:4 * 128] == 0.0) and np.all(l[:4] == 4.0)
+    assert np.all(np.isnan(o[4 * 128:])) and np.all(np.isnan(l[4:]))
+
+
+def test_invalid_metadata_multi_chunk_keeps_counters_clean(L, oracle):
+    """An invalid page inside a long request (several chunks) leaves that
+    request's sentinels, completes the others, and leaves the workspace ready."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    lens = [600, 300]
+    pool = 64
+    indptr, indices, last = ragged_table(rng, lens, pool)
+    bad = indices.copy()
+    bad[20] = pool + 5  # inside request 0, chunk 5 at chunk_pages=4
+    B, hq, hkv = 2, 8, 2
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=4)
+    out, lse = r.run(q, k, v, indptr, bad, last)
+    o = oracle.bf16_to_f32(out).reshape(B, hq * 128)
+    assert np.all(np.isnan(o[0])) and np.all(np.isnan(lse[:hq]))
+    ref_out, ref_lse = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v,
+                                           indptr, indices, last)
+    compare_decode(oracle, out.reshape(B, -1)[1], lse[hq:], ref_out.reshape(B, -1)[1],
+                   ref_lse[hq:])
+    ncnt = B * hkv * r.plan.info.group_tiles * 4
+    assert not r.workspace.cpu().numpy()[:ncnt].any()
+    out2, lse2 = r.run(q, k, v, indptr, indices, last)
+    compare_decode(oracle, out2, lse2, ref_out, ref_lse)
+
+
+def test_global_indptr_guard(L):
+    torch = pytest.importorskip("torch")
+    r = DecodeRunner(L, 2, 4, 4, 2)
+    z = torch.zeros(r.spec.kv_pages_numel, dtype=torch.bfloat16, device="cuda")
+    q = torch.zeros(r.spec.query_numel, dtype=torch.bfloat16, device="cuda")
+    # indptr[B] != len(page_indices): every request keeps its sentinels
+    out, lse = r.run_dev(q, z, z.clone(), to_dev_i32([0, 1, 2]), to_dev_i32([0, 1, 2]),
+                         to_dev_i32([16, 16]))
+    assert torch.isnan(out.float()).all() and torch.isnan(lse).all()
+
+
+def test_short_indptr_rejected_before_submission(L):
+    # crates/loom-infer-validation/src/gates/paged_batch_decode.rs:150-222
+    torch = pytest.importorskip("torch")
+    r = DecodeRunner(L, 2, 2, 4, 2)
+    s = r.spec
+    z = torch.zeros(s.kv_pages_numel, dtype=torch.bfloat16, device="cuda")
+    q = torch.zeros(s.query_numel, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(s.output_numel, dtype=torch.bfloat16, device="cuda")
+    lse = torch.zeros(s.lse_numel, dtype=torch.float32, device="cuda")
+    b, h = r.bindings(q, z, z.clone(), to_dev_i32([0, 1]), to_dev_i32([0, 0]),
+                      to_dev_i32([16, 16]), out, lse)
+    scope = r.queue.begin(b)
+    with pytest.raises(L.EnqueueError) as e:
+        r.plan.enqueue_into(scope, r.args(h))
+    assert (e.value.variant, e.value.operand, e.value.fields[:2]) == (
+        "LengthMismatch", "page_indptr", (3, 2))
+    comp = scope.finish()
+    assert comp.submitted() == 0
+    comp.wait()
+
+
+def test_command_runtime_checks(L):
+    torch = pytest.importorskip("torch")
+    r = DecodeRunner(L, 1, 1, 1, 1)
+    s = r.spec
+    x = torch.zeros(s.kv_pages_numel, dtype=torch.bfloat16, device="cuda")
+    b = r.queue.bindings(2)
+    h = b.bind_read_write(x)
+    with pytest.raises(L.CommandError) as e:
+        b.bind_read(x)  # overlaps a read-write lease
+    assert e.value.variant == "AliasedBinding"
+    b.bind_read(torch.zeros(4, dtype=torch.int32, device="cuda"))
+    with pytest.raises(L.CommandError) as e:
+        b.bind_read(torch.zeros(4, dtype=torch.int32, device="cuda"))
+    assert e.value.variant == "BindingCapacityExceeded"
+    with pytest.raises(L.CommandError) as e:
+        b.bind_read(torch.zeros(4, dtype=torch.int32))  # host memory
+    assert e.value.variant in ("BufferContextMismatch", "BindingCapacityExceeded")
+    assert b.take_read_write(h) is x
+    with pytest.raises(L.CommandError) as e:
+        b.take_read_write(h)
+    assert e.value.variant == "BindingSlotVacant"
+    other = r.queue.bindings(1)
+    scope = r.queue.begin(other)
+    with pytest.raises(L.CommandError) as e:
+        r.queue.begin(r.queue.bindings(1))  # one live scope per queue (Rust's &mut)
+    assert e.value.variant == "ScopeActive"
+    comp = scope.finish()
+    comp.wait()
+
+
+def test_full_c3_shape_sampled_requests(L, oracle):
+    """BASELINE config 3 at full size (64 requests, ragged 512..8192, GQA4, pool
+    65536): every request of a random sample is checked against the oracle and
+    the whole output is finite with LSE >= the max-score bound."""
+    torch = pytest.importorskip("torch")
+    log("decode full C3 shape")
+    rng = np.random.default_rng(0)
+    B, hq, hkv, pool = 64, 32, 8, 65536
+    lens = rng.integers(512, 8193, size=B)
+    pages = (lens + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
+    last = (lens - (pages - 1) * 16).astype(np.int32)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    q = torch.randn(B * hq * 128, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(pool * 16 * hkv * 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(pool * 16 * hkv * 128, generator=g, device="cuda").to(torch.bfloat16)
+    r = DecodeRunner(L, B, pool, hq, hkv, expected_kv_len=4352)
+    out, lse = r.run_dev(q, k, v, to_dev_i32(indptr), to_dev_i32(indices), to_dev_i32(last))
+    out_h, lse_h = bf16_host(out), lse.cpu().numpy()
+    assert np.all(np.isfinite(oracle.bf16_to_f32(out_h)))
+    sample = sorted(rng.choice(B, size=3, replace=False))
+    # host copies of only the pages the sampled requests use
+    s = oracle.paged_spec(1, pool, hq, hkv)
+    kk, vv = k.view(pool, -1), v.view(pool, -1)
+    for rq in sample:
+        pg = indices[indptr[rq]:indptr[rq + 1]]
+        sub_pool = len(pg)
+        kh = bf16_host(kk[torch.from_numpy(pg.astype(np.int64)).cuda()].reshape(-1))
+        vh = bf16_host(vv[torch.from_numpy(pg.astype(np.int64)).cuda()].reshape(-1))
+        qh = bf16_host(q[rq * hq * 128:(rq + 1) * hq * 128])
+        ss = oracle.paged_spec(1, sub_pool, hq, hkv)
+        ref_o, ref_l = oracle.paged_decode(ss, qh, kh, vh, [0, sub_pool],
+                                           np.arange(sub_pool, dtype=np.int32), [last[rq]])
+        st = compare_decode(oracle, out_h[rq * hq * 128:(rq + 1) * hq * 128],
+                            lse_h[rq * hq:(rq + 1) * hq], ref_o, ref_l)
+        log(f"  request {rq} len {lens[rq]}: {st}")

@@ -1,0 +1,143 @@
+"""hipGraph fixed-address capture and replay of the decode step (graph/mod.rs),
+checked replay by replay against eager execution and the oracle."""
+import sys
+
+import numpy as np
+import pytest
+
+from gpu_util import (DecodeRunner, bf16_host, compare_decode, ragged_table,
+                      seeded_normal_bf16, to_dev_bf16, to_dev_i32)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def L():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import loom_infer_hip as L
+    return L
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def test_decode_graph_replays_match_eager_and_oracle(L, oracle):
+    """Replays with eager work and host synchronization between them; every
+    replay is compared with the eager result (no memset nodes are captured; the
+    workspace counters are re-zeroed by the kernel itself)."""
+    import torch
+    log("graph decode replay")
+    rng = np.random.default_rng(21)
+    B, hq, hkv = 5, 32, 8
+    lens = [40, 1000, 17, 3000, 256]
+    pool = sum((x + 15) // 16 for x in lens) + 8
+    indptr, indices, last = ragged_table(rng, lens, pool)
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    ref_o, ref_l = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v, indptr,
+                                       indices, last)
+    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=4)
+    eager_o, eager_l = r.run(q, k, v, indptr, indices, last)
+    compare_decode(oracle, eager_o, eager_l, ref_o, ref_l)
+
+    tq, tk, tv = to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v)
+    tip, tix, tln = to_dev_i32(indptr), to_dev_i32(indices), to_dev_i32(last)
+    out = torch.full((B * hq * 128,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    lse = torch.full((B * hq,), float("nan"), dtype=torch.float32, device="cuda")
+    gq = L.GraphQueue(0, 1)
+    b = gq.bindings(9)
+    h = [b.bind_read(tq), b.bind_read(tk), b.bind_read(tv), b.bind_read(tip),
+         b.bind_read(tix), b.bind_read(tln), b.bind_read_write(out), b.bind_read_write(lse),
+         b.bind_read_write(r.workspace)]
+    args = L.Bf16PagedBatchDecodeArgs(h[0], h[1], h[2], h[3], h[4], h[5], h[6].write(),
+                                      h[7].write(), h[8].write())
+    graph = gq.capture(b, lambda scope: r.plan.enqueue_into(scope, args))
+    assert graph.commands() == 1
+    # external owners dropped before replay: the graph's bindings keep them alive
+    del tq, tk, tv, tip, tix, tln
+    exec_ = graph.instantiate()
+    for i in range(1, 4):
+        out.fill_(float("nan"))  # eager work between replays
+        torch.cuda.synchronize()
+        c = exec_.launch()
+        assert c.launch_index() == i
+        with pytest.raises(L.GraphError) as e:
+            exec_.launch()
+        assert e.value.variant == "ReplayInFlight"
+        c.wait()
+        assert np.array_equal(bf16_host(out), eager_o), f"replay {i}"
+        assert np.array_equal(lse.cpu().numpy(), eager_l), f"replay {i}"
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    ms = exec_.measure_launch_ms(start, end)
+    assert ms > 0
+    assert exec_.launches() == 4 and exec_.commands() == 1
+    b = exec_.into_bindings()
+    assert b.take_read_write(h[6]) is out
+
+
+def test_full_decode_step_graph(L, oracle):
+    """RoPE + 1-token append followed by paged decode, captured as one graph
+    (BASELINE config 5 at reduced batch): replays reproduce the eager step."""
+    import torch
+    log("graph full decode step")
+    rng = np.random.default_rng(55)
+    B, hq, hkv = 8, 32, 8
+    lens = np.clip(np.round(np.exp(np.log(2048) + 0.8 * rng.standard_normal(B))), 16,
+                   16384).astype(int)
+    pool = int(sum((x + 15) // 16 for x in lens)) + 16
+    indptr, indices, last = ragged_table(rng, list(lens), pool)
+    qn = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    kn = seeded_normal_bf16(oracle, rng, B * hkv * 128)
+    vn = seeded_normal_bf16(oracle, rng, B * hkv * 128)
+    kp = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    vp = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    # oracle step: append then decode with the rotated query
+    s = oracle.paged_spec(B, pool, hq, hkv)
+    ekp, evp = kp.copy(), vp.copy()
+    eq = oracle.append(s, qn, kn, vn, indptr, indices, last, ekp, evp)
+    ref_o, ref_l = oracle.paged_decode(s, eq, ekp, evp, indptr, indices, last)
+
+    dec = DecodeRunner(L, B, pool, hq, hkv)
+    ap = L.RopeProvider.load(0).plan_bf16_paged_append(L.Bf16RopePagedKvAppendSpec(B, pool, hq, hkv))
+    aws = torch.zeros(ap.workspace_bytes, dtype=torch.uint8, device="cuda")
+    t = dict(q=to_dev_bf16(qn), k=to_dev_bf16(kn), v=to_dev_bf16(vn), kp=to_dev_bf16(kp),
+             vp=to_dev_bf16(vp), ip=to_dev_i32(indptr), ix=to_dev_i32(indices),
+             ln=to_dev_i32(last))
+    qrot = torch.empty(B * hq * 128, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(B * hq * 128, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(B * hq, dtype=torch.float32, device="cuda")
+    gq = L.GraphQueue(0, 2)
+    b = gq.bindings(16)
+    hq_, hk, hv = b.bind_read(t["q"]), b.bind_read(t["k"]), b.bind_read(t["v"])
+    hip_, hix, hln = b.bind_read(t["ip"]), b.bind_read(t["ix"]), b.bind_read(t["ln"])
+    hqr = b.bind_read_write(qrot)
+    hkp, hvp = b.bind_read_write(t["kp"]), b.bind_read_write(t["vp"])
+    haws = b.bind_read_write(aws)
+    ho, hl, hws = b.bind_read_write(out), b.bind_read_write(lse), b.bind_read_write(dec.workspace)
+    a_args = L.Bf16RopePagedKvAppendArgs(hq_, hk, hv, hip_, hix, hln, hqr.write(), hkp.write(),
+                                         hvp.write(), haws.write())
+    d_args = L.Bf16PagedBatchDecodeArgs(hqr.read(), hkp.read(), hvp.read(), hip_, hix, hln,
+                                        ho.write(), hl.write(), hws.write())
+
+    def record(scope):
+        ap.enqueue_into(scope, a_args)
+        dec.plan.enqueue_into(scope, d_args)
+
+    exec_ = gq.capture(b, record).instantiate()
+    assert exec_.commands() == 2
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        exec_.launch().wait()
+        o, l = bf16_host(out), lse.cpu().numpy()
+        st = compare_decode(oracle, o, l, ref_o, ref_l)
+        log(f"  replay {i}: {st}")
+        if i == 0:
+            first = (o, l)
+        else:
+            assert np.array_equal(o, first[0]) and np.array_equal(l, first[1])
+    exec_.into_bindings()
