@@ -337,7 +337,7 @@ typedef struct loom_paged_decode_plan_info {
   uint32_t group_tiles;      /* ceil(group / group_tile) */
   uint64_t max_total_pages;
   uint64_t max_chunks;       /* state slots: ceil(max_total_pages/chunk_pages)+batch */
-  uint64_t workspace_bytes;  /* states + per-(request, kv-head, tile) counters */
+  uint64_t workspace_bytes;  /* max_chunks * Hq * 130 FP32 states */
   uint32_t block_threads;
   uint32_t device_cus;
 } loom_paged_decode_plan_info_t;
@@ -353,8 +353,8 @@ void loom_paged_decode_plan_get_info(const loom_paged_decode_plan_t *plan,
                                      loom_paged_decode_plan_info_t *info);
 
 /* Bf16PagedBatchDecodeArgs, decode.rs:1452-1487, plus the caller-owned
- * workspace (u8, exactly plan.workspace_bytes, zero-filled once before its
- * first use; every command leaves it zeroed again). */
+ * split-KV state workspace (u8, exactly plan.workspace_bytes; no
+ * initialization needed, contents are scratch between commands). */
 typedef struct loom_paged_decode_args {
   loom_handle_t query;         /* Read<bf16>  [B, Hq, 128] */
   loom_handle_t key_pages;     /* Read<bf16>  [pool, 16, Hkv, 128] */
@@ -367,7 +367,9 @@ typedef struct loom_paged_decode_args {
   loom_handle_t workspace;     /* Write<u8>   [workspace_bytes] */
 } loom_paged_decode_args_t;
 
-/* Bf16PagedBatchDecodePlan::enqueue_into, decode.rs:1199-1296: one kernel. */
+/* Bf16PagedBatchDecodePlan::enqueue_into, decode.rs:1199-1296: one command of
+ * two stream-ordered kernels (split-KV partials, then the merge of requests
+ * longer than one chunk). */
 loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
                                         loom_command_scope_t *scope,
                                         const loom_paged_decode_args_t *args,

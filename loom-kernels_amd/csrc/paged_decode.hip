@@ -18,11 +18,14 @@
 //     operand straight from 16-byte global loads;
 //   * online softmax in the log2 domain (v_exp_f32), P·V on the VALU in FP32
 //     with 16-byte V row loads (16 lanes cover one 256-byte row);
-//   * waves merge through LDS, chunks merge through an FP32 state workspace
-//     [chunk][Hq][130] = (max_log2, normalizer, acc[128]) (the split-K state
-//     layout of crates/loom-infer/src/attention/single_decode/mod.rs:10-13);
-//     the last chunk of a (request, kv-head, tile) to finish merges and writes
-//     O and LSE, then re-zeroes its arrival counter.
+//   * waves merge through LDS; a request that fits one chunk is finished in
+//     place.  Longer requests leave one FP32 state per (chunk, query head) in
+//     the workspace [chunk][Hq][130] = (max_log2, normalizer, acc[128]) (the
+//     split-K state layout of crates/loom-infer/src/attention/single_decode/
+//     mod.rs:10-13) and a second, stream-ordered merge kernel combines them.
+//     The kernel boundary makes the states visible across the 8 XCD L2s; an
+//     in-kernel last-arriver merge would need an agent-scope release per
+//     workgroup, i.e. an L2 write-back, which costs more than the launch.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -37,8 +40,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kMaxChunkPages = 64;
-constexpr uint32_t kPoison = 0x80000000u;
-constexpr uint32_t kCountMask = 0x7fffffffu;
+// Normalizer written into the states of a chunk whose pages failed the guard.
+constexpr float kPoisonNormalizer = -1.0f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -53,8 +56,7 @@ struct DecodeArgs {
   const int32_t *last;
   uint16_t *out;
   float *lse;
-  float *states;       // [max_chunks][hq][130]
-  uint32_t *counters;  // [batch][hkv][group_tiles]
+  float *states;  // [max_chunks][hq][130]
   int32_t batch;
   int32_t hq;
   int32_t hkv;
@@ -103,7 +105,6 @@ struct Smem {
   int wave_tot[kWaves];
   int req, split, nsplit;
   long long prefix;
-  int last_flag;
 };
 
 // One page of K and V for one wave: K rows as MFMA A fragments, V rows for the
@@ -193,7 +194,6 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
   const int tail = a.last[r];
   const int p0 = req_start + split * a.chunk_pages;
   const int npages = min(a.chunk_pages, req_end - p0);
-  uint32_t *counter = a.counters + ((int64_t)r * a.hkv + kvh) * a.group_tiles + gt;
 
   // ---- page validation for this chunk (decode.rs:284-289 guard) -----------
   int bad = 0;
@@ -203,18 +203,22 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
     bad = (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
   }
   bad = __syncthreads_or(bad);
+  const int g_base = gt * GT;
+  const int gcount = min(GT, a.group - g_base);
   if (bad) {
-    if (nsplit > 1 && tid == 0) {
-      atomicOr(counter, kPoison);
-      const uint32_t old = atomicAdd(counter, 1u);
-      if ((old & kCountMask) + 1 == (uint32_t)nsplit) atomicExch(counter, 0u);
+    // The request keeps its output sentinels: a single-chunk request simply
+    // writes nothing; a multi-chunk one marks this chunk's states so the
+    // merge kernel skips the whole request.
+    if (nsplit > 1 && tid < gcount) {
+      const int64_t qh = (int64_t)kvh * a.group + g_base + tid;
+      float *st = a.states + ((prefix + split) * a.hq + qh) * (int64_t)loom::kStateWidth;
+      st[0] = 0.0f;
+      st[1] = kPoisonNormalizer;
     }
     return;
   }
 
   // ---- Q fragment: column `col` is query head g of this tile -------------
-  const int g_base = gt * GT;
-  const int gcount = min(GT, a.group - g_base);
   const bool col_valid = col < gcount;
   u32x4 qf[4];
   {
@@ -258,52 +262,56 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
       if (quad == 0) sm.alpha[wave][col] = alpha;
     }
     wave_lds_fence();
-    // P·V: lane (col = 8-column slice, quad = rows 4*quad..4*quad+3)
-    float vf[4][8];
+    // P·V on lane (col = 8-column slice, quad = rows 4*quad..4*quad+3).  Columns
+    // of the tile beyond the group carry finite junk and are never stored.
+    f32x4 pp[GT];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const float al = sm.alpha[wave][g];
+      pp[g] = *reinterpret_cast<const f32x4 *>(&sm.p[wave][g][quad * 4]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= al;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bool ok = quad * 4 + j < valid_tokens;
+      float vf[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t wv = ok ? pr.v[j][e] : 0u;
-        vf[j][2 * e] = bf16_lo(wv);
-        vf[j][2 * e + 1] = bf16_hi(wv);
+        vf[2 * e] = bf16_lo(wv);
+        vf[2 * e + 1] = bf16_hi(wv);
       }
-    }
 #pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      if (g < gcount) {
-        const float al = sm.alpha[wave][g];
-        const f32x4 pp = *reinterpret_cast<const f32x4 *>(&sm.p[wave][g][quad * 4]);
+      for (int g = 0; g < GT; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float t = acc[g][e] * al;
-          t = fmaf(pp[0], vf[0][e], t);
-          t = fmaf(pp[1], vf[1][e], t);
-          t = fmaf(pp[2], vf[2][e], t);
-          t = fmaf(pp[3], vf[3][e], t);
-          acc[g][e] = t;
-        }
-      }
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pp[g][j], vf[e], acc[g][e]);
     }
     wave_lds_fence();
   };
 
-  // ---- main loop: pages wave, wave+4, ... with one page of prefetch -------
-  {
-    int i = wave;
-    PageRegs ra, rb;
-    if (i < npages) load_page(ra, a, sm.pages[i], lane, kvh);
-    while (i < npages) {
-      const int inext = i + kWaves;
-      if (inext < npages) load_page(rb, a, sm.pages[inext], lane, kvh);
-      process(ra, i);
-      i = inext;
-      if (i >= npages) break;
-      const int inext2 = i + kWaves;
-      if (inext2 < npages) load_page(ra, a, sm.pages[inext2], lane, kvh);
-      process(rb, i);
-      i = inext2;
+  // ---- main loop: pages wave, wave+4, ... of this chunk, three-deep ---------
+  // Every iteration issues the loads of the page two steps ahead before it
+  // consumes the current one.  Loads are unconditional (the index is clamped to
+  // the wave's last page) so the compiler can wait for exactly the oldest
+  // page's loads instead of draining the queue.
+  const int my_pages = npages > wave ? (npages - wave + kWaves - 1) / kWaves : 0;
+  if (my_pages > 0) {
+    auto page_of = [&](int it) { return sm.pages[wave + kWaves * min(it, my_pages - 1)]; };
+    PageRegs b0, b1, b2;
+    load_page(b0, a, page_of(0), lane, kvh);
+    load_page(b1, a, page_of(1), lane, kvh);
+    int it = 0;
+    while (true) {
+      load_page(b2, a, page_of(it + 2), lane, kvh);
+      process(b0, wave + kWaves * it);
+      if (++it >= my_pages) break;
+      load_page(b0, a, page_of(it + 2), lane, kvh);
+      process(b1, wave + kWaves * it);
+      if (++it >= my_pages) break;
+      load_page(b1, a, page_of(it + 2), lane, kvh);
+      process(b2, wave + kWaves * it);
+      if (++it >= my_pages) break;
     }
   }
 
@@ -360,43 +368,65 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
       st[2 + d] = O;
     }
   }
-  if (nsplit == 1) return;
+}
 
-  // ---- arrival: the last chunk merges all chunk states --------------------
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t old = atomicAdd(counter, 1u);
-    int flag = 0;
-    if ((old & kCountMask) + 1 == (uint32_t)nsplit) {
-      flag = (old & kPoison) ? 2 : 1;
-      atomicExch(counter, 0u);
-    }
-    sm.last_flag = flag;
+// Merges the chunk states of one (request, query head) into O and log2-LSE:
+// one workgroup of 128 lanes (one per output column) per state row, for the
+// requests that span more than one chunk.  Same request validity and chunk
+// schedule as the partial kernel; a poisoned chunk (invalid page) leaves the
+// request's sentinels untouched.
+__global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
+  __shared__ long long s_wave_sum[2][2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x / a.hq;
+  const int qh = blockIdx.x % a.hq;
+  const int32_t ip0 = a.indptr[0];
+  const int32_t ipB = a.indptr[a.batch];
+  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices) return;
+  // chunks before r and in total (the partial kernel's prefix scan)
+  long long before = 0, total = 0;
+  for (int rr = tid; rr < a.batch; rr += 128) {
+    const int32_t st = a.indptr[rr], en = a.indptr[rr + 1], tl = a.last[rr];
+    const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16;
+    const long long c = valid ? (en - st + a.chunk_pages - 1) / a.chunk_pages : 0;
+    total += c;
+    before += rr < r ? c : 0;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    before += __shfl_xor(before, o, 64);
+    total += __shfl_xor(total, o, 64);
+  }
+  if (lane == 0) {
+    s_wave_sum[wave][0] = before;
+    s_wave_sum[wave][1] = total;
   }
   __syncthreads();
-  if (sm.last_flag != 1) return;
-  __threadfence();
+  before = s_wave_sum[0][0] + s_wave_sum[1][0];
+  total = s_wave_sum[0][1] + s_wave_sum[1][1];
+  if (total > a.grid_slots) return;
+  const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+  if (!(st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16)) return;
+  const int nsplit = (en - st + a.chunk_pages - 1) / a.chunk_pages;
+  if (nsplit <= 1) return;
 
-  const float *req_states = a.states + (prefix * a.hq) * (int64_t)loom::kStateWidth;
-  const int64_t split_stride = (int64_t)a.hq * loom::kStateWidth;
-  for (int idx = tid; idx < GT * 128; idx += kThreads) {
-    const int g = idx >> 7, d = idx & 127;
-    if (g >= gcount) continue;
-    const int64_t qh = qh_base + g;
-    const float *st = req_states + qh * (int64_t)loom::kStateWidth;
-    float M = -INFINITY;
-    for (int sidx = 0; sidx < nsplit; ++sidx) M = fmaxf(M, st[sidx * split_stride]);
-    float L = 0.f, O = 0.f;
-    for (int sidx = 0; sidx < nsplit; ++sidx) {
-      const float *ss = st + sidx * split_stride;
-      const float f = fast_exp2(ss[0] - M);
-      L = fmaf(ss[1], f, L);
-      O = fmaf(ss[2 + d], f, O);
-    }
-    a.out[((int64_t)r * a.hq + qh) * 128 + d] = f32_to_bf16(O / L);
-    if (d == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(L);
+  const int64_t stride = (int64_t)a.hq * loom::kStateWidth;
+  const float *row = a.states + (before * a.hq + qh) * (int64_t)loom::kStateWidth;
+  float m = -INFINITY, l = 0.f, o = 0.f;
+  int poisoned = 0;
+  for (int sidx = 0; sidx < nsplit; ++sidx) {
+    const float *ss = row + sidx * stride;
+    const float ms = ss[0], ls = ss[1];
+    poisoned |= ls < 0.0f;
+    const float mn = fmaxf(m, ms);
+    const float fo = fast_exp2(m - mn), fs = fast_exp2(ms - mn);
+    l = l * fo + ls * fs;
+    o = o * fo + ss[2 + tid] * fs;
+    m = mn;
   }
+  if (poisoned) return;
+  a.out[((int64_t)r * a.hq + qh) * 128 + tid] = f32_to_bf16(o / l);
+  if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = m + __log2f(l);
 }
 
 }  // namespace
@@ -437,7 +467,9 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   if (options) opt = *options;
   const uint64_t B = spec->batch_size, hq = spec->num_query_heads, hkv = spec->num_kv_heads;
   const uint64_t group = hq / hkv;
-  const uint32_t gtile = group <= 4 ? 4u : 8u;
+  // Query heads per workgroup column block: the group rounded up to a power
+  // of two, at most 8 (P·V accumulators are GT x 8 floats per lane).
+  const uint32_t gtile = group <= 1 ? 1u : group <= 2 ? 2u : group <= 4 ? 4u : 8u;
   const uint64_t gtiles = (group + gtile - 1) / gtile;
   const uint64_t max_pages = opt.max_total_pages ? opt.max_total_pages : spec->max_num_pages;
   if (max_pages < B) return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
@@ -463,10 +495,9 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
 
   const uint64_t max_chunks = (max_pages + chunk - 1) / chunk + B;
   const uint64_t grid = max_chunks * hkv * gtiles;
-  if (grid > (uint64_t)INT32_MAX)
+  if (grid > (uint64_t)INT32_MAX || B * hq > (uint64_t)INT32_MAX)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged batch-decode", grid);
   const uint64_t state_bytes = max_chunks * hq * loom::kStateWidth * 4;
-  const uint64_t counter_bytes = ((B * hkv * gtiles * 4) + 255) / 256 * 256;
 
   auto *p = new loom_paged_decode_plan;
   p->device = provider->dev.device;
@@ -478,7 +509,7 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   i.group_tiles = (uint32_t)gtiles;
   i.max_total_pages = max_pages;
   i.max_chunks = max_chunks;
-  i.workspace_bytes = counter_bytes + state_bytes;
+  i.workspace_bytes = state_bytes;
   i.block_threads = kThreads;
   i.device_cus = (uint32_t)provider->dev.cus;
   *out = p;
@@ -544,10 +575,7 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.last = (const int32_t *)l[5]->ptr;
   a.out = (uint16_t *)l[6]->ptr;
   a.lse = (float *)l[7]->ptr;
-  const uint64_t counter_bytes =
-      ((s.batch_size * s.num_kv_heads * pi.group_tiles * 4) + 255) / 256 * 256;
-  a.counters = (uint32_t *)l[8]->ptr;
-  a.states = (float *)(l[8]->ptr + counter_bytes);
+  a.states = (float *)l[8]->ptr;
   a.batch = (int32_t)s.batch_size;
   a.hq = (int32_t)s.num_query_heads;
   a.hkv = (int32_t)s.num_kv_heads;
@@ -561,13 +589,21 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
 
   const uint64_t grid = (uint64_t)a.grid_slots * s.num_kv_heads * pi.group_tiles;
   hipStream_t stream = scope->queue->stream;
-  if (pi.group_tile == 4)
-    hipLaunchKernelGGL(paged_decode_split_kv_kernel<4>, dim3((unsigned)grid), dim3(kThreads), 0,
-                       stream, a);
-  else
-    hipLaunchKernelGGL(paged_decode_split_kv_kernel<8>, dim3((unsigned)grid), dim3(kThreads), 0,
-                       stream, a);
-  return loom::record_launch(scope, hipGetLastError(), err);
+  const dim3 g3((unsigned)grid), b3(kThreads);
+  switch (pi.group_tile) {
+    case 1: hipLaunchKernelGGL(paged_decode_split_kv_kernel<1>, g3, b3, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL(paged_decode_split_kv_kernel<2>, g3, b3, 0, stream, a); break;
+    case 4: hipLaunchKernelGGL(paged_decode_split_kv_kernel<4>, g3, b3, 0, stream, a); break;
+    default: hipLaunchKernelGGL(paged_decode_split_kv_kernel<8>, g3, b3, 0, stream, a); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) {
+    // One command: the split kernel, then the merge of multi-chunk requests.
+    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)(s.batch_size * s.num_query_heads)),
+                       dim3(128), 0, stream, a);
+    e = hipGetLastError();
+  }
+  return loom::record_launch(scope, e, err);
 }
 
 }  // extern "C"

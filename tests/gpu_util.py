@@ -53,7 +53,9 @@ class DecodeRunner:
         self.spec = L.Bf16PagedBatchDecodeSpec(batch, pool, hq, hkv, 128, 16)
         self.provider = L.DecodeProvider.load(0)
         self.plan = self.provider.plan_bf16_paged_batch(self.spec, **plan_opts)
-        self.workspace = torch.zeros(self.plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+        # deliberately not zeroed: the workspace is scratch between commands
+        self.workspace = torch.full((self.plan.workspace_bytes,), 0xFF, dtype=torch.uint8,
+                                    device="cuda")
         self.queue = L.CommandQueue(torch.cuda.current_stream(), 4)
 
     def bindings(self, q, k, v, indptr, indices, last, out, lse):

@@ -79,10 +79,7 @@ def test_seeded_shapes(L, oracle, name, B, hq, hkv, lens, chunk):
     out, lse = r.run(q, k, v, indptr, indices, last)
     log(f"  plan chunk={r.plan.info.chunk_pages} tile={r.plan.info.group_tile}x"
         f"{r.plan.info.group_tiles} {compare_decode(oracle, out, lse, ref_out, ref_lse)}")
-    # the arrival counters are left at zero for the next call
-    ws = r.workspace.cpu().numpy()
-    ncnt = B * hkv * r.plan.info.group_tiles * 4
-    assert not ws[:ncnt].any()
+    # a second call over the previous call's workspace contents is identical
     out2, lse2 = r.run(q, k, v, indptr, indices, last)
     assert np.array_equal(out2, out) and np.array_equal(lse2, lse)
 
@@ -118,9 +115,10 @@ def test_invalid_page_guard_preserves_sentinels(L):
     assert np.all(np.isnan(o[4 * 128:])) and np.all(np.isnan(l[4:]))
 
 
-def test_invalid_metadata_multi_chunk_keeps_counters_clean(L, oracle):
+def test_invalid_page_in_multi_chunk_request(L, oracle):
     """An invalid page inside a long request (several chunks) leaves that
-    request's sentinels, completes the others, and leaves the workspace ready."""
+    request's sentinels and completes the others; the next valid call over the
+    poisoned workspace is correct."""
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(5)
     lens = [600, 300]
@@ -140,8 +138,6 @@ def test_invalid_metadata_multi_chunk_keeps_counters_clean(L, oracle):
                                            indptr, indices, last)
     compare_decode(oracle, out.reshape(B, -1)[1], lse[hq:], ref_out.reshape(B, -1)[1],
                    ref_lse[hq:])
-    ncnt = B * hkv * r.plan.info.group_tiles * 4
-    assert not r.workspace.cpu().numpy()[:ncnt].any()
     out2, lse2 = r.run(q, k, v, indptr, indices, last)
     compare_decode(oracle, out2, lse2, ref_out, ref_lse)
 

@@ -26,7 +26,7 @@ def log(msg):
 def test_decode_graph_replays_match_eager_and_oracle(L, oracle):
     """Replays with eager work and host synchronization between them; every
     replay is compared with the eager result (no memset nodes are captured; the
-    workspace counters are re-zeroed by the kernel itself)."""
+    split-KV workspace is scratch and needs no clearing between replays)."""
     import torch
     log("graph decode replay")
     rng = np.random.default_rng(21)
