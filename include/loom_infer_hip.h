@@ -325,7 +325,7 @@ typedef enum loom_paged_decode_algorithm {
 /* Planner inputs.  Zero means "choose for this device". */
 typedef struct loom_paged_decode_plan_options {
   uint64_t max_total_pages; /* upper bound of page_indices length; 0 -> max_num_pages */
-  uint32_t chunk_pages;     /* pages per workgroup chunk (4..64, multiple of 4) */
+  uint32_t chunk_pages;     /* pages per workgroup chunk (4..256, multiple of 4) */
   uint32_t expected_kv_len; /* typical request length used to size chunks */
 } loom_paged_decode_plan_options_t;
 

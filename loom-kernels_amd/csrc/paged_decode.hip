@@ -39,7 +39,23 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kMaxChunkPages = 64;
+constexpr int kMaxChunkPages = 256;  // one page index per thread in the guard
+constexpr int kKRowBytes = 256 + 16;
+#ifndef LOOM_DECODE_DEPTH
+#define LOOM_DECODE_DEPTH 2
+#endif
+// Waves per SIMD the register allocation must allow (HIP's second launch
+// bound); more resident waves hide HBM latency better than deeper per-wave
+// prefetch on this kernel.
+#ifndef LOOM_DECODE_WAVES_TILE4
+#define LOOM_DECODE_WAVES_TILE4 2
+#endif
+template <int GT>
+constexpr int waves_per_eu() {
+  return GT <= 2 ? 3 : GT == 4 ? LOOM_DECODE_WAVES_TILE4 : 2;
+}
+// Pages in flight per wave (register buffers of 32 VGPRs each).
+constexpr int kDepth = LOOM_DECODE_DEPTH;
 // Normalizer written into the states of a chunk whose pages failed the guard.
 constexpr float kPoisonNormalizer = -1.0f;
 
@@ -84,6 +100,21 @@ __device__ __forceinline__ u32x4 load16(const uint16_t *p) {
   return *reinterpret_cast<const u32x4 *>(p);
 }
 
+// K/V pages are read exactly once per kv-head: nontemporal loads keep them
+// from displacing reusable lines in L2/MALL (measured on MI355X: a plain
+// streaming read tops out near 6.2 TB/s, a nontemporal one near 6.9 TB/s).
+#ifndef LOOM_DECODE_NT_K
+#define LOOM_DECODE_NT_K 1
+#endif
+#ifndef LOOM_DECODE_NT_V
+#define LOOM_DECODE_NT_V 1
+#endif
+template <bool NT>
+__device__ __forceinline__ u32x4 load16_stream(const uint16_t *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -102,13 +133,19 @@ struct Smem {
   float wm[kWaves][GT];
   float wl[kWaves][GT];
   float wacc[kWaves][GT][128];
+  // Per-wave K tile: 16 token rows of 256 bytes padded to kKRowBytes so the
+  // MFMA fragment reads (16 rows, same column) hit 16 distinct bank groups.
+  uint8_t ktile[kWaves][16 * kKRowBytes];
+  u32x4 qfrag[4][64];  // MFMA B fragments of the query tile, per lane
   int wave_tot[kWaves];
   int req, split, nsplit;
+  int req_start, req_end, tail;
   long long prefix;
 };
 
-// One page of K and V for one wave: K rows as MFMA A fragments, V rows for the
-// lane's 8-column slice.
+// One page of K and V for one wave, both as whole 256-byte rows: lane
+// (col = lane%16, quad = lane/16) holds columns [8*col, 8*col+8) of rows
+// 4*quad + j, j = 0..3, so every load instruction covers four full rows.
 struct PageRegs {
   u32x4 k[4];
   u32x4 v[4];
@@ -116,20 +153,18 @@ struct PageRegs {
 
 __device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page, int lane,
                                           int kvh) {
-  const int row = lane & 15, quad = lane >> 4;
-  const int64_t krow = ((int64_t)page * 16 + row) * a.hkv + kvh;
-  const uint16_t *kp = a.k + krow * 128 + quad * 32;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) r.k[c] = load16(kp + c * 8);
+  const int col = lane & 15, quad = lane >> 4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t vrow = ((int64_t)page * 16 + quad * 4 + j) * a.hkv + kvh;
-    r.v[j] = load16(a.v + vrow * 128 + row * 8);
+    const int64_t row = ((int64_t)page * 16 + quad * 4 + j) * a.hkv + kvh;
+    r.k[j] = load16_stream<LOOM_DECODE_NT_K>(a.k + row * 128 + col * 8);
+    r.v[j] = load16_stream<LOOM_DECODE_NT_V>(a.v + row * 128 + col * 8);
   }
 }
 
 template <int GT>
-__global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_split_kv_kernel(
+    DecodeArgs a) {
   __shared__ Smem<GT> sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
@@ -140,19 +175,20 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
   const int gt = w % a.group_tiles;
   const long long slot = w / a.group_tiles;
 
-  // ---- global metadata guard (decode.rs:233-246) --------------------------
+  // ---- flattened chunk schedule: prefix scan of chunks per request ---------
+  // The global guard words and each thread's (start, end, tail) are loaded in
+  // one round trip; the request found by the scan is handed over through LDS.
   const int32_t ip0 = a.indptr[0];
   const int32_t ipB = a.indptr[a.batch];
-  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices) return;
-
-  // ---- flattened chunk schedule: prefix scan of chunks per request ---------
   if (tid == 0) sm.req = -1;
   long long carry = 0;
   for (int base = 0; base < a.batch; base += kThreads) {
     const int r = base + tid;
-    int c = 0;
+    int c = 0, st = 0, en = 0, tl = 0;
     if (r < a.batch) {
-      const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+      st = a.indptr[r];
+      en = a.indptr[r + 1];
+      tl = a.last[r];
       const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16;
       c = valid ? (en - st + a.chunk_pages - 1) / a.chunk_pages : 0;
     }
@@ -177,34 +213,50 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
       sm.split = (int)(slot - excl);
       sm.nsplit = c;
       sm.prefix = excl;
+      sm.req_start = st;
+      sm.req_end = en;
+      sm.tail = tl;
     }
     carry += tot;
     __syncthreads();
   }
-  // More chunks than the grid covers only happens with overlapping request
-  // ranges; such metadata is rejected for the whole batch, consistently in
-  // every workgroup.
-  if (carry > a.grid_slots) return;
+  // Global guard (decode.rs:233-246), and more chunks than the grid covers
+  // (only possible with overlapping request ranges): the whole batch is
+  // rejected, consistently in every workgroup.
+  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices || carry > a.grid_slots) return;
   const int r = sm.req;
   if (r < 0) return;
   const int split = sm.split, nsplit = sm.nsplit;
   const long long prefix = sm.prefix;
-
-  const int32_t req_start = a.indptr[r], req_end = a.indptr[r + 1];
-  const int tail = a.last[r];
-  const int p0 = req_start + split * a.chunk_pages;
+  const int req_end = sm.req_end;
+  const int tail = sm.tail;
+  const int p0 = sm.req_start + split * a.chunk_pages;
   const int npages = min(a.chunk_pages, req_end - p0);
+  const int g_base = gt * GT;
+  const int gcount = min(GT, a.group - g_base);
 
+  // ---- page indices of this chunk, then the Q fragment (both in flight) ----
+  int pg = 0;
+  if (tid < npages) pg = a.indices[p0 + tid];
+  // Q fragment: column `col` is query head g of this tile; MFMA c contracts
+  // dims 32c + 8*quad + [0, 8), the slices the K fragments read from LDS.
+  // The fragments are identical in every wave; wave 0 parks them in LDS so they
+  // do not occupy 16 VGPRs through the page loop.
+  const bool col_valid = col < gcount;
+  if (wave == 0) {
+    const int qh = kvh * a.group + g_base + col;
+    const uint16_t *qp = a.q + ((int64_t)r * a.hq + qh) * 128 + quad * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      sm.qfrag[c][lane] = col_valid ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
+  }
   // ---- page validation for this chunk (decode.rs:284-289 guard) -----------
   int bad = 0;
   if (tid < npages) {
-    const int32_t pg = a.indices[p0 + tid];
     sm.pages[tid] = pg;
     bad = (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
   }
   bad = __syncthreads_or(bad);
-  const int g_base = gt * GT;
-  const int gcount = min(GT, a.group - g_base);
   if (bad) {
     // The request keeps its output sentinels: a single-chunk request simply
     // writes nothing; a multi-chunk one marks this chunk's states so the
@@ -218,16 +270,6 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
     return;
   }
 
-  // ---- Q fragment: column `col` is query head g of this tile -------------
-  const bool col_valid = col < gcount;
-  u32x4 qf[4];
-  {
-    const int qh = kvh * a.group + g_base + col;
-    const uint16_t *qp = a.q + ((int64_t)r * a.hq + qh) * 128 + quad * 32;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qf[c] = col_valid ? load16(qp + c * 8) : u32x4{0, 0, 0, 0};
-  }
-
   float m_run = -INFINITY, l_run = 0.0f;
   float acc[GT][8];
 #pragma unroll
@@ -238,11 +280,22 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
   auto process = [&](const PageRegs &pr, int page_idx) {
     const bool last_page = (p0 + page_idx == req_end - 1);
     const int valid_tokens = last_page ? tail : 16;
+    // K rows -> LDS tile -> MFMA A fragments (lane: token row `col`, dims
+    // 32c + 8*quad + [0, 8)).
+    uint8_t *kt = sm.ktile[wave];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4 *>(kt + (quad * 4 + j) * kKRowBytes + col * 16) = pr.k[j];
+    wave_lds_fence();
+    u32x4 kf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      kf[c] = *reinterpret_cast<const u32x4 *>(kt + col * kKRowBytes + (c * 4 + quad) * 16);
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pr.k[c]), as_bf16x8(qf[c]), s, 0,
-                                                  0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[c]), as_bf16x8(sm.qfrag[c][lane]),
+                                                  s, 0, 0, 0);
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -290,30 +343,28 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split_kv_kernel(DecodeA
     wave_lds_fence();
   };
 
-  // ---- main loop: pages wave, wave+4, ... of this chunk, three-deep ---------
-  // Every iteration issues the loads of the page two steps ahead before it
+  // ---- main loop: pages wave, wave+4, ... of this chunk, kDepth-deep --------
+  // Every step issues the loads of the page kDepth-1 steps ahead before it
   // consumes the current one.  Loads are unconditional (the index is clamped to
-  // the wave's last page) so the compiler can wait for exactly the oldest
-  // page's loads instead of draining the queue.
+  // the wave's last page) and the buffer rotation is unrolled, so the compiler
+  // waits for exactly the oldest page's loads instead of draining the queue.
   const int my_pages = npages > wave ? (npages - wave + kWaves - 1) / kWaves : 0;
   if (my_pages > 0) {
     auto page_of = [&](int it) { return sm.pages[wave + kWaves * min(it, my_pages - 1)]; };
-    PageRegs b0, b1, b2;
-    load_page(b0, a, page_of(0), lane, kvh);
-    load_page(b1, a, page_of(1), lane, kvh);
+    PageRegs buf[kDepth];
+#pragma unroll
+    for (int j = 0; j < kDepth - 1; ++j) load_page(buf[j], a, page_of(j), lane, kvh);
     int it = 0;
     while (true) {
-      load_page(b2, a, page_of(it + 2), lane, kvh);
-      process(b0, wave + kWaves * it);
-      if (++it >= my_pages) break;
-      load_page(b0, a, page_of(it + 2), lane, kvh);
-      process(b1, wave + kWaves * it);
-      if (++it >= my_pages) break;
-      load_page(b1, a, page_of(it + 2), lane, kvh);
-      process(b2, wave + kWaves * it);
-      if (++it >= my_pages) break;
+#pragma unroll
+      for (int s = 0; s < kDepth; ++s) {
+        load_page(buf[(s + kDepth - 1) % kDepth], a, page_of(it + kDepth - 1), lane, kvh);
+        process(buf[s], wave + kWaves * it);
+        if (++it >= my_pages) goto pages_done;
+      }
     }
   }
+pages_done:
 
   // ---- wave reduction over the 4 row quads ---------------------------------
   float l_tot = l_run + __shfl_xor(l_run, 16, 64);
@@ -412,21 +463,56 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
 
   const int64_t stride = (int64_t)a.hq * loom::kStateWidth;
   const float *row = a.states + (before * a.hq + qh) * (int64_t)loom::kStateWidth;
-  float m = -INFINITY, l = 0.f, o = 0.f;
+  // Pass 1: the global max and the poison marks, with the splits spread over
+  // the 128 lanes (one load round trip for up to 128 splits).
+  float mloc = -INFINITY;
   int poisoned = 0;
-  for (int sidx = 0; sidx < nsplit; ++sidx) {
+  for (int sidx = tid; sidx < nsplit; sidx += 128) {
     const float *ss = row + sidx * stride;
-    const float ms = ss[0], ls = ss[1];
-    poisoned |= ls < 0.0f;
-    const float mn = fmaxf(m, ms);
-    const float fo = fast_exp2(m - mn), fs = fast_exp2(ms - mn);
-    l = l * fo + ls * fs;
-    o = o * fo + ss[2 + tid] * fs;
-    m = mn;
+    mloc = fmaxf(mloc, ss[0]);
+    poisoned |= ss[1] < 0.0f;
   }
-  if (poisoned) return;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
+    poisoned |= __shfl_xor(poisoned, o, 64);
+  }
+  __shared__ float s_m[2];
+  __shared__ int s_p[2];
+  if (lane == 0) {
+    s_m[wave] = mloc;
+    s_p[wave] = poisoned;
+  }
+  __syncthreads();
+  if (s_p[0] | s_p[1]) return;
+  const float M = fmaxf(s_m[0], s_m[1]);
+  // Pass 2: weighted sums; the unroll keeps eight splits' loads in flight.
+  float l = 0.f, o = 0.f;
+  int sidx = 0;
+  for (; sidx + 8 <= nsplit; sidx += 8) {
+    float ms[8], ls[8], xs[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float *ss = row + (sidx + u) * stride;
+      ms[u] = ss[0];
+      ls[u] = ss[1];
+      xs[u] = ss[2 + tid];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float f = fast_exp2(ms[u] - M);
+      l = fmaf(ls[u], f, l);
+      o = fmaf(xs[u], f, o);
+    }
+  }
+  for (; sidx < nsplit; ++sidx) {
+    const float *ss = row + sidx * stride;
+    const float f = fast_exp2(ss[0] - M);
+    l = fmaf(ss[1], f, l);
+    o = fmaf(ss[2 + tid], f, o);
+  }
   a.out[((int64_t)r * a.hq + qh) * 128 + tid] = f32_to_bf16(o / l);
-  if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = m + __log2f(l);
+  if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(l);
 }
 
 }  // namespace

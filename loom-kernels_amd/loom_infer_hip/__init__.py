@@ -367,9 +367,12 @@ class CheckedBindings:
         return self._owned.pop(handle.handle.slot, None)
 
     def __del__(self):
-        if getattr(self, "_p", None) and not self._moved:
-            lib().loom_bindings_free(self._p)
-            self._p = None
+        try:
+            if getattr(self, "_p", None) and not self._moved:
+                lib().loom_bindings_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 def _stream_handle(stream) -> int:
@@ -411,11 +414,14 @@ class CommandCompletion:
         return b
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_command_completion_free(self._p)
-            self._bindings._p = None
-            self._queue._live = False
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_command_completion_free(self._p)
+                self._bindings._p = None
+                self._queue._live = False
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 class CommandScope:
@@ -438,11 +444,14 @@ class CommandScope:
         return CommandCompletion(out.value, self._bindings, self._queue)
 
     def __del__(self):
-        if getattr(self, "_p", None) and not self._capturing:
-            lib().loom_command_scope_free(self._p)
-            self._bindings._p = None
-            self._queue._live = False
-            self._p = None
+        try:
+            if getattr(self, "_p", None) and not self._capturing:
+                lib().loom_command_scope_free(self._p)
+                self._bindings._p = None
+                self._queue._live = False
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 class CommandQueue:
@@ -480,12 +489,15 @@ class CommandQueue:
         return CommandScope(out.value, bindings, self)
 
     def __del__(self):
-        # A queue still borrowed by an unsettled scope/completion (only possible
-        # when a reference cycle is collected) is left allocated rather than
-        # freed under its borrower.
-        if getattr(self, "_p", None) and not self._live:
-            lib().loom_command_queue_free(self._p)
-            self._p = None
+        try:
+            # A queue still borrowed by an unsettled scope/completion (only possible
+            # when a reference cycle is collected) is left allocated rather than
+            # freed under its borrower.
+            if getattr(self, "_p", None) and not self._live:
+                lib().loom_command_queue_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 # ---- paged decode ---------------------------------------------------------------
@@ -531,9 +543,12 @@ class Bf16PagedBatchDecodePlan:
         _call(lib().loom_paged_decode_enqueue, self._p, scope._p, C.byref(c))
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_paged_decode_plan_free(self._p)
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_paged_decode_plan_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 class DecodeProvider:
@@ -558,9 +573,12 @@ class DecodeProvider:
         return Bf16PagedBatchDecodePlan(out.value, spec)
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_decode_provider_free(self._p)
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_decode_provider_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 # ---- fused RoPE + append --------------------------------------------------------
@@ -615,9 +633,12 @@ class Bf16RopePagedKvAppendPlan:
         _call(lib().loom_rope_append_enqueue, self._p, scope._p, C.byref(c))
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_rope_append_plan_free(self._p)
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_rope_append_plan_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 class RopeProvider:
@@ -646,9 +667,12 @@ class RopeProvider:
         return Bf16RopePagedKvAppendPlan(out.value, spec)
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_rope_provider_free(self._p)
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_rope_provider_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 # ---- graphs ---------------------------------------------------------------------
@@ -669,9 +693,12 @@ class GraphLaunchCompletion:
         _call(lib().loom_graph_completion_wait, p)
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_graph_completion_free(self._p)
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_graph_completion_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 class GraphExec:
@@ -711,10 +738,13 @@ class GraphExec:
         return self._bindings
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_graph_exec_free(self._p)
-            self._bindings._p = None
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_graph_exec_free(self._p)
+                self._bindings._p = None
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 class CapturedGraph:
@@ -732,10 +762,13 @@ class CapturedGraph:
         return GraphExec(out.value, self._bindings)
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_captured_graph_free(self._p)
-            self._bindings._p = None
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_captured_graph_free(self._p)
+                self._bindings._p = None
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
 
 
 class GraphQueue:
@@ -781,6 +814,9 @@ class GraphQueue:
         return graph
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            lib().loom_graph_queue_free(self._p)
-            self._p = None
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_graph_queue_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass

@@ -5,7 +5,10 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libloom_infer_hip.so")
+# LOOM_INFER_HIP_LIB selects another build of the same library (for example an
+# instrumented or tuning build); the default is the in-tree build.
+LIB_PATH = os.environ.get("LOOM_INFER_HIP_LIB") or os.path.join(
+    os.path.dirname(_HERE), "lib", "libloom_infer_hip.so")
 
 u64, i32, u32, f32, vp = C.c_uint64, C.c_int32, C.c_uint32, C.c_float, C.c_void_p
 
