@@ -26,6 +26,10 @@ for _p in (ROOT, os.path.join(ROOT, "loom-kernels_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per decode launch on config 3 from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (partial + merge kernels), each scaled by the factor the same
+# counter reads for a plain copy of known size; profiles/ holds the runs.
+TRAFFIC_C3 = None
 
 
 def log(*a):
@@ -43,7 +47,7 @@ def algorithmic_decode_bytes(lens, B, hq, hkv):
 class DecodeCase:
     """Device-resident synthetic workload for one decode config."""
 
-    def __init__(self, L, name, B, hq, hkv, pool, lens, seed, chunk_pages=0):
+    def __init__(self, L, name, B, hq, hkv, pool, lens, seed, teams=0):
         import numpy as np
         import torch
         self.name, self.B, self.hq, self.hkv, self.pool = name, B, hq, hkv, pool
@@ -73,8 +77,7 @@ class DecodeCase:
         self.lse = torch.empty(B * hq, dtype=torch.float32, device=dev)
         self.spec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, 128, 16)
         self.plan = L.DecodeProvider.load(0).plan_bf16_paged_batch(
-            self.spec, max_total_pages=int(indptr[-1]), chunk_pages=chunk_pages,
-            expected_kv_len=int(self.lens.mean()))
+            self.spec, max_total_pages=int(indptr[-1]), teams=teams)
         self.ws = torch.zeros(self.plan.workspace_bytes, dtype=torch.uint8, device=dev)
         self.bytes = algorithmic_decode_bytes(self.lens, B, hq, hkv)
         self.L = L
@@ -89,17 +92,18 @@ class DecodeCase:
                                           h[7].write(), h[8].write())
 
 
-def time_eager(L, case, stream, steps, warmup):
+def _timed_enqueues(L, stream, n_bind, bind, enqueue, steps, warmup):
     """hipEvent pair around `steps` back-to-back enqueues on one stream, per call
-    (the reference's eager_stream_batch_cuda_event, benchmarks/matched.rs:141-173)."""
+    (the reference's eager_stream_batch_cuda_event, benchmarks/matched.rs:141-173).
+    The events are recorded on the stream the kernels are launched on."""
     import torch
     q = L.CommandQueue(stream, steps + warmup + 1)
-    b = q.bindings(9)
-    args = case.bind(b)
+    b = q.bindings(n_bind)
+    args = bind(b)
     with torch.cuda.stream(stream):
         scope = q.begin(b)
         for _ in range(warmup):
-            case.plan.enqueue_into(scope, args)
+            enqueue(scope, args)
         b = scope.finish().wait()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -107,22 +111,21 @@ def time_eager(L, case, stream, steps, warmup):
         torch.cuda.synchronize()
         start.record(stream)
         for _ in range(steps):
-            case.plan.enqueue_into(scope, args)
+            enqueue(scope, args)
         end.record(stream)
         b = scope.finish().wait()
         torch.cuda.synchronize()
     return start.elapsed_time(end) * 1000.0 / steps  # µs per call
 
 
-def time_graph(L, case, replays=20):
-    """One fixed-address replay + its completion event per sample (graph/mod.rs:301-323);
-    returns the median µs."""
+def _graph_replay(L, n_bind, n_cmds, bind, record, replays=20):
+    """One fixed-address replay + its completion event per sample
+    (graph/mod.rs:301-323); returns the median µs."""
     import torch
-    gq = L.GraphQueue(0, 1)
-    b = gq.bindings(9)
-    args = case.bind(b)
-    graph = gq.capture(b, lambda scope: case.plan.enqueue_into(scope, args))
-    exec_ = graph.instantiate()
+    gq = L.GraphQueue(0, n_cmds)
+    b = gq.bindings(n_bind)
+    args = bind(b)
+    exec_ = gq.capture(b, lambda scope: record(scope, args)).instantiate()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     samples = []
@@ -135,40 +138,164 @@ def time_graph(L, case, replays=20):
     return samples[len(samples) // 2]
 
 
-def cpu_baseline(case, budget_s=12.0):
-    """The oracle (single thread, the reference's loop order) on a bounded
-    sample of whole requests of the same workload, scaled to GB/s."""
+def time_eager(L, case, stream, steps, warmup):
+    return _timed_enqueues(L, stream, 9, case.bind, case.plan.enqueue_into, steps, warmup)
+
+
+def time_graph(L, case, replays=20):
+    return _graph_replay(L, 9, 1, case.bind, case.plan.enqueue_into, replays)
+
+
+class AppendCase:
+    """Device-resident fused RoPE + paged append workload.  With `n_new` None it
+    is the one-token contract (token at kv_len-1 of every request); otherwise the
+    explicit-token contract with n_new[r] tokens at the end of request r, given
+    in a seeded shuffled order."""
+
+    def __init__(self, L, B, hq, hkv, pool, lens, seed, n_new=None, share=None):
+        import numpy as np
+        import torch
+        rng = np.random.default_rng(seed)
+        lens = np.asarray(lens, dtype=np.int64)
+        if share is not None:  # a DecodeCase: same page table and K/V pools
+            indptr, indices, last = share.indptr_h, share.indices_h, share.last_h
+        else:
+            pages = (lens + 15) // 16
+            indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+            indices = rng.permutation(pool)[: int(indptr[-1])].astype(np.int32)
+            last = (lens - (pages - 1) * 16).astype(np.int32)
+        self.explicit = n_new is not None
+        if self.explicit:
+            bi = np.concatenate([np.full(n, r) for r, n in enumerate(n_new)]).astype(np.int32)
+            pos = np.concatenate([np.arange(l - n, l) for l, n in zip(lens, n_new)]).astype(np.int32)
+            perm = rng.permutation(len(bi))
+            bi, pos = bi[perm], pos[perm]
+            T = len(bi)
+            self.spec = L.Bf16RopePagedKvAppendTokensSpec(T, B, pool, hq, hkv,
+                                                          extended=T > 64)
+        else:
+            T = B
+            self.spec = L.Bf16RopePagedKvAppendSpec(B, pool, hq, hkv)
+        dev = "cuda"
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.T, self.B, self.hq, self.hkv = T, B, hq, hkv
+        self.q = torch.randn(T * hq * 128, generator=g, device=dev).to(torch.bfloat16)
+        self.k = torch.randn(T * hkv * 128, generator=g, device=dev).to(torch.bfloat16)
+        self.v = torch.randn(T * hkv * 128, generator=g, device=dev).to(torch.bfloat16)
+        if share is not None:
+            self.kp, self.vp = share.k, share.v
+            self.indptr, self.indices, self.last = share.indptr, share.indices, share.last
+        else:
+            n = pool * 16 * hkv * 128
+            self.kp = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+            self.vp = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+            self.indptr = torch.from_numpy(indptr).to(dev)
+            self.indices = torch.from_numpy(indices).to(dev)
+            self.last = torch.from_numpy(last).to(dev)
+        self.tables = (indptr, indices, last)
+        if self.explicit:
+            self.bi = torch.from_numpy(bi).to(dev)
+            self.pos = torch.from_numpy(pos).to(dev)
+        self.qo = torch.empty(T * hq * 128, dtype=torch.bfloat16, device=dev)
+        prov = L.RopeProvider.load(0)
+        self.plan = (prov.plan_bf16_paged_append_tokens(self.spec) if self.explicit
+                     else prov.plan_bf16_paged_append(self.spec))
+        self.ws = torch.zeros(self.plan.workspace_bytes, dtype=torch.uint8, device=dev)
+        # bytes the append must move: q in/out, new k/v in and out, metadata
+        self.bytes = (2 * T * hq * 128 * 2 + 2 * 2 * T * hkv * 128 * 2
+                      + 4 * (2 * B + 1 + int(indptr[-1])) + (8 * T if self.explicit else 0))
+        self.L = L
+
+    def bind(self, b, qo=None, kp=None, vp=None):
+        """Handles for the append; pass existing read-write handles to share the
+        query output and K/V pools with a decode in the same command scope."""
+        L = self.L
+        kp = b.bind_read_write(self.kp) if kp is None else kp
+        vp = b.bind_read_write(self.vp) if vp is None else vp
+        qo = b.bind_read_write(self.qo) if qo is None else qo
+        return L.Bf16RopePagedKvAppendArgs(
+            b.bind_read(self.q), b.bind_read(self.k), b.bind_read(self.v),
+            b.bind_read(self.indptr), b.bind_read(self.indices), b.bind_read(self.last),
+            qo.write(), kp.write(), vp.write(), b.bind_read_write(self.ws).write(),
+            b.bind_read(self.bi) if self.explicit else None,
+            b.bind_read(self.pos) if self.explicit else None)
+
+
+def time_append(L, case, stream, steps, warmup):
+    n = 12 if case.explicit else 10
+    return (_timed_enqueues(L, stream, n, case.bind, case.plan.enqueue_into, steps, warmup),
+            _graph_replay(L, n, 1, case.bind, case.plan.enqueue_into))
+
+
+def time_full_step(L, app, dec):
+    """Config 5: RoPE + one-token append writing the rotated query and the new
+    K/V rows, then paged decode reading them, captured as one graph."""
+    def bind(b):
+        qo, kp, vp = (b.bind_read_write(app.qo), b.bind_read_write(app.kp),
+                      b.bind_read_write(app.vp))
+        ip, ix, ln = b.bind_read(app.indptr), b.bind_read(app.indices), b.bind_read(app.last)
+        a = L.Bf16RopePagedKvAppendArgs(
+            b.bind_read(app.q), b.bind_read(app.k), b.bind_read(app.v), ip, ix, ln,
+            qo.write(), kp.write(), vp.write(), b.bind_read_write(app.ws).write())
+        d = L.Bf16PagedBatchDecodeArgs(
+            qo.read(), kp.read(), vp.read(), ip, ix, ln, b.bind_read_write(dec.out).write(),
+            b.bind_read_write(dec.lse).write(), b.bind_read_write(dec.ws).write())
+        return a, d
+
+    def record(scope, args):
+        app.plan.enqueue_into(scope, args[0])
+        dec.plan.enqueue_into(scope, args[1])
+    return _graph_replay(L, 16, 2, bind, record)
+
+
+def cpu_baseline(case, min_s=10.0, max_s=30.0):
+    """The oracle (single thread, the reference's loop order,
+    crates/loom-infer/src/attention/paged_decode/mod.rs:305-363) on whole
+    requests of the same workload: every request of the batch once, repeated
+    until at least `min_s` of CPU work, stopping early at `max_s`.  Each
+    request's pages are copied to the host (untimed) and renumbered."""
     import numpy as np
     import torch
     import oracle as O
-    # host copies of only the pages the sample touches, renumbered
-    order = np.argsort(case.lens)  # sample spans short to long requests evenly
-    pick = order[np.linspace(0, len(order) - 1, num=min(len(order), 8)).astype(int)]
-    done_bytes, t_total, reqs = 0, 0.0, 0
     kk = case.k.view(case.pool, -1)
     vv = case.v.view(case.pool, -1)
-    for r in pick:
-        pg = case.indices_h[case.indptr_h[r]:case.indptr_h[r + 1]].astype(np.int64)
-        idx = torch.from_numpy(pg).cuda()
-        kh = kk[idx].reshape(-1).view(torch.int16).cpu().numpy().view(np.uint16)
-        vh = vv[idx].reshape(-1).view(torch.int16).cpu().numpy().view(np.uint16)
-        qh = case.q[r * case.hq * 128:(r + 1) * case.hq * 128].view(torch.int16).cpu().numpy().view(np.uint16)
-        n = len(pg)
-        s = O.paged_spec(1, n, case.hq, case.hkv)
-        out = np.empty(case.hq * 128, np.uint16)
-        lse = np.empty(case.hq, np.float32)
-        t0 = time.perf_counter()
-        O.paged_decode_requests(s, qh, kh, vh, [0, n], np.arange(n, dtype=np.int32),
-                                [int(case.last_h[r])], 0, 1, out, lse)
-        t_total += time.perf_counter() - t0
-        done_bytes += algorithmic_decode_bytes([case.lens[r]], 1, case.hq, case.hkv)
-        reqs += 1
-        if t_total > budget_s:
+    done_bytes, t_total, reqs, passes = 0, 0.0, 0, 0
+    while t_total < min_s:
+        for r in range(case.B):
+            pg = case.indices_h[case.indptr_h[r]:case.indptr_h[r + 1]].astype(np.int64)
+            idx = torch.from_numpy(pg).cuda()
+            kh = kk[idx].reshape(-1).view(torch.int16).cpu().numpy().view(np.uint16)
+            vh = vv[idx].reshape(-1).view(torch.int16).cpu().numpy().view(np.uint16)
+            qh = (case.q[r * case.hq * 128:(r + 1) * case.hq * 128].view(torch.int16)
+                  .cpu().numpy().view(np.uint16))
+            n = len(pg)
+            s = O.paged_spec(1, n, case.hq, case.hkv)
+            out = np.empty(case.hq * 128, np.uint16)
+            lse = np.empty(case.hq, np.float32)
+            t0 = time.perf_counter()
+            O.paged_decode_requests(s, qh, kh, vh, [0, n], np.arange(n, dtype=np.int32),
+                                    [int(case.last_h[r])], 0, 1, out, lse)
+            t_total += time.perf_counter() - t0
+            done_bytes += algorithmic_decode_bytes([case.lens[r]], 1, case.hq, case.hkv)
+            reqs += 1
+            if t_total > max_s:
+                break
+        passes += 1
+        if t_total > max_s:
             break
-    return {"value": done_bytes / t_total / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reqs} whole requests of the same workload (lengths "
-                      f"{sorted(int(case.lens[r]) for r in pick[:reqs])}), oracle loop "
-                      f"order, {t_total:.1f} s, single thread on {platform.processor() or 'host'}"}
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"value": round(done_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{reqs} whole requests of the config-3 batch ({passes} pass(es) over "
+                      f"its 64 requests, {done_bytes / 1e9:.2f} GB algorithmic), C oracle in "
+                      f"the reference loop order, {t_total:.1f} s on 1 thread of {cpu} "
+                      f"(host has {os.cpu_count()} logical CPUs)"}
 
 
 def make_cases(L, quick=False):
@@ -196,18 +323,33 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="configs 1 and 3 only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help="run one config (prefix match, e.g. c3) and print its detail")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 20 plain device copies of MIB MiB (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: every GPU box here has one MI355X and the path "
               "has no cross-GPU component; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
+    if a.copy_calibration:
+        n = a.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n, "launches": 20}), flush=True)
+        return
     import loom_infer_hip as L
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()  # default priority
     detail = {}
     head = None
     for name, (B, hq, hkv, pool, lens) in make_cases(L, a.quick).items():
+        if a.only and not name.startswith(a.only):
+            continue
         log(f"[bench] setting up {name}")
         case = DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name))
         us = time_eager(L, case, stream, a.steps, a.warmup)
@@ -216,14 +358,40 @@ def main():
         detail[name] = {"us_per_call": round(us, 3), "graph_replay_us": round(g_us, 3),
                         "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                         "algorithmic_bytes": case.bytes,
-                        "chunk_pages": case.plan.info.chunk_pages,
+                        "teams": case.plan.info.teams,
                         "mean_kv_len": float(case.lens.mean())}
+        if name.startswith("c5"):
+            # the one-token append of the same step, then the whole step as one graph
+            app = AppendCase(L, B, hq, hkv, pool, lens, seed=5, share=case)
+            ap_us, ap_g = time_append(L, app, stream, a.steps, a.warmup)
+            step_g = time_full_step(L, app, case)
+            detail[name].update({"append_us_per_call": round(ap_us, 3),
+                                 "append_graph_replay_us": round(ap_g, 3),
+                                 "full_step_graph_replay_us": round(step_g, 3)})
+            del app
         log(f"[bench] {name}: {detail[name]}")
         if name.startswith("c3"):
             head = case
         else:
             del case
             torch.cuda.empty_cache()
+    if a.only:
+        print(json.dumps(detail), flush=True)
+        return
+    if not a.quick:
+        log("[bench] setting up c2_rope_append_b32_tokens")
+        import numpy as np
+        rng = np.random.default_rng(2)
+        existing = rng.integers(0, 4096, size=32)
+        n_new = rng.integers(1, 65, size=32)
+        app = AppendCase(L, 32, 32, 8, 16384, existing + n_new, seed=2, n_new=n_new)
+        ap_us, ap_g = time_append(L, app, stream, a.steps, a.warmup)
+        detail["c2_rope_append_b32_tokens"] = {
+            "us_per_call": round(ap_us, 3), "graph_replay_us": round(ap_g, 3),
+            "tokens": app.T, "algorithmic_bytes": app.bytes,
+            "GBps": round(app.bytes / (ap_us * 1e-6) / 1e9, 1)}
+        log(f"[bench] c2: {detail['c2_rope_append_b32_tokens']}")
+        del app
     c3 = detail["c3_gqa4_b64_ragged"]
     cpu = None if a.no_cpu else cpu_baseline(head)
     line = {
@@ -236,7 +404,9 @@ def main():
                                "ragged ctx U[512,8192], 65536-page pool (BASELINE config 3)",
                    "global_batch": 64, "seq_len": int(head.lens.max()), "parallelism": "none"},
         "roofline": {"bound": "hbm", "achieved": c3["GBps"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": c3["frac_hbm_peak"], "traffic": None},
+                     "unit": "GB/s", "frac": c3["frac_hbm_peak"], "traffic": TRAFFIC_C3,
+                     "kernel": "decode command (split-KV partial + merge), HIP events on "
+                               "its launch stream"},
         "cpu_baseline": cpu,
         "detail": detail,
     }

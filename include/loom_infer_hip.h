@@ -316,29 +316,32 @@ loom_status_t loom_decode_provider_load(int device, loom_decode_provider_t **out
 void loom_decode_provider_free(loom_decode_provider_t *provider);
 
 typedef enum loom_paged_decode_algorithm {
-  /* One workgroup per (request, kv-head, group tile, KV chunk of pages);
-   * the whole GQA group shares each K/V byte; chunks merge through a
-   * log2-LSE state workspace inside the same kernel. */
-  LOOM_PAGED_DECODE_SPLIT_KV_GROUP = 1
+  /* The valid requests' pages form one list cut into `teams` equal ranges;
+   * a team is one wave per (kv-head, tile of up to 8 query heads), so the
+   * whole GQA group shares each K/V byte.  Requests that cross a range
+   * boundary merge through log2-LSE states in a second kernel. */
+  LOOM_PAGED_DECODE_BALANCED_SPLIT_KV = 1
 } loom_paged_decode_algorithm_t;
 
 /* Planner inputs.  Zero means "choose for this device". */
 typedef struct loom_paged_decode_plan_options {
   uint64_t max_total_pages; /* upper bound of page_indices length; 0 -> max_num_pages */
-  uint32_t chunk_pages;     /* pages per workgroup chunk (4..256, multiple of 4) */
-  uint32_t expected_kv_len; /* typical request length used to size chunks */
+  uint32_t teams;           /* page ranges; 0 -> one wave per SIMD slot of the device */
+  uint32_t reserved;        /* must be zero */
 } loom_paged_decode_plan_options_t;
 
 typedef struct loom_paged_decode_plan_info {
   loom_paged_decode_spec_t spec;
   int32_t algorithm;
-  uint32_t chunk_pages;
-  uint32_t group_tile;       /* query heads per workgroup column block */
+  uint32_t teams;
+  uint32_t group_tile;       /* query heads per wave column block */
   uint32_t group_tiles;      /* ceil(group / group_tile) */
   uint64_t max_total_pages;
-  uint64_t max_chunks;       /* state slots: ceil(max_total_pages/chunk_pages)+batch */
-  uint64_t workspace_bytes;  /* max_chunks * Hq * 130 FP32 states */
+  uint64_t state_slots;      /* teams + batch */
+  uint64_t workspace_bytes;  /* header_bytes + state_slots * Hq * 132 FP32 */
+  uint64_t header_bytes;     /* (batch + 2) int64 page prefixes, 256-byte rounded */
   uint32_t block_threads;
+  uint32_t grid_blocks;
   uint32_t device_cus;
 } loom_paged_decode_plan_info_t;
 
@@ -368,8 +371,8 @@ typedef struct loom_paged_decode_args {
 } loom_paged_decode_args_t;
 
 /* Bf16PagedBatchDecodePlan::enqueue_into, decode.rs:1199-1296: one command of
- * two stream-ordered kernels (split-KV partials, then the merge of requests
- * longer than one chunk). */
+ * two stream-ordered kernels (balanced split-KV partials, then the merge of
+ * requests that cross a team's page range). */
 loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
                                         loom_command_scope_t *scope,
                                         const loom_paged_decode_args_t *args,

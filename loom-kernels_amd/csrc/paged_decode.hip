@@ -6,26 +6,31 @@
 // invalid request keeps its output sentinels; valid requests complete).
 //
 // Work decomposition (MI355X-first, not the reference's warp-per-head):
-//   * one workgroup (4 wave64) per (KV chunk, kv-head, group tile); a chunk is
-//     `chunk_pages` consecutive pages of one request.  The whole GQA group of
-//     the kv-head (up to 8 query heads per tile) shares every K/V byte, so K/V
-//     is read from HBM once per kv-head instead of once per query head;
-//   * chunk slots are flattened over ragged requests with a workgroup-local
-//     prefix scan of the page table, so the grid depends only on buffer
-//     capacities (graph-replay safe) and every workgroup carries real work;
+//   * the pages of all valid requests form one virtual list; it is cut into
+//     `teams` equal ranges, and each team is hkv x group-tiles waves, one per
+//     (kv-head, tile of up to 8 query heads), all walking the same pages.  The
+//     whole GQA group of a kv-head shares every K/V byte, so K/V is read from
+//     HBM once per kv-head; every wave gets the same number of pages whatever
+//     the lengths, and the grid is one wave per SIMD slot of the chip, so
+//     there is no tail of partially filled launch rounds;
+//   * the grid depends only on the plan (graph-replay safe); each workgroup
+//     rebuilds the virtual list with one prefix scan of the page table;
+//   * workgroup b runs on XCD b % 8, and the waves of a team are placed on one
+//     XCD, so the kv-heads of a page are fetched together through one L2;
 //   * per page, S = K·Qᵀ runs on MFMA (v_mfma_f32_16x16x32_bf16: 16 tokens x
-//     16 query columns x 32 dims, 4 issues for D=128); K rows feed the A
-//     operand straight from 16-byte global loads;
-//   * online softmax in the log2 domain (v_exp_f32), P·V on the VALU in FP32
-//     with 16-byte V row loads (16 lanes cover one 256-byte row);
-//   * waves merge through LDS; a request that fits one chunk is finished in
-//     place.  Longer requests leave one FP32 state per (chunk, query head) in
-//     the workspace [chunk][Hq][130] = (max_log2, normalizer, acc[128]) (the
-//     split-K state layout of crates/loom-infer/src/attention/single_decode/
-//     mod.rs:10-13) and a second, stream-ordered merge kernel combines them.
-//     The kernel boundary makes the states visible across the 8 XCD L2s; an
-//     in-kernel last-arriver merge would need an agent-scope release per
-//     workgroup, i.e. an L2 write-back, which costs more than the launch.
+//     16 query columns x 32 dims, 4 issues for D=128) with K staged through a
+//     padded LDS tile; online softmax in the log2 domain (v_exp_f32); P·V on
+//     the VALU in FP32;
+//   * K/V rows are fetched with raw buffer loads whose range covers only the
+//     valid rows of the page, so the look-ahead past a segment and the tail of
+//     a request's last page move no bytes;
+//   * a request inside one team's range is finished in place.  Otherwise each
+//     team leaves one FP32 state per (request, query head) in the workspace,
+//     (max_log2, normalizer, acc[128]) as in crates/loom-infer/src/attention/
+//     single_decode/mod.rs:10-13, and a second, stream-ordered merge kernel
+//     combines them.  The kernel boundary makes the states visible across the
+//     8 XCD L2s; an in-kernel last-arriver merge would need an agent-scope
+//     release per wave, i.e. an L2 write-back, which costs more than the launch.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -39,7 +44,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kMaxChunkPages = 256;  // one page index per thread in the guard
+constexpr int kLdsPrefix = 512;      // requests whose prefix and metadata stay in LDS
+constexpr int kMaxScanBlocks = 256;  // scan blocks of kThreads requests: batch <= 65536
+// FP32 split state: (max_log2, normalizer, 2 pad, acc[128]), 16-byte aligned.
+constexpr int kStateStride = 132;
 constexpr int kKRowBytes = 256 + 16;
 #ifndef LOOM_DECODE_DEPTH
 #define LOOM_DECODE_DEPTH 2
@@ -48,15 +56,18 @@ constexpr int kKRowBytes = 256 + 16;
 // bound); more resident waves hide HBM latency better than deeper per-wave
 // prefetch on this kernel.
 #ifndef LOOM_DECODE_WAVES_TILE4
-#define LOOM_DECODE_WAVES_TILE4 2
+#define LOOM_DECODE_WAVES_TILE4 3
 #endif
+constexpr int waves_per_eu_for(int gt) {
+  return gt <= 2 ? 3 : gt == 4 ? LOOM_DECODE_WAVES_TILE4 : 2;
+}
 template <int GT>
 constexpr int waves_per_eu() {
-  return GT <= 2 ? 3 : GT == 4 ? LOOM_DECODE_WAVES_TILE4 : 2;
+  return waves_per_eu_for(GT);
 }
 // Pages in flight per wave (register buffers of 32 VGPRs each).
 constexpr int kDepth = LOOM_DECODE_DEPTH;
-// Normalizer written into the states of a chunk whose pages failed the guard.
+// Normalizer written into a state whose pages failed the guard.
 constexpr float kPoisonNormalizer = -1.0f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -72,16 +83,19 @@ struct DecodeArgs {
   const int32_t *last;
   uint16_t *out;
   float *lse;
-  float *states;  // [max_chunks][hq][130]
+  // Workspace: header[0] = pages in the virtual list (-1: batch rejected),
+  // header[1 + r] = virtual page prefix of request r (r = 0..B); then the
+  // split states [teams + B][Hq][kStateStride].
+  int64_t *header;
+  float *states;
   int32_t batch;
   int32_t hq;
   int32_t hkv;
   int32_t group;
-  int32_t group_tiles;
-  int32_t chunk_pages;
+  int32_t members;  // hkv * group tiles: waves per team
+  int32_t teams;
   int64_t pool;
   int64_t n_indices;
-  int64_t grid_slots;  // chunk slots covered by the grid
   float scale_log2;
 };
 
@@ -109,10 +123,22 @@ __device__ __forceinline__ u32x4 load16(const uint16_t *p) {
 #ifndef LOOM_DECODE_NT_V
 #define LOOM_DECODE_NT_V 1
 #endif
+// Raw buffer loads of one page's rows for one kv-head.  The resource covers
+// exactly the valid rows of the page (none for a prefetch past the wave's last
+// page), so rows beyond it return zero without touching memory: the pipeline's
+// look-ahead and the tail of a request's last page cost no HBM traffic.
+// Cache policy bit 1 is NT on gfx950.
 template <bool NT>
-__device__ __forceinline__ u32x4 load16_stream(const uint16_t *p) {
-  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-  return *reinterpret_cast<const u32x4 *>(p);
+__device__ __forceinline__ u32x4 load16_rows(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  return __builtin_bit_cast(
+      u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, NT ? 2 : 0));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rows_rsrc(const uint16_t *base,
+                                                                int valid_rows, int hkv) {
+  // gfx9 word 3: 32-bit data format, no swizzle; stride 0 (raw addressing)
+  const int bytes = valid_rows > 0 ? ((valid_rows - 1) * hkv + 1) * 256 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -127,20 +153,17 @@ __device__ __forceinline__ void wave_lds_fence() {
 
 template <int GT>
 struct Smem {
-  int pages[kMaxChunkPages];
+  int64_t incl[kLdsPrefix];           // inclusive page prefix, requests < kLdsPrefix
+  int32_t req_st[kLdsPrefix];         // indptr[r] and last_page_len[r], same requests
+  int32_t req_tl[kLdsPrefix];
+  int64_t blk_excl[kMaxScanBlocks];   // exclusive page prefix of each scan block
+  int64_t wave_tot[kWaves];
   float p[kWaves][GT][16];
   float alpha[kWaves][GT];
-  float wm[kWaves][GT];
-  float wl[kWaves][GT];
-  float wacc[kWaves][GT][128];
   // Per-wave K tile: 16 token rows of 256 bytes padded to kKRowBytes so the
   // MFMA fragment reads (16 rows, same column) hit 16 distinct bank groups.
   uint8_t ktile[kWaves][16 * kKRowBytes];
-  u32x4 qfrag[4][64];  // MFMA B fragments of the query tile, per lane
-  int wave_tot[kWaves];
-  int req, split, nsplit;
-  int req_start, req_end, tail;
-  long long prefix;
+  u32x4 qfrag[kWaves][4][64];  // per wave: MFMA B fragments of its query tile
 };
 
 // One page of K and V for one wave, both as whole 256-byte rows: lane
@@ -151,138 +174,245 @@ struct PageRegs {
   u32x4 v[4];
 };
 
-__device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page, int lane,
-                                          int kvh) {
+// `page` and `valid_rows` are wave-uniform (the resource lives in SGPRs).
+__device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page,
+                                          int valid_rows, int lane, int kvh) {
   const int col = lane & 15, quad = lane >> 4;
+  const int64_t first = ((int64_t)page * 16 * a.hkv + kvh) * 128;
+  const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, valid_rows, a.hkv);
+  const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, valid_rows, a.hkv);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t row = ((int64_t)page * 16 + quad * 4 + j) * a.hkv + kvh;
-    r.k[j] = load16_stream<LOOM_DECODE_NT_K>(a.k + row * 128 + col * 8);
-    r.v[j] = load16_stream<LOOM_DECODE_NT_V>(a.v + row * 128 + col * 8);
+    const int off = (quad * 4 + j) * a.hkv * 256 + col * 16;
+    r.k[j] = load16_rows<LOOM_DECODE_NT_K>(rk, off);
+    r.v[j] = load16_rows<LOOM_DECODE_NT_V>(rv, off);
   }
+}
+
+// Wave-uniform values the compiler cannot prove uniform (loaded through the
+// vector path): pin them to SGPRs.
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uni64(int64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const int32_t hi = __builtin_amdgcn_readfirstlane((int)(x >> 32));
+  return ((int64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ int64_t shfl_up64(int64_t x, int o) {
+  const int lo = __shfl_up((int)(uint32_t)x, o, 64);
+  const int hi = __shfl_up((int)(x >> 32), o, 64);
+  return ((int64_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan64(int64_t x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = shfl_up64(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Pages request r contributes to the virtual page list (0 if the request fails
+// the per-request guard of decode.rs:430-478).
+__device__ __forceinline__ int request_pages(int32_t st, int32_t en, int32_t tl, int32_t ipB) {
+  const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16;
+  return valid ? en - st : 0;
+}
+
+// Teams split the virtual page list into equal ranges: team t owns
+// [team_start(t), team_start(t+1)).
+// floor(n / d) for 0 <= n < 2^53, d > 0, without the long 64-bit integer
+// division sequence: a double-precision estimate, corrected to the exact value.
+__device__ __forceinline__ int64_t floor_div(int64_t n, int64_t d) {
+  int64_t q = (int64_t)((double)n / (double)d);
+  while (q * d > n) --q;
+  while ((q + 1) * d <= n) ++q;
+  return q;
+}
+
+__device__ __forceinline__ int64_t team_start(int64_t total, int64_t t, int teams) {
+  return floor_div(total * t, teams);
+}
+// The team whose range holds virtual page v (0 <= v < total): the largest t
+// with team_start(t) <= v.
+__device__ __forceinline__ int64_t team_of(int64_t total, int64_t v, int teams) {
+  return floor_div((v + 1) * teams + total - 1, total) - 1;
+}
+
+// Teams in use for `total` virtual pages: at most the planned count, and at
+// least kMinTeamPages pages each (short batches are latency-bound: fewer, longer
+// page streams and shorter merges beat one page per wave).
+#ifndef LOOM_DECODE_MIN_TEAM_PAGES
+#define LOOM_DECODE_MIN_TEAM_PAGES 4
+#endif
+__device__ __forceinline__ int active_teams(int64_t total, int teams) {
+  const int64_t by_pages = total / LOOM_DECODE_MIN_TEAM_PAGES;
+  return (int)max<int64_t>(1, min<int64_t>(teams, by_pages));
 }
 
 template <int GT>
 __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_split_kv_kernel(
     DecodeArgs a) {
   __shared__ Smem<GT> sm;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps team state in SGPRs
   const int col = lane & 15, quad = lane >> 4;
 
-  int w = blockIdx.x;
-  const int kvh = w % a.hkv;
-  w /= a.hkv;
-  const int gt = w % a.group_tiles;
-  const long long slot = w / a.group_tiles;
-
-  // ---- flattened chunk schedule: prefix scan of chunks per request ---------
-  // The global guard words and each thread's (start, end, tail) are loaded in
-  // one round trip; the request found by the scan is handed over through LDS.
+  // ---- virtual page list: prefix scan of the valid requests' page counts ---
+  // The guard words and the first block's metadata are loaded together (one
+  // round trip); the global guard is applied after the scan.
   const int32_t ip0 = a.indptr[0];
   const int32_t ipB = a.indptr[a.batch];
-  if (tid == 0) sm.req = -1;
-  long long carry = 0;
-  for (int base = 0; base < a.batch; base += kThreads) {
+  int64_t carry = 0;
+  for (int base = 0, blk = 0; base < a.batch; base += kThreads, ++blk) {
     const int r = base + tid;
-    int c = 0, st = 0, en = 0, tl = 0;
+    int cnt = 0;
     if (r < a.batch) {
-      st = a.indptr[r];
-      en = a.indptr[r + 1];
-      tl = a.last[r];
-      const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16;
-      c = valid ? (en - st + a.chunk_pages - 1) / a.chunk_pages : 0;
+      const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+      cnt = request_pages(st, en, tl, ipB);
+      if (r < kLdsPrefix) {
+        sm.req_st[r] = st;
+        sm.req_tl[r] = tl;
+      }
     }
-    int x = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
+    const int64_t x = wave_incl_scan64(cnt, lane);
     if (lane == 63) sm.wave_tot[wave] = x;
     __syncthreads();
-    int before = 0, tot = 0;
+    int64_t before = 0, tot = 0;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) {
-      const int t = sm.wave_tot[i];
+      const int64_t t = sm.wave_tot[i];
       before += (i < wave) ? t : 0;
       tot += t;
     }
-    const long long incl = carry + before + x, excl = incl - c;
-    if (c > 0 && slot >= excl && slot < incl) {
-      sm.req = r;
-      sm.split = (int)(slot - excl);
-      sm.nsplit = c;
-      sm.prefix = excl;
-      sm.req_start = st;
-      sm.req_end = en;
-      sm.tail = tl;
+    const int64_t incl = carry + before + x;
+    if (r < a.batch) {
+      if (r < kLdsPrefix) sm.incl[r] = incl;
+      if (blockIdx.x == 0) a.header[1 + r] = incl - cnt;
     }
+    if (tid == 0) sm.blk_excl[blk] = carry;
     carry += tot;
     __syncthreads();
   }
-  // Global guard (decode.rs:233-246), and more chunks than the grid covers
-  // (only possible with overlapping request ranges): the whole batch is
-  // rejected, consistently in every workgroup.
-  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices || carry > a.grid_slots) return;
-  const int r = sm.req;
-  if (r < 0) return;
-  const int split = sm.split, nsplit = sm.nsplit;
-  const long long prefix = sm.prefix;
-  const int req_end = sm.req_end;
-  const int tail = sm.tail;
-  const int p0 = sm.req_start + split * a.chunk_pages;
-  const int npages = min(a.chunk_pages, req_end - p0);
+  const int64_t total = carry;
+  // Global guard (decode.rs:233-246): the whole batch is rejected, in every
+  // workgroup, and the merge kernel is told through the header.
+  const bool batch_ok = ip0 == 0 && ipB >= 0 && (int64_t)ipB == a.n_indices;
+  if (blockIdx.x == 0 && tid == 0) {
+    a.header[0] = batch_ok ? total : -1;
+    a.header[1 + a.batch] = total;
+  }
+  if (!batch_ok) return;
+
+  // ---- this wave's team and member ----------------------------------------
+  // Workgroup b runs on XCD b % 8.  The members of a team (the kv-heads and
+  // group tiles of one page range) are consecutive waves of one XCD, so they
+  // share its L2 and walk the same pages at the same time; team t lives on
+  // XCD t % 8, so any number of active teams spreads over all eight.
+  const int xcd_wave = (int)(blockIdx.x >> 3) * kWaves + wave;
+  const int teams = active_teams(total, a.teams);
+  const int team = (xcd_wave / a.members) * 8 + (int)(blockIdx.x & 7);
+  const int member = xcd_wave % a.members;
+  if (team >= teams) return;  // no workgroup barrier follows
+  const int kvh = member % a.hkv;
+  const int gt = member / a.hkv;
+  const int64_t v_begin = team_start(total, team, teams);
+  const int64_t v_end = team_start(total, team + 1, teams);
+  if (v_begin >= v_end) return;
+
+  // ---- the request holding v_begin ----------------------------------------
+  int r;
+  int64_t pre;
+  {
+    int found = -1;
+    int64_t inc = 0;
+    if (a.batch <= kLdsPrefix) {
+      for (int base = 0; base < a.batch && found < 0; base += 64) {
+        const int rr = base + lane;
+        const int64_t x = rr < a.batch ? sm.incl[rr] : INT64_MAX;
+        const uint64_t m = __ballot(x > v_begin);
+        if (m) {
+          found = base + __builtin_ctzll(m);
+          inc = sm.incl[found];
+        }
+      }
+    } else {
+      // the scan block holding v_begin, then its requests again from memory
+      int blk = 0;
+      const int nblk = (a.batch + kThreads - 1) / kThreads;
+      for (int b0 = 0; b0 < nblk; b0 += 64) {
+        const int bb = b0 + lane;
+        const uint64_t m = __ballot(bb < nblk && sm.blk_excl[bb] <= v_begin);
+        if (m) blk = b0 + 63 - __builtin_clzll(m);
+      }
+      int64_t c = sm.blk_excl[blk];
+      for (int base = blk * kThreads; found < 0 && base < a.batch; base += 64) {
+        const int rr = base + lane;
+        int cnt = 0;
+        if (rr < a.batch) cnt = request_pages(a.indptr[rr], a.indptr[rr + 1], a.last[rr], ipB);
+        const int64_t x = c + wave_incl_scan64(cnt, lane);
+        const uint64_t m = __ballot(rr < a.batch && x > v_begin);
+        if (m) {
+          const int l0 = __builtin_ctzll(m);
+          found = base + l0;
+          inc = __shfl(x, l0, 64);
+        }
+        c = __shfl(x, 63, 64);
+      }
+    }
+    if (found < 0) return;  // unreachable: v_begin < total
+    r = uni(found);
+    int cnt0;
+    if (r < kLdsPrefix) {
+      cnt0 = (int)(inc - (r > 0 ? sm.incl[r - 1] : 0));
+    } else {
+      cnt0 = request_pages(a.indptr[r], a.indptr[r + 1], a.last[r], ipB);
+    }
+    pre = uni64(inc - uni(cnt0));
+  }
+
   const int g_base = gt * GT;
   const int gcount = min(GT, a.group - g_base);
-
-  // ---- page indices of this chunk, then the Q fragment (both in flight) ----
-  int pg = 0;
-  if (tid < npages) pg = a.indices[p0 + tid];
-  // Q fragment: column `col` is query head g of this tile; MFMA c contracts
-  // dims 32c + 8*quad + [0, 8), the slices the K fragments read from LDS.
-  // The fragments are identical in every wave; wave 0 parks them in LDS so they
-  // do not occupy 16 VGPRs through the page loop.
   const bool col_valid = col < gcount;
-  if (wave == 0) {
-    const int qh = kvh * a.group + g_base + col;
-    const uint16_t *qp = a.q + ((int64_t)r * a.hq + qh) * 128 + quad * 8;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      sm.qfrag[c][lane] = col_valid ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
-  }
-  // ---- page validation for this chunk (decode.rs:284-289 guard) -----------
-  int bad = 0;
-  if (tid < npages) {
-    sm.pages[tid] = pg;
-    bad = (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
-  }
-  bad = __syncthreads_or(bad);
-  if (bad) {
-    // The request keeps its output sentinels: a single-chunk request simply
-    // writes nothing; a multi-chunk one marks this chunk's states so the
-    // merge kernel skips the whole request.
-    if (nsplit > 1 && tid < gcount) {
-      const int64_t qh = (int64_t)kvh * a.group + g_base + tid;
-      float *st = a.states + ((prefix + split) * a.hq + qh) * (int64_t)loom::kStateWidth;
-      st[0] = 0.0f;
-      st[1] = kPoisonNormalizer;
+  uint8_t *kt = sm.ktile[wave];
+
+  // Metadata of request rr: page count in the virtual list (0 if it fails the
+  // per-request guard), first page position and tail length; LDS copies for
+  // the first kLdsPrefix requests.
+  auto request_meta = [&](int rr, int32_t &st_out, int32_t &tl_out) -> int {
+    int c;
+    if (rr < kLdsPrefix) {
+      st_out = sm.req_st[rr];
+      tl_out = sm.req_tl[rr];
+      c = (int)(sm.incl[rr] - (rr > 0 ? sm.incl[rr - 1] : 0));
+    } else {
+      st_out = a.indptr[rr];
+      tl_out = a.last[rr];
+      c = request_pages(st_out, a.indptr[rr + 1], tl_out, ipB);
     }
-    return;
-  }
+    st_out = uni(st_out);
+    tl_out = uni(tl_out);
+    return uni(c);
+  };
+  // Page indices of the segment of up to 64 pages starting at virtual page
+  // `seg`: lane i holds the index of page i.
+  auto segment_indices = [&](int64_t seg, int64_t piece_end, int64_t pre, int32_t st, int &n,
+                             int &lp0) -> int {
+    n = (int)min<int64_t>(64, piece_end - seg);
+    lp0 = (int)(seg - pre);  // request-local position of the first page
+    return lane < n ? a.indices[st + lp0 + lane] : 0;
+  };
 
-  float m_run = -INFINITY, l_run = 0.0f;
+  float m_run, l_run;
   float acc[GT][8];
-#pragma unroll
-  for (int g = 0; g < GT; ++g)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
 
-  auto process = [&](const PageRegs &pr, int page_idx) {
-    const bool last_page = (p0 + page_idx == req_end - 1);
-    const int valid_tokens = last_page ? tail : 16;
+  // One page: S = K·Qᵀ on MFMA, online softmax, P·V on the VALU.  `rows` is
+  // the number of valid token rows (16, the request's tail on its last page,
+  // 0 for a page index that failed the guard).
+  auto process = [&](const PageRegs &pr, int rows) {
     // K rows -> LDS tile -> MFMA A fragments (lane: token row `col`, dims
     // 32c + 8*quad + [0, 8)).
-    uint8_t *kt = sm.ktile[wave];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       *reinterpret_cast<u32x4 *>(kt + (quad * 4 + j) * kKRowBytes + col * 16) = pr.k[j];
@@ -294,12 +424,11 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[c]), as_bf16x8(sm.qfrag[c][lane]),
-                                                  s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[c]),
+                                                  as_bf16x8(sm.qfrag[wave][c][lane]), s, 0, 0, 0);
     float sv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      sv[i] = (quad * 4 + i < valid_tokens) ? s[i] * a.scale_log2 : -INFINITY;
+    for (int i = 0; i < 4; ++i) sv[i] = (quad * 4 + i < rows) ? s[i] * a.scale_log2 : -INFINITY;
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -327,11 +456,11 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const bool ok = quad * 4 + j < valid_tokens;
+      // rows past the valid ones were loaded as zeros and have zero weight
       float vf[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t wv = ok ? pr.v[j][e] : 0u;
+        const uint32_t wv = pr.v[j][e];
         vf[2 * e] = bf16_lo(wv);
         vf[2 * e + 1] = bf16_hi(wv);
       }
@@ -343,174 +472,191 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     wave_lds_fence();
   };
 
-  // ---- main loop: pages wave, wave+4, ... of this chunk, kDepth-deep --------
-  // Every step issues the loads of the page kDepth-1 steps ahead before it
-  // consumes the current one.  Loads are unconditional (the index is clamped to
-  // the wave's last page) and the buffer rotation is unrolled, so the compiler
-  // waits for exactly the oldest page's loads instead of draining the queue.
-  const int my_pages = npages > wave ? (npages - wave + kWaves - 1) / kWaves : 0;
-  if (my_pages > 0) {
-    auto page_of = [&](int it) { return sm.pages[wave + kWaves * min(it, my_pages - 1)]; };
-    PageRegs buf[kDepth];
-#pragma unroll
-    for (int j = 0; j < kDepth - 1; ++j) load_page(buf[j], a, page_of(j), lane, kvh);
-    int it = 0;
-    while (true) {
-#pragma unroll
-      for (int s = 0; s < kDepth; ++s) {
-        load_page(buf[(s + kDepth - 1) % kDepth], a, page_of(it + kDepth - 1), lane, kvh);
-        process(buf[s], wave + kWaves * it);
-        if (++it >= my_pages) goto pages_done;
-      }
-    }
-  }
-pages_done:
+  // ---- pieces: the parts of requests inside [v_begin, v_end) --------------
+  int64_t v = v_begin;
+  while (true) {
+    int32_t st, tl;
+    const int cnt = request_meta(r, st, tl);  // r is a valid request: cnt > 0
+    const int64_t piece_end = min(v_end, pre + cnt);
+    const bool whole = v_begin <= pre && pre + cnt <= v_end;
 
-  // ---- wave reduction over the 4 row quads ---------------------------------
-  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+    // The first segment's page indices and the Q fragment are fetched in one
+    // round trip.  Q column `col` is query head g of this tile; MFMA c
+    // contracts dims 32c + 8*quad + [0, 8), the slices the K fragments read.
+    int seg_n, seg_lp0;
+    int seg_idx = segment_indices(v, piece_end, pre, st, seg_n, seg_lp0);
+    {
+      const int qh = kvh * a.group + g_base + col;
+      const uint16_t *qp = a.q + ((int64_t)r * a.hq + qh) * 128 + quad * 8;
+      u32x4 qr[4];
 #pragma unroll
-  for (int g = 0; g < GT; ++g)
+      for (int c = 0; c < 4; ++c) qr[c] = col_valid ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = acc[g][e];
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
-      acc[g][e] = x;
+      for (int c = 0; c < 4; ++c) sm.qfrag[wave][c][lane] = qr[c];
+      wave_lds_fence();
     }
-  if (quad == 0) {
-    if (col < GT) {
-      sm.wm[wave][col] = m_run;
-      sm.wl[wave][col] = l_tot;
-    }
+    m_run = -INFINITY;
+    l_run = 0.0f;
 #pragma unroll
     for (int g = 0; g < GT; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sm.wacc[wave][g][col * 8 + e] = acc[g][e];
-  }
-  __syncthreads();
+      for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+    bool bad = false;
 
-  // ---- workgroup merge of the 4 wave states --------------------------------
-  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
-  float *chunk_states = a.states + ((prefix + split) * a.hq) * (int64_t)loom::kStateWidth;
-  for (int idx = tid; idx < GT * 128; idx += kThreads) {
-    const int g = idx >> 7, d = idx & 127;
-    if (g >= gcount) continue;
-    float M = -INFINITY;
+    // Segments of up to 64 pages: one page index per lane, read back with
+    // v_readlane as the page loop walks them (decode.rs:284-289 guard on each).
+    for (int64_t seg = v; seg < piece_end; seg += 64) {
+      if (seg != v) seg_idx = segment_indices(seg, piece_end, pre, st, seg_n, seg_lp0);
+      const int n = seg_n, lp0 = seg_lp0, idx = seg_idx;
+      const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
+      bad |= __ballot(lane < n && !ok) != 0;
+      auto page_of = [&](int i) { return __builtin_amdgcn_readlane(idx, min(i, n - 1)); };
+      auto rows_of = [&](int i) {
+        if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
+        return lp0 + i == cnt - 1 ? tl : 16;
+      };
+      // kDepth-deep pipeline: each step issues the loads of the page kDepth-1
+      // steps ahead before consuming the current one.  Loads past the segment
+      // have no valid rows and touch no memory; the unrolled buffer rotation
+      // lets the compiler wait for exactly the oldest page's loads.
+      PageRegs buf[kDepth];
 #pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) M = fmaxf(M, sm.wm[wv][g]);
-    float L = 0.f, O = 0.f;
+      for (int j = 0; j < kDepth - 1; ++j) load_page(buf[j], a, page_of(j), rows_of(j), lane, kvh);
+      int i = 0;
+      while (true) {
 #pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) {
-      const float f = fast_exp2(sm.wm[wv][g] - M);
-      L = fmaf(sm.wl[wv][g], f, L);
-      O = fmaf(sm.wacc[wv][g][d], f, O);
-    }
-    const int64_t qh = qh_base + g;
-    if (nsplit == 1) {
-      a.out[((int64_t)r * a.hq + qh) * 128 + d] = f32_to_bf16(O / L);
-      if (d == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(L);
-    } else {
-      float *st = chunk_states + qh * (int64_t)loom::kStateWidth;
-      if (d == 0) {
-        st[0] = M;
-        st[1] = L;
+        for (int s = 0; s < kDepth; ++s) {
+          load_page(buf[(s + kDepth - 1) % kDepth], a, page_of(i + kDepth - 1),
+                    rows_of(i + kDepth - 1), lane, kvh);
+          process(buf[s], rows_of(i));
+          if (++i >= n) goto segment_done;
+        }
       }
-      st[2 + d] = O;
+    segment_done:;
     }
+
+    // ---- finish the piece: reduce the 4 row quads ---------------------------
+    float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = acc[g][e];
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        acc[g][e] = x;
+      }
+    const int64_t qh_base = (int64_t)kvh * a.group + g_base;
+    if (whole) {
+      // The request lies inside this wave's range: final output in place.  An
+      // invalid page index leaves the request's sentinels untouched.
+      if (!bad) {
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+          if (g >= gcount) break;
+          const float Lg = __shfl(l_tot, g, 64);
+          if (quad == 0) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              w[e] = (uint32_t)f32_to_bf16(acc[g][2 * e] / Lg) |
+                     ((uint32_t)f32_to_bf16(acc[g][2 * e + 1] / Lg) << 16);
+            *reinterpret_cast<u32x4 *>(a.out + ((int64_t)r * a.hq + qh_base + g) * 128 + col * 8) =
+                u32x4{w[0], w[1], w[2], w[3]};
+          }
+        }
+        if (lane < gcount) a.lse[(int64_t)r * a.hq + qh_base + lane] = m_run + __log2f(l_tot);
+      }
+    } else {
+      // Split request: one state per (team, request), slot team + r (unique:
+      // along the virtual list either the team or the request advances).
+      float *st_base = a.states + ((int64_t)(team + r) * a.hq + qh_base) * kStateStride;
+      if (bad) {
+        if (lane < gcount) {
+          st_base[lane * kStateStride] = 0.0f;
+          st_base[lane * kStateStride + 1] = kPoisonNormalizer;
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+          if (g >= gcount) break;
+          if (quad == 0) {
+            float *o = st_base + g * kStateStride + 4 + col * 8;
+            *reinterpret_cast<f32x4 *>(o) = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+            *reinterpret_cast<f32x4 *>(o + 4) = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+          }
+        }
+        if (lane < gcount) {
+          st_base[lane * kStateStride] = m_run;
+          st_base[lane * kStateStride + 1] = l_tot;
+        }
+      }
+    }
+
+    v = piece_end;
+    if (v >= v_end) break;
+    // next request with pages (v < total, so one exists)
+    pre += cnt;
+    do {
+      if (++r >= a.batch) return;  // unreachable: v < total
+    } while (request_meta(r, st, tl) == 0);
   }
 }
 
-// Merges the chunk states of one (request, query head) into O and log2-LSE:
-// one workgroup of 128 lanes (one per output column) per state row, for the
-// requests that span more than one chunk.  Same request validity and chunk
-// schedule as the partial kernel; a poisoned chunk (invalid page) leaves the
-// request's sentinels untouched.
+// Merges the states of one (request, query head) whose pages span several
+// teams into O and log2-LSE: 128 lanes, one per output column, one pass with
+// a running max over blocks of 16 teams (one load round trip per block).  The
+// header written by the partial kernel gives the request's virtual page
+// range; a poisoned state (invalid page index) leaves the request's sentinels.
 __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
-  __shared__ long long s_wave_sum[2][2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kBlock = 16;
+  const int tid = threadIdx.x;
   const int r = blockIdx.x / a.hq;
   const int qh = blockIdx.x % a.hq;
-  const int32_t ip0 = a.indptr[0];
-  const int32_t ipB = a.indptr[a.batch];
-  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices) return;
-  // chunks before r and in total (the partial kernel's prefix scan)
-  long long before = 0, total = 0;
-  for (int rr = tid; rr < a.batch; rr += 128) {
-    const int32_t st = a.indptr[rr], en = a.indptr[rr + 1], tl = a.last[rr];
-    const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16;
-    const long long c = valid ? (en - st + a.chunk_pages - 1) / a.chunk_pages : 0;
-    total += c;
-    before += rr < r ? c : 0;
-  }
+  const int64_t total = a.header[0];
+  const int64_t pre = a.header[1 + r], pend = a.header[2 + r];
+  if (total <= 0 || pend <= pre) return;
+  const int teams = active_teams(total, a.teams);
+  const int64_t t0 = team_of(total, pre, teams), t1 = team_of(total, pend - 1, teams);
+  if (t0 == t1) return;
+  const bool all_nonempty = total >= teams;
+  float M = -INFINITY, l = 0.f, o = 0.f;
+  bool poisoned = false;
+  for (int64_t t = t0; t <= t1; t += kBlock) {
+    float ms[kBlock], ls[kBlock], xs[kBlock];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    before += __shfl_xor(before, o, 64);
-    total += __shfl_xor(total, o, 64);
-  }
-  if (lane == 0) {
-    s_wave_sum[wave][0] = before;
-    s_wave_sum[wave][1] = total;
-  }
-  __syncthreads();
-  before = s_wave_sum[0][0] + s_wave_sum[1][0];
-  total = s_wave_sum[0][1] + s_wave_sum[1][1];
-  if (total > a.grid_slots) return;
-  const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
-  if (!(st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16)) return;
-  const int nsplit = (en - st + a.chunk_pages - 1) / a.chunk_pages;
-  if (nsplit <= 1) return;
-
-  const int64_t stride = (int64_t)a.hq * loom::kStateWidth;
-  const float *row = a.states + (before * a.hq + qh) * (int64_t)loom::kStateWidth;
-  // Pass 1: the global max and the poison marks, with the splits spread over
-  // the 128 lanes (one load round trip for up to 128 splits).
-  float mloc = -INFINITY;
-  int poisoned = 0;
-  for (int sidx = tid; sidx < nsplit; sidx += 128) {
-    const float *ss = row + sidx * stride;
-    mloc = fmaxf(mloc, ss[0]);
-    poisoned |= ss[1] < 0.0f;
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
-    poisoned |= __shfl_xor(poisoned, o, 64);
-  }
-  __shared__ float s_m[2];
-  __shared__ int s_p[2];
-  if (lane == 0) {
-    s_m[wave] = mloc;
-    s_p[wave] = poisoned;
-  }
-  __syncthreads();
-  if (s_p[0] | s_p[1]) return;
-  const float M = fmaxf(s_m[0], s_m[1]);
-  // Pass 2: weighted sums; the unroll keeps eight splits' loads in flight.
-  float l = 0.f, o = 0.f;
-  int sidx = 0;
-  for (; sidx + 8 <= nsplit; sidx += 8) {
-    float ms[8], ls[8], xs[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float *ss = row + (sidx + u) * stride;
-      ms[u] = ss[0];
-      ls[u] = ss[1];
-      xs[u] = ss[2 + tid];
+    for (int u = 0; u < kBlock; ++u) {
+      ms[u] = -INFINITY;
+      ls[u] = 0.f;
+      xs[u] = 0.f;
+      const int64_t tu = t + u;
+      if (tu <= t1 && (all_nonempty || team_start(total, tu, teams) <
+                                           team_start(total, tu + 1, teams))) {
+        const float *ss = a.states + ((tu + r) * a.hq + qh) * (int64_t)kStateStride;
+        ms[u] = ss[0];
+        ls[u] = ss[1];
+        xs[u] = ss[4 + tid];
+      }
     }
+    float mb = M;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float f = fast_exp2(ms[u] - M);
+    for (int u = 0; u < kBlock; ++u) {
+      mb = fmaxf(mb, ms[u]);
+      poisoned |= ls[u] < 0.0f;
+    }
+    const float sc = fast_exp2(M - mb);
+    l *= sc;
+    o *= sc;
+#pragma unroll
+    for (int u = 0; u < kBlock; ++u) {
+      const float f = fast_exp2(ms[u] - mb);
       l = fmaf(ls[u], f, l);
       o = fmaf(xs[u], f, o);
     }
+    M = mb;
   }
-  for (; sidx < nsplit; ++sidx) {
-    const float *ss = row + sidx * stride;
-    const float f = fast_exp2(ss[0] - M);
-    l = fmaf(ss[1], f, l);
-    o = fmaf(ss[2 + tid], f, o);
-  }
+  if (poisoned) return;
   a.out[((int64_t)r * a.hq + qh) * 128 + tid] = f32_to_bf16(o / l);
   if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(l);
 }
@@ -557,46 +703,44 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   // of two, at most 8 (P·V accumulators are GT x 8 floats per lane).
   const uint32_t gtile = group <= 1 ? 1u : group <= 2 ? 2u : group <= 4 ? 4u : 8u;
   const uint64_t gtiles = (group + gtile - 1) / gtile;
+  if (opt.reserved != 0) return fail(err, LOOM_PLAN_INVALID_OPTION, "reserved", opt.reserved);
   const uint64_t max_pages = opt.max_total_pages ? opt.max_total_pages : spec->max_num_pages;
   if (max_pages < B) return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
   if (max_pages > (uint64_t)INT32_MAX)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
 
-  // Chunk size: enough (request, kv-head, tile, chunk) workgroups to cover
-  // every CU several times at the expected length, and as long a chunk as
-  // that allows (fewer states to merge).
-  uint32_t chunk = opt.chunk_pages;
-  if (chunk == 0) {
-    const uint64_t expected = opt.expected_kv_len ? opt.expected_kv_len : 4096;
-    const uint64_t pages = (expected + loom::kPageSize - 1) / loom::kPageSize;
-    const uint64_t units = B * hkv * gtiles;
-    const uint64_t target_wgs = 8ull * (uint64_t)provider->dev.cus;
-    const uint64_t splits = std::max<uint64_t>(1, (target_wgs + units - 1) / units);
-    uint64_t c = (pages + splits - 1) / splits;
-    c = (c + 3) / 4 * 4;
-    chunk = (uint32_t)std::min<uint64_t>(kMaxChunkPages, std::max<uint64_t>(4, c));
-  }
-  if (chunk < 4 || chunk > (uint32_t)kMaxChunkPages || chunk % 4 != 0)
-    return fail(err, LOOM_PLAN_INVALID_OPTION, "chunk_pages", chunk);
+  if (B > (uint64_t)kMaxScanBlocks * kThreads)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "batch_size", B);
 
-  const uint64_t max_chunks = (max_pages + chunk - 1) / chunk + B;
-  const uint64_t grid = max_chunks * hkv * gtiles;
-  if (grid > (uint64_t)INT32_MAX || B * hq > (uint64_t)INT32_MAX)
+  // Teams: one wave per SIMD slot the kernel's register budget allows, so
+  // the whole grid is resident at once and every wave streams the same number
+  // of pages.
+  const uint64_t members = hkv * gtiles;
+  const uint64_t slots = (uint64_t)provider->dev.cus * 4 * waves_per_eu_for((int)gtile);
+  uint64_t teams = opt.teams ? opt.teams : std::max<uint64_t>(1, slots / members);
+  // Each XCD (every 8th workgroup) holds ceil(teams / 8) whole teams.
+  const uint64_t xcd_waves = (teams + 7) / 8 * members;
+  const uint64_t grid = (xcd_waves + kWaves - 1) / kWaves * 8;
+  if (grid > (uint64_t)INT32_MAX || teams > (uint64_t)INT32_MAX || B * hq > (uint64_t)INT32_MAX)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged batch-decode", grid);
-  const uint64_t state_bytes = max_chunks * hq * loom::kStateWidth * 4;
+  const uint64_t header_bytes = ((B + 2) * 8 + 255) / 256 * 256;
+  const uint64_t state_slots = teams + B;
+  const uint64_t state_bytes = state_slots * hq * kStateStride * 4;
 
   auto *p = new loom_paged_decode_plan;
   p->device = provider->dev.device;
   loom_paged_decode_plan_info_t &i = p->info;
   i.spec = *spec;
-  i.algorithm = LOOM_PAGED_DECODE_SPLIT_KV_GROUP;
-  i.chunk_pages = chunk;
+  i.algorithm = LOOM_PAGED_DECODE_BALANCED_SPLIT_KV;
+  i.teams = (uint32_t)teams;
   i.group_tile = gtile;
   i.group_tiles = (uint32_t)gtiles;
   i.max_total_pages = max_pages;
-  i.max_chunks = max_chunks;
-  i.workspace_bytes = state_bytes;
+  i.state_slots = state_slots;
+  i.workspace_bytes = header_bytes + state_bytes;
+  i.header_bytes = header_bytes;
   i.block_threads = kThreads;
+  i.grid_blocks = (uint32_t)grid;
   i.device_cus = (uint32_t)provider->dev.cus;
   *out = p;
   return loom::ok(err);
@@ -661,19 +805,19 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.last = (const int32_t *)l[5]->ptr;
   a.out = (uint16_t *)l[6]->ptr;
   a.lse = (float *)l[7]->ptr;
-  a.states = (float *)l[8]->ptr;
+  a.header = (int64_t *)l[8]->ptr;
+  a.states = (float *)(l[8]->ptr + pi.header_bytes);
   a.batch = (int32_t)s.batch_size;
   a.hq = (int32_t)s.num_query_heads;
   a.hkv = (int32_t)s.num_kv_heads;
   a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
-  a.group_tiles = (int32_t)pi.group_tiles;
-  a.chunk_pages = (int32_t)pi.chunk_pages;
+  a.members = (int32_t)(s.num_kv_heads * pi.group_tiles);
+  a.teams = (int32_t)pi.teams;
   a.pool = (int64_t)s.max_num_pages;
   a.n_indices = (int64_t)l[4]->numel;
-  a.grid_slots = (int64_t)((l[4]->numel + pi.chunk_pages - 1) / pi.chunk_pages + s.batch_size);
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
 
-  const uint64_t grid = (uint64_t)a.grid_slots * s.num_kv_heads * pi.group_tiles;
+  const uint64_t grid = pi.grid_blocks;
   hipStream_t stream = scope->queue->stream;
   const dim3 g3((unsigned)grid), b3(kThreads);
   switch (pi.group_tile) {
@@ -684,7 +828,7 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   }
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
-    // One command: the split kernel, then the merge of multi-chunk requests.
+    // One command: the partial kernel, then the merge of split requests.
     hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)(s.batch_size * s.num_query_heads)),
                        dim3(128), 0, stream, a);
     e = hipGetLastError();

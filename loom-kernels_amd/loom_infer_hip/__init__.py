@@ -532,7 +532,7 @@ class Bf16PagedBatchDecodePlan:
 
     @property
     def algorithm(self) -> str:
-        return {1: "split_kv_group"}[self.info.algorithm]
+        return {1: "balanced_split_kv"}[self.info.algorithm]
 
     @property
     def workspace_bytes(self) -> int:
@@ -565,8 +565,9 @@ class DecodeProvider:
         return cls(out.value, device)
 
     def plan_bf16_paged_batch(self, spec: Bf16PagedBatchDecodeSpec, max_total_pages: int = 0,
-                              chunk_pages: int = 0, expected_kv_len: int = 0):
-        opt = _ffi.PagedDecodePlanOptions(max_total_pages, chunk_pages, expected_kv_len)
+                              teams: int = 0):
+        """`teams` = number of equal page ranges (0: one wave per SIMD slot)."""
+        opt = _ffi.PagedDecodePlanOptions(max_total_pages, teams, 0)
         out = C.c_void_p()
         _call(lib().loom_decode_provider_plan_bf16_paged_batch, self._p, C.byref(spec._c),
               C.byref(opt), C.byref(out))

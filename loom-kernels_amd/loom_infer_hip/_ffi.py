@@ -36,14 +36,14 @@ class Handle(C.Structure):
 
 
 class PagedDecodePlanOptions(C.Structure):
-    _fields_ = [("max_total_pages", u64), ("chunk_pages", u32), ("expected_kv_len", u32)]
+    _fields_ = [("max_total_pages", u64), ("teams", u32), ("reserved", u32)]
 
 
 class PagedDecodePlanInfo(C.Structure):
-    _fields_ = [("spec", PagedDecodeSpec), ("algorithm", i32), ("chunk_pages", u32),
+    _fields_ = [("spec", PagedDecodeSpec), ("algorithm", i32), ("teams", u32),
                 ("group_tile", u32), ("group_tiles", u32), ("max_total_pages", u64),
-                ("max_chunks", u64), ("workspace_bytes", u64), ("block_threads", u32),
-                ("device_cus", u32)]
+                ("state_slots", u64), ("workspace_bytes", u64), ("header_bytes", u64),
+                ("block_threads", u32), ("grid_blocks", u32), ("device_cus", u32)]
 
 
 class PagedDecodeArgs(C.Structure):

@@ -43,30 +43,36 @@ def test_gate_fixtures(L, oracle, case):
     s = oracle.paged_spec(B, pool, hq, hkv)
     ref_out, ref_lse = oracle.paged_decode(s, q, k, v, case["indptr"], case["indices"],
                                            case["last"])
-    for chunk in (0, 4):
-        r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=chunk)
+    # default plan, one team (every request finished in place), and a few teams
+    # (requests split across page ranges, merged by the second kernel)
+    for teams in (0, 1, 3):
+        r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
         out, lse = r.run(q, k, v, case["indptr"], case["indices"], case["last"])
         stats = compare_decode(oracle, out, lse, ref_out, ref_lse)
-        log(f"  chunk={r.plan.info.chunk_pages} {stats}")
+        log(f"  teams={r.plan.info.teams} {stats}")
 
 
 SHAPES = [
-    # (name, B, hq, hkv, lens, chunk)
+    # (name, B, hq, hkv, lens, teams); teams 0 = the device default
     ("mha_c1_like", 1, 32, 32, [1024], 0),
     ("gqa4_ragged", 6, 32, 8, [1, 15, 16, 17, 700, 2049], 0),
-    ("gqa4_ragged_chunk4", 6, 32, 8, [1, 15, 16, 17, 700, 2049], 4),
-    ("gqa4_ragged_chunk64", 5, 32, 8, [3000, 33, 4097, 1, 64], 64),
+    ("gqa4_ragged_teams7", 6, 32, 8, [1, 15, 16, 17, 700, 2049], 7),
+    ("gqa4_ragged_teams1", 5, 32, 8, [3000, 33, 4097, 1, 64], 1),
+    ("gqa4_ragged_teams64", 5, 32, 8, [3000, 33, 4097, 1, 64], 64),
     ("gqa8_long", 1, 64, 8, [8192], 0),
     ("mqa_group8", 3, 8, 1, [16, 23, 48], 0),
     ("group16_two_tiles", 2, 16, 1, [300, 77], 0),
     ("group3", 3, 6, 2, [5, 40, 129], 4),
     ("group2", 2, 4, 2, [33, 1000], 0),
+    # more requests than the workgroup keeps in LDS: the block-wise search
+    ("batch1100_small", 1100, 4, 1, [1 + (i * 37) % 70 for i in range(1100)], 0),
+    ("batch1100_teams13", 1100, 8, 2, [1 + (i * 53) % 90 for i in range(1100)], 13),
 ]
 
 
-@pytest.mark.parametrize("name,B,hq,hkv,lens,chunk", SHAPES, ids=[s[0] for s in SHAPES])
-def test_seeded_shapes(L, oracle, name, B, hq, hkv, lens, chunk):
-    log(f"decode seeded shape {name} B={B} hq={hq} hkv={hkv} lens={lens} chunk={chunk}")
+@pytest.mark.parametrize("name,B,hq,hkv,lens,teams", SHAPES, ids=[s[0] for s in SHAPES])
+def test_seeded_shapes(L, oracle, name, B, hq, hkv, lens, teams):
+    log(f"decode seeded shape {name} B={B} hq={hq} hkv={hkv} teams={teams}")
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     pool = sum((x + 15) // 16 for x in lens) + 3
     indptr, indices, last = ragged_table(rng, lens, pool)
@@ -75,9 +81,9 @@ def test_seeded_shapes(L, oracle, name, B, hq, hkv, lens, chunk):
     v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
     s = oracle.paged_spec(B, pool, hq, hkv)
     ref_out, ref_lse = oracle.paged_decode(s, q, k, v, indptr, indices, last)
-    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=chunk)
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
     out, lse = r.run(q, k, v, indptr, indices, last)
-    log(f"  plan chunk={r.plan.info.chunk_pages} tile={r.plan.info.group_tile}x"
+    log(f"  plan teams={r.plan.info.teams} tile={r.plan.info.group_tile}x"
         f"{r.plan.info.group_tiles} {compare_decode(oracle, out, lse, ref_out, ref_lse)}")
     # a second call over the previous call's workspace contents is identical
     out2, lse2 = r.run(q, k, v, indptr, indices, last)
@@ -93,7 +99,7 @@ def test_closed_form_zero_query(L, oracle):
     q = np.zeros(B * hq * 128, np.uint16)
     k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
     v = oracle.bf16_from_f32(rng.integers(-4, 5, pool * 16 * hkv * 128).astype(np.float32))
-    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=4)
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=3)
     out, lse = r.run(q, k, v, indptr, indices, last)
     np.testing.assert_allclose(lse, np.repeat(np.log2(lens), hq), atol=2e-6)
     ref_out, _ = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v, indptr,
@@ -115,8 +121,8 @@ def test_invalid_page_guard_preserves_sentinels(L):
     assert np.all(np.isnan(o[4 * 128:])) and np.all(np.isnan(l[4:]))
 
 
-def test_invalid_page_in_multi_chunk_request(L, oracle):
-    """An invalid page inside a long request (several chunks) leaves that
+def test_invalid_page_in_split_request(L, oracle):
+    """An invalid page inside a request split over several teams leaves that
     request's sentinels and completes the others; the next valid call over the
     poisoned workspace is correct."""
     torch = pytest.importorskip("torch")
@@ -125,12 +131,12 @@ def test_invalid_page_in_multi_chunk_request(L, oracle):
     pool = 64
     indptr, indices, last = ragged_table(rng, lens, pool)
     bad = indices.copy()
-    bad[20] = pool + 5  # inside request 0, chunk 5 at chunk_pages=4
+    bad[20] = pool + 5  # inside request 0 (38 pages), in the second of 8 teams
     B, hq, hkv = 2, 8, 2
     q = seeded_normal_bf16(oracle, rng, B * hq * 128)
     k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
     v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
-    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=4)
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=8)
     out, lse = r.run(q, k, v, indptr, bad, last)
     o = oracle.bf16_to_f32(out).reshape(B, hq * 128)
     assert np.all(np.isnan(o[0])) and np.all(np.isnan(lse[:hq]))
@@ -140,6 +146,35 @@ def test_invalid_page_in_multi_chunk_request(L, oracle):
                    ref_lse[hq:])
     out2, lse2 = r.run(q, k, v, indptr, indices, last)
     compare_decode(oracle, out2, lse2, ref_out, ref_lse)
+
+
+@pytest.mark.parametrize("teams", [0, 1, 5])
+def test_invalid_request_leaves_sentinels(L, oracle, teams):
+    """Requests failing the per-request guard (decode.rs:430-478: last page
+    length outside 1..16, empty range) contribute no pages; the others are
+    computed as usual, also when the pages around them are split over teams."""
+    rng = np.random.default_rng(8)
+    lens = [100, 50, 300, 20, 64]
+    B, hq, hkv = len(lens), 8, 2
+    pool = sum((x + 15) // 16 for x in lens) + 2
+    indptr, indices, last = ragged_table(rng, lens, pool)
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    ref_out, ref_lse = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v,
+                                           indptr, indices, last)
+    bad_last = np.array(last, copy=True)
+    bad_last[1] = 0
+    bad_last[3] = 17
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
+    out, lse = r.run(q, k, v, indptr, indices, bad_last)
+    o = oracle.bf16_to_f32(out).reshape(B, hq * 128)
+    l = lse.reshape(B, hq)
+    for rq in (1, 3):
+        assert np.all(np.isnan(o[rq])) and np.all(np.isnan(l[rq]))
+    for rq in (0, 2, 4):
+        compare_decode(oracle, out.reshape(B, -1)[rq], l[rq], ref_out.reshape(B, -1)[rq],
+                       ref_lse.reshape(B, hq)[rq])
 
 
 def test_global_indptr_guard(L):
@@ -222,7 +257,7 @@ def test_full_c3_shape_sampled_requests(L, oracle):
     q = torch.randn(B * hq * 128, generator=g, device="cuda").to(torch.bfloat16)
     k = torch.randn(pool * 16 * hkv * 128, generator=g, device="cuda").to(torch.bfloat16)
     v = torch.randn(pool * 16 * hkv * 128, generator=g, device="cuda").to(torch.bfloat16)
-    r = DecodeRunner(L, B, pool, hq, hkv, expected_kv_len=4352)
+    r = DecodeRunner(L, B, pool, hq, hkv)
     out, lse = r.run_dev(q, k, v, to_dev_i32(indptr), to_dev_i32(indices), to_dev_i32(last))
     out_h, lse_h = bf16_host(out), lse.cpu().numpy()
     assert np.all(np.isfinite(oracle.bf16_to_f32(out_h)))

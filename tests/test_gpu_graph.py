@@ -39,7 +39,7 @@ def test_decode_graph_replays_match_eager_and_oracle(L, oracle):
     v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
     ref_o, ref_l = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v, indptr,
                                        indices, last)
-    r = DecodeRunner(L, B, pool, hq, hkv, chunk_pages=4)
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=7)
     eager_o, eager_l = r.run(q, k, v, indptr, indices, last)
     compare_decode(oracle, eager_o, eager_l, ref_o, ref_l)
 
