@@ -8,11 +8,13 @@
 //
 // MI355X design:
 //   * validation runs once per command, not once per workgroup: a small grid
-//     checks the whole page-index array in parallel; the last workgroup to
-//     arrive checks the request table, every token's (request, position,
-//     slot), sorts the T slot keys in LDS (bitonic) to find duplicate physical
-//     slots in O(T log^2 T), and publishes one validity word;
-//   * the apply kernel runs one workgroup per token: 64 lanes compute the
+//     checks the whole page-index array and every token's (request, position,
+//     slot) in parallel, one token per thread, and records the slot keys; the
+//     last workgroup to arrive checks the request table, finds duplicate
+//     physical slots with an LDS hash set in O(T), and publishes one validity
+//     word;
+//   * the apply kernel runs one workgroup per token: it reads the recorded
+//     slot instead of walking the page table again, 64 lanes compute the
 //     token's 64 (sin, cos) pairs once into LDS, then 16 lanes per 256-byte
 //     head row rotate Q/K and scatter K/V rows into the page slot with 16-byte
 //     loads and stores;
@@ -32,7 +34,18 @@ namespace {
 constexpr int kValidateThreads = 256;
 constexpr int kApplyThreads = 256;
 constexpr int kIndicesPerValidateBlock = 8192;
-constexpr int kMaxSortKeys = LOOM_APPEND_MAX_TOKENS_EXTENDED;
+constexpr int kMaxTokens = LOOM_APPEND_MAX_TOKENS_EXTENDED;
+// Workspace: 64 header words ([0] validity, [1] bad accumulator, [2] arrival
+// counter), then the T slot keys (u32) and the T positions (i32).
+constexpr int kWsHeaderWords = 64;
+constexpr uint32_t kEmptyKey = 0xffffffffu;
+// LDS hash set for duplicate slots: a power of two >= 2T.
+constexpr int kHashSlots = 2 * kMaxTokens;
+__host__ __device__ constexpr int hash_slots(int tokens) {
+  int n = 64;
+  while (n < 2 * tokens) n <<= 1;
+  return n;
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -48,7 +61,7 @@ struct AppendArgs {
   uint16_t *q_out;
   uint16_t *k_pages;
   uint16_t *v_pages;
-  uint32_t *ws;  // [0] valid flag, [1] bad accumulator, [2] arrivals
+  uint32_t *ws;  // header words, then slot keys and positions
   int32_t tokens;
   int32_t batch;
   int32_t hq;
@@ -85,13 +98,21 @@ __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int *req,
   return true;
 }
 
+// Validation, all-or-nothing.  Workgroup b checks page indices
+// [b*8192, (b+1)*8192) (rope/mod.rs:143-150) and tokens [b*256, (b+1)*256)
+// (paged_append/mod.rs:262-309), one token per thread, and records each
+// token's physical slot key and position in the workspace for the apply
+// kernel.  The last workgroup to arrive checks the request table
+// (paged_decode/mod.rs:164-205), finds duplicate physical slots with an LDS
+// hash set over all T keys, and publishes one validity word.
 __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(AppendArgs a) {
-  __shared__ uint32_t keys[kMaxSortKeys];
+  __shared__ uint32_t table[kHashSlots];
   __shared__ int s_last;
   const int tid = threadIdx.x;
   uint32_t *flag = a.ws, *bad_acc = a.ws + 1, *arrivals = a.ws + 2;
+  uint32_t *keys = a.ws + kWsHeaderWords;
+  int32_t *positions = reinterpret_cast<int32_t *>(keys + a.tokens);
 
-  // Whole page-index array (rope/mod.rs:143-150): this block's range.
   int bad = 0;
   const int64_t lo = (int64_t)blockIdx.x * kIndicesPerValidateBlock;
   const int64_t hi = min(lo + kIndicesPerValidateBlock, a.n_indices);
@@ -99,10 +120,22 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
     const int32_t pg = a.indices[i];
     bad |= (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
   }
+  const int t = blockIdx.x * kValidateThreads + tid;
+  if (t < a.tokens) {
+    int r, p, off;
+    int64_t pg;
+    uint32_t key = kEmptyKey;
+    if (token_slot(a, t, &r, &p, &pg, &off))
+      key = (uint32_t)(pg * 16 + off);
+    else
+      bad = 1;
+    keys[t] = key;
+    positions[t] = p;
+  }
   bad = __syncthreads_or(bad);
   if (tid == 0) {
     if (bad) atomicOr(bad_acc, 1u);
-    __threadfence();
+    __threadfence();  // keys and positions visible before the arrival
     const uint32_t old = atomicAdd(arrivals, 1u);
     s_last = (old + 1 == gridDim.x) ? 1 : 0;
   }
@@ -110,71 +143,74 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
   if (!s_last) return;
   __threadfence();
 
-  // Last block: request table (paged_decode/mod.rs:164-205).
+  // Last workgroup: the request table, then duplicate slots.
   bad = 0;
   if (tid == 0) bad |= (a.indptr[0] != 0 || (int64_t)a.indptr[a.batch] != a.n_indices);
   for (int r = tid; r < a.batch; r += kValidateThreads) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
     bad |= (en <= st || tl < 1 || tl > 16) ? 1 : 0;
   }
-  // Tokens (paged_append/mod.rs:262-309) and their slot keys.
-  int n = 1;
-  while (n < a.tokens) n <<= 1;
-  for (int t = tid; t < n; t += kValidateThreads) {
-    uint32_t key = 0xffffffffu;
-    if (t < a.tokens) {
-      int r, p, off;
-      int64_t pg;
-      if (token_slot(a, t, &r, &p, &pg, &off))
-        key = (uint32_t)(pg * 16 + off);
-      else
-        bad = 1;
-    }
-    keys[t] = key;
-  }
+  const int slots = hash_slots(a.tokens);
+  for (int i = tid; i < slots; i += kValidateThreads) table[i] = kEmptyKey;
   bad = __syncthreads_or(bad);
-  // Bitonic sort of the keys; equal neighbours are duplicate physical slots.
-  if (!bad) {
-    for (int size = 2; size <= n; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < n; i += kValidateThreads) {
-          const int j = i ^ stride;
-          if (j > i) {
-            const uint32_t x = keys[i], y = keys[j];
-            const bool up = (i & size) == 0;
-            if ((x > y) == up) {
-              keys[i] = y;
-              keys[j] = x;
-            }
-          }
+  if (!bad && atomicAdd(bad_acc, 0u) == 0u) {
+    // Open addressing at load <= 1/2: every probe sequence ends at an empty
+    // slot or at the same key (a duplicate).
+    int dup = 0;
+    const uint32_t mask = (uint32_t)slots - 1u;
+    for (int i = tid; i < a.tokens; i += kValidateThreads) {
+      const uint32_t key = __atomic_load_n(&keys[i], __ATOMIC_RELAXED);
+      uint32_t h = (key * 0x9E3779B1u) >> 16 & mask;
+      while (true) {
+        const uint32_t prev = atomicCAS(&table[h], kEmptyKey, key);
+        if (prev == kEmptyKey) break;
+        if (prev == key) {
+          dup = 1;
+          break;
         }
-        __syncthreads();
+        h = (h + 1u) & mask;
       }
     }
-    int dup = 0;
-    for (int i = tid; i + 1 < a.tokens; i += kValidateThreads)
-      dup |= (keys[i] == keys[i + 1]) ? 1 : 0;
     bad = __syncthreads_or(dup);
+  } else {
+    bad = 1;
   }
   if (tid == 0) {
-    const uint32_t prior_bad = atomicAdd(bad_acc, 0u);
-    *flag = (bad || prior_bad) ? 0u : 1u;
+    *flag = bad ? 0u : 1u;
     atomicExch(bad_acc, 0u);
     atomicExch(arrivals, 0u);
   }
 }
 
+// Apply: one workgroup per token.  The validity word, the token's slot and
+// position and the first rows of Q/K/V are fetched in one round trip; 64
+// lanes compute the token's (sin, cos) pairs into LDS; 16 lanes per 256-byte
+// head row rotate Q/K and scatter K/V into the page slot with 16-byte stores.
 __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs a) {
   __shared__ float s_cos[64], s_sin[64];
   __shared__ int s_ok;
   const int tid = threadIdx.x;
   const int t = blockIdx.x;
-  if (tid == 0) s_ok = (__atomic_load_n(a.ws, __ATOMIC_RELAXED) == 1u) ? 1 : 0;
-  __syncthreads();
-  if (!s_ok) return;
-  int r, pos, off;
-  int64_t page;
-  if (!token_slot(a, t, &r, &pos, &page, &off)) return;  // unreachable after validation
+  const uint32_t *keys = a.ws + kWsHeaderWords;
+  const int32_t *positions = reinterpret_cast<const int32_t *>(keys + a.tokens);
+  const uint32_t ok = __atomic_load_n(a.ws, __ATOMIC_RELAXED);
+  const uint32_t key = keys[t];
+  const int pos = positions[t];
+  const int c = tid & 15;
+  const int rows = a.hq + a.hkv;
+  // first row slice of this thread, loaded before the flag is known
+  int row = tid >> 4;
+  u32x4 x0 = {0, 0, 0, 0}, xp0 = {0, 0, 0, 0}, v0 = {0, 0, 0, 0};
+  if (row < rows) {
+    const bool is_kv = row >= a.hq;
+    const uint16_t *src = is_kv ? a.k + ((int64_t)t * a.hkv + row - a.hq) * 128
+                                : a.q + ((int64_t)t * a.hq + row) * 128;
+    x0 = *reinterpret_cast<const u32x4 *>(src + c * 8);
+    xp0 = *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
+    if (is_kv)
+      v0 = *reinterpret_cast<const u32x4 *>(a.v + ((int64_t)t * a.hkv + row - a.hq) * 128 + c * 8);
+  }
+  if (tid == 0) s_ok = ok == 1u;
   if (tid < 64) {
     const float angle = (float)pos * a.inv_freq[tid];
     // sin/cos of the FP32 angle evaluated in FP64 and rounded once: the
@@ -187,25 +223,19 @@ __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs 
     s_cos[tid] = (float)cos(ad);
   }
   __syncthreads();
+  if (!s_ok) return;
+  const int64_t page = key >> 4;
+  const int off = key & 15;
 
-  const int c = tid & 15;
-  const int rows = a.hq + a.hkv;
-  for (int row = tid >> 4; row < rows; row += kApplyThreads / 16) {
-    const uint16_t *src;
-    uint16_t *dst;
+  for (bool first = true; row < rows; row += kApplyThreads / 16, first = false) {
     const bool is_kv = row >= a.hq;
-    int64_t kv_dst = 0;
-    if (!is_kv) {
-      src = a.q + ((int64_t)t * a.hq + row) * 128;
-      dst = a.q_out + ((int64_t)t * a.hq + row) * 128;
-    } else {
-      const int kh = row - a.hq;
-      src = a.k + ((int64_t)t * a.hkv + kh) * 128;
-      kv_dst = ((page * 16 + off) * a.hkv + kh) * 128;
-      dst = a.k_pages + kv_dst;
-    }
-    const u32x4 x = *reinterpret_cast<const u32x4 *>(src + c * 8);
-    const u32x4 xp = *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
+    const int kh = row - a.hq;
+    const uint16_t *src = is_kv ? a.k + ((int64_t)t * a.hkv + kh) * 128
+                                : a.q + ((int64_t)t * a.hq + row) * 128;
+    const int64_t kv_dst = ((page * 16 + off) * a.hkv + kh) * 128;
+    uint16_t *dst = is_kv ? a.k_pages + kv_dst : a.q_out + ((int64_t)t * a.hq + row) * 128;
+    const u32x4 x = first ? x0 : *reinterpret_cast<const u32x4 *>(src + c * 8);
+    const u32x4 xp = first ? xp0 : *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
     u32x4 o;
     {
 #pragma clang fp contract(off)
@@ -228,9 +258,9 @@ __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs 
     }
     *reinterpret_cast<u32x4 *>(dst + c * 8) = o;
     if (is_kv) {
-      const int kh = row - a.hq;
-      const u32x4 vv =
-          *reinterpret_cast<const u32x4 *>(a.v + ((int64_t)t * a.hkv + kh) * 128 + c * 8);
+      const u32x4 vv = first ? v0
+                             : *reinterpret_cast<const u32x4 *>(
+                                   a.v + ((int64_t)t * a.hkv + kh) * 128 + c * 8);
       *reinterpret_cast<u32x4 *>(a.v_pages + kv_dst + c * 8) = vv;
     }
   }
@@ -271,7 +301,7 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
   uint64_t rows = s.num_query_heads + s.num_kv_heads, states;
   if (rows < s.num_query_heads || __builtin_mul_overflow(tokens, rows, &states))
     return fail(err, LOOM_PLAN_STATE_COUNT_OVERFLOW, "RoPE");
-  if (states > (uint64_t)INT32_MAX || tokens > (uint64_t)kMaxSortKeys)
+  if (states > (uint64_t)INT32_MAX || tokens > (uint64_t)kMaxTokens)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE", states);
   // Slot keys are page*16+offset in 32 bits.
   if (s.max_num_pages >= (1ull << 28))
@@ -282,7 +312,7 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
   p->info.num_query_heads = s.num_query_heads;
   p->info.num_kv_heads = s.num_kv_heads;
   p->info.explicit_tokens = explicit_tokens ? 1 : 0;
-  p->info.workspace_bytes = 256;
+  p->info.workspace_bytes = (kWsHeaderWords + 2 * tokens) * 4;
   p->info.validate_blocks = 0;  // depends on the bound page_indices length
   p->max_num_pages = s.max_num_pages;
   // rope/mod.rs:148-149 with rope_scale = 1, rope_theta = 1e4, rotary_dim = 128
@@ -395,8 +425,9 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   a.n_indices = (int64_t)L(6)->numel;
   for (int i = 0; i < 64; ++i) a.inv_freq[i] = plan->inv_freq[i];
 
-  const uint64_t vblocks =
-      std::max<uint64_t>(1, (L(6)->numel + kIndicesPerValidateBlock - 1) / kIndicesPerValidateBlock);
+  const uint64_t vblocks = std::max<uint64_t>(
+      std::max<uint64_t>(1, (L(6)->numel + kIndicesPerValidateBlock - 1) / kIndicesPerValidateBlock),
+      (T + kValidateThreads - 1) / kValidateThreads);
   hipStream_t stream = scope->queue->stream;
   // One command (one completion slot) of two stream-ordered kernels.
   hipLaunchKernelGGL(append_validate_kernel, dim3((unsigned)vblocks), dim3(kValidateThreads), 0,
