@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode launch on config 3 from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (partial + merge kernels), each scaled by the factor the same
 # counter reads for a plain copy of known size; profiles/ holds the runs.
-TRAFFIC_C3 = None
+TRAFFIC_C3 = 1.1628e9
 
 
 def log(*a):
@@ -375,10 +375,7 @@ def main():
         else:
             del case
             torch.cuda.empty_cache()
-    if a.only:
-        print(json.dumps(detail), flush=True)
-        return
-    if not a.quick:
+    if not a.quick and (not a.only or "c2_rope_append_b32_tokens".startswith(a.only)):
         log("[bench] setting up c2_rope_append_b32_tokens")
         import numpy as np
         rng = np.random.default_rng(2)
@@ -392,6 +389,9 @@ def main():
             "GBps": round(app.bytes / (ap_us * 1e-6) / 1e9, 1)}
         log(f"[bench] c2: {detail['c2_rope_append_b32_tokens']}")
         del app
+    if a.only:
+        print(json.dumps(detail), flush=True)
+        return
     c3 = detail["c3_gqa4_b64_ragged"]
     cpu = None if a.no_cpu else cpu_baseline(head)
     line = {

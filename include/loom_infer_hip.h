@@ -3,7 +3,7 @@
  * implementation of Loom Infer's paged-KV decode path:
  *
  *   fused NeoX RoPE + paged K/V append  ->  paged decode attention
- *   (split over KV pages with an in-kernel log2-LSE merge)  ->  hipGraph
+ *   (balanced split over KV pages, then a log2-LSE merge kernel)  ->  hipGraph
  *   fixed-address capture and replay.
  *
  * The ABI mirrors the reference's Rust contract sequence
