@@ -298,6 +298,107 @@ def cpu_baseline(case, min_s=10.0, max_s=30.0):
                       f"(host has {os.cpu_count()} logical CPUs)"}
 
 
+def reference_shapes(L, stream, samples=30):
+    """The reference's own published shapes (its H20 records):
+    tiny decode and append fixtures, whose time is launch latency.  Eager = the
+    mean of 100 back-to-back calls between two events, median over `samples`
+    batches (benchmarks/matched.rs:141-173); graph = one replay plus its
+    completion event, median over `samples` (graph/mod.rs:301-323).  The page
+    tables are the reference's gate fixtures; values are synthetic."""
+    import numpy as np
+    import torch
+    g = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_digests.json")))
+    dev = "cuda"
+    out = {}
+
+    def med(xs):
+        xs = sorted(xs)
+        return round(xs[len(xs) // 2], 3)
+
+    def eager_and_graph(n_bind, bind, enqueue):
+        eg = [_timed_enqueues(L, stream, n_bind, bind, enqueue, 100, 10 if i == 0 else 2)
+              for i in range(samples)]
+        return med(eg), round(_graph_replay(L, n_bind, 1, bind, enqueue, replays=samples), 3)
+
+    # Platform context: the same two measurements around one tiny torch kernel
+    # (eager) and a torch-captured hipGraph of it, on the same stream.
+    x = torch.zeros(16, device=dev)
+    tg = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        x.add_(1)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(tg, stream=stream):
+            x.add_(1)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for key, fn in (("platform_one_kernel_graph_replay_us", tg.replay),
+                    ("platform_one_kernel_eager_single_us", lambda: x.add_(1))):
+        ts = []
+        for i in range(samples + 3):
+            with torch.cuda.stream(stream):
+                ev0.record(stream)
+                fn()
+                ev1.record(stream)
+            ev1.synchronize()
+            if i >= 3:
+                ts.append(ev0.elapsed_time(ev1) * 1000.0)
+        out[key] = med(ts)
+    del tg
+
+    for c in g["paged_decode"]["cases"]:
+        B, pool, hq, hkv = c["batch"], c["pool"], c["hq"], c["hkv"]
+        spec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, 128, 16)
+        plan = L.DecodeProvider.load(0).plan_bf16_paged_batch(
+            spec, max_total_pages=len(c["indices"]))
+        t = [torch.randn(n, device=dev).to(torch.bfloat16) for n in
+             (B * hq * 128, pool * 16 * hkv * 128, pool * 16 * hkv * 128)]
+        ip, ix, ln = (torch.tensor(c[k], dtype=torch.int32, device=dev)
+                      for k in ("indptr", "indices", "last"))
+        o = torch.empty(B * hq * 128, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(B * hq, dtype=torch.float32, device=dev)
+        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=dev)
+
+        def bind(b):
+            return L.Bf16PagedBatchDecodeArgs(
+                b.bind_read(t[0]), b.bind_read(t[1]), b.bind_read(t[2]), b.bind_read(ip),
+                b.bind_read(ix), b.bind_read(ln), b.bind_read_write(o).write(),
+                b.bind_read_write(lse).write(), b.bind_read_write(ws).write())
+        e, gr = eager_and_graph(9, bind, plan.enqueue_into)
+        out["decode_" + c["name"]] = {"eager_us": e, "graph_replay_us": gr,
+                                      "teams": plan.info.teams}
+    for name in ("append_one_token", "append_tokens_t6"):
+        c = g[name]
+        explicit = "tokens" in c
+        B, pool, hq, hkv = c["batch"], c["pool"], c["hq"], c["hkv"]
+        T = c["tokens"] if explicit else B
+        prov = L.RopeProvider.load(0)
+        if explicit:
+            plan = prov.plan_bf16_paged_append_tokens(
+                L.Bf16RopePagedKvAppendTokensSpec(T, B, pool, hq, hkv))
+        else:
+            plan = prov.plan_bf16_paged_append(L.Bf16RopePagedKvAppendSpec(B, pool, hq, hkv))
+        q, k, v = (torch.randn(T * h * 128, device=dev).to(torch.bfloat16) for h in (hq, hkv, hkv))
+        kp = torch.zeros(pool * 16 * hkv * 128, dtype=torch.bfloat16, device=dev)
+        vp = torch.zeros_like(kp)
+        qo = torch.empty_like(q)
+        ip, ix, ln = (torch.tensor(c[k], dtype=torch.int32, device=dev)
+                      for k in ("indptr", "indices", "last"))
+        bi = torch.tensor(c.get("batch_indices", [0]), dtype=torch.int32, device=dev)
+        ps = torch.tensor(c.get("positions", [0]), dtype=torch.int32, device=dev)
+        ws = torch.zeros(plan.workspace_bytes, dtype=torch.uint8, device=dev)
+
+        def bind(b):
+            return L.Bf16RopePagedKvAppendArgs(
+                b.bind_read(q), b.bind_read(k), b.bind_read(v), b.bind_read(ip),
+                b.bind_read(ix), b.bind_read(ln), b.bind_read_write(qo).write(),
+                b.bind_read_write(kp).write(), b.bind_read_write(vp).write(),
+                b.bind_read_write(ws).write(), b.bind_read(bi) if explicit else None,
+                b.bind_read(ps) if explicit else None)
+        e, gr = eager_and_graph(12 if explicit else 10, bind, plan.enqueue_into)
+        out[name] = {"eager_us": e, "graph_replay_us": gr, "tokens": T}
+    return out
+
+
 def make_cases(L, quick=False):
     import numpy as np
     rng = np.random.default_rng(2026)
@@ -389,6 +490,10 @@ def main():
             "GBps": round(app.bytes / (ap_us * 1e-6) / 1e9, 1)}
         log(f"[bench] c2: {detail['c2_rope_append_b32_tokens']}")
         del app
+    if not a.quick and (not a.only or a.only == "ref"):
+        log("[bench] reference published shapes")
+        detail["reference_shapes"] = reference_shapes(L, stream)
+        log(f"[bench] {detail['reference_shapes']}")
     if a.only:
         print(json.dumps(detail), flush=True)
         return
