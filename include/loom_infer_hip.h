@@ -320,13 +320,17 @@ typedef enum loom_paged_decode_algorithm {
    * a team is one wave per (kv-head, tile of up to 8 query heads), so the
    * whole GQA group shares each K/V byte.  Requests that cross a range
    * boundary merge through log2-LSE states in a second kernel. */
-  LOOM_PAGED_DECODE_BALANCED_SPLIT_KV = 1
+  LOOM_PAGED_DECODE_BALANCED_SPLIT_KV = 1,
+  /* Small page capacity (max_total_pages <= 32, teams option 0): one
+   * workgroup per (request, kv-head, tile), one launch, no split. */
+  LOOM_PAGED_DECODE_DIRECT = 2
 } loom_paged_decode_algorithm_t;
 
 /* Planner inputs.  Zero means "choose for this device". */
 typedef struct loom_paged_decode_plan_options {
   uint64_t max_total_pages; /* upper bound of page_indices length; 0 -> max_num_pages */
-  uint32_t teams;           /* page ranges; 0 -> one wave per SIMD slot of the device */
+  uint32_t teams;           /* page ranges; 0 -> chosen for the device (or the direct
+                               algorithm when max_total_pages <= 32) */
   uint32_t reserved;        /* must be zero */
 } loom_paged_decode_plan_options_t;
 
@@ -431,7 +435,8 @@ typedef struct loom_rope_append_args {
 
 /* enqueue_into, rope/mod.rs:758-830 / :846-934: a metadata-validation kernel
  * (whole page table, batch indices, positions, duplicate physical slots) and
- * the rotate+scatter kernel, stream ordered.  Invalid device metadata leaves
+ * the rotate+scatter kernel, stream ordered; commands with T <= 64 and at most
+ * 4096 page indices run as one kernel that validates in every workgroup.  Invalid device metadata leaves
  * every output untouched (the reference's sentinel guard). */
 loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
                                        loom_command_scope_t *scope,

@@ -48,6 +48,11 @@ constexpr int kLdsPrefix = 512;      // requests whose prefix and metadata stay 
 constexpr int kMaxScanBlocks = 256;  // scan blocks of kThreads requests: batch <= 65536
 // FP32 split state: (max_log2, normalizer, 2 pad, acc[128]), 16-byte aligned.
 constexpr int kStateStride = 132;
+// Plans whose page capacity is at most this use the direct kernel (one launch,
+// no split): such calls are launch- and latency-bound.
+#ifndef LOOM_DECODE_DIRECT_MAX_PAGES
+#define LOOM_DECODE_DIRECT_MAX_PAGES 32
+#endif
 constexpr int kKRowBytes = 256 + 16;
 #ifndef LOOM_DECODE_DEPTH
 #define LOOM_DECODE_DEPTH 2
@@ -240,6 +245,148 @@ __device__ __forceinline__ int64_t team_of(int64_t total, int64_t v, int teams) 
   return floor_div((v + 1) * teams + total - 1, total) - 1;
 }
 
+// Per-wave decode of one (request, kv-head, tile of GT query heads): the
+// online-softmax state over the pages the wave streams, and the page step.
+template <int GT>
+struct WaveDecoder {
+  const DecodeArgs &a;
+  uint8_t *kt;          // this wave's K tile (16 rows of kKRowBytes)
+  u32x4 (*qfrag)[64];   // [4][64] MFMA B fragments of the query tile
+  float (*pbuf)[16];    // [GT][16] probabilities of the current page
+  float *alpha;         // [GT] rescale factors of the current page
+  int lane, col, quad, kvh;
+  float m_run, l_run;
+  float acc[GT][8];
+
+  __device__ void reset() {
+    m_run = -INFINITY;
+    l_run = 0.0f;
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+  }
+
+  // Q fragment: column `col` is query head qh0 + col (zero beyond gcount);
+  // MFMA c contracts dims 32c + 8*quad + [0, 8), the slices the K fragments
+  // read.  `prefetched` lets the caller issue other loads before the LDS write.
+  __device__ void load_q(int r, int qh0, int gcount, u32x4 (&qr)[4]) const {
+    const uint16_t *qp = a.q + ((int64_t)r * a.hq + qh0 + col) * 128 + quad * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qr[c] = col < gcount ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
+  }
+  __device__ void store_q(const u32x4 (&qr)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qfrag[c][lane] = qr[c];
+    wave_lds_fence();
+  }
+
+  // One page: S = K·Qᵀ on MFMA, online softmax, P·V on the VALU.  `rows` is
+  // the number of valid token rows (16, the request's tail on its last page,
+  // 0 for a page index that failed the guard).
+  __device__ void process(const PageRegs &pr, int rows) {
+    // K rows -> LDS tile -> MFMA A fragments (lane: token row `col`, dims
+    // 32c + 8*quad + [0, 8)).
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4 *>(kt + (quad * 4 + j) * kKRowBytes + col * 16) = pr.k[j];
+    wave_lds_fence();
+    u32x4 kf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      kf[c] = *reinterpret_cast<const u32x4 *>(kt + col * kKRowBytes + (c * 4 + quad) * 16);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[c]), as_bf16x8(qfrag[c][lane]), s,
+                                                  0, 0, 0);
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = (quad * 4 + i < rows) ? s[i] * a.scale_log2 : -INFINITY;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float al = fast_exp2(m_run - m_new);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_new);
+    l_run = l_run * al + ((p[0] + p[1]) + (p[2] + p[3]));
+    m_run = m_new;
+    if (col < GT) {
+      *reinterpret_cast<f32x4 *>(&pbuf[col][quad * 4]) = f32x4{p[0], p[1], p[2], p[3]};
+      if (quad == 0) alpha[col] = al;
+    }
+    wave_lds_fence();
+    // P·V on lane (col = 8-column slice, quad = rows 4*quad..4*quad+3).  Columns
+    // of the tile beyond the group carry finite junk and are never stored.
+    f32x4 pp[GT];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const float ag = alpha[g];
+      pp[g] = *reinterpret_cast<const f32x4 *>(&pbuf[g][quad * 4]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // rows past the valid ones were loaded as zeros and have zero weight
+      float vf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t wv = pr.v[j][e];
+        vf[2 * e] = bf16_lo(wv);
+        vf[2 * e + 1] = bf16_hi(wv);
+      }
+#pragma unroll
+      for (int g = 0; g < GT; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pp[g][j], vf[e], acc[g][e]);
+    }
+    wave_lds_fence();
+  }
+
+  // Streams pages 0..n-1 (n >= 1) through a kDepth-deep pipeline: each step
+  // issues the loads of the page kDepth-1 steps ahead before consuming the
+  // current one.  Loads past the end have no valid rows and touch no memory;
+  // the unrolled buffer rotation lets the compiler wait for exactly the
+  // oldest page's loads.  page_of(i) / rows_of(i) must be wave-uniform.
+  template <class PageOf, class RowsOf>
+  __device__ void stream(int n, PageOf page_of, RowsOf rows_of) {
+    PageRegs buf[kDepth];
+#pragma unroll
+    for (int j = 0; j < kDepth - 1; ++j) load_page(buf[j], a, page_of(j), rows_of(j), lane, kvh);
+    int i = 0;
+    while (true) {
+#pragma unroll
+      for (int s = 0; s < kDepth; ++s) {
+        load_page(buf[(s + kDepth - 1) % kDepth], a, page_of(i + kDepth - 1),
+                  rows_of(i + kDepth - 1), lane, kvh);
+        process(buf[s], rows_of(i));
+        if (++i >= n) return;
+      }
+    }
+  }
+
+  // Sums the 4 row quads: afterwards every lane of column c holds the
+  // accumulators of its 8-column slice, and lane g (quad 0) the max and the
+  // returned normalizer of query column g.
+  __device__ float reduce() {
+    float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = acc[g][e];
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        acc[g][e] = x;
+      }
+    return l_tot;
+  }
+};
+
 // Teams in use for `total` virtual pages: at most the planned count, and at
 // least kMinTeamPages pages each (short batches are latency-bound: fewer, longer
 // page streams and shorter merges beat one page per wave).
@@ -374,7 +521,6 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
 
   const int g_base = gt * GT;
   const int gcount = min(GT, a.group - g_base);
-  const bool col_valid = col < gcount;
   uint8_t *kt = sm.ktile[wave];
 
   // Metadata of request rr: page count in the virtual list (0 if it fails the
@@ -404,73 +550,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     return lane < n ? a.indices[st + lp0 + lane] : 0;
   };
 
-  float m_run, l_run;
-  float acc[GT][8];
-
-  // One page: S = K·Qᵀ on MFMA, online softmax, P·V on the VALU.  `rows` is
-  // the number of valid token rows (16, the request's tail on its last page,
-  // 0 for a page index that failed the guard).
-  auto process = [&](const PageRegs &pr, int rows) {
-    // K rows -> LDS tile -> MFMA A fragments (lane: token row `col`, dims
-    // 32c + 8*quad + [0, 8)).
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<u32x4 *>(kt + (quad * 4 + j) * kKRowBytes + col * 16) = pr.k[j];
-    wave_lds_fence();
-    u32x4 kf[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      kf[c] = *reinterpret_cast<const u32x4 *>(kt + col * kKRowBytes + (c * 4 + quad) * 16);
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[c]),
-                                                  as_bf16x8(sm.qfrag[wave][c][lane]), s, 0, 0, 0);
-    float sv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sv[i] = (quad * 4 + i < rows) ? s[i] * a.scale_log2 : -INFINITY;
-    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_new);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m_run = m_new;
-    if (col < GT) {
-      *reinterpret_cast<f32x4 *>(&sm.p[wave][col][quad * 4]) = f32x4{p[0], p[1], p[2], p[3]};
-      if (quad == 0) sm.alpha[wave][col] = alpha;
-    }
-    wave_lds_fence();
-    // P·V on lane (col = 8-column slice, quad = rows 4*quad..4*quad+3).  Columns
-    // of the tile beyond the group carry finite junk and are never stored.
-    f32x4 pp[GT];
-#pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      const float al = sm.alpha[wave][g];
-      pp[g] = *reinterpret_cast<const f32x4 *>(&sm.p[wave][g][quad * 4]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] *= al;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // rows past the valid ones were loaded as zeros and have zero weight
-      float vf[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t wv = pr.v[j][e];
-        vf[2 * e] = bf16_lo(wv);
-        vf[2 * e + 1] = bf16_hi(wv);
-      }
-#pragma unroll
-      for (int g = 0; g < GT; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pp[g][j], vf[e], acc[g][e]);
-    }
-    wave_lds_fence();
-  };
+  WaveDecoder<GT> w{a, kt, sm.qfrag[wave], sm.p[wave], sm.alpha[wave], lane, col, quad, kvh};
 
   // ---- pieces: the parts of requests inside [v_begin, v_end) --------------
   int64_t v = v_begin;
@@ -486,21 +566,11 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     int seg_n, seg_lp0;
     int seg_idx = segment_indices(v, piece_end, pre, st, seg_n, seg_lp0);
     {
-      const int qh = kvh * a.group + g_base + col;
-      const uint16_t *qp = a.q + ((int64_t)r * a.hq + qh) * 128 + quad * 8;
       u32x4 qr[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) qr[c] = col_valid ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) sm.qfrag[wave][c][lane] = qr[c];
-      wave_lds_fence();
+      w.load_q(r, kvh * a.group + g_base, gcount, qr);
+      w.store_q(qr);
     }
-    m_run = -INFINITY;
-    l_run = 0.0f;
-#pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+    w.reset();
     bool bad = false;
 
     // Segments of up to 64 pages: one page index per lane, read back with
@@ -515,38 +585,13 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
         if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
         return lp0 + i == cnt - 1 ? tl : 16;
       };
-      // kDepth-deep pipeline: each step issues the loads of the page kDepth-1
-      // steps ahead before consuming the current one.  Loads past the segment
-      // have no valid rows and touch no memory; the unrolled buffer rotation
-      // lets the compiler wait for exactly the oldest page's loads.
-      PageRegs buf[kDepth];
-#pragma unroll
-      for (int j = 0; j < kDepth - 1; ++j) load_page(buf[j], a, page_of(j), rows_of(j), lane, kvh);
-      int i = 0;
-      while (true) {
-#pragma unroll
-        for (int s = 0; s < kDepth; ++s) {
-          load_page(buf[(s + kDepth - 1) % kDepth], a, page_of(i + kDepth - 1),
-                    rows_of(i + kDepth - 1), lane, kvh);
-          process(buf[s], rows_of(i));
-          if (++i >= n) goto segment_done;
-        }
-      }
-    segment_done:;
+      w.stream(n, page_of, rows_of);
     }
 
-    // ---- finish the piece: reduce the 4 row quads ---------------------------
-    float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
-#pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float x = acc[g][e];
-        x += __shfl_xor(x, 16, 64);
-        x += __shfl_xor(x, 32, 64);
-        acc[g][e] = x;
-      }
+    // ---- finish the piece ---------------------------------------------------
+    const float l_tot = w.reduce();
+    const float m_run = w.m_run;
+    const auto &acc = w.acc;
     const int64_t qh_base = (int64_t)kvh * a.group + g_base;
     if (whole) {
       // The request lies inside this wave's range: final output in place.  An
@@ -601,6 +646,103 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     do {
       if (++r >= a.batch) return;  // unreachable: v < total
     } while (request_meta(r, st, tl) == 0);
+  }
+}
+
+// Direct decode for small page tables: one workgroup per (request, kv-head,
+// tile), its 4 waves taking pages w, w+4, ... of the request and merging in
+// LDS, so the request finishes in one launch (no scan, no split states, no
+// merge kernel).  Used when the plan's page capacity is small, where the call
+// is launch- and latency-bound.
+template <int GT>
+struct DirectSmem {
+  float p[kWaves][GT][16];
+  float alpha[kWaves][GT];
+  uint8_t ktile[kWaves][16 * kKRowBytes];
+  u32x4 qfrag[kWaves][4][64];
+  float wm[kWaves][GT];
+  float wl[kWaves][GT];
+  float wacc[kWaves][GT][128];
+};
+
+template <int GT>
+__global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_direct_kernel(
+    DecodeArgs a) {
+  __shared__ DirectSmem<GT> sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, quad = lane >> 4;
+  const int kvh = (int)(blockIdx.x % a.hkv);
+  const int rest = (int)(blockIdx.x / a.hkv);
+  const int gt = rest % a.members;  // members = group tiles for this kernel
+  const int r = rest / a.members;
+
+  // Guards (decode.rs:233-246 global, :430-478 per request), one round trip.
+  const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
+  const int32_t st = uni(a.indptr[r]), en = uni(a.indptr[r + 1]), tl = uni(a.last[r]);
+  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices) return;
+  const int cnt = request_pages(st, en, tl, ipB);
+  if (cnt == 0) return;
+
+  const int g_base = gt * GT;
+  const int gcount = min(GT, a.group - g_base);
+  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
+                    lane, col, quad, kvh};
+  // this wave's pages: request-local positions wave + 4i
+  const int mine = cnt > wave ? (cnt - wave + kWaves - 1) / kWaves : 0;
+  bool bad = false;
+  {
+    u32x4 qr[4];
+    int idx = 0;
+    if (lane < min(mine, 64)) idx = a.indices[st + wave + kWaves * lane];
+    w.load_q(r, kvh * a.group + g_base, gcount, qr);
+    w.store_q(qr);
+    w.reset();
+    for (int s0 = 0; s0 < mine; s0 += 64) {
+      if (s0 > 0) idx = lane < min(mine - s0, 64) ? a.indices[st + wave + kWaves * (s0 + lane)] : 0;
+      const int n = min(mine - s0, 64);
+      const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
+      bad |= __ballot(lane < n && !ok) != 0;
+      auto page_of = [&](int i) { return __builtin_amdgcn_readlane(idx, min(i, n - 1)); };
+      auto rows_of = [&](int i) {
+        if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
+        return wave + kWaves * (s0 + i) == cnt - 1 ? tl : 16;
+      };
+      w.stream(n, page_of, rows_of);
+    }
+  }
+  const float l_tot = w.reduce();
+  if (quad == 0) {
+    if (col < GT) {
+      sm.wm[wave][col] = w.m_run;
+      sm.wl[wave][col] = l_tot;
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.wacc[wave][g][col * 8 + e] = w.acc[g][e];
+  }
+  // An invalid page index anywhere in the request keeps its sentinels.
+  if (__syncthreads_or(bad)) return;
+
+  // Workgroup merge of the 4 wave states (a wave without pages has max -inf
+  // and weight 0).
+  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
+  for (int idx = tid; idx < GT * 128; idx += kThreads) {
+    const int g = idx >> 7, d = idx & 127;
+    if (g >= gcount) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) M = fmaxf(M, sm.wm[wv][g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const float f = fast_exp2(sm.wm[wv][g] - M);
+      L = fmaf(sm.wl[wv][g], f, L);
+      O = fmaf(sm.wacc[wv][g][d], f, O);
+    }
+    a.out[((int64_t)r * a.hq + qh_base + g) * 128 + d] = f32_to_bf16(O / L);
+    if (d == 0) a.lse[(int64_t)r * a.hq + qh_base + g] = M + __log2f(L);
   }
 }
 
@@ -712,6 +854,29 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   if (B > (uint64_t)kMaxScanBlocks * kThreads)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "batch_size", B);
 
+  if (opt.teams == 0 && max_pages <= LOOM_DECODE_DIRECT_MAX_PAGES) {
+    const uint64_t grid = B * gtiles * hkv;
+    if (grid > (uint64_t)INT32_MAX || B * hq > (uint64_t)INT32_MAX)
+      return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged batch-decode", grid);
+    auto *p = new loom_paged_decode_plan;
+    p->device = provider->dev.device;
+    loom_paged_decode_plan_info_t &i = p->info;
+    i.spec = *spec;
+    i.algorithm = LOOM_PAGED_DECODE_DIRECT;
+    i.teams = 0;
+    i.group_tile = gtile;
+    i.group_tiles = (uint32_t)gtiles;
+    i.max_total_pages = max_pages;
+    i.state_slots = 0;
+    i.workspace_bytes = 256;  // unused by this algorithm; kept for a uniform operand list
+    i.header_bytes = 0;
+    i.block_threads = kThreads;
+    i.grid_blocks = (uint32_t)grid;
+    i.device_cus = (uint32_t)provider->dev.cus;
+    *out = p;
+    return loom::ok(err);
+  }
+
   // Teams: one wave per SIMD slot the kernel's register budget allows, so
   // the whole grid is resident at once and every wave streams the same number
   // of pages.
@@ -811,7 +976,9 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.hq = (int32_t)s.num_query_heads;
   a.hkv = (int32_t)s.num_kv_heads;
   a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
-  a.members = (int32_t)(s.num_kv_heads * pi.group_tiles);
+  const bool direct = pi.algorithm == LOOM_PAGED_DECODE_DIRECT;
+  // the direct kernel indexes (request, tile, kv-head) and takes the tile count here
+  a.members = (int32_t)(direct ? pi.group_tiles : s.num_kv_heads * pi.group_tiles);
   a.teams = (int32_t)pi.teams;
   a.pool = (int64_t)s.max_num_pages;
   a.n_indices = (int64_t)l[4]->numel;
@@ -820,6 +987,15 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   const uint64_t grid = pi.grid_blocks;
   hipStream_t stream = scope->queue->stream;
   const dim3 g3((unsigned)grid), b3(kThreads);
+  if (direct) {
+    switch (pi.group_tile) {
+      case 1: hipLaunchKernelGGL(paged_decode_direct_kernel<1>, g3, b3, 0, stream, a); break;
+      case 2: hipLaunchKernelGGL(paged_decode_direct_kernel<2>, g3, b3, 0, stream, a); break;
+      case 4: hipLaunchKernelGGL(paged_decode_direct_kernel<4>, g3, b3, 0, stream, a); break;
+      default: hipLaunchKernelGGL(paged_decode_direct_kernel<8>, g3, b3, 0, stream, a); break;
+    }
+    return loom::record_launch(scope, hipGetLastError(), err);
+  }
   switch (pi.group_tile) {
     case 1: hipLaunchKernelGGL(paged_decode_split_kv_kernel<1>, g3, b3, 0, stream, a); break;
     case 2: hipLaunchKernelGGL(paged_decode_split_kv_kernel<2>, g3, b3, 0, stream, a); break;

@@ -18,6 +18,9 @@
 //     token's 64 (sin, cos) pairs once into LDS, then 16 lanes per 256-byte
 //     head row rotate Q/K and scatter K/V rows into the page slot with 16-byte
 //     loads and stores;
+//   * small commands (T <= 64, <= 4096 page indices) run as one launch in
+//     which every workgroup validates the whole command itself (the
+//     reference's approach), so there is no second kernel;
 //   * inverse frequencies come from the host's powf (the reference's exact
 //     values); angle = pos * inv_freq in FP32; products are rounded separately
 //     (no FMA contraction) as in the Rust reference.
@@ -38,6 +41,9 @@ constexpr int kMaxTokens = LOOM_APPEND_MAX_TOKENS_EXTENDED;
 // Workspace: 64 header words ([0] validity, [1] bad accumulator, [2] arrival
 // counter), then the T slot keys (u32) and the T positions (i32).
 constexpr int kWsHeaderWords = 64;
+// Commands this small run as one fused launch (every workgroup validates).
+constexpr int kFusedMaxTokens = 64;
+constexpr int64_t kFusedMaxIndices = 4096;
 constexpr uint32_t kEmptyKey = 0xffffffffu;
 // LDS hash set for duplicate slots: a power of two >= 2T.
 constexpr int kHashSlots = 2 * kMaxTokens;
@@ -182,35 +188,31 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
   }
 }
 
-// Apply: one workgroup per token.  The validity word, the token's slot and
-// position and the first rows of Q/K/V are fetched in one round trip; 64
-// lanes compute the token's (sin, cos) pairs into LDS; 16 lanes per 256-byte
-// head row rotate Q/K and scatter K/V into the page slot with 16-byte stores.
-__global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs a) {
-  __shared__ float s_cos[64], s_sin[64];
-  __shared__ int s_ok;
-  const int tid = threadIdx.x;
-  const int t = blockIdx.x;
-  const uint32_t *keys = a.ws + kWsHeaderWords;
-  const int32_t *positions = reinterpret_cast<const int32_t *>(keys + a.tokens);
-  const uint32_t ok = __atomic_load_n(a.ws, __ATOMIC_RELAXED);
-  const uint32_t key = keys[t];
-  const int pos = positions[t];
-  const int c = tid & 15;
-  const int rows = a.hq + a.hkv;
-  // first row slice of this thread, loaded before the flag is known
-  int row = tid >> 4;
-  u32x4 x0 = {0, 0, 0, 0}, xp0 = {0, 0, 0, 0}, v0 = {0, 0, 0, 0};
-  if (row < rows) {
+// The first row slice of thread `tid` for token t (Q rows, then K rows with
+// their V row), loaded before the command's validity is known so the loads
+// overlap the metadata round trips.
+struct RowSlice {
+  u32x4 x, xp, v;
+};
+
+__device__ __forceinline__ RowSlice load_first_slice(const AppendArgs &a, int t, int tid) {
+  RowSlice f = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+  const int c = tid & 15, row = tid >> 4;
+  if (row < a.hq + a.hkv) {
     const bool is_kv = row >= a.hq;
     const uint16_t *src = is_kv ? a.k + ((int64_t)t * a.hkv + row - a.hq) * 128
                                 : a.q + ((int64_t)t * a.hq + row) * 128;
-    x0 = *reinterpret_cast<const u32x4 *>(src + c * 8);
-    xp0 = *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
+    f.x = *reinterpret_cast<const u32x4 *>(src + c * 8);
+    f.xp = *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
     if (is_kv)
-      v0 = *reinterpret_cast<const u32x4 *>(a.v + ((int64_t)t * a.hkv + row - a.hq) * 128 + c * 8);
+      f.v = *reinterpret_cast<const u32x4 *>(a.v + ((int64_t)t * a.hkv + row - a.hq) * 128 + c * 8);
   }
-  if (tid == 0) s_ok = ok == 1u;
+  return f;
+}
+
+// (sin, cos) of the token's 64 angles into LDS, by threads 0..63.
+__device__ __forceinline__ void token_sincos(const AppendArgs &a, int pos, int tid, float *s_sin,
+                                             float *s_cos) {
   if (tid < 64) {
     const float angle = (float)pos * a.inv_freq[tid];
     // sin/cos of the FP32 angle evaluated in FP64 and rounded once: the
@@ -222,11 +224,16 @@ __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs 
     s_sin[tid] = (float)sin(ad);
     s_cos[tid] = (float)cos(ad);
   }
-  __syncthreads();
-  if (!s_ok) return;
-  const int64_t page = key >> 4;
-  const int off = key & 15;
+}
 
+// Rotates Q/K rows of token t (NeoX split-half) and scatters K/V into slot
+// (page, off): 16 lanes per 256-byte head row, 16-byte loads and stores.
+__device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t page, int off,
+                                            int tid, const float *s_sin, const float *s_cos,
+                                            const RowSlice &first_slice) {
+  const int c = tid & 15;
+  const int rows = a.hq + a.hkv;
+  int row = tid >> 4;
   for (bool first = true; row < rows; row += kApplyThreads / 16, first = false) {
     const bool is_kv = row >= a.hq;
     const int kh = row - a.hq;
@@ -234,8 +241,8 @@ __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs 
                                 : a.q + ((int64_t)t * a.hq + row) * 128;
     const int64_t kv_dst = ((page * 16 + off) * a.hkv + kh) * 128;
     uint16_t *dst = is_kv ? a.k_pages + kv_dst : a.q_out + ((int64_t)t * a.hq + row) * 128;
-    const u32x4 x = first ? x0 : *reinterpret_cast<const u32x4 *>(src + c * 8);
-    const u32x4 xp = first ? xp0 : *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
+    const u32x4 x = first ? first_slice.x : *reinterpret_cast<const u32x4 *>(src + c * 8);
+    const u32x4 xp = first ? first_slice.xp : *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
     u32x4 o;
     {
 #pragma clang fp contract(off)
@@ -258,12 +265,85 @@ __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs 
     }
     *reinterpret_cast<u32x4 *>(dst + c * 8) = o;
     if (is_kv) {
-      const u32x4 vv = first ? v0
+      const u32x4 vv = first ? first_slice.v
                              : *reinterpret_cast<const u32x4 *>(
                                    a.v + ((int64_t)t * a.hkv + kh) * 128 + c * 8);
       *reinterpret_cast<u32x4 *>(a.v_pages + kv_dst + c * 8) = vv;
     }
   }
+}
+
+// Apply: one workgroup per token.  The validity word, the token's slot and
+// position and the first rows of Q/K/V are fetched in one round trip; 64
+// lanes compute the token's (sin, cos) pairs into LDS; then the rows.
+__global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs a) {
+  __shared__ float s_cos[64], s_sin[64];
+  __shared__ int s_ok;
+  const int tid = threadIdx.x;
+  const int t = blockIdx.x;
+  const uint32_t *keys = a.ws + kWsHeaderWords;
+  const int32_t *positions = reinterpret_cast<const int32_t *>(keys + a.tokens);
+  const uint32_t ok = __atomic_load_n(a.ws, __ATOMIC_RELAXED);
+  const uint32_t key = keys[t];
+  const int pos = positions[t];
+  const RowSlice first = load_first_slice(a, t, tid);
+  if (tid == 0) s_ok = ok == 1u;
+  token_sincos(a, pos, tid, s_sin, s_cos);
+  __syncthreads();
+  if (!s_ok) return;
+  apply_token(a, t, key >> 4, key & 15, tid, s_sin, s_cos, first);
+}
+
+// Small commands (T <= 64 tokens, <= 4096 page indices): one launch.  Every
+// workgroup (one per token) validates the whole command itself, as the
+// reference's kernels do, and applies its own token only if all of it is
+// valid, so the all-or-nothing guard needs no second kernel.
+__global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(AppendArgs a) {
+  __shared__ float s_cos[64], s_sin[64];
+  __shared__ uint32_t s_keys[kFusedMaxTokens];
+  __shared__ int s_pos[kFusedMaxTokens];
+  const int tid = threadIdx.x;
+  const int t = blockIdx.x;
+  const RowSlice first = load_first_slice(a, t, tid);
+
+  int bad = 0;
+  // page indices (rope/mod.rs:143-150)
+#pragma unroll 4
+  for (int64_t i = tid; i < a.n_indices; i += kApplyThreads) {
+    const int32_t pg = a.indices[i];
+    bad |= (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
+  }
+  // request table (paged_decode/mod.rs:164-205)
+  if (tid == 0) bad |= (a.indptr[0] != 0 || (int64_t)a.indptr[a.batch] != a.n_indices);
+  for (int r = tid; r < a.batch; r += kApplyThreads) {
+    const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+    bad |= (en <= st || tl < 1 || tl > 16) ? 1 : 0;
+  }
+  // tokens (paged_append/mod.rs:262-309)
+  if (tid < a.tokens) {
+    int r, p, off;
+    int64_t pg;
+    uint32_t key = 0xffffffffu;
+    if (token_slot(a, tid, &r, &p, &pg, &off))
+      key = (uint32_t)(pg * 16 + off);
+    else
+      bad = 1;
+    s_keys[tid] = key;
+    s_pos[tid] = p;
+  }
+  bad = __syncthreads_or(bad);
+  if (bad) return;
+  // duplicate physical slots: token i against every earlier token
+  int dup = 0;
+  if (tid < a.tokens) {
+    const uint32_t k = s_keys[tid];
+    for (int j = 0; j < tid; ++j) dup |= s_keys[j] == k;
+  }
+  const int pos = s_pos[t];
+  token_sincos(a, pos, tid, s_sin, s_cos);
+  if (__syncthreads_or(dup)) return;
+  const uint32_t key = s_keys[t];
+  apply_token(a, t, key >> 4, key & 15, tid, s_sin, s_cos, first);
 }
 
 }  // namespace
@@ -429,6 +509,11 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
       std::max<uint64_t>(1, (L(6)->numel + kIndicesPerValidateBlock - 1) / kIndicesPerValidateBlock),
       (T + kValidateThreads - 1) / kValidateThreads);
   hipStream_t stream = scope->queue->stream;
+  if (T <= (uint64_t)kFusedMaxTokens && (int64_t)L(6)->numel <= kFusedMaxIndices) {
+    hipLaunchKernelGGL(append_fused_small_kernel, dim3((unsigned)T), dim3(kApplyThreads), 0,
+                       stream, a);
+    return loom::record_launch(scope, hipGetLastError(), err);
+  }
   // One command (one completion slot) of two stream-ordered kernels.
   hipLaunchKernelGGL(append_validate_kernel, dim3((unsigned)vblocks), dim3(kValidateThreads), 0,
                      stream, a);

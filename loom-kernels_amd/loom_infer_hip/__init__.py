@@ -24,6 +24,7 @@ missing, importing the provider fails loudly.
 from __future__ import annotations
 
 import ctypes as C
+import threading
 from dataclasses import dataclass
 from typing import Any, Callable, Optional, Sequence
 
@@ -131,6 +132,21 @@ def _call(fn, *args):
     err = _ffi.Error()
     rc = fn(*args, C.byref(err))
     _raise(rc, err)
+
+
+_tls = threading.local()
+
+
+def _enqueue(fn, plan_p, scope_p, args_ref):
+    """The hot enqueue call: one preallocated error record per thread and the
+    args struct built once per Args value."""
+    err = getattr(_tls, "err", None)
+    if err is None:
+        err = _tls.err = _ffi.Error()
+        _tls.err_ref = C.byref(err)
+    rc = fn(plan_p, scope_p, args_ref, _tls.err_ref)
+    if rc:
+        _raise(rc, err)
 
 
 def _i32_array(values) -> tuple:
@@ -501,7 +517,7 @@ class CommandQueue:
 
 
 # ---- paged decode ---------------------------------------------------------------
-@dataclass
+@dataclass(frozen=True)
 class Bf16PagedBatchDecodeArgs:
     """decode.rs:1452-1487 plus the split-KV state workspace."""
     query: Read
@@ -519,6 +535,11 @@ class Bf16PagedBatchDecodeArgs:
             "query", "key_pages", "value_pages", "page_indptr", "page_indices",
             "last_page_len", "output", "lse", "workspace")])
 
+    def __post_init__(self):
+        c = self._c()
+        object.__setattr__(self, "_struct", c)
+        object.__setattr__(self, "_ref", C.byref(c))
+
 
 class Bf16PagedBatchDecodePlan:
     def __init__(self, ptr, spec):
@@ -532,15 +553,14 @@ class Bf16PagedBatchDecodePlan:
 
     @property
     def algorithm(self) -> str:
-        return {1: "balanced_split_kv"}[self.info.algorithm]
+        return {1: "balanced_split_kv", 2: "direct"}[self.info.algorithm]
 
     @property
     def workspace_bytes(self) -> int:
         return self.info.workspace_bytes
 
     def enqueue_into(self, scope: CommandScope, args: Bf16PagedBatchDecodeArgs):
-        c = args._c()
-        _call(lib().loom_paged_decode_enqueue, self._p, scope._p, C.byref(c))
+        _enqueue(_ffi.load().loom_paged_decode_enqueue, self._p, scope._p, args._ref)
 
     def __del__(self):
         try:
@@ -583,7 +603,7 @@ class DecodeProvider:
 
 
 # ---- fused RoPE + append --------------------------------------------------------
-@dataclass
+@dataclass(frozen=True)
 class Bf16RopePagedKvAppendArgs:
     """rope/mod.rs:963-1003 plus the validation workspace."""
     query: Read
@@ -604,6 +624,11 @@ class Bf16RopePagedKvAppendArgs:
             "query", "key", "value", "batch_indices", "positions", "page_indptr",
             "page_indices", "last_page_len", "query_output", "key_pages", "value_pages",
             "workspace")])
+
+    def __post_init__(self):
+        c = self._c()
+        object.__setattr__(self, "_struct", c)
+        object.__setattr__(self, "_ref", C.byref(c))
 
 
 def Bf16RopePagedKvAppendTokensArgs(query, key, value, batch_indices, positions, page_indptr,
@@ -630,8 +655,7 @@ class Bf16RopePagedKvAppendPlan:
         return self.info.workspace_bytes
 
     def enqueue_into(self, scope: CommandScope, args: Bf16RopePagedKvAppendArgs):
-        c = args._c()
-        _call(lib().loom_rope_append_enqueue, self._p, scope._p, C.byref(c))
+        _enqueue(_ffi.load().loom_rope_append_enqueue, self._p, scope._p, args._ref)
 
     def __del__(self):
         try:

@@ -216,6 +216,43 @@ def test_explicit_guards_preserve_all_sentinels(L, oracle, name, bi, pos, ix):
     assert np.array_equal(kp, ks) and np.array_equal(vp, vs)
 
 
+@pytest.mark.parametrize("dup", [False, True], ids=["valid", "duplicate_slot"])
+def test_small_command_on_the_two_kernel_path(L, oracle, dup):
+    """A few tokens over a page table longer than the fused single-launch path
+    takes (4096 indices): the parallel validation + apply kernels, valid and
+    with a duplicate physical slot (every output keeps its sentinels)."""
+    rng = np.random.default_rng(12)
+    B, hq, hkv = 2, 4, 2
+    lens = np.array([40, 4200 * 16 - 3])
+    pages = (lens + 15) // 16
+    pool = int(pages.sum()) + 5
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
+    last = (lens - (pages - 1) * 16).astype(np.int32)
+    bi = np.array([1, 0, 1], np.int32)
+    pos = np.array([lens[1] - 1, 39, lens[1] - 2 if not dup else lens[1] - 1], np.int32)
+    T = 3
+    q = oracle.bf16_from_f32(rng.standard_normal(T * hq * 128, dtype=np.float32))
+    k = oracle.bf16_from_f32(rng.standard_normal(T * hkv * 128, dtype=np.float32))
+    v = oracle.bf16_from_f32(rng.standard_normal(T * hkv * 128, dtype=np.float32))
+    kp = np.full(pool * 16 * hkv * 128, 0x3F80, np.uint16)
+    vp = np.full(pool * 16 * hkv * 128, 0x4000, np.uint16)
+    spec = L.Bf16RopePagedKvAppendTokensSpec(T, B, pool, hq, hkv)
+    r = AppendRunner(L, spec, True)
+    qo, okp, ovp = r.run(q, k, v, bi, pos, indptr, indices, last, kp, vp)
+    if dup:
+        assert np.all(np.isnan(oracle.bf16_to_f32(qo)))
+        assert np.array_equal(okp, kp) and np.array_equal(ovp, vp)
+        return
+    s = oracle.paged_spec(B, pool, hq, hkv)
+    ekp, evp = kp.copy(), vp.copy()
+    eq = oracle.append_tokens(s, T, q, k, v, bi, pos, indptr, indices, last, ekp, evp)
+    for got, want in ((qo, eq), (okp, ekp)):
+        ok, _ = within_one_ulp(oracle, got, want)
+        assert ok
+    assert np.array_equal(ovp, evp)
+
+
 def test_bulk_append_config2_shape(L, oracle):
     """32 requests each appending U{1..64} tokens (~1040) into
     a 16384-page pool with existing lengths U[0,4095] (extended contract)."""

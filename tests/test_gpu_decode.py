@@ -64,6 +64,10 @@ SHAPES = [
     ("group16_two_tiles", 2, 16, 1, [300, 77], 0),
     ("group3", 3, 6, 2, [5, 40, 129], 4),
     ("group2", 2, 4, 2, [33, 1000], 0),
+    # small page tables: the direct kernel (one workgroup per request/kv-head/tile)
+    ("direct_gqa4", 5, 32, 8, [1, 15, 17, 100, 260], 0),
+    ("direct_group16", 3, 16, 1, [33, 200, 7], 0),
+    ("direct_mha", 2, 8, 8, [64, 190], 0),
     # more requests than the workgroup keeps in LDS: the block-wise search
     ("batch1100_small", 1100, 4, 1, [1 + (i * 37) % 70 for i in range(1100)], 0),
     ("batch1100_teams13", 1100, 8, 2, [1 + (i * 53) % 90 for i in range(1100)], 13),
@@ -83,7 +87,7 @@ def test_seeded_shapes(L, oracle, name, B, hq, hkv, lens, teams):
     ref_out, ref_lse = oracle.paged_decode(s, q, k, v, indptr, indices, last)
     r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
     out, lse = r.run(q, k, v, indptr, indices, last)
-    log(f"  plan teams={r.plan.info.teams} tile={r.plan.info.group_tile}x"
+    log(f"  plan {r.plan.algorithm} teams={r.plan.info.teams} tile={r.plan.info.group_tile}x"
         f"{r.plan.info.group_tiles} {compare_decode(oracle, out, lse, ref_out, ref_lse)}")
     # a second call over the previous call's workspace contents is identical
     out2, lse2 = r.run(q, k, v, indptr, indices, last)
@@ -148,13 +152,15 @@ def test_invalid_page_in_split_request(L, oracle):
     compare_decode(oracle, out2, lse2, ref_out, ref_lse)
 
 
-@pytest.mark.parametrize("teams", [0, 1, 5])
-def test_invalid_request_leaves_sentinels(L, oracle, teams):
+@pytest.mark.parametrize("lens,teams", [([100, 50, 300, 20, 64], 0), ([100, 50, 300, 20, 64], 1),
+                                        ([100, 50, 300, 20, 64], 5), ([20, 5, 40, 3, 30], 0)],
+                         ids=["balanced", "one_team", "five_teams", "direct"])
+def test_invalid_request_leaves_sentinels(L, oracle, lens, teams):
     """Requests failing the per-request guard (decode.rs:430-478: last page
-    length outside 1..16, empty range) contribute no pages; the others are
-    computed as usual, also when the pages around them are split over teams."""
+    length outside 1..16) contribute no pages; the others are computed as
+    usual, also when the pages around them are split over teams, and on the
+    direct (small page table) kernel."""
     rng = np.random.default_rng(8)
-    lens = [100, 50, 300, 20, 64]
     B, hq, hkv = len(lens), 8, 2
     pool = sum((x + 15) // 16 for x in lens) + 2
     indptr, indices, last = ragged_table(rng, lens, pool)
