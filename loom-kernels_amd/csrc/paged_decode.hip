@@ -80,19 +80,21 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct DecodeArgs {
-  const uint16_t *q;
-  const uint16_t *k;
-  const uint16_t *v;
-  const int32_t *indptr;
-  const int32_t *indices;
-  const int32_t *last;
-  uint16_t *out;
-  float *lse;
+  // Distinct buffers (the binding rules forbid a writable operand aliasing any
+  // other), so uniform loads of the metadata can go through the scalar cache.
+  const uint16_t *__restrict__ q;
+  const uint16_t *__restrict__ k;
+  const uint16_t *__restrict__ v;
+  const int32_t *__restrict__ indptr;
+  const int32_t *__restrict__ indices;
+  const int32_t *__restrict__ last;
+  uint16_t *__restrict__ out;
+  float *__restrict__ lse;
   // Workspace: header[0] = pages in the virtual list (-1: batch rejected),
   // header[1 + r] = virtual page prefix of request r (r = 0..B); then the
   // split states [teams + B][Hq][kStateStride].
-  int64_t *header;
-  float *states;
+  int64_t *__restrict__ header;
+  float *__restrict__ states;
   int32_t batch;
   int32_t hq;
   int32_t hkv;
@@ -155,6 +157,7 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+
 
 template <int GT>
 struct Smem {
@@ -541,58 +544,101 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     tl_out = uni(tl_out);
     return uni(c);
   };
-  // Page indices of the segment of up to 64 pages starting at virtual page
-  // `seg`: lane i holds the index of page i.
-  auto segment_indices = [&](int64_t seg, int64_t piece_end, int64_t pre, int32_t st, int &n,
-                             int &lp0) -> int {
-    n = (int)min<int64_t>(64, piece_end - seg);
-    lp0 = (int)(seg - pre);  // request-local position of the first page
-    return lane < n ? a.indices[st + lp0 + lane] : 0;
+  WaveDecoder<GT> w{a, kt, sm.qfrag[wave], sm.p[wave], sm.alpha[wave], lane, col, quad, kvh};
+  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
+
+  // ---- one continuous page stream over [v_begin, v_end) --------------------
+  // Two cursors walk the virtual list: the load cursor kDepth-1 pages ahead of
+  // the process cursor.  Page indices come in blocks of 64 (one per lane, read
+  // back with v_readlane), the next block fetched while the current one is
+  // used, so the K/V pipeline does not drain at request or block boundaries;
+  // at a request boundary the process side finishes the piece and fetches the
+  // next request's Q while the next pages' loads are in flight.
+  struct Cursor {
+    int r;
+    int64_t pre;
+    int cnt;
+    int32_t st, tl;
+  };
+  auto advance = [&](Cursor &c, int64_t vv) {
+    while (vv >= c.pre + c.cnt) {
+      c.pre += c.cnt;
+      do {
+        if (++c.r >= a.batch) {  // unreachable: vv < total
+          c.cnt = INT32_MAX;
+          return;
+        }
+        c.cnt = request_meta(c.r, c.st, c.tl);
+      } while (c.cnt == 0);
+    }
+  };
+  // Page indices of virtual pages [v0, v0 + 64) (lane i: page v0 + i; 0 past
+  // the range).  Each lane walks forward from cursor c (at or before v0) to
+  // the request holding its page: requests with no pages are skipped.
+  auto block_indices = [&](const Cursor &c, int64_t v0) -> int {
+    const int64_t vv = v0 + lane;
+    if (vv >= v_end) return 0;
+    int rr = c.r, cn = c.cnt;
+    int64_t pr = c.pre;
+    int32_t sto = c.st;
+    while (vv >= pr + cn) {
+      pr += cn;
+      do {
+        ++rr;
+        if (rr < kLdsPrefix) {
+          sto = sm.req_st[rr];
+          cn = (int)(sm.incl[rr] - sm.incl[rr - 1]);
+        } else {
+          sto = a.indptr[rr];
+          cn = request_pages(sto, a.indptr[rr + 1], a.last[rr], ipB);
+        }
+      } while (cn == 0);
+    }
+    return a.indices[sto + (int)(vv - pr)];
+  };
+  const int n = (int)(v_end - v_begin);
+  int ib = 0, ib_next = 0;  // index blocks: current and next
+  // Page index and valid rows of virtual page vl (0 rows: past the range, or
+  // an index failing the guard of decode.rs:284-289).
+  auto describe = [&](Cursor &c, int64_t vl, int &page, int &rows) {
+    page = 0;
+    rows = 0;
+    if (vl >= v_end) return;
+    advance(c, vl);
+    const int k = (int)(vl - v_begin);
+    if ((k & 63) == 0 && k > 0) {
+      ib = ib_next;
+      if (k + 64 < n) ib_next = block_indices(c, vl + 64);
+    }
+    const int32_t idx = __builtin_amdgcn_readlane(ib, k & 63);
+    if (idx >= 0 && (int64_t)idx < a.pool) {
+      page = idx;
+      rows = (int)(vl - c.pre) == c.cnt - 1 ? c.tl : 16;
+    }
   };
 
-  WaveDecoder<GT> w{a, kt, sm.qfrag[wave], sm.p[wave], sm.alpha[wave], lane, col, quad, kvh};
+  Cursor lc;
+  lc.r = r;
+  lc.pre = pre;
+  lc.cnt = request_meta(r, lc.st, lc.tl);
+  Cursor pc = lc;
+  bool bad = false;
+  ib = block_indices(lc, v_begin);
+  if (n > 64) ib_next = block_indices(lc, v_begin + 64);
 
-  // ---- pieces: the parts of requests inside [v_begin, v_end) --------------
-  int64_t v = v_begin;
-  while (true) {
-    int32_t st, tl;
-    const int cnt = request_meta(r, st, tl);  // r is a valid request: cnt > 0
-    const int64_t piece_end = min(v_end, pre + cnt);
-    const bool whole = v_begin <= pre && pre + cnt <= v_end;
-
-    // The first segment's page indices and the Q fragment are fetched in one
-    // round trip.  Q column `col` is query head g of this tile; MFMA c
-    // contracts dims 32c + 8*quad + [0, 8), the slices the K fragments read.
-    int seg_n, seg_lp0;
-    int seg_idx = segment_indices(v, piece_end, pre, st, seg_n, seg_lp0);
-    {
-      u32x4 qr[4];
-      w.load_q(r, kvh * a.group + g_base, gcount, qr);
-      w.store_q(qr);
-    }
+  auto begin_piece = [&]() {
+    u32x4 qr[4];
+    w.load_q(pc.r, kvh * a.group + g_base, gcount, qr);
+    w.store_q(qr);
     w.reset();
-    bool bad = false;
-
-    // Segments of up to 64 pages: one page index per lane, read back with
-    // v_readlane as the page loop walks them (decode.rs:284-289 guard on each).
-    for (int64_t seg = v; seg < piece_end; seg += 64) {
-      if (seg != v) seg_idx = segment_indices(seg, piece_end, pre, st, seg_n, seg_lp0);
-      const int n = seg_n, lp0 = seg_lp0, idx = seg_idx;
-      const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
-      bad |= __ballot(lane < n && !ok) != 0;
-      auto page_of = [&](int i) { return __builtin_amdgcn_readlane(idx, min(i, n - 1)); };
-      auto rows_of = [&](int i) {
-        if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
-        return lp0 + i == cnt - 1 ? tl : 16;
-      };
-      w.stream(n, page_of, rows_of);
-    }
-
-    // ---- finish the piece ---------------------------------------------------
+    bad = false;
+  };
+  auto finish_piece = [&]() {
+    const int rr = pc.r;
+    const bool whole = v_begin <= pc.pre && pc.pre + pc.cnt <= v_end;
     const float l_tot = w.reduce();
     const float m_run = w.m_run;
     const auto &acc = w.acc;
-    const int64_t qh_base = (int64_t)kvh * a.group + g_base;
     if (whole) {
       // The request lies inside this wave's range: final output in place.  An
       // invalid page index leaves the request's sentinels untouched.
@@ -602,21 +648,21 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
           if (g >= gcount) break;
           const float Lg = __shfl(l_tot, g, 64);
           if (quad == 0) {
-            uint32_t w[4];
+            uint32_t o[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              w[e] = (uint32_t)f32_to_bf16(acc[g][2 * e] / Lg) |
+              o[e] = (uint32_t)f32_to_bf16(acc[g][2 * e] / Lg) |
                      ((uint32_t)f32_to_bf16(acc[g][2 * e + 1] / Lg) << 16);
-            *reinterpret_cast<u32x4 *>(a.out + ((int64_t)r * a.hq + qh_base + g) * 128 + col * 8) =
-                u32x4{w[0], w[1], w[2], w[3]};
+            *reinterpret_cast<u32x4 *>(a.out + ((int64_t)rr * a.hq + qh_base + g) * 128 +
+                                       col * 8) = u32x4{o[0], o[1], o[2], o[3]};
           }
         }
-        if (lane < gcount) a.lse[(int64_t)r * a.hq + qh_base + lane] = m_run + __log2f(l_tot);
+        if (lane < gcount) a.lse[(int64_t)rr * a.hq + qh_base + lane] = m_run + __log2f(l_tot);
       }
     } else {
       // Split request: one state per (team, request), slot team + r (unique:
       // along the virtual list either the team or the request advances).
-      float *st_base = a.states + ((int64_t)(team + r) * a.hq + qh_base) * kStateStride;
+      float *st_base = a.states + ((int64_t)(team + rr) * a.hq + qh_base) * kStateStride;
       if (bad) {
         if (lane < gcount) {
           st_base[lane * kStateStride] = 0.0f;
@@ -638,15 +684,57 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
         }
       }
     }
+  };
 
-    v = piece_end;
-    if (v >= v_end) break;
-    // next request with pages (v < total, so one exists)
-    pre += cnt;
-    do {
-      if (++r >= a.batch) return;  // unreachable: v < total
-    } while (request_meta(r, st, tl) == 0);
+  // Pipeline: page v+kDepth-1 is issued before page v is consumed; the
+  // unrolled buffer rotation lets the compiler wait for exactly the oldest
+  // page's loads.
+  PageRegs buf[kDepth];
+  int brows[kDepth];
+#pragma unroll
+  for (int j = 0; j < kDepth - 1; ++j) {
+    int pg;
+    describe(lc, v_begin + j, pg, brows[j]);
+    load_page(buf[j], a, pg, brows[j], lane, kvh);
   }
+  // Issue priority by progress (see the page loop): every wave starts high.
+  __builtin_amdgcn_s_setprio(3);
+  begin_piece();
+  int64_t v = v_begin;
+  int i = 0;
+  while (true) {
+#pragma unroll
+    for (int s = 0; s < kDepth; ++s) {
+      {
+        const int nb = (s + kDepth - 1) % kDepth;
+        int pg;
+        describe(lc, v + kDepth - 1, pg, brows[nb]);
+        load_page(buf[nb], a, pg, brows[nb], lane, kvh);
+      }
+      if (v >= pc.pre + pc.cnt) {
+        finish_piece();
+        advance(pc, v);
+        begin_piece();
+      }
+      bad |= brows[s] == 0;
+      w.process(buf[s], brows[s]);
+      ++v;
+      if (++i >= n) goto stream_done;
+      // Waves ahead of schedule yield issue priority to the ones behind: all
+      // waves have the same number of pages, but the SIMD arbiter favours the
+      // oldest waves, so without this the first workgroups on a CU finish far
+      // earlier and the last ones stream alone at the end (measured: wave end
+      // times spread over 88..196 us on config 3; 131..178 us with this).
+      if ((i & 7) == 0) {
+        const int q = (4 * i) / n;
+        if (q == 1) __builtin_amdgcn_s_setprio(2);
+        else if (q == 2) __builtin_amdgcn_s_setprio(1);
+        else if (q >= 3) __builtin_amdgcn_s_setprio(0);
+      }
+    }
+  }
+stream_done:
+  finish_piece();
 }
 
 // Direct decode for small page tables: one workgroup per (request, kv-head,
@@ -804,6 +892,7 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
 }
 
 }  // namespace
+
 
 // ---- provider / plan / enqueue -----------------------------------------------
 struct loom_decode_provider {
