@@ -294,3 +294,34 @@ def test_bulk_append_config2_shape(L, oracle):
     ekr[rows] = 0
     assert np.array_equal(okr, ekr)
     assert np.array_equal(ovp, evp)
+
+
+def test_large_position_stays_finite_and_matches(L, oracle):
+    """One token at position 32767 (rope/tests.rs:61-81 on the device): the
+    rotation at large angles stays finite and within the RoPE tolerance."""
+    rng = np.random.default_rng(32767)
+    B, hq, hkv = 1, 4, 2
+    kv_len = 32768
+    pages = kv_len // 16
+    pool = pages + 3
+    indptr = np.array([0, pages], np.int32)
+    indices = rng.permutation(pool)[:pages].astype(np.int32)
+    last = np.array([16], np.int32)
+    q = oracle.bf16_from_f32(rng.standard_normal(B * hq * 128, dtype=np.float32))
+    k = oracle.bf16_from_f32(rng.standard_normal(B * hkv * 128, dtype=np.float32))
+    v = oracle.bf16_from_f32(rng.standard_normal(B * hkv * 128, dtype=np.float32))
+    kp = np.zeros(pool * 16 * hkv * 128, np.uint16)
+    vp = np.zeros(pool * 16 * hkv * 128, np.uint16)
+    s = oracle.paged_spec(B, pool, hq, hkv)
+    ekp, evp = kp.copy(), vp.copy()
+    eq = oracle.append(s, q, k, v, indptr, indices, last, ekp, evp)
+    spec = L.Bf16RopePagedKvAppendSpec(B, pool, hq, hkv)
+    r = AppendRunner(L, spec, False)
+    qo, okp, ovp = r.run(q, k, v, None, None, indptr, indices, last, kp, vp)
+    assert np.all(np.isfinite(oracle.bf16_to_f32(qo)))
+    assert within_rope_tolerance(oracle, qo, eq, q)
+    row = (indices[-1] * 16 + 15) * hkv
+    got_k = okp.reshape(-1, 128)[row:row + hkv].reshape(-1)
+    want_k = ekp.reshape(-1, 128)[row:row + hkv].reshape(-1)
+    assert within_rope_tolerance(oracle, got_k, want_k, k)
+    assert np.array_equal(ovp, evp)

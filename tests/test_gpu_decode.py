@@ -283,3 +283,79 @@ def test_full_c3_shape_sampled_requests(L, oracle):
         st = compare_decode(oracle, out_h[rq * hq * 128:(rq + 1) * hq * 128],
                             lse_h[rq * hq:(rq + 1) * hq], ref_o, ref_l)
         log(f"  request {rq} len {lens[rq]}: {st}")
+
+
+def test_plan_selection_and_rejections(L):
+    """Planner behaviour (the reference's algorithm-selection test,
+    decode.rs:1657-1698, for this build's two algorithms)."""
+    prov = L.DecodeProvider.load(0)
+    small = L.Bf16PagedBatchDecodeSpec(4, 8, 16, 4, 128, 16)
+    p = prov.plan_bf16_paged_batch(small)
+    assert p.algorithm == "direct" and p.info.grid_blocks == 4 * 4
+    p = prov.plan_bf16_paged_batch(small, teams=3)
+    assert p.algorithm == "balanced_split_kv" and p.info.teams == 3
+    big = L.Bf16PagedBatchDecodeSpec(64, 65536, 32, 8, 128, 16)
+    p = prov.plan_bf16_paged_batch(big)
+    info = p.info
+    assert p.algorithm == "balanced_split_kv" and info.group_tile == 4 and info.group_tiles == 1
+    # one wave per SIMD slot: teams x members waves fill the grid's XCD slices
+    assert info.teams * 8 <= info.grid_blocks * 4 and info.grid_blocks % 8 == 0
+    assert info.state_slots == info.teams + 64
+    assert info.workspace_bytes == info.header_bytes + info.state_slots * 32 * 132 * 4
+    grp = L.Bf16PagedBatchDecodeSpec(2, 64, 48, 2, 128, 16)  # group 24: 8-wide tiles x 3
+    p = prov.plan_bf16_paged_batch(grp, teams=5)
+    assert (p.info.group_tile, p.info.group_tiles) == (8, 3)
+    with pytest.raises(L.PlanError) as e:
+        prov.plan_bf16_paged_batch(big, max_total_pages=63)  # fewer pages than requests
+    assert e.value.variant == "InvalidOption"
+    huge = L.Bf16PagedBatchDecodeSpec(65537, 65537, 8, 8, 128, 16)
+    with pytest.raises(L.PlanError) as e:
+        prov.plan_bf16_paged_batch(huge)
+    assert e.value.variant == "StateCountOutOfRange"
+
+
+@pytest.mark.parametrize("teams", [0, 4], ids=["direct", "balanced"])
+def test_enqueue_rejections_submit_nothing(L, teams):
+    """Exact operand lengths, page_indices bounds and 16-byte alignment are
+    checked before anything is submitted (decode.rs:1216-1251)."""
+    torch = pytest.importorskip("torch")
+    B, pool, hq, hkv = 2, 8, 8, 2
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
+    s = r.spec
+    dev = "cuda"
+
+    def bufs():
+        return dict(q=torch.zeros(s.query_numel, dtype=torch.bfloat16, device=dev),
+                    k=torch.zeros(s.kv_pages_numel, dtype=torch.bfloat16, device=dev),
+                    v=torch.zeros(s.kv_pages_numel, dtype=torch.bfloat16, device=dev),
+                    ip=to_dev_i32([0, 1, 2]), ix=to_dev_i32([0, 1]), ln=to_dev_i32([16, 16]),
+                    o=torch.zeros(s.output_numel, dtype=torch.bfloat16, device=dev),
+                    l=torch.zeros(s.lse_numel, dtype=torch.float32, device=dev))
+
+    def attempt(**over):
+        t = bufs()
+        t.update(over)
+        b, h = r.bindings(t["q"], t["k"], t["v"], t["ip"], t["ix"], t["ln"], t["o"], t["l"])
+        scope = r.queue.begin(b)
+        try:
+            with pytest.raises(L.EnqueueError) as e:
+                r.plan.enqueue_into(scope, r.args(h))
+        finally:
+            comp = scope.finish()
+            assert comp.submitted() == 0
+            comp.wait()
+        return e.value
+
+    e = attempt(q=torch.zeros(s.query_numel + 8, dtype=torch.bfloat16, device=dev))
+    assert (e.variant, e.operand) == ("LengthMismatch", "Q")
+    e = attempt(ln=to_dev_i32([16]))
+    assert (e.variant, e.operand) == ("LengthMismatch", "last_page_len")
+    e = attempt(l=torch.zeros(s.lse_numel + 1, dtype=torch.float32, device=dev))
+    assert (e.variant, e.operand) == ("LengthMismatch", "LSE")
+    e = attempt(ix=to_dev_i32([0]))
+    assert e.variant == "PageIndicesTooShort"
+    e = attempt(ix=to_dev_i32(list(range(pool + 1))))
+    assert e.variant == "PageIndicesTooLong"
+    q2 = torch.zeros(s.query_numel + 8, dtype=torch.bfloat16, device=dev)[1:1 + s.query_numel]
+    e = attempt(q=q2)
+    assert (e.variant, e.operand) == ("MisalignedBuffer", "Q")

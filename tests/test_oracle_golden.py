@@ -320,6 +320,16 @@ def test_rope_zero_position_is_identity(oracle):
     assert np.array_equal(qo, q) and np.array_equal(ko, k)
 
 
+def test_rope_large_position_stays_finite(oracle):
+    # crates/loom-infer/src/rope/tests.rs:61-81
+    q = np.full(128, oracle.bf16_from_f32(np.array([0.25], np.float32))[0], np.uint16)
+    k = np.full(128, oracle.bf16_from_f32(np.array([-0.5], np.float32))[0], np.uint16)
+    qo, ko = oracle.rope_pos_ids(1, 1, 1, q, k, [32767])
+    assert np.all(np.isfinite(oracle.bf16_to_f32(qo))) and np.all(np.isfinite(oracle.bf16_to_f32(ko)))
+    # |rotated| <= |x1| + |x2| elementwise
+    assert np.all(np.abs(oracle.bf16_to_f32(qo)) <= 0.5 + 2 ** -8)
+
+
 def test_rope_rejects_negative_position(oracle):
     with pytest.raises(oracle.OracleError) as e:
         oracle.rope_pos_ids(1, 1, 1, np.zeros(2, np.uint16), np.zeros(2, np.uint16), [-1],
