@@ -118,6 +118,32 @@ def _timed_enqueues(L, stream, n_bind, bind, enqueue, steps, warmup):
     return start.elapsed_time(end) * 1000.0 / steps  # µs per call
 
 
+def _timed_rotating(L, stream, n_bind, binders, enqueue, steps, warmup):
+    """Like _timed_enqueues, but call i uses input set i % len(binders): with
+    the sets together larger than the 256 MB Infinity Cache, every call reads
+    its inputs from HBM (the cold-cache figure for small configs)."""
+    import torch
+    q = L.CommandQueue(stream, steps + warmup + 1)
+    b = q.bindings(n_bind * len(binders))
+    args = [bind(b) for bind in binders]
+    with torch.cuda.stream(stream):
+        scope = q.begin(b)
+        for i in range(warmup):
+            enqueue(scope, args[i % len(args)])
+        b = scope.finish().wait()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        scope = q.begin(b)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for i in range(steps):
+            enqueue(scope, args[i % len(args)])
+        end.record(stream)
+        b = scope.finish().wait()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
 def _graph_replay(L, n_bind, n_cmds, bind, record, replays=20):
     """One fixed-address replay + its completion event per sample
     (graph/mod.rs:301-323); returns the median µs."""
@@ -356,7 +382,7 @@ def reference_shapes(L, stream, samples=30):
                       for k in ("indptr", "indices", "last"))
         o = torch.empty(B * hq * 128, dtype=torch.bfloat16, device=dev)
         lse = torch.empty(B * hq, dtype=torch.float32, device=dev)
-        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(plan.workspace_bytes, dtype=torch.uint8, device=dev)
 
         def bind(b):
             return L.Bf16PagedBatchDecodeArgs(
@@ -461,6 +487,15 @@ def main():
                         "algorithmic_bytes": case.bytes,
                         "teams": case.plan.info.teams,
                         "mean_kv_len": float(case.lens.mean())}
+        if name.startswith("c1"):
+            # cold: 16 copies of the workload (537 MB) used round-robin
+            copies = [case] + [DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name) + i)
+                               for i in range(1, 16)]
+            cold = _timed_rotating(L, stream, 9, [c.bind for c in copies],
+                                   case.plan.enqueue_into, a.steps, a.warmup)
+            detail[name].update({"cold_us_per_call": round(cold, 3),
+                                 "cold_GBps": round(case.bytes / (cold * 1e-6) / 1e9, 1)})
+            del copies
         if name.startswith("c5"):
             # the one-token append of the same step, then the whole step as one graph
             app = AppendCase(L, B, hq, hkv, pool, lens, seed=5, share=case)
@@ -484,8 +519,31 @@ def main():
         n_new = rng.integers(1, 65, size=32)
         app = AppendCase(L, 32, 32, 8, 16384, existing + n_new, seed=2, n_new=n_new)
         ap_us, ap_g = time_append(L, app, stream, a.steps, a.warmup)
+        # cold: 24 sets of the token inputs and query outputs (each ~20 MB)
+        # rotated over the same page pools
+        extra = []
+        for i in range(1, 24):
+            x = object.__new__(AppendCase)
+            x.__dict__.update(app.__dict__)
+            x.q, x.k, x.v = (torch.randn_like(t) for t in (app.q, app.k, app.v))
+            x.qo = torch.empty_like(app.qo)
+            x.ws = torch.zeros_like(app.ws)
+            extra.append(x)
+        shared = {}  # the page pools are bound read-write once per binding set
+
+        def binder(x):
+            def bind(b):
+                if not shared:
+                    shared["kp"] = b.bind_read_write(app.kp)
+                    shared["vp"] = b.bind_read_write(app.vp)
+                return x.bind(b, kp=shared["kp"], vp=shared["vp"])
+            return bind
+        cold = _timed_rotating(L, stream, 12, [binder(x) for x in [app] + extra],
+                               app.plan.enqueue_into, a.steps, a.warmup)
+        del extra
         detail["c2_rope_append_b32_tokens"] = {
             "us_per_call": round(ap_us, 3), "graph_replay_us": round(ap_g, 3),
+            "cold_us_per_call": round(cold, 3),
             "tokens": app.T, "algorithmic_bytes": app.bytes,
             "GBps": round(app.bytes / (ap_us * 1e-6) / 1e9, 1)}
         log(f"[bench] c2: {detail['c2_rope_append_b32_tokens']}")
