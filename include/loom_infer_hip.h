@@ -383,6 +383,90 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
                                         loom_error_t *err);
 
 /* ------------------------------------------------------------------------ */
+/* Contiguous single decode, crates/loom-infer/src/attention/single_decode/    */
+/* mod.rs:15-194 and decode.rs:1016-1064, :1108-1181, :1301-1450: Q/O        */
+/* [Hq, 128], K/V [kv_len, Hkv, 128] (NHD, contiguous), LSE [Hq] log2.        */
+typedef struct loom_single_decode_spec {
+  uint64_t kv_len;
+  uint64_t num_query_heads;
+  uint64_t num_kv_heads;
+  float softmax_scale;
+} loom_single_decode_spec_t;
+
+typedef struct loom_single_decode_split_k_spec {
+  loom_single_decode_spec_t decode;
+  uint64_t partitions;
+} loom_single_decode_split_k_spec_t;
+
+/* Bf16SingleDecodeSpec::new, single_decode/mod.rs:31-70. */
+loom_status_t loom_single_decode_spec_new(uint64_t kv_len, uint64_t num_query_heads,
+                                          uint64_t num_kv_heads, uint64_t head_dim,
+                                          loom_single_decode_spec_t *out, loom_error_t *err);
+/* Bf16SingleDecodeSplitKSpec::new, single_decode/mod.rs:131-145. */
+loom_status_t loom_single_decode_split_k_spec_new(const loom_single_decode_spec_t *decode,
+                                                  uint64_t partitions,
+                                                  loom_single_decode_split_k_spec_t *out,
+                                                  loom_error_t *err);
+/* partition_token_range, single_decode/mod.rs:167-181: balanced contiguous
+ * partitions (the first kv_len % P get one token more).  LOOM_OK, or
+ * LOOM_INVALID_PARTITION_COUNT for the reference's None. */
+loom_status_t loom_single_decode_split_k_partition_token_range(
+    const loom_single_decode_split_k_spec_t *spec, uint64_t partition, uint64_t *start,
+    uint64_t *end);
+
+typedef struct loom_single_decode_plan loom_single_decode_plan_t;
+typedef struct loom_single_decode_split_k_plan loom_single_decode_split_k_plan_t;
+
+/* DecodeProvider::plan_bf16, decode.rs:1016-1032: one workgroup per
+ * (kv-head, tile of up to 8 query heads) streams the whole KV range. */
+loom_status_t loom_decode_provider_plan_bf16(const loom_decode_provider_t *provider,
+                                             const loom_single_decode_spec_t *spec,
+                                             loom_single_decode_plan_t **out, loom_error_t *err);
+void loom_single_decode_plan_free(loom_single_decode_plan_t *plan);
+
+/* Bf16SingleDecodeArgs, decode.rs:1394-1420. */
+typedef struct loom_single_decode_args {
+  loom_handle_t query;  /* Read<bf16>  [Hq, 128] */
+  loom_handle_t key;    /* Read<bf16>  [kv_len, Hkv, 128] */
+  loom_handle_t value;  /* Read<bf16>  [kv_len, Hkv, 128] */
+  loom_handle_t output; /* Write<bf16> [Hq, 128] */
+  loom_handle_t lse;    /* Write<f32>  [Hq] */
+} loom_single_decode_args_t;
+
+/* Bf16SingleDecodePlan::enqueue_into, decode.rs:1120-1180: one command. */
+loom_status_t loom_single_decode_enqueue(const loom_single_decode_plan_t *plan,
+                                         loom_command_scope_t *scope,
+                                         const loom_single_decode_args_t *args,
+                                         loom_error_t *err);
+
+/* DecodeProvider::plan_bf16_split_k, decode.rs:1034-1064: one wave per
+ * (partition, kv-head, tile) writes the partition's log2-domain states. */
+loom_status_t loom_decode_provider_plan_bf16_split_k(
+    const loom_decode_provider_t *provider, const loom_single_decode_split_k_spec_t *spec,
+    loom_single_decode_split_k_plan_t **out, loom_error_t *err);
+void loom_single_decode_split_k_plan_free(loom_single_decode_split_k_plan_t *plan);
+/* workspace_required_bytes, decode.rs:1316-1320: Hq * partitions * 130 * 4. */
+uint64_t loom_single_decode_split_k_workspace_bytes(const loom_single_decode_split_k_plan_t *plan);
+
+/* Bf16SingleDecodeSplitKArgs, decode.rs:1422-1450: the workspace holds the
+ * partial states [Hq, partitions, 130] = (max_log2, normalizer, acc[128]). */
+typedef struct loom_single_decode_split_k_args {
+  loom_handle_t query;
+  loom_handle_t key;
+  loom_handle_t value;
+  loom_handle_t workspace; /* ReadWrite<f32> [Hq * partitions * 130] */
+  loom_handle_t output;
+  loom_handle_t lse;
+} loom_single_decode_split_k_args_t;
+
+/* Bf16SingleDecodeSplitKPlan::enqueue_into, decode.rs:1322-1392: two
+ * commands (partials, then the merge) in one scope. */
+loom_status_t loom_single_decode_split_k_enqueue(const loom_single_decode_split_k_plan_t *plan,
+                                                 loom_command_scope_t *scope,
+                                                 const loom_single_decode_split_k_args_t *args,
+                                                 loom_error_t *err);
+
+/* ------------------------------------------------------------------------ */
 /* Fused RoPE + paged append provider, crates/loom-infer-cuda/src/rope/mod.rs */
 typedef struct loom_rope_provider loom_rope_provider_t;
 typedef struct loom_rope_append_plan loom_rope_append_plan_t;

@@ -332,6 +332,57 @@ loom_status_t loom_paged_decode_spec_new(uint64_t batch, uint64_t pool, uint64_t
   return loom::ok(err);
 }
 
+// single_decode/mod.rs:31-70.
+loom_status_t loom_single_decode_spec_new(uint64_t kv_len, uint64_t hq, uint64_t hkv,
+                                          uint64_t head_dim, loom_single_decode_spec_t *out,
+                                          loom_error_t *err) {
+  if (!out) return fail(err, LOOM_NULL_ARGUMENT, "out");
+  if (kv_len == 0 || hq == 0 || hkv == 0 || head_dim == 0) return fail(err, LOOM_ZERO_DIMENSION);
+  if (head_dim != loom::kHeadDim)
+    return fail(err, LOOM_UNSUPPORTED_HEAD_DIMENSION, nullptr, loom::kHeadDim, head_dim);
+  if (hq % hkv != 0) return fail(err, LOOM_INVALID_HEAD_MAPPING, nullptr, hq, hkv);
+  uint64_t t;
+  if (mul_ovf(hq, head_dim, &t)) return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  if (mul_ovf(hkv, head_dim, &t) || mul_ovf(kv_len, t, &t))
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  out->kv_len = kv_len;
+  out->num_query_heads = hq;
+  out->num_kv_heads = hkv;
+  out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
+  return loom::ok(err);
+}
+
+// single_decode/mod.rs:131-145.
+loom_status_t loom_single_decode_split_k_spec_new(const loom_single_decode_spec_t *decode,
+                                                  uint64_t partitions,
+                                                  loom_single_decode_split_k_spec_t *out,
+                                                  loom_error_t *err) {
+  if (!decode || !out) return fail(err, LOOM_NULL_ARGUMENT, "decode");
+  if (partitions == 0 || partitions > decode->kv_len)
+    return fail(err, LOOM_INVALID_PARTITION_COUNT, nullptr, partitions, decode->kv_len);
+  uint64_t t;
+  if (mul_ovf(decode->num_query_heads, partitions, &t) ||
+      mul_ovf(t, loom::kStateWidth, &t) || mul_ovf(t, 4, &t))
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  out->decode = *decode;
+  out->partitions = partitions;
+  return loom::ok(err);
+}
+
+// single_decode/mod.rs:167-181.
+loom_status_t loom_single_decode_split_k_partition_token_range(
+    const loom_single_decode_split_k_spec_t *spec, uint64_t partition, uint64_t *start,
+    uint64_t *end) {
+  if (!spec || !start || !end) return LOOM_NULL_ARGUMENT;
+  const uint64_t P = spec->partitions, L = spec->decode.kv_len;
+  if (partition >= P) return LOOM_INVALID_PARTITION_COUNT;
+  const uint64_t base = L / P, rem = L % P;
+  const uint64_t s0 = partition * base + (partition < rem ? partition : rem);
+  *start = s0;
+  *end = s0 + base + (partition < rem ? 1 : 0);
+  return LOOM_OK;
+}
+
 // paged_decode/mod.rs:152-213.
 loom_status_t loom_paged_decode_validate_page_table(const loom_paged_decode_spec_t *s,
                                                     const int32_t *indptr, uint64_t n_indptr,

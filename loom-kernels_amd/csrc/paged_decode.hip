@@ -182,11 +182,13 @@ struct PageRegs {
   u32x4 v[4];
 };
 
-// `page` and `valid_rows` are wave-uniform (the resource lives in SGPRs).
-__device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page,
+// 16 consecutive token rows starting at token row `token0` of the NHD K/V
+// buffers (a page of a paged cache, or any 16 tokens of a contiguous one).
+// `token0` and `valid_rows` are wave-uniform (the resource lives in SGPRs).
+__device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int64_t token0,
                                           int valid_rows, int lane, int kvh) {
   const int col = lane & 15, quad = lane >> 4;
-  const int64_t first = ((int64_t)page * 16 * a.hkv + kvh) * 128;
+  const int64_t first = (token0 * a.hkv + kvh) * 128;
   const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, valid_rows, a.hkv);
   const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, valid_rows, a.hkv);
 #pragma unroll
@@ -195,6 +197,11 @@ __device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int 
     r.k[j] = load16_rows<LOOM_DECODE_NT_K>(rk, off);
     r.v[j] = load16_rows<LOOM_DECODE_NT_V>(rv, off);
   }
+}
+
+__device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page,
+                                          int valid_rows, int lane, int kvh) {
+  load_rows(r, a, (int64_t)page * 16, valid_rows, lane, kvh);
 }
 
 // Wave-uniform values the compiler cannot prove uniform (loaded through the
@@ -349,21 +356,22 @@ struct WaveDecoder {
     wave_lds_fence();
   }
 
-  // Streams pages 0..n-1 (n >= 1) through a kDepth-deep pipeline: each step
-  // issues the loads of the page kDepth-1 steps ahead before consuming the
-  // current one.  Loads past the end have no valid rows and touch no memory;
-  // the unrolled buffer rotation lets the compiler wait for exactly the
-  // oldest page's loads.  page_of(i) / rows_of(i) must be wave-uniform.
-  template <class PageOf, class RowsOf>
-  __device__ void stream(int n, PageOf page_of, RowsOf rows_of) {
+  // Streams 16-row blocks 0..n-1 (n >= 1) through a kDepth-deep pipeline:
+  // each step issues the loads of the block kDepth-1 steps ahead before
+  // consuming the current one.  Loads past the end have no valid rows and
+  // touch no memory; the unrolled buffer rotation lets the compiler wait for
+  // exactly the oldest block's loads.  tok_of(i) (first token row of block i)
+  // and rows_of(i) must be wave-uniform.
+  template <class TokOf, class RowsOf>
+  __device__ void stream(int n, TokOf tok_of, RowsOf rows_of) {
     PageRegs buf[kDepth];
 #pragma unroll
-    for (int j = 0; j < kDepth - 1; ++j) load_page(buf[j], a, page_of(j), rows_of(j), lane, kvh);
+    for (int j = 0; j < kDepth - 1; ++j) load_rows(buf[j], a, tok_of(j), rows_of(j), lane, kvh);
     int i = 0;
     while (true) {
 #pragma unroll
       for (int s = 0; s < kDepth; ++s) {
-        load_page(buf[(s + kDepth - 1) % kDepth], a, page_of(i + kDepth - 1),
+        load_rows(buf[(s + kDepth - 1) % kDepth], a, tok_of(i + kDepth - 1),
                   rows_of(i + kDepth - 1), lane, kvh);
         process(buf[s], rows_of(i));
         if (++i >= n) return;
@@ -791,12 +799,14 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_dir
       const int n = min(mine - s0, 64);
       const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
       bad |= __ballot(lane < n && !ok) != 0;
-      auto page_of = [&](int i) { return __builtin_amdgcn_readlane(idx, min(i, n - 1)); };
+      auto tok_of = [&](int i) {
+        return (int64_t)__builtin_amdgcn_readlane(idx, min(i, n - 1)) * 16;
+      };
       auto rows_of = [&](int i) {
         if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
         return wave + kWaves * (s0 + i) == cnt - 1 ? tl : 16;
       };
-      w.stream(n, page_of, rows_of);
+      w.stream(n, tok_of, rows_of);
     }
   }
   const float l_tot = w.reduce();
@@ -891,8 +901,168 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
   if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(l);
 }
 
-}  // namespace
+// ---- contiguous single decode -------------------------------------------------
+// K/V [kv_len, Hkv, 128] contiguous (single_decode/mod.rs:15-20): any 16
+// consecutive tokens form a block with the paged layout's row stride, so the
+// page step, the loads and the range-limited buffer resources are shared.
 
+// Bf16SingleDecodePlan: one workgroup per (kv-head, tile); wave w takes the
+// 16-token blocks w, w+4, ... and the 4 wave states merge in LDS.
+template <int GT>
+__global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_kernel(
+    DecodeArgs a, int64_t kv_len) {
+  __shared__ DirectSmem<GT> sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, quad = lane >> 4;
+  const int kvh = (int)(blockIdx.x % a.hkv);
+  const int gt = (int)(blockIdx.x / a.hkv);
+  const int g_base = gt * GT;
+  const int gcount = min(GT, a.group - g_base);
+  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
+                    lane, col, quad, kvh};
+  const int64_t nblk = (kv_len + 15) / 16;
+  const int mine = nblk > wave ? (int)((nblk - wave + kWaves - 1) / kWaves) : 0;
+  {
+    u32x4 qr[4];
+    w.load_q(0, kvh * a.group + g_base, gcount, qr);
+    w.store_q(qr);
+  }
+  w.reset();
+  if (mine > 0) {
+    auto tok_of = [&](int i) { return (int64_t)(wave + kWaves * min(i, mine - 1)) * 16; };
+    auto rows_of = [&](int i) {
+      if (i >= mine) return 0;
+      return (int)min<int64_t>(16, kv_len - (int64_t)(wave + kWaves * i) * 16);
+    };
+    w.stream(mine, tok_of, rows_of);
+  }
+  const float l_tot = w.reduce();
+  if (quad == 0) {
+    if (col < GT) {
+      sm.wm[wave][col] = w.m_run;
+      sm.wl[wave][col] = l_tot;
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.wacc[wave][g][col * 8 + e] = w.acc[g][e];
+  }
+  __syncthreads();
+  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
+  for (int idx = tid; idx < GT * 128; idx += kThreads) {
+    const int g = idx >> 7, d = idx & 127;
+    if (g >= gcount) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) M = fmaxf(M, sm.wm[wv][g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const float f = fast_exp2(sm.wm[wv][g] - M);
+      L = fmaf(sm.wl[wv][g], f, L);
+      O = fmaf(sm.wacc[wv][g][d], f, O);
+    }
+    a.out[(qh_base + g) * 128 + d] = f32_to_bf16(O / L);
+    if (d == 0) a.lse[qh_base + g] = M + __log2f(L);
+  }
+}
+
+// Bf16SingleDecodeSplitKPlan partials: one wave per (partition, kv-head,
+// tile) over the partition's balanced token range (single_decode/mod.rs:
+// 167-181), writing (max_log2, normalizer, acc[128]) per query head into the
+// workspace [Hq, partitions, 130] (single_decode/mod.rs:10-13, :183-193).
+template <int GT>
+__global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_split_k_kernel(
+    DecodeArgs a, int64_t kv_len, int partitions, float *__restrict__ ws) {
+  __shared__ DirectSmem<GT> sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, quad = lane >> 4;
+  const int64_t wid = (int64_t)blockIdx.x * kWaves + wave;
+  if (wid >= (int64_t)partitions * a.members) return;  // no workgroup barrier follows
+  const int part = (int)(wid / a.members), member = (int)(wid % a.members);
+  const int kvh = member % a.hkv, gt = member / a.hkv;
+  const int g_base = gt * GT;
+  const int gcount = min(GT, a.group - g_base);
+  const int64_t base = kv_len / partitions, rem = kv_len % partitions;
+  const int64_t start = part * base + min<int64_t>(part, rem);
+  const int64_t end = start + base + (part < rem ? 1 : 0);
+  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
+                    lane, col, quad, kvh};
+  {
+    u32x4 qr[4];
+    w.load_q(0, kvh * a.group + g_base, gcount, qr);
+    w.store_q(qr);
+  }
+  w.reset();
+  const int nb = (int)((end - start + 15) / 16);
+  auto tok_of = [&](int i) { return start + (int64_t)min(i, nb - 1) * 16; };
+  auto rows_of = [&](int i) {
+    return i >= nb ? 0 : (int)min<int64_t>(16, end - start - (int64_t)i * 16);
+  };
+  w.stream(nb, tok_of, rows_of);
+  const float l_tot = w.reduce();
+  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
+  for (int g = 0; g < gcount; ++g) {
+    float *st = ws + ((qh_base + g) * partitions + part) * (int64_t)loom::kStateWidth;
+    if (quad == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        *reinterpret_cast<float2 *>(st + 2 + col * 8 + e) = float2{w.acc[g][e], w.acc[g][e + 1]};
+    }
+  }
+  if (lane < gcount) {
+    float *st = ws + ((qh_base + lane) * partitions + part) * (int64_t)loom::kStateWidth;
+    st[0] = w.m_run;
+    st[1] = l_tot;
+  }
+}
+
+// Split-K merge (single_decode/mod.rs:332-381): one workgroup of 128 lanes
+// (one per output column) per query head.
+__global__ __launch_bounds__(128) void single_decode_split_k_merge_kernel(
+    DecodeArgs a, int partitions, const float *__restrict__ ws) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qh = blockIdx.x;
+  const float *row = ws + (int64_t)qh * partitions * loom::kStateWidth;
+  float mloc = -INFINITY;
+  for (int p = tid; p < partitions; p += 128) mloc = fmaxf(mloc, row[(int64_t)p * loom::kStateWidth]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
+  __shared__ float s_m[2];
+  if (lane == 0) s_m[wave] = mloc;
+  __syncthreads();
+  const float M = fmaxf(s_m[0], s_m[1]);
+  float l = 0.f, o = 0.f;
+  int p = 0;
+  for (; p + 8 <= partitions; p += 8) {
+    float ms[8], ls[8], xs[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float *ss = row + (int64_t)(p + u) * loom::kStateWidth;
+      ms[u] = ss[0];
+      ls[u] = ss[1];
+      xs[u] = ss[2 + tid];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float f = fast_exp2(ms[u] - M);
+      l = fmaf(ls[u], f, l);
+      o = fmaf(xs[u], f, o);
+    }
+  }
+  for (; p < partitions; ++p) {
+    const float *ss = row + (int64_t)p * loom::kStateWidth;
+    const float f = fast_exp2(ss[0] - M);
+    l = fmaf(ss[1], f, l);
+    o = fmaf(ss[2 + tid], f, o);
+  }
+  a.out[(int64_t)qh * 128 + tid] = f32_to_bf16(o / l);
+  if (tid == 0) a.lse[qh] = M + __log2f(l);
+}
+
+}  // namespace
 
 // ---- provider / plan / enqueue -----------------------------------------------
 struct loom_decode_provider {
@@ -903,6 +1073,40 @@ struct loom_paged_decode_plan {
   loom_paged_decode_plan_info_t info;
   int device = 0;
 };
+
+struct loom_single_decode_plan {
+  loom_single_decode_spec_t spec;
+  uint32_t group_tile = 1, group_tiles = 1;
+};
+
+struct loom_single_decode_split_k_plan {
+  loom_single_decode_split_k_spec_t spec;
+  uint32_t group_tile = 1, group_tiles = 1;
+};
+
+namespace {
+uint32_t group_tile_for(uint64_t group) {
+  return group <= 1 ? 1u : group <= 2 ? 2u : group <= 4 ? 4u : 8u;
+}
+
+// Single-decode argument block shared by both plans (batch of one request).
+DecodeArgs single_args(const loom_single_decode_spec_t &s, uint32_t gtiles, uintptr_t q,
+                       uintptr_t k, uintptr_t v, uintptr_t o, uintptr_t lse) {
+  DecodeArgs a{};
+  a.q = (const uint16_t *)q;
+  a.k = (const uint16_t *)k;
+  a.v = (const uint16_t *)v;
+  a.out = (uint16_t *)o;
+  a.lse = (float *)lse;
+  a.batch = 1;
+  a.hq = (int32_t)s.num_query_heads;
+  a.hkv = (int32_t)s.num_kv_heads;
+  a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
+  a.members = (int32_t)(s.num_kv_heads * gtiles);
+  a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
+  return a;
+}
+}  // namespace
 
 extern "C" {
 
@@ -1099,6 +1303,156 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
     e = hipGetLastError();
   }
   return loom::record_launch(scope, e, err);
+}
+
+
+// ---- contiguous single decode: plans and enqueue -------------------------------
+loom_status_t loom_decode_provider_plan_bf16(const loom_decode_provider_t *provider,
+                                             const loom_single_decode_spec_t *spec,
+                                             loom_single_decode_plan_t **out, loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  // decode.rs:1020-1023: the launch range of the query heads
+  if (spec->num_query_heads > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "single-decode query heads",
+                spec->num_query_heads);
+  auto *p = new loom_single_decode_plan;
+  p->spec = *spec;
+  const uint64_t group = spec->num_query_heads / spec->num_kv_heads;
+  p->group_tile = group_tile_for(group);
+  p->group_tiles = (uint32_t)((group + p->group_tile - 1) / p->group_tile);
+  *out = p;
+  return loom::ok(err);
+}
+
+void loom_single_decode_plan_free(loom_single_decode_plan_t *p) { delete p; }
+
+loom_status_t loom_decode_provider_plan_bf16_split_k(
+    const loom_decode_provider_t *provider, const loom_single_decode_split_k_spec_t *spec,
+    loom_single_decode_split_k_plan_t **out, loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  const loom_single_decode_spec_t &d = spec->decode;
+  if (d.num_query_heads > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "single-decode query heads",
+                d.num_query_heads);
+  const uint64_t group = d.num_query_heads / d.num_kv_heads;
+  const uint32_t gtile = group_tile_for(group);
+  const uint64_t gtiles = (group + gtile - 1) / gtile;
+  // decode.rs:1041-1046: the partial states (here: waves) must fit the grid
+  const uint64_t waves = spec->partitions * d.num_kv_heads * gtiles;
+  if (spec->partitions > (uint64_t)INT32_MAX || waves / kWaves + 1 > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "single-decode partial states",
+                spec->partitions * d.num_query_heads);
+  auto *p = new loom_single_decode_split_k_plan;
+  p->spec = *spec;
+  p->group_tile = gtile;
+  p->group_tiles = (uint32_t)gtiles;
+  *out = p;
+  return loom::ok(err);
+}
+
+void loom_single_decode_split_k_plan_free(loom_single_decode_split_k_plan_t *p) { delete p; }
+
+uint64_t loom_single_decode_split_k_workspace_bytes(const loom_single_decode_split_k_plan_t *p) {
+  return p ? p->spec.decode.num_query_heads * p->spec.partitions * loom::kStateWidth * 4 : 0;
+}
+
+namespace {
+// decode.rs:1683-1696 checks 4-byte alignment for its packed pairs; these
+// kernels move 16 bytes per lane (Q, K, V) and write 2-byte O elements.
+loom_status_t require_aligned(const char *name, uintptr_t ptr, uintptr_t alignment,
+                              loom_error_t *err) {
+  if (ptr % alignment != 0)
+    return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, name, (int64_t)ptr, (int64_t)alignment);
+  return LOOM_OK;
+}
+}  // namespace
+
+loom_status_t loom_single_decode_enqueue(const loom_single_decode_plan_t *plan,
+                                         loom_command_scope_t *scope,
+                                         const loom_single_decode_args_t *args,
+                                         loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_single_decode_spec_t &s = plan->spec;
+  static const loom::OperandSpec ops[5] = {{"Q", LOOM_DTYPE_BF16, false},
+                                           {"K", LOOM_DTYPE_BF16, false},
+                                           {"V", LOOM_DTYPE_BF16, false},
+                                           {"O", LOOM_DTYPE_BF16, true},
+                                           {"LSE", LOOM_DTYPE_F32, true}};
+  const loom_handle_t hs[5] = {args->query, args->key, args->value, args->output, args->lse};
+  const loom::Lease *l[5];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, 5, l, err);
+  if (rc) return rc;
+  const uint64_t qn = s.num_query_heads * loom::kHeadDim;
+  const uint64_t kvn = s.kv_len * s.num_kv_heads * loom::kHeadDim;
+  const uint64_t want[5] = {qn, kvn, kvn, qn, s.num_query_heads};
+  for (int i = 0; i < 5; ++i)
+    if (l[i]->numel != want[i])
+      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
+  for (int i : {0, 1, 2})
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+  if ((rc = require_aligned("O", l[3]->ptr, 4, err))) return rc;
+  DecodeArgs a = single_args(s, plan->group_tiles, l[0]->ptr, l[1]->ptr, l[2]->ptr, l[3]->ptr,
+                             l[4]->ptr);
+  const dim3 g3((unsigned)(s.num_kv_heads * plan->group_tiles)), b3(kThreads);
+  hipStream_t stream = scope->queue->stream;
+  const int64_t L = (int64_t)s.kv_len;
+  switch (plan->group_tile) {
+    case 1: hipLaunchKernelGGL(single_decode_kernel<1>, g3, b3, 0, stream, a, L); break;
+    case 2: hipLaunchKernelGGL(single_decode_kernel<2>, g3, b3, 0, stream, a, L); break;
+    case 4: hipLaunchKernelGGL(single_decode_kernel<4>, g3, b3, 0, stream, a, L); break;
+    default: hipLaunchKernelGGL(single_decode_kernel<8>, g3, b3, 0, stream, a, L); break;
+  }
+  return loom::record_launch(scope, hipGetLastError(), err);
+}
+
+loom_status_t loom_single_decode_split_k_enqueue(const loom_single_decode_split_k_plan_t *plan,
+                                                 loom_command_scope_t *scope,
+                                                 const loom_single_decode_split_k_args_t *args,
+                                                 loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_single_decode_spec_t &s = plan->spec.decode;
+  // decode.rs:1327: both commands must fit before either is submitted
+  if (scope->submitted + 2 > scope->queue->max_commands)
+    return fail(err, LOOM_CMD_COMMAND_CAPACITY_EXCEEDED, nullptr, scope->queue->max_commands);
+  static const loom::OperandSpec ops[6] = {
+      {"Q", LOOM_DTYPE_BF16, false},        {"K", LOOM_DTYPE_BF16, false},
+      {"V", LOOM_DTYPE_BF16, false},        {"workspace", LOOM_DTYPE_F32, true},
+      {"O", LOOM_DTYPE_BF16, true},         {"LSE", LOOM_DTYPE_F32, true}};
+  const loom_handle_t hs[6] = {args->query, args->key,    args->value,
+                               args->workspace, args->output, args->lse};
+  const loom::Lease *l[6];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, 6, l, err);
+  if (rc) return rc;
+  const uint64_t qn = s.num_query_heads * loom::kHeadDim;
+  const uint64_t kvn = s.kv_len * s.num_kv_heads * loom::kHeadDim;
+  const uint64_t wsn = s.num_query_heads * plan->spec.partitions * loom::kStateWidth;
+  const uint64_t want[6] = {qn, kvn, kvn, wsn, qn, s.num_query_heads};
+  for (int i = 0; i < 6; ++i)
+    if (l[i]->numel != want[i])
+      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
+  for (int i : {0, 1, 2})
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+  if ((rc = require_aligned("workspace", l[3]->ptr, 8, err))) return rc;
+  if ((rc = require_aligned("O", l[4]->ptr, 4, err))) return rc;
+  DecodeArgs a = single_args(s, plan->group_tiles, l[0]->ptr, l[1]->ptr, l[2]->ptr, l[4]->ptr,
+                             l[5]->ptr);
+  float *ws = (float *)l[3]->ptr;
+  const int P = (int)plan->spec.partitions;
+  const uint64_t waves = (uint64_t)P * a.members;
+  const dim3 g3((unsigned)((waves + kWaves - 1) / kWaves)), b3(kThreads);
+  hipStream_t stream = scope->queue->stream;
+  const int64_t L = (int64_t)s.kv_len;
+  switch (plan->group_tile) {
+    case 1: hipLaunchKernelGGL(single_decode_split_k_kernel<1>, g3, b3, 0, stream, a, L, P, ws); break;
+    case 2: hipLaunchKernelGGL(single_decode_split_k_kernel<2>, g3, b3, 0, stream, a, L, P, ws); break;
+    case 4: hipLaunchKernelGGL(single_decode_split_k_kernel<4>, g3, b3, 0, stream, a, L, P, ws); break;
+    default: hipLaunchKernelGGL(single_decode_split_k_kernel<8>, g3, b3, 0, stream, a, L, P, ws); break;
+  }
+  rc = loom::record_launch(scope, hipGetLastError(), err);
+  if (rc) return rc;
+  hipLaunchKernelGGL(single_decode_split_k_merge_kernel, dim3((unsigned)s.num_query_heads),
+                     dim3(128), 0, stream, a, P, (const float *)ws);
+  return loom::record_launch(scope, hipGetLastError(), err);
 }
 
 }  // extern "C"

@@ -571,6 +571,126 @@ class Bf16PagedBatchDecodePlan:
             pass
 
 
+# ---- contiguous single decode -------------------------------------------------
+class Bf16SingleDecodeSpec:
+    """single_decode/mod.rs:15-121: Q/O [Hq, 128], K/V [kv_len, Hkv, 128]."""
+
+    def __init__(self, kv_len, num_query_heads, num_kv_heads, head_dim=HEAD_DIM):
+        self._c = _ffi.SingleDecodeSpec()
+        _call(lib().loom_single_decode_spec_new, kv_len, num_query_heads, num_kv_heads,
+              head_dim, C.byref(self._c))
+
+    kv_len = property(lambda s: s._c.kv_len)
+    num_query_heads = property(lambda s: s._c.num_query_heads)
+    num_kv_heads = property(lambda s: s._c.num_kv_heads)
+    softmax_scale = property(lambda s: s._c.softmax_scale)
+    query_numel = property(lambda s: s.num_query_heads * HEAD_DIM)
+    kv_numel = property(lambda s: s.kv_len * s.num_kv_heads * HEAD_DIM)
+    output_numel = query_numel
+    lse_numel = property(lambda s: s.num_query_heads)
+
+
+class Bf16SingleDecodeSplitKSpec:
+    """single_decode/mod.rs:122-194: balanced contiguous token partitions."""
+
+    def __init__(self, decode: Bf16SingleDecodeSpec, partitions: int):
+        self._c = _ffi.SingleDecodeSplitKSpec()
+        _call(lib().loom_single_decode_split_k_spec_new, C.byref(decode._c), partitions,
+              C.byref(self._c))
+        self.decode = decode
+
+    partitions = property(lambda s: s._c.partitions)
+    partial_state_count = property(lambda s: s.decode.num_query_heads * s.partitions)
+    workspace_numel = property(lambda s: s.partial_state_count * PARTIAL_STATE_WIDTH)
+
+    def partition_token_range(self, partition: int):
+        st, en = C.c_uint64(), C.c_uint64()
+        rc = lib().loom_single_decode_split_k_partition_token_range(
+            C.byref(self._c), partition, C.byref(st), C.byref(en))
+        return None if rc else (st.value, en.value)
+
+
+@dataclass(frozen=True)
+class Bf16SingleDecodeArgs:
+    """decode.rs:1394-1420."""
+    query: Read
+    key: Read
+    value: Read
+    output: Write
+    lse: Write
+
+    def __post_init__(self):
+        c = _ffi.SingleDecodeArgs(*[_h(getattr(self, f)) for f in (
+            "query", "key", "value", "output", "lse")])
+        object.__setattr__(self, "_struct", c)
+        object.__setattr__(self, "_ref", C.byref(c))
+
+
+@dataclass(frozen=True)
+class Bf16SingleDecodeSplitKArgs:
+    """decode.rs:1422-1450 (workspace: ReadWrite<f32> [Hq, partitions, 130])."""
+    query: Read
+    key: Read
+    value: Read
+    workspace: "ReadWrite"
+    output: Write
+    lse: Write
+
+    def __post_init__(self):
+        c = _ffi.SingleDecodeSplitKArgs(*[_h(getattr(self, f)) for f in (
+            "query", "key", "value", "workspace", "output", "lse")])
+        object.__setattr__(self, "_struct", c)
+        object.__setattr__(self, "_ref", C.byref(c))
+
+
+class Bf16SingleDecodePlan:
+    def __init__(self, ptr, spec):
+        self._p = ptr
+        self._spec = spec
+
+    def spec(self):
+        return self._spec
+
+    def enqueue_into(self, scope: CommandScope, args: Bf16SingleDecodeArgs):
+        _enqueue(_ffi.load().loom_single_decode_enqueue, self._p, scope._p, args._ref)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_single_decode_plan_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
+
+
+class Bf16SingleDecodeSplitKPlan:
+    def __init__(self, ptr, spec):
+        self._p = ptr
+        self._spec = spec
+
+    def spec(self):
+        return self._spec
+
+    @property
+    def workspace_required_bytes(self) -> int:
+        return lib().loom_single_decode_split_k_workspace_bytes(self._p)
+
+    @property
+    def workspace_required_numel(self) -> int:
+        return self.workspace_required_bytes // 4
+
+    def enqueue_into(self, scope: CommandScope, args: Bf16SingleDecodeSplitKArgs):
+        _enqueue(_ffi.load().loom_single_decode_split_k_enqueue, self._p, scope._p, args._ref)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_single_decode_split_k_plan_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
+
+
 class DecodeProvider:
     """decode.rs:1001-1104."""
 
@@ -583,6 +703,19 @@ class DecodeProvider:
         out = C.c_void_p()
         _call(lib().loom_decode_provider_load, device, C.byref(out))
         return cls(out.value, device)
+
+    def plan_bf16(self, spec: Bf16SingleDecodeSpec) -> Bf16SingleDecodePlan:
+        """decode.rs:1016-1032."""
+        out = C.c_void_p()
+        _call(lib().loom_decode_provider_plan_bf16, self._p, C.byref(spec._c), C.byref(out))
+        return Bf16SingleDecodePlan(out.value, spec)
+
+    def plan_bf16_split_k(self, spec: Bf16SingleDecodeSplitKSpec) -> Bf16SingleDecodeSplitKPlan:
+        """decode.rs:1034-1064."""
+        out = C.c_void_p()
+        _call(lib().loom_decode_provider_plan_bf16_split_k, self._p, C.byref(spec._c),
+              C.byref(out))
+        return Bf16SingleDecodeSplitKPlan(out.value, spec)
 
     def plan_bf16_paged_batch(self, spec: Bf16PagedBatchDecodeSpec, max_total_pages: int = 0,
                               teams: int = 0):

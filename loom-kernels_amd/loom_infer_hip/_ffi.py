@@ -52,6 +52,23 @@ class PagedDecodeArgs(C.Structure):
                                       "workspace")]
 
 
+class SingleDecodeSpec(C.Structure):
+    _fields_ = [("kv_len", u64), ("num_query_heads", u64), ("num_kv_heads", u64),
+                ("softmax_scale", f32)]
+
+
+class SingleDecodeSplitKSpec(C.Structure):
+    _fields_ = [("decode", SingleDecodeSpec), ("partitions", u64)]
+
+
+class SingleDecodeArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key", "value", "output", "lse")]
+
+
+class SingleDecodeSplitKArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key", "value", "workspace", "output", "lse")]
+
+
 class RopeAppendPlanInfo(C.Structure):
     _fields_ = [("tokens", u64), ("batch_size", u64), ("num_query_heads", u64),
                 ("num_kv_heads", u64), ("explicit_tokens", i32), ("workspace_bytes", u64),
@@ -112,6 +129,18 @@ SIGNATURES = {
     "loom_paged_decode_plan_free": (None, [vp]),
     "loom_paged_decode_plan_get_info": (None, [vp, P(PagedDecodePlanInfo)]),
     "loom_paged_decode_enqueue": (i32, [vp, vp, P(PagedDecodeArgs), E]),
+    "loom_single_decode_spec_new": (i32, [u64] * 4 + [P(SingleDecodeSpec), E]),
+    "loom_single_decode_split_k_spec_new": (
+        i32, [P(SingleDecodeSpec), u64, P(SingleDecodeSplitKSpec), E]),
+    "loom_single_decode_split_k_partition_token_range": (
+        i32, [P(SingleDecodeSplitKSpec), u64, P(u64), P(u64)]),
+    "loom_decode_provider_plan_bf16": (i32, [vp, P(SingleDecodeSpec), P(vp), E]),
+    "loom_single_decode_plan_free": (None, [vp]),
+    "loom_single_decode_enqueue": (i32, [vp, vp, P(SingleDecodeArgs), E]),
+    "loom_decode_provider_plan_bf16_split_k": (i32, [vp, P(SingleDecodeSplitKSpec), P(vp), E]),
+    "loom_single_decode_split_k_plan_free": (None, [vp]),
+    "loom_single_decode_split_k_workspace_bytes": (u64, [vp]),
+    "loom_single_decode_split_k_enqueue": (i32, [vp, vp, P(SingleDecodeSplitKArgs), E]),
     "loom_rope_provider_load": (i32, [C.c_int, P(vp), E]),
     "loom_rope_provider_free": (None, [vp]),
     "loom_rope_provider_plan_bf16_paged_append": (i32, [vp, P(RopeAppendSpec), P(vp), E]),

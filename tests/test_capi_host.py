@@ -190,3 +190,27 @@ def test_command_errors_before_any_device_work(L):
     with pytest.raises(L.CommandError) as e:
         L.CommandQueue(0, 0)
     assert e.value.variant == "ZeroCommandCapacity"
+
+
+def test_single_decode_contracts(L, oracle):
+    # crates/loom-infer/src/attention/single_decode/mod.rs:31-70, :131-181
+    s = L.Bf16SingleDecodeSpec(127, 16, 4)
+    assert (s.kv_len, s.num_query_heads, s.num_kv_heads) == (127, 16, 4)
+    assert (s.query_numel, s.kv_numel, s.lse_numel) == (16 * 128, 127 * 4 * 128, 16)
+    assert s.softmax_scale == np.float32(1.0 / np.sqrt(np.float32(128.0)))
+    for args, variant in [((0, 8, 8), "ZeroDimension"), ((7, 8, 3), "InvalidHeadMapping")]:
+        with pytest.raises(L.ContractError) as e:
+            L.Bf16SingleDecodeSpec(*args)
+        assert e.value.variant == variant
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16SingleDecodeSpec(7, 8, 8, 64)
+    assert e.value.variant == "UnsupportedHeadDimension"
+    for p in (0, 128):
+        with pytest.raises(L.ContractError) as e:
+            L.Bf16SingleDecodeSplitKSpec(s, p)
+        assert (e.value.variant, e.value.fields[:2]) == ("InvalidPartitionCount", (p, 127))
+    for kv_len, parts in [(7, 3), (33, 6), (127, 10), (5, 5), (1, 1)]:
+        sk = L.Bf16SingleDecodeSplitKSpec(L.Bf16SingleDecodeSpec(kv_len, 8, 1), parts)
+        assert sk.workspace_numel == 8 * parts * 130
+        for p in range(parts + 1):
+            assert sk.partition_token_range(p) == oracle.split_k_partition(kv_len, parts, p)
