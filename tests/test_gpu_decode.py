@@ -359,3 +359,23 @@ def test_enqueue_rejections_submit_nothing(L, teams):
     q2 = torch.zeros(s.query_numel + 8, dtype=torch.bfloat16, device=dev)[1:1 + s.query_numel]
     e = attempt(q=q2)
     assert (e.variant, e.operand) == ("MisalignedBuffer", "Q")
+
+
+def test_max_batch_65536(L, oracle):
+    """The largest admitted batch (65536 requests, 256 scan blocks): ragged
+    1..3-page requests, MQA 2/1 heads, teams 0 and 97, against the oracle."""
+    log("decode max batch 65536")
+    rng = np.random.default_rng(65536)
+    B, hq, hkv = 65536, 2, 1
+    lens = rng.integers(1, 49, size=B)
+    pool = int(sum((x + 15) // 16 for x in lens)) + 7
+    indptr, indices, last = ragged_table(rng, list(lens), pool)
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    ref_o, ref_l = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v, indptr,
+                                       indices, last)
+    for teams in (0, 97):
+        r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
+        out, lse = r.run(q, k, v, indptr, indices, last)
+        log(f"  teams={r.plan.info.teams} {compare_decode(oracle, out, lse, ref_o, ref_l)}")
