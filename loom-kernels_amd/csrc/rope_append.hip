@@ -36,7 +36,7 @@ namespace {
 
 constexpr int kValidateThreads = 256;
 constexpr int kApplyThreads = 256;
-constexpr int kIndicesPerValidateBlock = 8192;
+constexpr int kIndicesPerValidateBlock = 2048;  // 8 per thread
 constexpr int kMaxTokens = LOOM_APPEND_MAX_TOKENS_EXTENDED;
 // Workspace: 64 header words ([0] validity, [1] bad accumulator, [2] arrival
 // counter), then the T slot keys (u32) and the T positions (i32).
@@ -120,12 +120,17 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
   int32_t *positions = reinterpret_cast<int32_t *>(keys + a.tokens);
 
   int bad = 0;
+  // this workgroup's page indices: all loads issued before any is tested
   const int64_t lo = (int64_t)blockIdx.x * kIndicesPerValidateBlock;
-  const int64_t hi = min(lo + kIndicesPerValidateBlock, a.n_indices);
-  for (int64_t i = lo + tid; i < hi; i += kValidateThreads) {
-    const int32_t pg = a.indices[i];
-    bad |= (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
+  int32_t pgs[kIndicesPerValidateBlock / kValidateThreads];
+#pragma unroll
+  for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j) {
+    const int64_t i = lo + j * kValidateThreads + tid;
+    pgs[j] = i < a.n_indices ? a.indices[i] : 0;
   }
+#pragma unroll
+  for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j)
+    bad |= (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool) ? 1 : 0;
   const int t = blockIdx.x * kValidateThreads + tid;
   if (t < a.tokens) {
     int r, p, off;
