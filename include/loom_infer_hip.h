@@ -321,8 +321,9 @@ typedef enum loom_paged_decode_algorithm {
    * whole GQA group shares each K/V byte.  Requests that cross a range
    * boundary merge through log2-LSE states in a second kernel. */
   LOOM_PAGED_DECODE_BALANCED_SPLIT_KV = 1,
-  /* Small page capacity (max_total_pages <= 32, teams option 0): one
-   * workgroup per (request, kv-head, tile), one launch, no split. */
+  /* Small page capacity (max_total_pages <= 128, teams option 0): one
+   * workgroup of 4-16 waves per (request, kv-head, tile), one launch, no
+   * split. */
   LOOM_PAGED_DECODE_DIRECT = 2
 } loom_paged_decode_algorithm_t;
 
@@ -330,7 +331,7 @@ typedef enum loom_paged_decode_algorithm {
 typedef struct loom_paged_decode_plan_options {
   uint64_t max_total_pages; /* upper bound of page_indices length; 0 -> max_num_pages */
   uint32_t teams;           /* page ranges; 0 -> chosen for the device (or the direct
-                               algorithm when max_total_pages <= 32) */
+                               algorithm when max_total_pages <= 128) */
   uint32_t reserved;        /* must be zero */
 } loom_paged_decode_plan_options_t;
 

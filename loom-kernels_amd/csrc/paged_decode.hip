@@ -51,7 +51,7 @@ constexpr int kStateStride = 132;
 // Plans whose page capacity is at most this use the direct kernel (one launch,
 // no split): such calls are launch- and latency-bound.
 #ifndef LOOM_DECODE_DIRECT_MAX_PAGES
-#define LOOM_DECODE_DIRECT_MAX_PAGES 32
+#define LOOM_DECODE_DIRECT_MAX_PAGES 128
 #endif
 constexpr int kKRowBytes = 256 + 16;
 #ifndef LOOM_DECODE_DEPTH
@@ -750,21 +750,23 @@ stream_done:
 // LDS, so the request finishes in one launch (no scan, no split states, no
 // merge kernel).  Used when the plan's page capacity is small, where the call
 // is launch- and latency-bound.
-template <int GT>
+template <int GT, int W = kWaves>
 struct DirectSmem {
-  float p[kWaves][GT][16];
-  float alpha[kWaves][GT];
-  uint8_t ktile[kWaves][16 * kKRowBytes];
-  u32x4 qfrag[kWaves][4][64];
-  float wm[kWaves][GT];
-  float wl[kWaves][GT];
-  float wacc[kWaves][GT][128];
+  float p[W][GT][16];
+  float alpha[W][GT];
+  uint8_t ktile[W][16 * kKRowBytes];
+  u32x4 qfrag[W][4][64];
+  float wm[W][GT];
+  float wl[W][GT];
+  float wacc[W][GT][128];
 };
 
-template <int GT>
-__global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_direct_kernel(
+// W waves per workgroup (4 for the tiniest tables; 8 when a request may hold
+// more pages, so each wave streams fewer of them).
+template <int GT, int W>
+__global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direct_kernel(
     DecodeArgs a) {
-  __shared__ DirectSmem<GT> sm;
+  __shared__ DirectSmem<GT, W> sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, quad = lane >> 4;
@@ -784,18 +786,18 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_dir
   const int gcount = min(GT, a.group - g_base);
   WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
                     lane, col, quad, kvh};
-  // this wave's pages: request-local positions wave + 4i
-  const int mine = cnt > wave ? (cnt - wave + kWaves - 1) / kWaves : 0;
+  // this wave's pages: request-local positions wave + W*i
+  const int mine = cnt > wave ? (cnt - wave + W - 1) / W : 0;
   bool bad = false;
   {
     u32x4 qr[4];
     int idx = 0;
-    if (lane < min(mine, 64)) idx = a.indices[st + wave + kWaves * lane];
+    if (lane < min(mine, 64)) idx = a.indices[st + wave + W * lane];
     w.load_q(r, kvh * a.group + g_base, gcount, qr);
     w.store_q(qr);
     w.reset();
     for (int s0 = 0; s0 < mine; s0 += 64) {
-      if (s0 > 0) idx = lane < min(mine - s0, 64) ? a.indices[st + wave + kWaves * (s0 + lane)] : 0;
+      if (s0 > 0) idx = lane < min(mine - s0, 64) ? a.indices[st + wave + W * (s0 + lane)] : 0;
       const int n = min(mine - s0, 64);
       const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
       bad |= __ballot(lane < n && !ok) != 0;
@@ -804,7 +806,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_dir
       };
       auto rows_of = [&](int i) {
         if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
-        return wave + kWaves * (s0 + i) == cnt - 1 ? tl : 16;
+        return wave + W * (s0 + i) == cnt - 1 ? tl : 16;
       };
       w.stream(n, tok_of, rows_of);
     }
@@ -823,18 +825,18 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_dir
   // An invalid page index anywhere in the request keeps its sentinels.
   if (__syncthreads_or(bad)) return;
 
-  // Workgroup merge of the 4 wave states (a wave without pages has max -inf
+  // Workgroup merge of the W wave states (a wave without pages has max -inf
   // and weight 0).
   const int64_t qh_base = (int64_t)kvh * a.group + g_base;
-  for (int idx = tid; idx < GT * 128; idx += kThreads) {
+  for (int idx = tid; idx < GT * 128; idx += W * 64) {
     const int g = idx >> 7, d = idx & 127;
     if (g >= gcount) continue;
     float M = -INFINITY;
 #pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) M = fmaxf(M, sm.wm[wv][g]);
+    for (int wv = 0; wv < W; ++wv) M = fmaxf(M, sm.wm[wv][g]);
     float L = 0.f, O = 0.f;
 #pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) {
+    for (int wv = 0; wv < W; ++wv) {
       const float f = fast_exp2(sm.wm[wv][g] - M);
       L = fmaf(sm.wl[wv][g], f, L);
       O = fmaf(sm.wacc[wv][g][d], f, O);
@@ -1148,6 +1150,9 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "batch_size", B);
 
   if (opt.teams == 0 && max_pages <= LOOM_DECODE_DIRECT_MAX_PAGES) {
+    // More waves per request when a request may hold more pages; 16-wave
+    // workgroups only where the page step fits 128 VGPRs (tiles of <= 2 heads).
+    const uint32_t waves = max_pages <= 32 ? 4 : gtile <= 2 ? 16 : 8;
     const uint64_t grid = B * gtiles * hkv;
     if (grid > (uint64_t)INT32_MAX || B * hq > (uint64_t)INT32_MAX)
       return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged batch-decode", grid);
@@ -1163,7 +1168,7 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
     i.state_slots = 0;
     i.workspace_bytes = 256;  // unused by this algorithm; kept for a uniform operand list
     i.header_bytes = 0;
-    i.block_threads = kThreads;
+    i.block_threads = waves * 64;
     i.grid_blocks = (uint32_t)grid;
     i.device_cus = (uint32_t)provider->dev.cus;
     *out = p;
@@ -1281,11 +1286,26 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   hipStream_t stream = scope->queue->stream;
   const dim3 g3((unsigned)grid), b3(kThreads);
   if (direct) {
-    switch (pi.group_tile) {
-      case 1: hipLaunchKernelGGL(paged_decode_direct_kernel<1>, g3, b3, 0, stream, a); break;
-      case 2: hipLaunchKernelGGL(paged_decode_direct_kernel<2>, g3, b3, 0, stream, a); break;
-      case 4: hipLaunchKernelGGL(paged_decode_direct_kernel<4>, g3, b3, 0, stream, a); break;
-      default: hipLaunchKernelGGL(paged_decode_direct_kernel<8>, g3, b3, 0, stream, a); break;
+    const dim3 bd(pi.block_threads);
+    if (pi.block_threads == 4 * 64) {
+      switch (pi.group_tile) {
+        case 1: hipLaunchKernelGGL((paged_decode_direct_kernel<1, 4>), g3, bd, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((paged_decode_direct_kernel<2, 4>), g3, bd, 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((paged_decode_direct_kernel<4, 4>), g3, bd, 0, stream, a); break;
+        default: hipLaunchKernelGGL((paged_decode_direct_kernel<8, 4>), g3, bd, 0, stream, a); break;
+      }
+    } else if (pi.block_threads == 16 * 64) {
+      if (pi.group_tile == 1)
+        hipLaunchKernelGGL((paged_decode_direct_kernel<1, 16>), g3, bd, 0, stream, a);
+      else
+        hipLaunchKernelGGL((paged_decode_direct_kernel<2, 16>), g3, bd, 0, stream, a);
+    } else {
+      switch (pi.group_tile) {
+        case 1: hipLaunchKernelGGL((paged_decode_direct_kernel<1, 8>), g3, bd, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((paged_decode_direct_kernel<2, 8>), g3, bd, 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((paged_decode_direct_kernel<4, 8>), g3, bd, 0, stream, a); break;
+        default: hipLaunchKernelGGL((paged_decode_direct_kernel<8, 8>), g3, bd, 0, stream, a); break;
+      }
     }
     return loom::record_launch(scope, hipGetLastError(), err);
   }

@@ -68,6 +68,10 @@ SHAPES = [
     ("direct_gqa4", 5, 32, 8, [1, 15, 17, 100, 260], 0),
     ("direct_group16", 3, 16, 1, [33, 200, 7], 0),
     ("direct_mha", 2, 8, 8, [64, 190], 0),
+    ("direct8_gqa4", 3, 32, 8, [500, 33, 700], 0),
+    ("direct16_mha", 2, 8, 8, [900, 1000], 0),
+    ("direct16_group2", 2, 4, 2, [700, 1200], 0),
+    ("direct8_group16", 2, 16, 1, [1500, 17], 0),
     # more requests than the workgroup keeps in LDS: the block-wise search
     ("batch1100_small", 1100, 4, 1, [1 + (i * 37) % 70 for i in range(1100)], 0),
     ("batch1100_teams13", 1100, 8, 2, [1 + (i * 53) % 90 for i in range(1100)], 13),
@@ -125,7 +129,8 @@ def test_invalid_page_guard_preserves_sentinels(L):
     assert np.all(np.isnan(o[4 * 128:])) and np.all(np.isnan(l[4:]))
 
 
-def test_invalid_page_in_split_request(L, oracle):
+@pytest.mark.parametrize("teams", [8, 0], ids=["balanced", "direct"])
+def test_invalid_page_in_split_request(L, oracle, teams):
     """An invalid page inside a request split over several teams leaves that
     request's sentinels and completes the others; the next valid call over the
     poisoned workspace is correct."""
@@ -140,7 +145,7 @@ def test_invalid_page_in_split_request(L, oracle):
     q = seeded_normal_bf16(oracle, rng, B * hq * 128)
     k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
     v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
-    r = DecodeRunner(L, B, pool, hq, hkv, teams=8)
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
     out, lse = r.run(q, k, v, indptr, bad, last)
     o = oracle.bf16_to_f32(out).reshape(B, hq * 128)
     assert np.all(np.isnan(o[0])) and np.all(np.isnan(lse[:hq]))
@@ -292,6 +297,14 @@ def test_plan_selection_and_rejections(L):
     small = L.Bf16PagedBatchDecodeSpec(4, 8, 16, 4, 128, 16)
     p = prov.plan_bf16_paged_batch(small)
     assert p.algorithm == "direct" and p.info.grid_blocks == 4 * 4
+    assert p.info.block_threads == 256
+    mid = L.Bf16PagedBatchDecodeSpec(2, 100, 8, 8, 128, 16)
+    p = prov.plan_bf16_paged_batch(mid)
+    assert p.algorithm == "direct" and p.info.block_threads == 1024  # 16 waves, 1-head tiles
+    p = prov.plan_bf16_paged_batch(L.Bf16PagedBatchDecodeSpec(2, 100, 32, 8, 128, 16))
+    assert p.algorithm == "direct" and p.info.block_threads == 512
+    p = prov.plan_bf16_paged_batch(L.Bf16PagedBatchDecodeSpec(2, 129, 32, 8, 128, 16))
+    assert p.algorithm == "balanced_split_kv"
     p = prov.plan_bf16_paged_batch(small, teams=3)
     assert p.algorithm == "balanced_split_kv" and p.info.teams == 3
     big = L.Bf16PagedBatchDecodeSpec(64, 65536, 32, 8, 128, 16)
