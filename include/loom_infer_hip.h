@@ -327,12 +327,20 @@ typedef enum loom_paged_decode_algorithm {
   LOOM_PAGED_DECODE_DIRECT = 2
 } loom_paged_decode_algorithm_t;
 
+/* Plan flag (no reference counterpart; the reference rejects rebinding and
+ * graph updates, graph/mod.rs:3-6): the page_indices operand is a capacity.
+ * The device guard accepts page_indptr[B] <= len(page_indices) instead of
+ * requiring equality, and entries past page_indptr[B] are ignored, so one
+ * captured graph can be replayed as an engine rewrites the page table in
+ * place between steps (growing sequences, new pages). */
+#define LOOM_PLAN_PAGE_INDICES_CAPACITY 1u
+
 /* Planner inputs.  Zero means "choose for this device". */
 typedef struct loom_paged_decode_plan_options {
   uint64_t max_total_pages; /* upper bound of page_indices length; 0 -> max_num_pages */
   uint32_t teams;           /* page ranges; 0 -> chosen for the device (or the direct
                                algorithm when max_total_pages <= 128) */
-  uint32_t reserved;        /* must be zero */
+  uint32_t flags;           /* 0 or LOOM_PLAN_PAGE_INDICES_CAPACITY */
 } loom_paged_decode_plan_options_t;
 
 typedef struct loom_paged_decode_plan_info {
@@ -348,6 +356,7 @@ typedef struct loom_paged_decode_plan_info {
   uint32_t block_threads;
   uint32_t grid_blocks;
   uint32_t device_cus;
+  uint32_t flags;
 } loom_paged_decode_plan_info_t;
 
 /* DecodeProvider::plan_bf16_paged_batch, decode.rs:1067-1103.  The plan
@@ -495,6 +504,14 @@ loom_status_t loom_rope_provider_plan_bf16_paged_append(const loom_rope_provider
 loom_status_t loom_rope_provider_plan_bf16_paged_append_tokens(
     const loom_rope_provider_t *provider, const loom_rope_append_tokens_spec_t *spec,
     loom_rope_append_plan_t **out, loom_error_t *err);
+/* The same two plans with plan flags (0 or LOOM_PLAN_PAGE_INDICES_CAPACITY;
+ * no reference counterpart). */
+loom_status_t loom_rope_provider_plan_bf16_paged_append_flags(
+    const loom_rope_provider_t *provider, const loom_rope_append_spec_t *spec, uint32_t flags,
+    loom_rope_append_plan_t **out, loom_error_t *err);
+loom_status_t loom_rope_provider_plan_bf16_paged_append_tokens_flags(
+    const loom_rope_provider_t *provider, const loom_rope_append_tokens_spec_t *spec,
+    uint32_t flags, loom_rope_append_plan_t **out, loom_error_t *err);
 void loom_rope_append_plan_free(loom_rope_append_plan_t *plan);
 void loom_rope_append_plan_get_info(const loom_rope_append_plan_t *plan,
                                     loom_rope_append_plan_info_t *info);

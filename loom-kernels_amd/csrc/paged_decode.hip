@@ -104,7 +104,18 @@ struct DecodeArgs {
   int64_t pool;
   int64_t n_indices;
   float scale_log2;
+  // page_indices is a capacity: the global guard accepts indptr[B] <= its
+  // length instead of requiring equality (fixed-address graphs replayed over
+  // changing page tables).
+  int32_t indices_capacity;
 };
+
+// decode.rs:233-246: indptr[B] is the page_indices length (or, for plans made
+// with LOOM_PLAN_PAGE_INDICES_CAPACITY, at most that length).
+__device__ __forceinline__ bool batch_pages_ok(const DecodeArgs &a, int32_t ipB) {
+  return ipB >= 0 && (a.indices_capacity ? (int64_t)ipB <= a.n_indices
+                                         : (int64_t)ipB == a.n_indices);
+}
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -456,7 +467,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
   const int64_t total = carry;
   // Global guard (decode.rs:233-246): the whole batch is rejected, in every
   // workgroup, and the merge kernel is told through the header.
-  const bool batch_ok = ip0 == 0 && ipB >= 0 && (int64_t)ipB == a.n_indices;
+  const bool batch_ok = ip0 == 0 && batch_pages_ok(a, ipB);
   if (blockIdx.x == 0 && tid == 0) {
     a.header[0] = batch_ok ? total : -1;
     a.header[1 + a.batch] = total;
@@ -778,7 +789,7 @@ __global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direc
   // Guards (decode.rs:233-246 global, :430-478 per request), one round trip.
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
   const int32_t st = uni(a.indptr[r]), en = uni(a.indptr[r + 1]), tl = uni(a.last[r]);
-  if (ip0 != 0 || ipB < 0 || (int64_t)ipB != a.n_indices) return;
+  if (ip0 != 0 || !batch_pages_ok(a, ipB)) return;
   const int cnt = request_pages(st, en, tl, ipB);
   if (cnt == 0) return;
 
@@ -1140,7 +1151,8 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   // of two, at most 8 (P·V accumulators are GT x 8 floats per lane).
   const uint32_t gtile = group <= 1 ? 1u : group <= 2 ? 2u : group <= 4 ? 4u : 8u;
   const uint64_t gtiles = (group + gtile - 1) / gtile;
-  if (opt.reserved != 0) return fail(err, LOOM_PLAN_INVALID_OPTION, "reserved", opt.reserved);
+  if (opt.flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
   const uint64_t max_pages = opt.max_total_pages ? opt.max_total_pages : spec->max_num_pages;
   if (max_pages < B) return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
   if (max_pages > (uint64_t)INT32_MAX)
@@ -1171,6 +1183,7 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
     i.block_threads = waves * 64;
     i.grid_blocks = (uint32_t)grid;
     i.device_cus = (uint32_t)provider->dev.cus;
+    i.flags = opt.flags;
     *out = p;
     return loom::ok(err);
   }
@@ -1205,6 +1218,7 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   i.block_threads = kThreads;
   i.grid_blocks = (uint32_t)grid;
   i.device_cus = (uint32_t)provider->dev.cus;
+  i.flags = opt.flags;
   *out = p;
   return loom::ok(err);
 }
@@ -1280,6 +1294,7 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.teams = (int32_t)pi.teams;
   a.pool = (int64_t)s.max_num_pages;
   a.n_indices = (int64_t)l[4]->numel;
+  a.indices_capacity = (pi.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
 
   const uint64_t grid = pi.grid_blocks;

@@ -74,6 +74,9 @@ struct AppendArgs {
   int32_t hkv;
   int64_t pool;
   int64_t n_indices;
+  // page_indices is a capacity (LOOM_PLAN_PAGE_INDICES_CAPACITY): only the
+  // first indptr[B] entries are part of the page table.
+  int32_t indices_capacity;
   float inv_freq[64];
 };
 
@@ -86,12 +89,24 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 // Request and token geometry shared by both kernels.  Returns false for any
 // invalid mapping; on success fills the physical slot.
-__device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int *req, int *pos,
-                                           int64_t *page, int *off) {
+// Entries of page_indices that belong to the page table: all of them, or the
+// first indptr[B] for capacity plans (ipB = indptr[B]).
+__device__ __forceinline__ int64_t table_pages(const AppendArgs &a, int32_t ipB) {
+  return a.indices_capacity ? min<int64_t>(max(ipB, 0), a.n_indices) : a.n_indices;
+}
+// rope/mod.rs:143-150 and paged_decode/mod.rs:164-170: indptr[0] = 0 and
+// indptr[B] = len(page_indices) (<= for capacity plans).
+__device__ __forceinline__ bool table_bounds_bad(const AppendArgs &a, int32_t ip0, int32_t ipB) {
+  return ip0 != 0 || ipB < 0 ||
+         (a.indices_capacity ? (int64_t)ipB > a.n_indices : (int64_t)ipB != a.n_indices);
+}
+
+__device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t pages, int *req,
+                                           int *pos, int64_t *page, int *off) {
   const int r = a.batch_indices ? a.batch_indices[t] : t;
   if (r < 0 || r >= a.batch) return false;
   const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
-  if (st < 0 || en <= st || (int64_t)en > a.n_indices || tl < 1 || tl > 16) return false;
+  if (st < 0 || en <= st || (int64_t)en > pages || tl < 1 || tl > 16) return false;
   const int kv_len = (en - st - 1) * 16 + tl;
   const int p = a.batch_indices ? a.positions[t] : kv_len - 1;
   if (p < 0 || p >= kv_len) return false;
@@ -121,6 +136,7 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
 
   int bad = 0;
   // this workgroup's page indices: all loads issued before any is tested
+  const int32_t ipB = a.indptr[a.batch];
   const int64_t lo = (int64_t)blockIdx.x * kIndicesPerValidateBlock;
   int32_t pgs[kIndicesPerValidateBlock / kValidateThreads];
 #pragma unroll
@@ -128,15 +144,17 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
     const int64_t i = lo + j * kValidateThreads + tid;
     pgs[j] = i < a.n_indices ? a.indices[i] : 0;
   }
+  const int64_t pages = table_pages(a, ipB);
 #pragma unroll
   for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j)
-    bad |= (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool) ? 1 : 0;
+    bad |= (lo + j * kValidateThreads + tid < pages &&
+            (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool)) ? 1 : 0;
   const int t = blockIdx.x * kValidateThreads + tid;
   if (t < a.tokens) {
     int r, p, off;
     int64_t pg;
     uint32_t key = kEmptyKey;
-    if (token_slot(a, t, &r, &p, &pg, &off))
+    if (token_slot(a, t, pages, &r, &p, &pg, &off))
       key = (uint32_t)(pg * 16 + off);
     else
       bad = 1;
@@ -156,7 +174,7 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
 
   // Last workgroup: the request table, then duplicate slots.
   bad = 0;
-  if (tid == 0) bad |= (a.indptr[0] != 0 || (int64_t)a.indptr[a.batch] != a.n_indices);
+  if (tid == 0) bad |= table_bounds_bad(a, a.indptr[0], a.indptr[a.batch]) ? 1 : 0;
   for (int r = tid; r < a.batch; r += kValidateThreads) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
     bad |= (en <= st || tl < 1 || tl > 16) ? 1 : 0;
@@ -312,14 +330,16 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
   const RowSlice first = load_first_slice(a, t, tid);
 
   int bad = 0;
+  const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
+  const int64_t pages = table_pages(a, ipB);
   // page indices (rope/mod.rs:143-150)
 #pragma unroll 4
-  for (int64_t i = tid; i < a.n_indices; i += kApplyThreads) {
+  for (int64_t i = tid; i < pages; i += kApplyThreads) {
     const int32_t pg = a.indices[i];
     bad |= (pg < 0 || (int64_t)pg >= a.pool) ? 1 : 0;
   }
   // request table (paged_decode/mod.rs:164-205)
-  if (tid == 0) bad |= (a.indptr[0] != 0 || (int64_t)a.indptr[a.batch] != a.n_indices);
+  if (tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
   for (int r = tid; r < a.batch; r += kApplyThreads) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
     bad |= (en <= st || tl < 1 || tl > 16) ? 1 : 0;
@@ -329,7 +349,7 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
     int r, p, off;
     int64_t pg;
     uint32_t key = 0xffffffffu;
-    if (token_slot(a, tid, &r, &p, &pg, &off))
+    if (token_slot(a, tid, pages, &r, &p, &pg, &off))
       key = (uint32_t)(pg * 16 + off);
     else
       bad = 1;
@@ -360,6 +380,7 @@ struct loom_rope_provider {
 struct loom_rope_append_plan {
   loom_rope_append_plan_info_t info;
   uint64_t max_num_pages = 0;
+  uint32_t flags = 0;
   float inv_freq[64];
 };
 
@@ -380,8 +401,10 @@ loom_status_t loom_rope_provider_load(int device, loom_rope_provider_t **out, lo
 void loom_rope_provider_free(loom_rope_provider_t *p) { delete p; }
 
 static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t tokens,
-                               bool explicit_tokens, loom_rope_append_plan_t **out,
-                               loom_error_t *err) {
+                               bool explicit_tokens, uint32_t flags,
+                               loom_rope_append_plan_t **out, loom_error_t *err) {
+  if (flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
   // rope/mod.rs:628-682: states = tokens * (Hq + Hkv) must fit the grid.
   uint64_t rows = s.num_query_heads + s.num_kv_heads, states;
   if (rows < s.num_query_heads || __builtin_mul_overflow(tokens, rows, &states))
@@ -400,6 +423,7 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
   p->info.workspace_bytes = (kWsHeaderWords + 2 * tokens) * 4;
   p->info.validate_blocks = 0;  // depends on the bound page_indices length
   p->max_num_pages = s.max_num_pages;
+  p->flags = flags;
   // rope/mod.rs:148-149 with rope_scale = 1, rope_theta = 1e4, rotary_dim = 128
   // (paged_append/mod.rs:395-403): the reference's exact FP32 inverse frequencies.
   for (int i = 0; i < 64; ++i) {
@@ -415,14 +439,28 @@ loom_status_t loom_rope_provider_plan_bf16_paged_append(const loom_rope_provider
                                                         loom_rope_append_plan_t **out,
                                                         loom_error_t *err) {
   if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
-  return make_plan(spec->paged, spec->paged.batch_size, false, out, err);
+  return make_plan(spec->paged, spec->paged.batch_size, false, 0, out, err);
+}
+
+loom_status_t loom_rope_provider_plan_bf16_paged_append_flags(
+    const loom_rope_provider_t *provider, const loom_rope_append_spec_t *spec, uint32_t flags,
+    loom_rope_append_plan_t **out, loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  return make_plan(spec->paged, spec->paged.batch_size, false, flags, out, err);
 }
 
 loom_status_t loom_rope_provider_plan_bf16_paged_append_tokens(
     const loom_rope_provider_t *provider, const loom_rope_append_tokens_spec_t *spec,
     loom_rope_append_plan_t **out, loom_error_t *err) {
   if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
-  return make_plan(spec->paged, spec->tokens, true, out, err);
+  return make_plan(spec->paged, spec->tokens, true, 0, out, err);
+}
+
+loom_status_t loom_rope_provider_plan_bf16_paged_append_tokens_flags(
+    const loom_rope_provider_t *provider, const loom_rope_append_tokens_spec_t *spec,
+    uint32_t flags, loom_rope_append_plan_t **out, loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  return make_plan(spec->paged, spec->tokens, true, flags, out, err);
 }
 
 void loom_rope_append_plan_free(loom_rope_append_plan_t *p) { delete p; }
@@ -508,6 +546,7 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   a.hkv = (int32_t)hkv;
   a.pool = (int64_t)plan->max_num_pages;
   a.n_indices = (int64_t)L(6)->numel;
+  a.indices_capacity = (plan->flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
   for (int i = 0; i < 64; ++i) a.inv_freq[i] = plan->inv_freq[i];
 
   const uint64_t vblocks = std::max<uint64_t>(

@@ -33,6 +33,7 @@ from . import _ffi
 HEAD_DIM = 128
 PAGE_SIZE = 16
 PARTIAL_STATE_WIDTH = 130
+PLAN_PAGE_INDICES_CAPACITY = 1
 ROPE_PAGED_KV_APPEND_MAX_TOKENS = 64
 ROPE_PAGED_KV_APPEND_MAX_TOKENS_EXTENDED = 8192
 
@@ -718,9 +719,11 @@ class DecodeProvider:
         return Bf16SingleDecodeSplitKPlan(out.value, spec)
 
     def plan_bf16_paged_batch(self, spec: Bf16PagedBatchDecodeSpec, max_total_pages: int = 0,
-                              teams: int = 0):
-        """`teams` = number of equal page ranges (0: one wave per SIMD slot)."""
-        opt = _ffi.PagedDecodePlanOptions(max_total_pages, teams, 0)
+                              teams: int = 0, indices_capacity: bool = False):
+        """`teams` = number of equal page ranges (0: chosen for the device);
+        `indices_capacity`: page_indices is a capacity (LOOM_PLAN_PAGE_INDICES_CAPACITY)."""
+        opt = _ffi.PagedDecodePlanOptions(max_total_pages, teams,
+                                          PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0)
         out = C.c_void_p()
         _call(lib().loom_decode_provider_plan_bf16_paged_batch, self._p, C.byref(spec._c),
               C.byref(opt), C.byref(out))
@@ -812,16 +815,19 @@ class RopeProvider:
         _call(lib().loom_rope_provider_load, device, C.byref(out))
         return cls(out.value, device)
 
-    def plan_bf16_paged_append(self, spec: Bf16RopePagedKvAppendSpec):
+    def plan_bf16_paged_append(self, spec: Bf16RopePagedKvAppendSpec,
+                               indices_capacity: bool = False):
         out = C.c_void_p()
-        _call(lib().loom_rope_provider_plan_bf16_paged_append, self._p, C.byref(spec._c),
-              C.byref(out))
+        _call(lib().loom_rope_provider_plan_bf16_paged_append_flags, self._p, C.byref(spec._c),
+              PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0, C.byref(out))
         return Bf16RopePagedKvAppendPlan(out.value, spec)
 
-    def plan_bf16_paged_append_tokens(self, spec: Bf16RopePagedKvAppendTokensSpec):
+    def plan_bf16_paged_append_tokens(self, spec: Bf16RopePagedKvAppendTokensSpec,
+                                      indices_capacity: bool = False):
         out = C.c_void_p()
-        _call(lib().loom_rope_provider_plan_bf16_paged_append_tokens, self._p,
-              C.byref(spec._c), C.byref(out))
+        _call(lib().loom_rope_provider_plan_bf16_paged_append_tokens_flags, self._p,
+              C.byref(spec._c), PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0,
+              C.byref(out))
         return Bf16RopePagedKvAppendPlan(out.value, spec)
 
     def __del__(self):

@@ -36,14 +36,15 @@ class Handle(C.Structure):
 
 
 class PagedDecodePlanOptions(C.Structure):
-    _fields_ = [("max_total_pages", u64), ("teams", u32), ("reserved", u32)]
+    _fields_ = [("max_total_pages", u64), ("teams", u32), ("flags", u32)]
 
 
 class PagedDecodePlanInfo(C.Structure):
     _fields_ = [("spec", PagedDecodeSpec), ("algorithm", i32), ("teams", u32),
                 ("group_tile", u32), ("group_tiles", u32), ("max_total_pages", u64),
                 ("state_slots", u64), ("workspace_bytes", u64), ("header_bytes", u64),
-                ("block_threads", u32), ("grid_blocks", u32), ("device_cus", u32)]
+                ("block_threads", u32), ("grid_blocks", u32), ("device_cus", u32),
+                ("flags", u32)]
 
 
 class PagedDecodeArgs(C.Structure):
@@ -146,6 +147,10 @@ SIGNATURES = {
     "loom_rope_provider_plan_bf16_paged_append": (i32, [vp, P(RopeAppendSpec), P(vp), E]),
     "loom_rope_provider_plan_bf16_paged_append_tokens": (
         i32, [vp, P(RopeAppendTokensSpec), P(vp), E]),
+    "loom_rope_provider_plan_bf16_paged_append_flags": (
+        i32, [vp, P(RopeAppendSpec), u32, P(vp), E]),
+    "loom_rope_provider_plan_bf16_paged_append_tokens_flags": (
+        i32, [vp, P(RopeAppendTokensSpec), u32, P(vp), E]),
     "loom_rope_append_plan_free": (None, [vp]),
     "loom_rope_append_plan_get_info": (None, [vp, P(RopeAppendPlanInfo)]),
     "loom_rope_append_enqueue": (i32, [vp, vp, P(RopeAppendArgs), E]),

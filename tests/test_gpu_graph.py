@@ -141,3 +141,91 @@ def test_full_decode_step_graph(L, oracle):
         else:
             assert np.array_equal(o, first[0]) and np.array_equal(l, first[1])
     exec_.into_bindings()
+
+
+@pytest.mark.parametrize("cap", [200, 5000], ids=["fused_append", "two_kernel_append"])
+def test_serving_loop_replays_one_graph_over_changing_page_tables(L, oracle, cap):
+    """A decode step graph (one-token RoPE append + paged decode) captured once
+    and replayed over 8 steps while the page table is rewritten in place:
+    every request grows by one token per step and takes a new page when its
+    last one fills.  The plans are made with LOOM_PLAN_PAGE_INDICES_CAPACITY,
+    so the fixed page_indices buffer is a capacity and the entries past
+    indptr[B] (left as garbage) are ignored.  Each replay is checked against
+    the oracle's append + decode on host copies of the pools."""
+    import torch
+    log("graph serving loop with page-table updates")
+    rng = np.random.default_rng(808)
+    B, hq, hkv, pool = 4, 32, 8, 320
+    lens = np.array([40, 15, 100, 64])
+    free = list(rng.permutation(pool))
+    pages = [[int(free.pop()) for _ in range((n + 15) // 16)] for n in lens]
+
+    def table():
+        indptr = np.concatenate([[0], np.cumsum([len(p) for p in pages])]).astype(np.int32)
+        indices = np.concatenate(pages).astype(np.int32)
+        last = np.array([n - (len(p) - 1) * 16 for n, p in zip(lens, pages)], np.int32)
+        return indptr, indices, last
+
+    kp_h = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    vp_h = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    dev = "cuda"
+    t_kp, t_vp = to_dev_bf16(kp_h), to_dev_bf16(vp_h)
+    t_ip = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+    t_ix = torch.full((cap,), -7, dtype=torch.int32, device=dev)
+    t_ln = torch.zeros(B, dtype=torch.int32, device=dev)
+    t_q = torch.zeros(B * hq * 128, dtype=torch.bfloat16, device=dev)
+    t_k = torch.zeros(B * hkv * 128, dtype=torch.bfloat16, device=dev)
+    t_v = torch.zeros(B * hkv * 128, dtype=torch.bfloat16, device=dev)
+    qrot = torch.empty(B * hq * 128, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(B * hq * 128, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B * hq, dtype=torch.float32, device=dev)
+    dspec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, 128, 16)
+    dplan = L.DecodeProvider.load(0).plan_bf16_paged_batch(dspec, max_total_pages=cap,
+                                                           indices_capacity=True)
+    aplan = L.RopeProvider.load(0).plan_bf16_paged_append(
+        L.Bf16RopePagedKvAppendSpec(B, pool, hq, hkv), indices_capacity=True)
+    dws = torch.zeros(dplan.workspace_bytes, dtype=torch.uint8, device=dev)
+    aws = torch.zeros(aplan.workspace_bytes, dtype=torch.uint8, device=dev)
+    gq = L.GraphQueue(0, 2)
+    b = gq.bindings(16)
+    hqn, hk, hv = b.bind_read(t_q), b.bind_read(t_k), b.bind_read(t_v)
+    hip_, hix, hln = b.bind_read(t_ip), b.bind_read(t_ix), b.bind_read(t_ln)
+    hqr, hkp, hvp = b.bind_read_write(qrot), b.bind_read_write(t_kp), b.bind_read_write(t_vp)
+    hws_a, ho, hl = b.bind_read_write(aws), b.bind_read_write(out), b.bind_read_write(lse)
+    hws_d = b.bind_read_write(dws)
+    a_args = L.Bf16RopePagedKvAppendArgs(hqn, hk, hv, hip_, hix, hln, hqr.write(), hkp.write(),
+                                         hvp.write(), hws_a.write())
+    d_args = L.Bf16PagedBatchDecodeArgs(hqr.read(), hkp.read(), hvp.read(), hip_, hix, hln,
+                                        ho.write(), hl.write(), hws_d.write())
+
+    def record(scope):
+        aplan.enqueue_into(scope, a_args)
+        dplan.enqueue_into(scope, d_args)
+
+    exec_ = gq.capture(b, record).instantiate()
+    s = oracle.paged_spec(B, pool, hq, hkv)
+    for step in range(8):
+        lens += 1
+        for r in range(B):
+            if (lens[r] + 15) // 16 > len(pages[r]):
+                pages[r].append(int(free.pop()))
+        indptr, indices, last = table()
+        qn = seeded_normal_bf16(oracle, rng, B * hq * 128)
+        kn = seeded_normal_bf16(oracle, rng, B * hkv * 128)
+        vn = seeded_normal_bf16(oracle, rng, B * hkv * 128)
+        # rewrite the metadata and token inputs in place (fixed addresses)
+        t_ip.copy_(torch.from_numpy(indptr))
+        t_ix[: len(indices)].copy_(torch.from_numpy(indices))
+        t_ix[len(indices):].fill_(-7)
+        t_ln.copy_(torch.from_numpy(last))
+        t_q.copy_(to_dev_bf16(qn))
+        t_k.copy_(to_dev_bf16(kn))
+        t_v.copy_(to_dev_bf16(vn))
+        torch.cuda.synchronize()
+        exec_.launch().wait()
+        eq = oracle.append(s, qn, kn, vn, indptr, indices, last, kp_h, vp_h)  # updates pools
+        ref_o, ref_l = oracle.paged_decode(s, eq, kp_h, vp_h, indptr, indices, last)
+        st = compare_decode(oracle, bf16_host(out), lse.cpu().numpy(), ref_o, ref_l)
+        log(f"  step {step}: lens {lens.tolist()} pages {len(indices)} {st}")
+    assert np.array_equal(bf16_host(t_vp), vp_h)
+    exec_.into_bindings()
