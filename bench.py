@@ -425,6 +425,36 @@ def reference_shapes(L, stream, samples=30):
     return out
 
 
+def cpu_append_baseline(app, min_s=3.0):
+    """The oracle's explicit-token append (rope/mod.rs + paged_append/mod.rs:
+    429-489, single thread) on the config-2 command, repeated for at least
+    `min_s`.  Pages no token writes are renumbered onto one shared page so the
+    host pools hold only the touched pages (the work per token is unchanged)."""
+    import numpy as np
+    import torch
+    import oracle as O
+    indptr, indices, last = (np.asarray(x) for x in app.tables)
+    bi = app.bi.cpu().numpy()
+    pos = app.pos.cpu().numpy()
+    touched = sorted({int(indices[indptr[r] + p // 16]) for r, p in zip(bi, pos)})
+    remap = {pg: i + 1 for i, pg in enumerate(touched)}
+    idx2 = np.array([remap.get(int(x), 0) for x in indices], np.int32)
+    pool = len(touched) + 1
+    s = O.paged_spec(app.B, pool, app.hq, app.hkv)
+    q, k, v = (t.view(torch.int16).cpu().numpy().view(np.uint16) for t in (app.q, app.k, app.v))
+    kp = np.zeros(pool * 16 * app.hkv * 128, np.uint16)
+    vp = np.zeros_like(kp)
+    calls, t_total = 0, 0.0
+    while t_total < min_s:
+        t0 = time.perf_counter()
+        O.append_tokens(s, app.T, q, k, v, bi, pos, indptr, idx2, last, kp, vp, max_tokens=8192)
+        t_total += time.perf_counter() - t0
+        calls += 1
+    return {"value": round(t_total / calls * 1e6, 1), "unit": "us/call", "cores": 1,
+            "kind": "port", "sample": f"{calls} whole config-2 commands ({app.T} tokens), "
+                                      f"{t_total:.1f} s, single thread"}
+
+
 def make_cases(L, quick=False):
     import numpy as np
     rng = np.random.default_rng(2026)
@@ -546,6 +576,8 @@ def main():
             "cold_us_per_call": round(cold, 3),
             "tokens": app.T, "algorithmic_bytes": app.bytes,
             "GBps": round(app.bytes / (ap_us * 1e-6) / 1e9, 1)}
+        if not a.no_cpu:
+            detail["c2_rope_append_b32_tokens"]["cpu_baseline"] = cpu_append_baseline(app)
         log(f"[bench] c2: {detail['c2_rope_append_b32_tokens']}")
         del app
     if not a.quick and (not a.only or a.only == "ref"):
