@@ -55,6 +55,12 @@ class PagedSpec(C.Structure):
                 ("softmax_scale", C.c_float)]
 
 
+class PrefillSpec(C.Structure):
+    _fields_ = [("batch_size", C.c_size_t), ("nnz_qo", C.c_size_t),
+                ("max_num_pages", C.c_size_t), ("num_query_heads", C.c_size_t),
+                ("num_kv_heads", C.c_size_t), ("softmax_scale", C.c_float)]
+
+
 class SingleSpec(C.Structure):
     _fields_ = [("kv_len", C.c_size_t), ("num_query_heads", C.c_size_t),
                 ("num_kv_heads", C.c_size_t), ("softmax_scale", C.c_float)]
@@ -81,6 +87,7 @@ def lib():
         _lib.lo_digest_f32.restype = C.c_uint64
         _lib.lo_deterministic_bf16.argtypes = [C.c_size_t, C.c_uint64, C.c_void_p]
         _lib.lo_paged_request_kv_len.restype = C.c_int64
+        _lib.lo_prefill_causal_kv_end.restype = C.c_int64
     return _lib
 
 
@@ -186,6 +193,56 @@ def paged_decode_requests(spec, q, k, v, indptr, indices, last, r0, r1, out, lse
     lib().lo_paged_decode_requests(C.byref(spec), _p(q), _p(k), _p(v), _p(indptr),
                                    _p(indices), _p(last), C.c_size_t(r0), C.c_size_t(r1),
                                    _p(out), _p(lse))
+
+
+# ---- paged causal prefill --------------------------------------------------
+def prefill_spec(batch, nnz_qo, pool, hq, hkv, head_dim=128, page_size=16) -> PrefillSpec:
+    s, e = PrefillSpec(), _Err()
+    _check(lib().lo_prefill_spec_new(*(C.c_size_t(x) for x in (batch, nnz_qo, pool, hq, hkv,
+                                                                 head_dim, page_size)),
+                                     C.byref(s), C.byref(e)), e)
+    return s
+
+
+def prefill_validate(spec, qo_indptr, indptr, indices, last):
+    qo_indptr, indptr, indices, last = (_i32(x) for x in (qo_indptr, indptr, indices, last))
+    e = _Err()
+    _check(lib().lo_prefill_validate(C.byref(spec), _p(qo_indptr), C.c_size_t(qo_indptr.size),
+                                     _p(indptr), C.c_size_t(indptr.size), _p(indices),
+                                     C.c_size_t(indices.size), _p(last),
+                                     C.c_size_t(last.size), C.byref(e)), e)
+
+
+def prefill_causal_kv_end(spec, qo_indptr, indptr, last, request, query_index):
+    qo_indptr, indptr, last = (_i32(x) for x in (qo_indptr, indptr, last))
+    r = lib().lo_prefill_causal_kv_end(C.byref(spec), _p(qo_indptr), _p(indptr), _p(last),
+                                       C.c_size_t(request), C.c_size_t(query_index))
+    return None if r < 0 else int(r)
+
+
+def prefill(spec, q, k, v, qo_indptr, indptr, indices, last):
+    """Returns (out bf16 bits [nnz_qo,Hq,128], lse f32 [nnz_qo,Hq]); raises OracleError."""
+    qo_indptr, indptr, indices, last = (_i32(x) for x in (qo_indptr, indptr, indices, last))
+    q, k, v = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v))
+    nq = spec.nnz_qo * spec.num_query_heads * HEAD_DIM
+    out = np.full(nq, 0x7FC0, dtype=np.uint16)
+    lse = np.full(spec.nnz_qo * spec.num_query_heads, np.nan, dtype=np.float32)
+    e = _Err()
+    _check(lib().lo_prefill_reference(
+        C.byref(spec), _p(q), C.c_size_t(q.size), _p(k), C.c_size_t(k.size), _p(v),
+        C.c_size_t(v.size), _p(qo_indptr), C.c_size_t(qo_indptr.size), _p(indptr),
+        C.c_size_t(indptr.size), _p(indices), C.c_size_t(indices.size), _p(last),
+        C.c_size_t(last.size), _p(out), C.c_size_t(out.size), _p(lse), C.c_size_t(lse.size),
+        C.byref(e)), e)
+    return out, lse
+
+
+def prefill_requests(spec, q, k, v, qo_indptr, indptr, indices, last, r0, r1, out, lse):
+    """Restated loop over requests [r0, r1) (used for the bounded CPU baseline)."""
+    qo_indptr, indptr, indices, last = (_i32(x) for x in (qo_indptr, indptr, indices, last))
+    lib().lo_prefill_requests(C.byref(spec), _p(q), _p(k), _p(v), _p(qo_indptr), _p(indptr),
+                              _p(indices), _p(last), C.c_size_t(r0), C.c_size_t(r1),
+                              _p(out), _p(lse))
 
 
 # ---- single decode / split-K ----------------------------------------------

@@ -559,3 +559,153 @@ int lo_append_tokens_reference(const lo_paged_spec *s, size_t tokens, size_t max
   free(slots);
   return rc;
 }
+
+/* ------------------------------------------------------------------------ */
+/* paged_prefill/mod.rs:30-91 Bf16PagedPrefillSpec::new. */
+int lo_prefill_spec_new(size_t batch, size_t nnz_qo, size_t pool, size_t hq, size_t hkv,
+                        size_t head_dim, size_t page_size, lo_prefill_spec *out,
+                        lo_error *err) {
+  if (batch == 0 || nnz_qo == 0 || pool == 0 || hq == 0 || hkv == 0 || head_dim == 0 ||
+      page_size == 0)
+    return fail(err, LO_ZERO_DIMENSION, NULL, 0, 0, 0, 0);
+  if (head_dim != HEAD_DIM)
+    return fail(err, LO_UNSUPPORTED_HEAD_DIMENSION, NULL, HEAD_DIM, (int64_t)head_dim, 0, 0);
+  if (page_size != PAGE_SIZE)
+    return fail(err, LO_UNSUPPORTED_PAGE_SIZE, NULL, PAGE_SIZE, (int64_t)page_size, 0, 0);
+  if (hq % hkv != 0)
+    return fail(err, LO_INVALID_HEAD_MAPPING, NULL, (int64_t)hq, (int64_t)hkv, 0, 0);
+  if (nnz_qo > (size_t)INT32_MAX) return fail(err, LO_ELEMENT_COUNT_OVERFLOW, NULL, 0, 0, 0, 0);
+  size_t t;
+  if (batch == SIZE_MAX || mul_overflows(nnz_qo, hq, &t) || mul_overflows(t, head_dim, &t))
+    return fail(err, LO_ELEMENT_COUNT_OVERFLOW, NULL, 0, 0, 0, 0);
+  if (mul_overflows(pool, page_size, &t) || mul_overflows(t, hkv, &t) ||
+      mul_overflows(t, head_dim, &t))
+    return fail(err, LO_ELEMENT_COUNT_OVERFLOW, NULL, 0, 0, 0, 0);
+  out->batch_size = batch;
+  out->nnz_qo = nnz_qo;
+  out->max_num_pages = pool;
+  out->num_query_heads = hq;
+  out->num_kv_heads = hkv;
+  out->softmax_scale = 1.0f / sqrtf((float)head_dim);
+  return LO_OK;
+}
+
+/* paged_prefill/mod.rs:161-274 validate_metadata and validate_query_indptr. */
+int lo_prefill_validate(const lo_prefill_spec *s, const int32_t *qo, size_t n_qo,
+                        const int32_t *indptr, size_t n_indptr, const int32_t *indices,
+                        size_t n_indices, const int32_t *last, size_t n_last, lo_error *err) {
+  int rc;
+  const size_t B = s->batch_size;
+  if ((rc = require_len(err, "qo_indptr", n_qo, B + 1))) return rc;
+  if ((rc = require_len(err, "page_indptr", n_indptr, B + 1))) return rc;
+  if ((rc = require_len(err, "last_page_len", n_last, B))) return rc;
+  if (qo[0] != 0) return fail(err, LO_INVALID_INDPTR_START, "qo_indptr", qo[0], 0, 0, 0);
+  for (size_t r = 0; r < B; ++r) {
+    if (qo[r + 1] < qo[r])
+      return fail(err, LO_NON_MONOTONIC_INDPTR, "qo_indptr", (int64_t)r, qo[r], qo[r + 1], 0);
+    if (qo[r + 1] == qo[r]) return fail(err, LO_EMPTY_RAGGED_REQUEST, "qo_indptr", (int64_t)r,
+                                        0, 0, 0);
+  }
+  if ((rc = require_len(err, "qo_indptr", (size_t)qo[B], s->nnz_qo))) return rc;
+  if (indptr[0] != 0) return fail(err, LO_INVALID_PAGE_INDPTR_START, NULL, indptr[0], 0, 0, 0);
+  for (size_t r = 0; r < B; ++r) {
+    int32_t start = indptr[r], end = indptr[r + 1];
+    if (end < start)
+      return fail(err, LO_NON_MONOTONIC_PAGE_INDPTR, NULL, (int64_t)r, start, end, 0);
+    if (end == start) return fail(err, LO_EMPTY_PAGED_REQUEST, NULL, (int64_t)r, 0, 0, 0);
+    int32_t tail = last[r];
+    if (tail < 1 || tail > (int32_t)PAGE_SIZE)
+      return fail(err, LO_INVALID_LAST_PAGE_LENGTH, NULL, (int64_t)r, tail, PAGE_SIZE, 0);
+    int64_t qo_len = (int64_t)qo[r + 1] - qo[r];
+    int64_t kv_len = ((int64_t)end - start - 1) * (int64_t)PAGE_SIZE + tail;
+    if (qo_len > kv_len)
+      return fail(err, LO_RAGGED_QUERY_LONGER_THAN_KV, NULL, (int64_t)r, qo_len, kv_len, 0);
+  }
+  if ((rc = require_len(err, "page_indices", n_indices, (size_t)indptr[B]))) return rc;
+  for (size_t p = 0; p < n_indices; ++p) {
+    int32_t idx = indices[p];
+    if (idx < 0 || (size_t)idx >= s->max_num_pages)
+      return fail(err, LO_PAGE_INDEX_OUT_OF_RANGE, NULL, (int64_t)p, idx,
+                  (int64_t)s->max_num_pages, 0);
+  }
+  return LO_OK;
+}
+
+/* paged_prefill/mod.rs:374-383: kv_len - qo_len + query_index + 1. */
+int64_t lo_prefill_causal_kv_end(const lo_prefill_spec *s, const int32_t *qo,
+                                 const int32_t *indptr, const int32_t *last, size_t request,
+                                 size_t query_index) {
+  if (request >= s->batch_size) return -1;
+  int64_t qo_len = (int64_t)qo[request + 1] - qo[request];
+  if ((int64_t)query_index >= qo_len) return -1;
+  int64_t kv_len = lo_paged_request_kv_len(indptr, last, s->batch_size, request);
+  return kv_len - qo_len + (int64_t)query_index + 1;
+}
+
+/* paged_prefill/mod.rs:405-446: per (query row, query head), the online
+ * softmax over the causal KV prefix, in the natural-log domain; LSE is
+ * converted to log2 at the end. */
+void lo_prefill_requests(const lo_prefill_spec *s, const uint16_t *q, const uint16_t *k,
+                         const uint16_t *v, const int32_t *qo, const int32_t *indptr,
+                         const int32_t *indices, const int32_t *last, size_t r0, size_t r1,
+                         uint16_t *out, float *lse) {
+  const size_t hq = s->num_query_heads, hkv = s->num_kv_heads, group = hq / hkv;
+  float state[HEAD_DIM];
+  for (size_t r = r0; r < r1; ++r) {
+    const size_t page_start = (size_t)indptr[r];
+    for (size_t row = (size_t)qo[r]; row < (size_t)qo[r + 1]; ++row) {
+      const int64_t end =
+          lo_prefill_causal_kv_end(s, qo, indptr, last, r, row - (size_t)qo[r]);
+      for (size_t h = 0; h < hq; ++h) {
+        const uint16_t *qrow = q + (row * hq + h) * HEAD_DIM;
+        const size_t kvh = h / group;
+        float max_score = 0.0f, normalizer = 0.0f;
+        memset(state, 0, sizeof(state));
+        for (int64_t t = 0; t < end; ++t) {
+          size_t page = (size_t)indices[page_start + (size_t)t / PAGE_SIZE];
+          size_t kv_off = ((page * PAGE_SIZE + (size_t)t % PAGE_SIZE) * hkv + kvh) * HEAD_DIM;
+          float score = dot_bf16(qrow, k + kv_off) * s->softmax_scale;
+          if (t == 0) {
+            max_score = score;
+            normalizer = 1.0f;
+            for (unsigned c = 0; c < HEAD_DIM; ++c) state[c] = lo_bf16_to_f32(v[kv_off + c]);
+            continue;
+          }
+          float next_max = fmaxf(max_score, score);
+          float prev_w = expf(max_score - next_max);
+          float cur_w = expf(score - next_max);
+          normalizer = normalizer * prev_w + cur_w;
+          for (unsigned c = 0; c < HEAD_DIM; ++c)
+            state[c] = state[c] * prev_w + lo_bf16_to_f32(v[kv_off + c]) * cur_w;
+          max_score = next_max;
+        }
+        uint16_t *orow = out + (row * hq + h) * HEAD_DIM;
+        for (unsigned c = 0; c < HEAD_DIM; ++c)
+          orow[c] = lo_bf16_from_f32(state[c] / normalizer);
+        lse[row * hq + h] = (max_score + logf(normalizer)) * LOG2E_F32;
+      }
+    }
+  }
+}
+
+/* paged_prefill/mod.rs:386-446 paged_prefill_bf16_reference. */
+int lo_prefill_reference(const lo_prefill_spec *s, const uint16_t *q, size_t nq,
+                         const uint16_t *k, size_t nk, const uint16_t *v, size_t nv,
+                         const int32_t *qo, size_t n_qo, const int32_t *indptr,
+                         size_t n_indptr, const int32_t *indices, size_t n_indices,
+                         const int32_t *last, size_t n_last, uint16_t *out, size_t nout,
+                         float *lse, size_t nlse, lo_error *err) {
+  const size_t qn = s->nnz_qo * s->num_query_heads * HEAD_DIM;
+  const size_t kvn = s->max_num_pages * PAGE_SIZE * s->num_kv_heads * HEAD_DIM;
+  int rc;
+  if ((rc = require_len(err, "Q", nq, qn))) return rc;
+  if ((rc = require_len(err, "K_pages", nk, kvn))) return rc;
+  if ((rc = require_len(err, "V_pages", nv, kvn))) return rc;
+  if ((rc = require_len(err, "O", nout, qn))) return rc;
+  if ((rc = require_len(err, "LSE", nlse, s->nnz_qo * s->num_query_heads))) return rc;
+  if ((rc = lo_prefill_validate(s, qo, n_qo, indptr, n_indptr, indices, n_indices, last, n_last,
+                                err)))
+    return rc;
+  lo_prefill_requests(s, q, k, v, qo, indptr, indices, last, 0, s->batch_size, out, lse);
+  return LO_OK;
+}

@@ -19,6 +19,12 @@
  *   - paged decode, single decode (direct and split-K), one-token append and
  *     explicit-token append: output digests recorded in the reference's H20
  *     correctness records where the GPU matched the CPU oracle bit for bit;
+ *   - paged prefill: the known-answer outputs of the reference's unit tests
+ *     (bottom-right mask over physical pages, GQA head mapping with reused
+ *     pages), bit equality with the pinned paged decode when every request
+ *     has one query row, the fixture digests of its evidence records, and the
+ *     f64 brute force (its recorded output digests come from GPU runs with
+ *     bit mismatches, so they are not oracle pins);
  *   - validation: the known-answer mapping tables and error matrices of the
  *     reference's unit tests;
  *   - closed forms (Q=0 => mean(V), LSE=log2(L); RoPE pos 0 = identity) and
@@ -135,6 +141,35 @@ int lo_split_k_partials_reference(const lo_single_spec *s, size_t partitions,
 int lo_split_k_merge_reference(const lo_single_spec *s, size_t partitions,
                                const float *workspace, uint16_t *out, float *lse,
                                lo_error *err);
+
+/* ---- paged causal prefill (paged_prefill/mod.rs) ---- */
+typedef struct lo_prefill_spec {
+  size_t batch_size, nnz_qo, max_num_pages, num_query_heads, num_kv_heads;
+  float softmax_scale;
+} lo_prefill_spec;
+int lo_prefill_spec_new(size_t batch, size_t nnz_qo, size_t pool, size_t hq, size_t hkv,
+                        size_t head_dim, size_t page_size, lo_prefill_spec *out,
+                        lo_error *err);
+int lo_prefill_validate(const lo_prefill_spec *s, const int32_t *qo_indptr, size_t n_qo,
+                        const int32_t *page_indptr, size_t n_indptr, const int32_t *indices,
+                        size_t n_indices, const int32_t *last, size_t n_last, lo_error *err);
+/* causal_kv_end (paged_prefill/mod.rs:374-383): -1 for the reference's None. */
+int64_t lo_prefill_causal_kv_end(const lo_prefill_spec *s, const int32_t *qo_indptr,
+                                 const int32_t *page_indptr, const int32_t *last,
+                                 size_t request, size_t query_index);
+int lo_prefill_reference(const lo_prefill_spec *s, const uint16_t *q, size_t nq,
+                         const uint16_t *k, size_t nk, const uint16_t *v, size_t nv,
+                         const int32_t *qo_indptr, size_t n_qo, const int32_t *page_indptr,
+                         size_t n_indptr, const int32_t *indices, size_t n_indices,
+                         const int32_t *last, size_t n_last, uint16_t *out, size_t nout,
+                         float *lse, size_t nlse, lo_error *err);
+/* The same loop restricted to requests [r0, r1) (bounded CPU-baseline sample;
+ * metadata must already be valid). */
+void lo_prefill_requests(const lo_prefill_spec *s, const uint16_t *q, const uint16_t *k,
+                         const uint16_t *v, const int32_t *qo_indptr,
+                         const int32_t *page_indptr, const int32_t *indices,
+                         const int32_t *last, size_t r0, size_t r1, uint16_t *out,
+                         float *lse);
 
 /* ---- RoPE (rope/mod.rs) ---- */
 int lo_rope_pos_ids_reference(size_t tokens, size_t qh, size_t kh, size_t head_dim,
