@@ -477,6 +477,115 @@ loom_status_t loom_single_decode_split_k_enqueue(const loom_single_decode_split_
                                                  loom_error_t *err);
 
 /* ------------------------------------------------------------------------ */
+/* Paged causal prefill, crates/loom-infer/src/attention/paged_prefill/mod.rs  */
+/* Q/O [nnz_qo, Hq, 128] ragged by qo_indptr; K/V pages [pool, 16, Hkv, 128]  */
+/* (NHD) by page_indptr / page_indices / last_page_len; LSE [nnz_qo, Hq]       */
+/* log2.  Bottom-right causal mask: row i of a request with qo_len rows sees   */
+/* KV tokens 0 .. kv_len - qo_len + i.                                         */
+typedef struct loom_paged_prefill_spec {
+  uint64_t batch_size;
+  uint64_t nnz_qo;
+  uint64_t max_num_pages;
+  uint64_t num_query_heads;
+  uint64_t num_kv_heads;
+  float softmax_scale;
+} loom_paged_prefill_spec_t;
+
+/* Bf16PagedPrefillSpec::new, paged_prefill/mod.rs:30-91. */
+loom_status_t loom_paged_prefill_spec_new(uint64_t batch_size, uint64_t nnz_qo,
+                                          uint64_t max_num_pages, uint64_t num_query_heads,
+                                          uint64_t num_kv_heads, uint64_t head_dim,
+                                          uint64_t page_size, loom_paged_prefill_spec_t *out,
+                                          loom_error_t *err);
+/* validate_metadata, paged_prefill/mod.rs:161-264 (host metadata). */
+loom_status_t loom_paged_prefill_validate_metadata(const loom_paged_prefill_spec_t *spec,
+                                                   const int32_t *qo_indptr, uint64_t n_qo,
+                                                   const int32_t *page_indptr, uint64_t n_indptr,
+                                                   const int32_t *page_indices,
+                                                   uint64_t n_indices,
+                                                   const int32_t *last_page_len,
+                                                   uint64_t n_last, loom_error_t *err);
+/* causal_kv_end, paged_prefill/mod.rs:374-383, on validated metadata:
+ * LOOM_OK, or LOOM_EMPTY_RAGGED_REQUEST for the reference's None (request or
+ * query index out of range). */
+loom_status_t loom_paged_prefill_causal_kv_end(const loom_paged_prefill_spec_t *spec,
+                                               const int32_t *qo_indptr,
+                                               const int32_t *page_indptr,
+                                               const int32_t *last_page_len, uint64_t request,
+                                               uint64_t query_index, uint64_t *end);
+
+typedef struct loom_prefill_provider loom_prefill_provider_t;
+typedef struct loom_paged_prefill_plan loom_paged_prefill_plan_t;
+
+/* PrefillProvider::load (crates/loom-infer-cuda/src/attention/prefill.rs:2278-2288). */
+loom_status_t loom_prefill_provider_load(int device, loom_prefill_provider_t **out,
+                                         loom_error_t *err);
+void loom_prefill_provider_free(loom_prefill_provider_t *provider);
+
+typedef enum loom_paged_prefill_algorithm {
+  /* One workgroup of `waves` waves per (request, kv-head, tile of 16
+   * flattened (query row, group head) pairs).  The waves split the tile's
+   * causal page range; per page, S = K·Qᵀ and O += P·V both run on MFMA, and
+   * the wave states merge in LDS.  No workspace. */
+  LOOM_PAGED_PREFILL_ROW_TILE = 1
+} loom_paged_prefill_algorithm_t;
+
+typedef struct loom_paged_prefill_plan_options {
+  uint32_t waves; /* waves per workgroup: 0 (chosen from the spec), 4, 8 or 16 */
+  uint32_t flags; /* 0 or LOOM_PLAN_PAGE_INDICES_CAPACITY */
+} loom_paged_prefill_plan_options_t;
+
+typedef struct loom_paged_prefill_plan_info {
+  loom_paged_prefill_spec_t spec;
+  int32_t algorithm;
+  uint32_t waves;
+  uint64_t row_tiles;  /* upper bound of tiles over any valid qo_indptr:
+                          floor((nnz_qo * group + 15 * batch) / 16) */
+  uint32_t block_threads;
+  uint64_t grid_blocks; /* row_tiles * Hkv */
+  uint32_t flags;
+} loom_paged_prefill_plan_info_t;
+
+/* PrefillProvider::plan_bf16_paged, prefill.rs:2289-2330.  The plan depends
+ * only on the spec (and options), never on metadata contents. */
+loom_status_t loom_prefill_provider_plan_bf16_paged(const loom_prefill_provider_t *provider,
+                                                    const loom_paged_prefill_spec_t *spec,
+                                                    loom_paged_prefill_plan_t **out,
+                                                    loom_error_t *err);
+/* The same plan with planner options (no reference counterpart). */
+loom_status_t loom_prefill_provider_plan_bf16_paged_options(
+    const loom_prefill_provider_t *provider, const loom_paged_prefill_spec_t *spec,
+    const loom_paged_prefill_plan_options_t *options, loom_paged_prefill_plan_t **out,
+    loom_error_t *err);
+void loom_paged_prefill_plan_free(loom_paged_prefill_plan_t *plan);
+void loom_paged_prefill_plan_get_info(const loom_paged_prefill_plan_t *plan,
+                                      loom_paged_prefill_plan_info_t *info);
+
+/* Bf16PagedPrefillArgs, prefill.rs:2852-2890. */
+typedef struct loom_paged_prefill_args {
+  loom_handle_t query;         /* Read<bf16>  [nnz_qo, Hq, 128] */
+  loom_handle_t key_pages;     /* Read<bf16>  [pool, 16, Hkv, 128] */
+  loom_handle_t value_pages;   /* Read<bf16>  [pool, 16, Hkv, 128] */
+  loom_handle_t qo_indptr;     /* Read<i32>   [B+1] */
+  loom_handle_t page_indptr;   /* Read<i32>   [B+1] */
+  loom_handle_t page_indices;  /* Read<i32>   [>= B] */
+  loom_handle_t last_page_len; /* Read<i32>   [B] */
+  loom_handle_t output;        /* Write<bf16> [nnz_qo, Hq, 128] */
+  loom_handle_t lse;           /* Write<f32>  [nnz_qo, Hq], log2 domain */
+} loom_paged_prefill_args_t;
+
+/* Bf16PagedPrefillPlan::enqueue_into, prefill.rs:2447-2560: one command, one
+ * kernel.  Device guards as prefill.rs:293-342: invalid global metadata leaves
+ * every output untouched; a request with an invalid page range, last-page
+ * length, page index or qo_len > kv_len keeps its sentinels, and so does every
+ * request after the first malformed qo_indptr range.  Q, K, V and O must be
+ * 16-byte aligned (the reference asks 4: this kernel moves 16-byte rows). */
+loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
+                                         loom_command_scope_t *scope,
+                                         const loom_paged_prefill_args_t *args,
+                                         loom_error_t *err);
+
+/* ------------------------------------------------------------------------ */
 /* Fused RoPE + paged append provider, crates/loom-infer-cuda/src/rope/mod.rs */
 typedef struct loom_rope_provider loom_rope_provider_t;
 typedef struct loom_rope_append_plan loom_rope_append_plan_t;

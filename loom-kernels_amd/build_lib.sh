@@ -12,7 +12,7 @@ HIPCC="${HIPCC:-/opt/rocm/bin/hipcc}"
 FLAGS=(--offload-arch=gfx950 -O3 -std=c++17 -fPIC -Wall -Wno-unused-function -Wno-unused-value -Wno-unused-result
        -Xclang -target-feature -Xclang -packed-fp32-ops
        -I"$root/include" -I"$here/csrc")
-srcs=(contract.cpp runtime.cpp paged_decode.hip rope_append.hip)
+srcs=(contract.cpp runtime.cpp paged_decode.hip paged_prefill.hip rope_append.hip)
 pids=()
 for s in "${srcs[@]}"; do
   "$HIPCC" -x hip "${FLAGS[@]}" -c "$here/csrc/$s" -o "$obj/${s%.*}.o" \

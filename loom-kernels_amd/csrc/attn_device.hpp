@@ -1,0 +1,92 @@
+// Device helpers shared by the attention kernels of libloom_infer_hip.so
+// (gfx950): BF16 storage conversions, 16-byte and range-limited raw buffer
+// loads of NHD K/V rows, and wave-level primitives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace loom_dev {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// half::bf16::from_f32 (round to nearest even, quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+
+__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+
+// K/V pages are read exactly once per kv-head: nontemporal loads keep them
+// from displacing reusable lines in L2/MALL (measured on MI355X: a plain
+// streaming read tops out near 6.2 TB/s, a nontemporal one near 6.9 TB/s).
+#ifndef LOOM_DECODE_NT_K
+#define LOOM_DECODE_NT_K 1
+#endif
+#ifndef LOOM_DECODE_NT_V
+#define LOOM_DECODE_NT_V 1
+#endif
+// Raw buffer loads of one page's rows for one kv-head.  The resource covers
+// exactly the valid rows of the page (none for a prefetch past the wave's last
+// page), so rows beyond it return zero without touching memory: the pipeline's
+// look-ahead and the tail of a request's last page cost no HBM traffic.
+// Cache policy bit 1 is NT on gfx950.
+template <bool NT>
+__device__ __forceinline__ u32x4 load16_rows(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  return __builtin_bit_cast(
+      u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, NT ? 2 : 0));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rows_rsrc(const uint16_t *base,
+                                                                int valid_rows, int hkv) {
+  // gfx9 word 3: 32-bit data format, no swizzle; stride 0 (raw addressing)
+  const int bytes = valid_rows > 0 ? ((valid_rows - 1) * hkv + 1) * 256 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave-uniform values the compiler cannot prove uniform (loaded through the
+// vector path): pin them to SGPRs.
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uni64(int64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const int32_t hi = __builtin_amdgcn_readfirstlane((int)(x >> 32));
+  return ((int64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ int64_t shfl_up64(int64_t x, int o) {
+  const int lo = __shfl_up((int)(uint32_t)x, o, 64);
+  const int hi = __shfl_up((int)(x >> 32), o, 64);
+  return ((int64_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan64(int64_t x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = shfl_up64(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+}  // namespace loom_dev

@@ -52,6 +52,21 @@ void format_message(loom_error_t *e) {
       snprintf(m, n, "attention partition count must be in 1..=%lld, got %lld",
                (long long)f[1], (long long)f[0]);
       break;
+    case LOOM_INVALID_INDPTR_START:
+      snprintf(m, n, "%s must start at zero, got %lld", op, (long long)f[0]);
+      break;
+    case LOOM_NON_MONOTONIC_INDPTR:
+      snprintf(m, n, "%s must be nondecreasing at request %lld, got %lld then %lld", op,
+               (long long)f[0], (long long)f[1], (long long)f[2]);
+      break;
+    case LOOM_EMPTY_RAGGED_REQUEST:
+      snprintf(m, n, "%s request %lld has zero length", op, (long long)f[0]);
+      break;
+    case LOOM_RAGGED_QUERY_LONGER_THAN_KV:
+      snprintf(m, n,
+               "ragged prefill request %lld has query length %lld greater than KV length %lld",
+               (long long)f[0], (long long)f[1], (long long)f[2]);
+      break;
     case LOOM_INVALID_PAGE_INDPTR_START:
       snprintf(m, n, "page indptr must start at zero, got %lld", (long long)f[0]);
       break;
@@ -562,6 +577,87 @@ loom_status_t loom_rope_append_tokens_validate_metadata(
     }
   }
   return loom::ok(err);
+}
+
+// ---- paged causal prefill (paged_prefill/mod.rs) ------------------------------
+// Bf16PagedPrefillSpec::new, paged_prefill/mod.rs:30-91.
+loom_status_t loom_paged_prefill_spec_new(uint64_t batch, uint64_t nnz_qo, uint64_t pool,
+                                          uint64_t hq, uint64_t hkv, uint64_t head_dim,
+                                          uint64_t page_size, loom_paged_prefill_spec_t *out,
+                                          loom_error_t *err) {
+  if (!out) return fail(err, LOOM_NULL_ARGUMENT, "out");
+  if (batch == 0 || nnz_qo == 0 || pool == 0 || hq == 0 || hkv == 0 || head_dim == 0 ||
+      page_size == 0)
+    return fail(err, LOOM_ZERO_DIMENSION);
+  if (head_dim != loom::kHeadDim)
+    return fail(err, LOOM_UNSUPPORTED_HEAD_DIMENSION, nullptr, loom::kHeadDim, head_dim);
+  if (page_size != loom::kPageSize)
+    return fail(err, LOOM_UNSUPPORTED_PAGE_SIZE, nullptr, loom::kPageSize, page_size);
+  if (hq % hkv != 0) return fail(err, LOOM_INVALID_HEAD_MAPPING, nullptr, hq, hkv);
+  if (nnz_qo > (uint64_t)INT32_MAX) return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  uint64_t t;
+  if (batch == UINT64_MAX || mul_ovf(nnz_qo, hq, &t) || mul_ovf(t, head_dim, &t))
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  if (mul_ovf(pool, page_size, &t) || mul_ovf(t, hkv, &t) || mul_ovf(t, head_dim, &t))
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  out->batch_size = batch;
+  out->nnz_qo = nnz_qo;
+  out->max_num_pages = pool;
+  out->num_query_heads = hq;
+  out->num_kv_heads = hkv;
+  out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
+  return loom::ok(err);
+}
+
+// validate_metadata + validate_query_indptr, paged_prefill/mod.rs:161-264.
+loom_status_t loom_paged_prefill_validate_metadata(const loom_paged_prefill_spec_t *s,
+                                                   const int32_t *qo, uint64_t n_qo,
+                                                   const int32_t *indptr, uint64_t n_indptr,
+                                                   const int32_t *indices, uint64_t n_indices,
+                                                   const int32_t *last, uint64_t n_last,
+                                                   loom_error_t *err) {
+  if (!s) return fail(err, LOOM_NULL_ARGUMENT, "spec");
+  const uint64_t B = s->batch_size;
+  loom_status_t rc;
+  if ((rc = require_len(err, "qo_indptr", n_qo, B + 1))) return rc;
+  if ((rc = require_len(err, "page_indptr", n_indptr, B + 1))) return rc;
+  if ((rc = require_len(err, "last_page_len", n_last, B))) return rc;
+  if (qo[0] != 0) return fail(err, LOOM_INVALID_INDPTR_START, "qo_indptr", qo[0]);
+  for (uint64_t r = 0; r < B; ++r) {
+    if (qo[r + 1] < qo[r])
+      return fail(err, LOOM_NON_MONOTONIC_INDPTR, "qo_indptr", r, qo[r], qo[r + 1]);
+    if (qo[r + 1] == qo[r]) return fail(err, LOOM_EMPTY_RAGGED_REQUEST, "qo_indptr", r);
+  }
+  if ((rc = require_len(err, "qo_indptr", (uint64_t)qo[B], s->nnz_qo))) return rc;
+  if (indptr[0] != 0) return fail(err, LOOM_INVALID_PAGE_INDPTR_START, nullptr, indptr[0]);
+  for (uint64_t r = 0; r < B; ++r) {
+    const int32_t a = indptr[r], b = indptr[r + 1];
+    if (b < a) return fail(err, LOOM_NON_MONOTONIC_PAGE_INDPTR, nullptr, r, a, b);
+    if (b == a) return fail(err, LOOM_EMPTY_PAGED_REQUEST, nullptr, r);
+    if (last[r] < 1 || last[r] > (int32_t)loom::kPageSize)
+      return fail(err, LOOM_INVALID_LAST_PAGE_LENGTH, nullptr, r, last[r], loom::kPageSize);
+    const int64_t qo_len = (int64_t)qo[r + 1] - qo[r];
+    const int64_t kv_len = kv_len_of(indptr, last, r);
+    if (qo_len > kv_len)
+      return fail(err, LOOM_RAGGED_QUERY_LONGER_THAN_KV, nullptr, r, qo_len, kv_len);
+  }
+  if ((rc = require_len(err, "page_indices", n_indices, (uint64_t)indptr[B]))) return rc;
+  for (uint64_t p = 0; p < n_indices; ++p)
+    if (indices[p] < 0 || (uint64_t)indices[p] >= s->max_num_pages)
+      return fail(err, LOOM_PAGE_INDEX_OUT_OF_RANGE, nullptr, p, indices[p], s->max_num_pages);
+  return loom::ok(err);
+}
+
+// causal_kv_end, paged_prefill/mod.rs:374-383.
+loom_status_t loom_paged_prefill_causal_kv_end(const loom_paged_prefill_spec_t *s,
+                                               const int32_t *qo, const int32_t *indptr,
+                                               const int32_t *last, uint64_t request,
+                                               uint64_t query_index, uint64_t *end) {
+  if (!s || !end || request >= s->batch_size) return LOOM_EMPTY_RAGGED_REQUEST;
+  const int64_t qo_len = (int64_t)qo[request + 1] - qo[request];
+  if ((int64_t)query_index >= qo_len) return LOOM_EMPTY_RAGGED_REQUEST;
+  *end = (uint64_t)(kv_len_of(indptr, last, request) - qo_len + (int64_t)query_index + 1);
+  return LOOM_OK;
 }
 
 }  // extern "C"

@@ -1,0 +1,536 @@
+// Paged causal prefill attention for gfx950 (MI355X), BF16 NHD D128 page-16
+// caches, ragged query rows.
+//
+// Semantics: crates/loom-infer/src/attention/paged_prefill/mod.rs:386-446 (the
+// CPU reference: bottom-right causal mask, row i of a request with qo_len rows
+// sees KV tokens 0 .. kv_len - qo_len + i) with the device metadata guards of
+// crates/loom-infer-cuda/src/attention/prefill.rs:293-342 (invalid global
+// metadata writes nothing; an invalid request keeps its sentinels).
+//
+// Work decomposition (MI355X-first, not the reference's warp per (row, head)):
+//   * the query rows of one request and the query heads of one kv-head's GQA
+//     group are flattened, (row, group head) -> row * group + head, and cut
+//     into tiles of 16; a workgroup owns one (tile, kv-head), so the 16
+//     columns share every K/V byte it reads;
+//   * the tile's causal page range (up to its last column's end) is split
+//     over W waves (page w, w + W, ...); each wave streams its pages through
+//     a two-deep register pipeline of raw buffer loads whose range covers only
+//     the page's valid rows;
+//   * per page, S = K·Qᵀ is four v_mfma_f32_16x16x32_bf16 (16 tokens x 16
+//     columns x 128 dims) with K loaded straight into the A-fragment layout,
+//     the online softmax runs in the log2 domain with a per-column causal
+//     mask, and O += P·V is eight column blocks of v_mfma_f32_16x16x16_bf16:
+//     the S accumulator already has the A-fragment layout of Pᵀ, and the V
+//     rows as loaded give each lane the four tokens of one head dimension.
+//     P is split into a BF16 high part and a BF16 residual, two MFMAs per
+//     block, so the weights carry 16 significant bits (relative error below
+//     2^-15 against FP32 weights);
+//   * the W wave states merge in LDS (max, rescale, deterministic tree sum)
+//     and wave 0 writes O and the log2 LSE.
+// No workspace and one launch; the grid depends only on the plan.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "attn_device.hpp"
+#include "loom_internal.hpp"
+
+using loom::fail;
+using namespace loom_dev;
+
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+struct PrefillArgs {
+  const uint16_t *__restrict__ q;
+  const uint16_t *__restrict__ k;
+  const uint16_t *__restrict__ v;
+  const int32_t *__restrict__ qo;
+  const int32_t *__restrict__ indptr;
+  const int32_t *__restrict__ indices;
+  const int32_t *__restrict__ last;
+  uint16_t *__restrict__ out;
+  float *__restrict__ lse;
+  int32_t batch;
+  int32_t nnz;
+  int32_t hq;
+  int32_t hkv;
+  int32_t group;
+  int64_t pool;
+  int64_t n_indices;
+  float scale_log2;
+  int32_t indices_capacity;
+};
+
+// Tile count given to a request whose qo range is malformed: larger than any
+// tile index, so neither it nor any later request owns a tile (the reference's
+// request search returns at the first malformed range, prefill.rs:303-313).
+constexpr int64_t kNoTiles = (int64_t)1 << 50;
+
+template <int W>
+struct PrefillSmem {
+  int64_t wave_tot[W];
+  int32_t req;
+  int32_t tile0;
+  u32x4 qfrag[4][64];  // MFMA B fragments of the tile's 16 query columns
+  float m[W][16];      // per-wave running max (log2 domain) per column
+  float l[W][16];      // per-wave normalizer per column
+  f32x4 red[W / 2 > 0 ? W / 2 : 1][4][64];  // tree-sum staging, half the accumulators
+};
+
+// One page of K (A-fragment layout) and V (row layout) for one wave.
+// K: lane (col, quad) holds dims [32c + 8 quad, +8) of token row col.
+// V: lane (col, quad) holds dims [8 col, +8) of token rows 4 quad + j.
+struct PrefillPage {
+  u32x4 k[4];
+  u32x4 v[4];
+};
+
+__device__ __forceinline__ void load_prefill_page(PrefillPage &p, const PrefillArgs &a,
+                                                  int64_t token0, int rows, int lane, int kvh) {
+  const int col = lane & 15, quad = lane >> 4;
+  const int64_t first = (token0 * a.hkv + kvh) * 128;
+  const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, rows, a.hkv);
+  const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, rows, a.hkv);
+  const int row_bytes = a.hkv * 256;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) p.k[c] = load16_rows<false>(rk, col * row_bytes + (32 * c + 8 * quad) * 2);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p.v[j] = load16_rows<false>(rv, (quad * 4 + j) * row_bytes + col * 16);
+}
+
+// Upper 16 bits of two floats packed into one register (lo <- a, hi <- b).
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ s16x4 as_s16x4(uint32_t lo, uint32_t hi) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(s16x4, u32x2{lo, hi});
+}
+
+struct PrefillWave {
+  const PrefillArgs &a;
+  const u32x4 (*qfrag)[64];
+  int lane, col, quad, kvh;
+  int64_t end_col;  // causal end (exclusive) of this lane's column, 0 if unused
+  float m_run, l_run;
+  f32x4 acc[8];     // acc[e][r] = O[column 4 quad + r][dim 8 col + e]
+
+  __device__ void reset() {
+    m_run = -INFINITY;
+    l_run = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // `lt0`: logical token index of the page's first row in the request.
+  __device__ void process(const PrefillPage &pg, int64_t lt0) {
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pg.k[c]), as_bf16x8(qfrag[c][lane]),
+                                                  s, 0, 0, 0);
+    // s[i] = S[token 4 quad + i][column col]; tokens at or past the column's
+    // causal end (which also covers the rows past kv_len) are masked.
+    const int64_t vis = end_col - lt0;
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = (quad * 4 + i < vis) ? s[i] * a.scale_log2 : -INFINITY;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // column with nothing visible yet
+    const float al = fast_exp2(m_run - m_use);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_use);
+    l_run = l_run * al + ((p[0] + p[1]) + (p[2] + p[3]));
+    m_run = m_new;
+    // rows of acc are columns 4 quad + r: fetch their rescale factors
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(al, quad * 4 + r, 64);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e][r] *= ar;
+    }
+    // Pᵀ as the A fragment (lane: column col, tokens 4 quad + [0, 4)): BF16
+    // high part and BF16 residual.
+    uint32_t pb[4], rb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pb[i] = __float_as_uint(p[i]);
+      rb[i] = __float_as_uint(p[i] - __uint_as_float(pb[i] & 0xffff0000u));
+    }
+    const s16x4 a_hi = as_s16x4(pack_hi16(pb[0], pb[1]), pack_hi16(pb[2], pb[3]));
+    const s16x4 a_lo = as_s16x4(pack_hi16(rb[0], rb[1]), pack_hi16(rb[2], rb[3]));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // B fragment of dim 8 col + e: tokens 4 quad + [0, 4) from the V rows
+      const int w = e >> 1;
+      const s16x4 b =
+          (e & 1) ? as_s16x4(pack_hi16(pg.v[0][w], pg.v[1][w]), pack_hi16(pg.v[2][w], pg.v[3][w]))
+                  : as_s16x4(pack_lo16(pg.v[0][w], pg.v[1][w]), pack_lo16(pg.v[2][w], pg.v[3][w]));
+      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a_hi, b, acc[e], 0, 0, 0);
+      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a_lo, b, acc[e], 0, 0, 0);
+    }
+  }
+
+  // Pages 0..n-1 of this wave's share.  D = 2: a two-deep pipeline (the loads
+  // of page i+1 are issued before page i is consumed); D = 1: load then use
+  // (for 16-wave workgroups, where the other waves hide the latency and the
+  // register budget is 128).  page_tok(i): physical token row of page i's
+  // first row; rows_of(i): valid rows (0 past the end); lt_of(i): logical
+  // token of its first row.  All wave-uniform.
+  template <int D, class PageTok, class RowsOf, class LtOf>
+  __device__ void stream(int n, PageTok page_tok, RowsOf rows_of, LtOf lt_of) {
+    if constexpr (D == 1) {
+      for (int i = 0; i < n; ++i) {
+        PrefillPage pg;
+        load_prefill_page(pg, a, page_tok(i), rows_of(i), lane, kvh);
+        process(pg, lt_of(i));
+      }
+    } else {
+      PrefillPage buf[2];
+      load_prefill_page(buf[0], a, page_tok(0), rows_of(0), lane, kvh);
+      int i = 0;
+      while (true) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          load_prefill_page(buf[s ^ 1], a, page_tok(i + 1), rows_of(i + 1), lane, kvh);
+          process(buf[s], lt_of(i));
+          if (++i >= n) return;
+        }
+      }
+    }
+  }
+};
+
+template <int W>
+__global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
+  __shared__ PrefillSmem<W> sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, quad = lane >> 4;
+  const int kvh = (int)(blockIdx.x % a.hkv);
+  const int64_t tile = blockIdx.x / a.hkv;
+
+  // Global guards (prefill.rs:293-300), one round trip.
+  const int32_t qo0 = a.qo[0], qoB = a.qo[a.batch];
+  const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
+  const bool pages_ok = ipB >= 0 && (a.indices_capacity ? (int64_t)ipB <= a.n_indices
+                                                        : (int64_t)ipB == a.n_indices);
+  if (qo0 != 0 || qoB != a.nnz || ip0 != 0 || !pages_ok) return;
+
+  // Locate the request owning this tile: prefix of the requests' tile counts.
+  if (tid == 0) sm.req = -1;
+  int64_t carry = 0;
+  for (int base = 0; base < a.batch; base += W * 64) {
+    const int r = base + tid;
+    int64_t cnt = 0;
+    if (r < a.batch) {
+      const int32_t s0 = a.qo[r], s1 = a.qo[r + 1];
+      cnt = (s0 >= 0 && s1 > s0 && s1 <= a.nnz) ? ((int64_t)(s1 - s0) * a.group + 15) / 16
+                                                : kNoTiles;
+    }
+    const int64_t x = wave_incl_scan64(cnt, lane);
+    if (lane == 63) sm.wave_tot[wave] = x;
+    __syncthreads();
+    int64_t before = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const int64_t t = sm.wave_tot[i];
+      before += (i < wave) ? t : 0;
+      tot += t;
+    }
+    const int64_t incl = carry + before + x;
+    if (r < a.batch && tile < incl && tile >= incl - cnt && cnt != kNoTiles) {
+      sm.req = r;
+      sm.tile0 = (int32_t)(tile - (incl - cnt));
+    }
+    carry += tot;
+    __syncthreads();
+    if (carry > tile) break;
+  }
+  const int r = uni(sm.req);
+  if (r < 0) return;
+  const int tile0 = uni(sm.tile0);
+
+  // Per-request guards (prefill.rs:316-342).
+  const int32_t qs = uni(a.qo[r]), qe = uni(a.qo[r + 1]);
+  const int32_t ps = uni(a.indptr[r]), pe = uni(a.indptr[r + 1]), tl = uni(a.last[r]);
+  if (ps < 0 || pe <= ps || pe > ipB || tl < 1 || tl > 16) return;
+  const int req_pages = pe - ps;
+  const int64_t kv_len = (int64_t)(req_pages - 1) * 16 + tl;
+  const int qo_len = qe - qs;
+  if ((int64_t)qo_len > kv_len) return;
+
+  // This lane's column and the tile's page range.
+  const int64_t fcols = (int64_t)qo_len * a.group;
+  const int64_t f = (int64_t)tile0 * 16 + col;
+  const bool colv = f < fcols;
+  const int qi = colv ? (int)(f / a.group) : 0;
+  const int gh = colv ? (int)(f - (int64_t)qi * a.group) : 0;
+  const int64_t f_last = min<int64_t>((int64_t)tile0 * 16 + 15, fcols - 1);
+  const int64_t tile_end = kv_len - qo_len + f_last / a.group + 1;
+  const int npages = (int)((tile_end + 15) / 16);
+
+  // Every page index of the request is checked (the reference rejects the
+  // whole request), strided over the workgroup; the verdict is read after
+  // the stream.
+  bool bad = false;
+  for (int i = tid; i < req_pages; i += W * 64) {
+    const int32_t x = a.indices[ps + i];
+    bad |= x < 0 || (int64_t)x >= a.pool;
+  }
+  if (wave == 0) {
+    const uint16_t *qp = a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 +
+                         quad * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sm.qfrag[c][lane] = colv ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
+  }
+  __syncthreads();
+
+  PrefillWave w{a, sm.qfrag, lane, col, quad, kvh};
+  w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
+  w.reset();
+  const int mine = npages > wave ? (npages - wave + W - 1) / W : 0;
+  for (int s0 = 0; s0 < mine; s0 += 64) {
+    const int n = min(mine - s0, 64);
+    const int idx = lane < n ? a.indices[ps + wave + W * (s0 + lane)] : 0;
+    const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
+    auto page_tok = [&](int i) {
+      return (int64_t)__builtin_amdgcn_readlane(idx, min(i, n - 1)) * 16;
+    };
+    auto rows_of = [&](int i) {
+      if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
+      return wave + W * (s0 + i) == req_pages - 1 ? (int)tl : 16;
+    };
+    auto lt_of = [&](int i) { return (int64_t)(wave + W * (s0 + i)) * 16; };
+    w.template stream<(W >= 16 ? 1 : 2)>(n, page_tok, rows_of, lt_of);
+  }
+
+  // Wave states -> LDS; an invalid page index anywhere in the request keeps
+  // its sentinels.
+  float l_tot = w.l_run + __shfl_xor(w.l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (quad == 0) {
+    sm.m[wave][col] = w.m_run;
+    sm.l[wave][col] = l_tot;
+  }
+  if (__syncthreads_or(bad)) return;
+
+  float M[4];
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    const int c = quad * 4 + r4;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int wv = 0; wv < W; ++wv) mm = fmaxf(mm, sm.m[wv][c]);
+    M[r4] = mm;
+    const float fac = mm == -INFINITY ? 0.0f : fast_exp2(sm.m[wave][c] - mm);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w.acc[e][r4] *= fac;
+  }
+  // Deterministic tree sum of the W accumulators, half of them per pass.
+#pragma unroll
+  for (int s = W / 2; s >= 1; s >>= 1) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (wave >= s && wave < 2 * s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sm.red[wave - s][e][lane] = w.acc[4 * h + e];
+      __syncthreads();
+      if (wave < s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w.acc[4 * h + e] += sm.red[wave][e][lane];
+      __syncthreads();
+    }
+  }
+  if (wave != 0) return;
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    const int c = quad * 4 + r4;
+    const int64_t fc = (int64_t)tile0 * 16 + c;
+    if (fc >= fcols) continue;
+    float L = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < W; ++wv) L = fmaf(sm.l[wv][c], fast_exp2(sm.m[wv][c] - M[r4]), L);
+    const int rq = (int)(fc / a.group);
+    const int hh = (int)(fc - (int64_t)rq * a.group);
+    const int64_t row_head = (int64_t)(qs + rq) * a.hq + (int64_t)kvh * a.group + hh;
+    u32x4 o;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2)
+      o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] / L) |
+              ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] / L) << 16);
+    *reinterpret_cast<u32x4 *>(a.out + row_head * 128 + col * 8) = o;
+    if (col == 0) a.lse[row_head] = M[r4] + __log2f(L);
+  }
+}
+
+}  // namespace
+
+// ---- provider / plan / enqueue -----------------------------------------------
+struct loom_prefill_provider {
+  loom::DeviceInfo dev;
+};
+
+struct loom_paged_prefill_plan {
+  loom_paged_prefill_plan_info_t info;
+};
+
+namespace {
+// Waves per workgroup from the average page capacity per request (the
+// reference picks its kernel the same way, prefill.rs:2417-2426): short
+// tables are latency-bound (fewer waves, cheaper merge), long ones split the
+// causal range over more waves.
+uint32_t waves_for(const loom_paged_prefill_spec_t &s) {
+  const uint64_t avg_pages = s.max_num_pages / s.batch_size;
+  return avg_pages <= 8 ? 4u : avg_pages <= 32 ? 8u : 16u;
+}
+
+loom_status_t require_aligned(const char *name, uintptr_t ptr, uintptr_t alignment,
+                              loom_error_t *err) {
+  if (ptr % alignment != 0)
+    return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, name, (int64_t)ptr, (int64_t)alignment);
+  return LOOM_OK;
+}
+}  // namespace
+
+extern "C" {
+
+loom_status_t loom_prefill_provider_load(int device, loom_prefill_provider_t **out,
+                                         loom_error_t *err) {
+  if (!out) return fail(err, LOOM_NULL_ARGUMENT, "out");
+  loom::DeviceInfo dev;
+  loom_status_t rc = loom::query_device(device, &dev, err);
+  if (rc) return rc;
+  if (!dev.gfx950) return fail(err, LOOM_PLAN_UNSUPPORTED_DEVICE, nullptr, device);
+  auto *p = new loom_prefill_provider;
+  p->dev = dev;
+  *out = p;
+  return loom::ok(err);
+}
+
+void loom_prefill_provider_free(loom_prefill_provider_t *p) { delete p; }
+
+loom_status_t loom_prefill_provider_plan_bf16_paged_options(
+    const loom_prefill_provider_t *provider, const loom_paged_prefill_spec_t *spec,
+    const loom_paged_prefill_plan_options_t *options, loom_paged_prefill_plan_t **out,
+    loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  const loom_paged_prefill_plan_options_t opt =
+      options ? *options : loom_paged_prefill_plan_options_t{0, 0};
+  if (opt.flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
+  if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
+  // prefill.rs:2293-2298: the (row, head) states must fit the launch range;
+  // here the grid is tiles x kv-heads and the kernel indexes with int32.
+  const uint64_t group = spec->num_query_heads / spec->num_kv_heads;
+  const uint64_t states = spec->nnz_qo * spec->num_query_heads;
+  if (states > (uint64_t)INT32_MAX || spec->batch_size > (uint64_t)INT32_MAX - 1)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged prefill", states);
+  const uint64_t cols = spec->nnz_qo * group;
+  const uint64_t tiles = std::min(cols, (cols + 15 * spec->batch_size) / 16);
+  const uint64_t grid = tiles * spec->num_kv_heads;
+  if (grid > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged prefill", states);
+  auto *p = new loom_paged_prefill_plan;
+  p->info.spec = *spec;
+  p->info.algorithm = LOOM_PAGED_PREFILL_ROW_TILE;
+  p->info.waves = opt.waves ? opt.waves : waves_for(*spec);
+  p->info.row_tiles = tiles;
+  p->info.block_threads = p->info.waves * 64;
+  p->info.grid_blocks = grid;
+  p->info.flags = opt.flags;
+  *out = p;
+  return loom::ok(err);
+}
+
+loom_status_t loom_prefill_provider_plan_bf16_paged(const loom_prefill_provider_t *provider,
+                                                    const loom_paged_prefill_spec_t *spec,
+                                                    loom_paged_prefill_plan_t **out,
+                                                    loom_error_t *err) {
+  return loom_prefill_provider_plan_bf16_paged_options(provider, spec, nullptr, out, err);
+}
+
+void loom_paged_prefill_plan_free(loom_paged_prefill_plan_t *p) { delete p; }
+
+void loom_paged_prefill_plan_get_info(const loom_paged_prefill_plan_t *p,
+                                      loom_paged_prefill_plan_info_t *info) {
+  if (p && info) *info = p->info;
+}
+
+// Bf16PagedPrefillPlan::enqueue_into, prefill.rs:2456-2560.
+loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
+                                         loom_command_scope_t *scope,
+                                         const loom_paged_prefill_args_t *args,
+                                         loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_paged_prefill_spec_t &s = plan->info.spec;
+  static const loom::OperandSpec ops[9] = {
+      {"Q", LOOM_DTYPE_BF16, false},           {"K_pages", LOOM_DTYPE_BF16, false},
+      {"V_pages", LOOM_DTYPE_BF16, false},     {"qo_indptr", LOOM_DTYPE_I32, false},
+      {"page_indptr", LOOM_DTYPE_I32, false},  {"page_indices", LOOM_DTYPE_I32, false},
+      {"last_page_len", LOOM_DTYPE_I32, false}, {"O", LOOM_DTYPE_BF16, true},
+      {"LSE", LOOM_DTYPE_F32, true}};
+  const loom_handle_t hs[9] = {args->query,       args->key_pages,   args->value_pages,
+                               args->qo_indptr,   args->page_indptr, args->page_indices,
+                               args->last_page_len, args->output,    args->lse};
+  const loom::Lease *l[9];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, 9, l, err);
+  if (rc) return rc;
+  // prefill.rs:2474-2495: exact spans, page_indices at least B entries.
+  const uint64_t qn = s.nnz_qo * s.num_query_heads * loom::kHeadDim;
+  const uint64_t kvn = s.max_num_pages * loom::kPageSize * s.num_kv_heads * loom::kHeadDim;
+  const uint64_t want[9] = {qn, kvn, kvn, s.batch_size + 1, s.batch_size + 1, 0,
+                            s.batch_size, qn, s.nnz_qo * s.num_query_heads};
+  for (int i = 0; i < 9; ++i) {
+    if (i == 5) {
+      if (l[5]->numel < s.batch_size)
+        return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_SHORT, "page_indices", s.batch_size,
+                    l[5]->numel);
+      continue;
+    }
+    if (l[i]->numel != want[i])
+      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
+  }
+  for (int i : {0, 1, 2, 7})
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+  PrefillArgs a{};
+  a.q = (const uint16_t *)l[0]->ptr;
+  a.k = (const uint16_t *)l[1]->ptr;
+  a.v = (const uint16_t *)l[2]->ptr;
+  a.qo = (const int32_t *)l[3]->ptr;
+  a.indptr = (const int32_t *)l[4]->ptr;
+  a.indices = (const int32_t *)l[5]->ptr;
+  a.last = (const int32_t *)l[6]->ptr;
+  a.out = (uint16_t *)l[7]->ptr;
+  a.lse = (float *)l[8]->ptr;
+  a.batch = (int32_t)s.batch_size;
+  a.nnz = (int32_t)s.nnz_qo;
+  a.hq = (int32_t)s.num_query_heads;
+  a.hkv = (int32_t)s.num_kv_heads;
+  a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
+  a.pool = (int64_t)s.max_num_pages;
+  a.n_indices = (int64_t)l[5]->numel;
+  a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
+  a.indices_capacity = (plan->info.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
+  hipStream_t stream = scope->queue->stream;
+  const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
+  switch (plan->info.waves) {
+    case 4: hipLaunchKernelGGL(paged_prefill_kernel<4>, grid, block, 0, stream, a); break;
+    case 8: hipLaunchKernelGGL(paged_prefill_kernel<8>, grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL(paged_prefill_kernel<16>, grid, block, 0, stream, a); break;
+  }
+  return loom::record_launch(scope, hipGetLastError(), err);
+}
+
+}  // extern "C"

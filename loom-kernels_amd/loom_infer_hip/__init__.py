@@ -738,6 +738,167 @@ class DecodeProvider:
             pass
 
 
+# ---- paged causal prefill ---------------------------------------------------------
+class PagedPrefillMetadata:
+    """Validated metadata view (paged_prefill/mod.rs:277-384)."""
+
+    def __init__(self, spec: "Bf16PagedPrefillSpec", qo_indptr, indptr, indices, last):
+        self.spec = spec
+        self.qo_indptr = list(qo_indptr)
+        self.page_indptr = list(indptr)
+        self.page_indices = list(indices)
+        self.last_page_len = list(last)
+
+    def request_query_range(self, request: int):
+        if request >= self.spec.batch_size:
+            return None
+        return self.qo_indptr[request], self.qo_indptr[request + 1]
+
+    def request_page_range(self, request: int):
+        if request >= self.spec.batch_size:
+            return None
+        return self.page_indptr[request], self.page_indptr[request + 1]
+
+    def request_kv_len(self, request: int):
+        if request >= self.spec.batch_size:
+            return None
+        st, en = self.request_page_range(request)
+        return (en - st - 1) * PAGE_SIZE + self.last_page_len[request]
+
+    def causal_kv_end(self, request: int, query_index: int):
+        qo, _ = _i32_array(self.qo_indptr)
+        ip, _ = _i32_array(self.page_indptr)
+        ln, _ = _i32_array(self.last_page_len)
+        out = C.c_uint64()
+        rc = lib().loom_paged_prefill_causal_kv_end(C.byref(self.spec._c), qo, ip, ln, request,
+                                                    query_index, C.byref(out))
+        return None if rc else out.value
+
+    def physical_page_for_token(self, request: int, token: int):
+        kv = self.request_kv_len(request)
+        if kv is None or token >= kv:
+            return None
+        return self.page_indices[self.page_indptr[request] + token // PAGE_SIZE], token % PAGE_SIZE
+
+
+class Bf16PagedPrefillSpec:
+    """paged_prefill/mod.rs:11-159."""
+
+    def __init__(self, batch_size, nnz_qo, max_num_pages, num_query_heads, num_kv_heads,
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE):
+        self._c = _ffi.PagedPrefillSpec()
+        _call(lib().loom_paged_prefill_spec_new, batch_size, nnz_qo, max_num_pages,
+              num_query_heads, num_kv_heads, head_dim, page_size, C.byref(self._c))
+
+    batch_size = property(lambda s: s._c.batch_size)
+    nnz_qo = property(lambda s: s._c.nnz_qo)
+    max_num_pages = property(lambda s: s._c.max_num_pages)
+    num_query_heads = property(lambda s: s._c.num_query_heads)
+    num_kv_heads = property(lambda s: s._c.num_kv_heads)
+    softmax_scale = property(lambda s: s._c.softmax_scale)
+    head_dim = property(lambda s: HEAD_DIM)
+    page_size = property(lambda s: PAGE_SIZE)
+    gqa_group_size = property(lambda s: s.num_query_heads // s.num_kv_heads)
+    query_numel = property(lambda s: s.nnz_qo * s.num_query_heads * HEAD_DIM)
+    kv_pages_numel = property(lambda s: s.max_num_pages * PAGE_SIZE * s.num_kv_heads * HEAD_DIM)
+    output_numel = property(lambda s: s.query_numel)
+    lse_numel = property(lambda s: s.nnz_qo * s.num_query_heads)
+    indptr_numel = property(lambda s: s.batch_size + 1)
+    last_page_len_numel = property(lambda s: s.batch_size)
+
+    def kv_head_for_query_head(self, query_head: int):
+        return query_head // self.gqa_group_size if query_head < self.num_query_heads else None
+
+    def validate_metadata(self, qo_indptr, indptr, indices, last) -> PagedPrefillMetadata:
+        qo, nqo = _i32_array(qo_indptr)
+        ip, nip = _i32_array(indptr)
+        ix, nix = _i32_array(indices)
+        ln, nln = _i32_array(last)
+        _call(lib().loom_paged_prefill_validate_metadata, C.byref(self._c), qo, nqo, ip, nip,
+              ix, nix, ln, nln)
+        return PagedPrefillMetadata(self, qo_indptr, indptr, indices, last)
+
+
+@dataclass(frozen=True)
+class Bf16PagedPrefillArgs:
+    """prefill.rs:2852-2890."""
+    query: Read
+    key_pages: Read
+    value_pages: Read
+    qo_indptr: Read
+    page_indptr: Read
+    page_indices: Read
+    last_page_len: Read
+    output: Write
+    lse: Write
+
+    def __post_init__(self):
+        c = _ffi.PagedPrefillArgs(*[_h(getattr(self, f)) for f in (
+            "query", "key_pages", "value_pages", "qo_indptr", "page_indptr", "page_indices",
+            "last_page_len", "output", "lse")])
+        object.__setattr__(self, "_struct", c)
+        object.__setattr__(self, "_ref", C.byref(c))
+
+
+class Bf16PagedPrefillPlan:
+    def __init__(self, ptr, spec):
+        self._p = ptr
+        self._spec = spec
+        self.info = _ffi.PagedPrefillPlanInfo()
+        lib().loom_paged_prefill_plan_get_info(self._p, C.byref(self.info))
+
+    def spec(self):
+        return self._spec
+
+    @property
+    def algorithm(self) -> str:
+        return {1: "row_tile"}[self.info.algorithm]
+
+    def enqueue_into(self, scope: CommandScope, args: Bf16PagedPrefillArgs):
+        _enqueue(_ffi.load().loom_paged_prefill_enqueue, self._p, scope._p, args._ref)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_paged_prefill_plan_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
+
+
+class PrefillProvider:
+    """prefill.rs:2278-2330 (the paged plan)."""
+
+    def __init__(self, ptr, device):
+        self._p = ptr
+        self.device = device
+
+    @classmethod
+    def load(cls, device: int = 0) -> "PrefillProvider":
+        out = C.c_void_p()
+        _call(lib().loom_prefill_provider_load, device, C.byref(out))
+        return cls(out.value, device)
+
+    def plan_bf16_paged(self, spec: Bf16PagedPrefillSpec, waves: int = 0,
+                        indices_capacity: bool = False) -> Bf16PagedPrefillPlan:
+        """`waves` per workgroup (0: chosen from the spec; 4, 8 or 16);
+        `indices_capacity`: page_indices is a capacity (LOOM_PLAN_PAGE_INDICES_CAPACITY)."""
+        opt = _ffi.PagedPrefillPlanOptions(waves,
+                                           PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0)
+        out = C.c_void_p()
+        _call(lib().loom_prefill_provider_plan_bf16_paged_options, self._p, C.byref(spec._c),
+              C.byref(opt), C.byref(out))
+        return Bf16PagedPrefillPlan(out.value, spec)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_prefill_provider_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
+
+
 # ---- fused RoPE + append --------------------------------------------------------
 @dataclass(frozen=True)
 class Bf16RopePagedKvAppendArgs:

@@ -70,6 +70,27 @@ class SingleDecodeSplitKArgs(C.Structure):
     _fields_ = [(n, Handle) for n in ("query", "key", "value", "workspace", "output", "lse")]
 
 
+class PagedPrefillSpec(C.Structure):
+    _fields_ = [("batch_size", u64), ("nnz_qo", u64), ("max_num_pages", u64),
+                ("num_query_heads", u64), ("num_kv_heads", u64), ("softmax_scale", f32)]
+
+
+class PagedPrefillPlanOptions(C.Structure):
+    _fields_ = [("waves", u32), ("flags", u32)]
+
+
+class PagedPrefillPlanInfo(C.Structure):
+    _fields_ = [("spec", PagedPrefillSpec), ("algorithm", i32), ("waves", u32),
+                ("row_tiles", u64), ("block_threads", u32), ("grid_blocks", u64),
+                ("flags", u32)]
+
+
+class PagedPrefillArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key_pages", "value_pages", "qo_indptr",
+                                      "page_indptr", "page_indices", "last_page_len",
+                                      "output", "lse")]
+
+
 class RopeAppendPlanInfo(C.Structure):
     _fields_ = [("tokens", u64), ("batch_size", u64), ("num_query_heads", u64),
                 ("num_kv_heads", u64), ("explicit_tokens", i32), ("workspace_bytes", u64),
@@ -142,6 +163,19 @@ SIGNATURES = {
     "loom_single_decode_split_k_plan_free": (None, [vp]),
     "loom_single_decode_split_k_workspace_bytes": (u64, [vp]),
     "loom_single_decode_split_k_enqueue": (i32, [vp, vp, P(SingleDecodeSplitKArgs), E]),
+    "loom_paged_prefill_spec_new": (i32, [u64] * 7 + [P(PagedPrefillSpec), E]),
+    "loom_paged_prefill_validate_metadata": (
+        i32, [P(PagedPrefillSpec), pi32, u64, pi32, u64, pi32, u64, pi32, u64, E]),
+    "loom_paged_prefill_causal_kv_end": (
+        i32, [P(PagedPrefillSpec), pi32, pi32, pi32, u64, u64, P(u64)]),
+    "loom_prefill_provider_load": (i32, [C.c_int, P(vp), E]),
+    "loom_prefill_provider_free": (None, [vp]),
+    "loom_prefill_provider_plan_bf16_paged": (i32, [vp, P(PagedPrefillSpec), P(vp), E]),
+    "loom_prefill_provider_plan_bf16_paged_options": (
+        i32, [vp, P(PagedPrefillSpec), P(PagedPrefillPlanOptions), P(vp), E]),
+    "loom_paged_prefill_plan_free": (None, [vp]),
+    "loom_paged_prefill_plan_get_info": (None, [vp, P(PagedPrefillPlanInfo)]),
+    "loom_paged_prefill_enqueue": (i32, [vp, vp, P(PagedPrefillArgs), E]),
     "loom_rope_provider_load": (i32, [C.c_int, P(vp), E]),
     "loom_rope_provider_free": (None, [vp]),
     "loom_rope_provider_plan_bf16_paged_append": (i32, [vp, P(RopeAppendSpec), P(vp), E]),

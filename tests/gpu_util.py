@@ -108,3 +108,39 @@ def compare_decode(oracle, out, lse, ref_out, ref_lse, max_abs=0.015625, mean_ab
     return dict(max_abs=float(diff.max()), mean_abs=float(diff.mean()),
                 lse_max_abs=float(ld.max()),
                 bit_mismatches=int(np.sum(out != ref_out)))
+
+
+class PrefillRunner:
+    """Plans once and runs paged prefill via the C ABI on torch's current stream."""
+
+    def __init__(self, L, batch, nnz_qo, pool, hq, hkv, **plan_opts):
+        torch = torch_dev()
+        self.L = L
+        self.spec = L.Bf16PagedPrefillSpec(batch, nnz_qo, pool, hq, hkv, 128, 16)
+        self.provider = L.PrefillProvider.load(0)
+        self.plan = self.provider.plan_bf16_paged(self.spec, **plan_opts)
+        self.queue = L.CommandQueue(torch.cuda.current_stream(), 4)
+
+    def run_dev(self, q, k, v, qo, indptr, indices, last, out=None, lse=None):
+        torch = torch_dev()
+        s = self.spec
+        if out is None:
+            out = nan_bf16(s.output_numel)
+        if lse is None:
+            lse = torch.full((s.lse_numel,), float("nan"), dtype=torch.float32, device="cuda")
+        b = self.queue.bindings(9)
+        h = [b.bind_read(x) for x in (q, k, v, qo, indptr, indices, last)]
+        h += [b.bind_read_write(out), b.bind_read_write(lse)]
+        scope = self.queue.begin(b)
+        self.plan.enqueue_into(scope, self.L.Bf16PagedPrefillArgs(
+            h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7].write(), h[8].write()))
+        comp = scope.finish()
+        assert comp.submitted() == 1
+        b = comp.wait()
+        return b.take_read_write(h[7]), b.take_read_write(h[8])
+
+    def run(self, q_u16, k_u16, v_u16, qo, indptr, indices, last):
+        out, lse = self.run_dev(to_dev_bf16(q_u16), to_dev_bf16(k_u16), to_dev_bf16(v_u16),
+                                to_dev_i32(qo), to_dev_i32(indptr), to_dev_i32(indices),
+                                to_dev_i32(last))
+        return bf16_host(out), lse.cpu().numpy()

@@ -214,3 +214,32 @@ def test_single_decode_contracts(L, oracle):
         assert sk.workspace_numel == 8 * parts * 130
         for p in range(parts + 1):
             assert sk.partition_token_range(p) == oracle.split_k_partition(kv_len, parts, p)
+
+
+def test_paged_prefill_contracts_match_oracle(L, oracle):
+    # crates/loom-infer/src/attention/paged_prefill/mod.rs:30-383 through the
+    # C ABI, against the oracle (pinned by the reference's unit tests).
+    import test_oracle_prefill as P
+    s = L.Bf16PagedPrefillSpec(2, 3, 6, 4, 2)
+    assert (s.nnz_qo, s.query_numel, s.kv_pages_numel, s.lse_numel) == (3, 3 * 512, 6 * 16 * 256, 12)
+    assert s.softmax_scale == np.float32(1.0 / np.sqrt(np.float32(128.0)))
+    m = s.validate_metadata([0, 2, 3], [0, 2, 4], [4, 1, 5, 2], [3, 16])
+    os_ = oracle.prefill_spec(2, 3, 6, 4, 2)
+    for r in range(3):
+        for i in range(3):
+            assert m.causal_kv_end(r, i) == oracle.prefill_causal_kv_end(
+                os_, [0, 2, 3], [0, 2, 4], [3, 16], r, i)
+    assert m.physical_page_for_token(0, 18) == (1, 2) and m.physical_page_for_token(0, 19) is None
+    s2 = L.Bf16PagedPrefillSpec(2, 3, 4, 4, 2)
+    for args, (variant, buf, fields) in P.MALFORMED:
+        with pytest.raises(L.ContractError) as e:
+            s2.validate_metadata(*args)
+        assert (e.value.variant, e.value.fields) == (variant, fields), args
+        if buf:
+            assert e.value.operand == buf
+    for dims, variant in [((0, 1, 1, 1, 1), "ZeroDimension"), ((1, 1, 1, 6, 4), "InvalidHeadMapping"),
+                          ((1, 2 ** 31, 1, 1, 1), "ElementCountOverflow"),
+                          ((1, 1, 2 ** 64 - 1, 1, 1), "ElementCountOverflow")]:
+        with pytest.raises(L.ContractError) as e:
+            L.Bf16PagedPrefillSpec(*dims)
+        assert e.value.variant == variant
