@@ -425,6 +425,55 @@ def reference_shapes(L, stream, samples=30):
     return out
 
 
+def prefill_shapes(L, stream, samples=30):
+    """Paged causal prefill at the five shapes the reference times on H20
+    (benchmarks/matched.rs:1355-1425; its eager and long-eager records): eager
+    and graph-replay µs as in reference_shapes, with the reference's H20 medians
+    (loom-infer and FlashInfer) beside them.  Values are synthetic; the page
+    tables are the reference's.  For each shape the algorithmic work is stated:
+    K/V bytes of the distinct pages read once per kv-head and the causal
+    QK+PV FLOPs."""
+    import torch
+    g = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_digests.json")))
+    dev = "cuda"
+    out = {}
+    for c in g["paged_prefill"]["cases"] + g["paged_prefill_long"]["cases"]:
+        B, nnz, pool, hq, hkv = c["batch"], c["nnz_qo"], c["pool"], c["hq"], c["hkv"]
+        spec = L.Bf16PagedPrefillSpec(B, nnz, pool, hq, hkv)
+        plan = L.PrefillProvider.load(0).plan_bf16_paged(spec)
+        t = [torch.randn(n, device=dev).to(torch.bfloat16) for n in
+             (nnz * hq * 128, pool * 16 * hkv * 128, pool * 16 * hkv * 128)]
+        qo, ip, ix, ln = (torch.tensor(c[k], dtype=torch.int32, device=dev)
+                          for k in ("qo_indptr", "indptr", "indices", "last"))
+        o = torch.empty(nnz * hq * 128, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(nnz * hq, dtype=torch.float32, device=dev)
+
+        def bind(b):
+            return L.Bf16PagedPrefillArgs(
+                b.bind_read(t[0]), b.bind_read(t[1]), b.bind_read(t[2]), b.bind_read(qo),
+                b.bind_read(ip), b.bind_read(ix), b.bind_read(ln), b.bind_read_write(o).write(),
+                b.bind_read_write(lse).write())
+        eg = sorted(_timed_enqueues(L, stream, 9, bind, plan.enqueue_into, 100,
+                                    10 if i == 0 else 2) for i in range(samples))
+        gr = _graph_replay(L, 9, 1, bind, plan.enqueue_into, replays=samples)
+        flops, kv_tokens = 0, 0
+        for r in range(B):
+            kv = (c["indptr"][r + 1] - c["indptr"][r] - 1) * 16 + c["last"][r]
+            n = c["qo_indptr"][r + 1] - c["qo_indptr"][r]
+            kv_tokens += kv
+            flops += sum(kv - n + i + 1 for i in range(n)) * hq * 128 * 4
+        e = eg[len(eg) // 2]
+        out[c["name"]] = {
+            "eager_us": round(e, 3), "graph_replay_us": round(gr, 3),
+            "waves": plan.info.waves, "grid_blocks": plan.info.grid_blocks,
+            "causal_gflop": round(flops / 1e9, 4), "TFLOPs": round(flops / (e * 1e-6) / 1e12, 3),
+            "kv_bytes": kv_tokens * hkv * 512,
+            "h20_loom_eager_us": c.get("loom_h20_eager_median_us", c.get("loom_h20_median_us")),
+            "h20_flashinfer_eager_us": c.get("flashinfer_h20_eager_median_us",
+                                             c.get("flashinfer_h20_median_us"))}
+    return out
+
+
 def cpu_append_baseline(app, min_s=3.0):
     """The oracle's explicit-token append (rope/mod.rs + paged_append/mod.rs:
     429-489, single thread) on the config-2 command, repeated for at least
@@ -584,6 +633,10 @@ def main():
         log("[bench] reference published shapes")
         detail["reference_shapes"] = reference_shapes(L, stream)
         log(f"[bench] {detail['reference_shapes']}")
+    if not a.quick and (not a.only or a.only == "prefill"):
+        log("[bench] paged prefill at the reference's shapes")
+        detail["paged_prefill"] = prefill_shapes(L, stream)
+        log(f"[bench] {detail['paged_prefill']}")
     if a.only:
         print(json.dumps(detail), flush=True)
         return

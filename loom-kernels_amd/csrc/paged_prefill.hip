@@ -69,11 +69,20 @@ struct PrefillArgs {
 // request search returns at the first malformed range, prefill.rs:303-313).
 constexpr int64_t kNoTiles = (int64_t)1 << 50;
 
+// Pages in flight per wave (32 VGPRs each): 16-wave workgroups have 128
+// registers per lane and no room for a prefetch; 4 and 8 waves use two (deeper
+// pipelines measured slower on the small shapes).
+#ifndef LOOM_PREFILL_DEPTH
+#define LOOM_PREFILL_DEPTH 2
+#endif
+constexpr int prefill_depth(int w) { return w >= 16 ? 1 : LOOM_PREFILL_DEPTH; }
+
 template <int W>
 struct PrefillSmem {
   int64_t wave_tot[W];
   int32_t req;
   int32_t tile0;
+  int32_t meta[5];     // the located request's qo_indptr pair, page_indptr pair, tail
   u32x4 qfrag[4][64];  // MFMA B fragments of the tile's 16 query columns
   float m[W][16];      // per-wave running max (log2 domain) per column
   float l[W][16];      // per-wave normalizer per column
@@ -113,13 +122,32 @@ __device__ __forceinline__ s16x4 as_s16x4(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(s16x4, u32x2{lo, hi});
 }
 
+// Max / sum over the four 16-lane rows of a wave (the lanes l, l^16, l^32,
+// l^48 share a query column): v_permlane16_swap / v_permlane32_swap, no LDS.
+__device__ __forceinline__ float quad_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 struct PrefillWave {
   const PrefillArgs &a;
   const u32x4 (*qfrag)[64];
   int lane, col, quad, kvh;
   int64_t end_col;  // causal end (exclusive) of this lane's column, 0 if unused
   float m_run, l_run;
-  f32x4 acc[8];     // acc[e][r] = O[column 4 quad + r][dim 8 col + e]
+  f32x4 acc[8];     // acc[e][r] = O[column col][dim 32 quad + 8 r + e]
 
   __device__ void reset() {
     m_run = -INFINITY;
@@ -137,13 +165,11 @@ struct PrefillWave {
                                                   s, 0, 0, 0);
     // s[i] = S[token 4 quad + i][column col]; tokens at or past the column's
     // causal end (which also covers the rows past kv_len) are masked.
-    const int64_t vis = end_col - lt0;
+    const int vis = (int)max<int64_t>(-1, min<int64_t>(16, end_col - lt0));
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = (quad * 4 + i < vis) ? s[i] * a.scale_log2 : -INFINITY;
-    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mx = quad_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // column with nothing visible yet
     const float al = fast_exp2(m_run - m_use);
@@ -152,14 +178,9 @@ struct PrefillWave {
     for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_use);
     l_run = l_run * al + ((p[0] + p[1]) + (p[2] + p[3]));
     m_run = m_new;
-    // rows of acc are columns 4 quad + r: fetch their rescale factors
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(al, quad * 4 + r, 64);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e][r] *= ar;
-    }
-    // Pᵀ as the A fragment (lane: column col, tokens 4 quad + [0, 4)): BF16
+    for (int e = 0; e < 8; ++e) acc[e] *= al;
+    // Pᵀ as the B fragment (lane: column col, tokens 4 quad + [0, 4)): BF16
     // high part and BF16 residual.
     uint32_t pb[4], rb[4];
 #pragma unroll
@@ -167,45 +188,39 @@ struct PrefillWave {
       pb[i] = __float_as_uint(p[i]);
       rb[i] = __float_as_uint(p[i] - __uint_as_float(pb[i] & 0xffff0000u));
     }
-    const s16x4 a_hi = as_s16x4(pack_hi16(pb[0], pb[1]), pack_hi16(pb[2], pb[3]));
-    const s16x4 a_lo = as_s16x4(pack_hi16(rb[0], rb[1]), pack_hi16(rb[2], rb[3]));
+    const s16x4 p_hi = as_s16x4(pack_hi16(pb[0], pb[1]), pack_hi16(pb[2], pb[3]));
+    const s16x4 p_lo = as_s16x4(pack_hi16(rb[0], rb[1]), pack_hi16(rb[2], rb[3]));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      // B fragment of dim 8 col + e: tokens 4 quad + [0, 4) from the V rows
+      // Vᵀ block e as the A fragment: row col is dim 8 col + e, tokens
+      // 4 quad + [0, 4) straight from the V rows this lane loaded
       const int w = e >> 1;
-      const s16x4 b =
+      const s16x4 vt =
           (e & 1) ? as_s16x4(pack_hi16(pg.v[0][w], pg.v[1][w]), pack_hi16(pg.v[2][w], pg.v[3][w]))
                   : as_s16x4(pack_lo16(pg.v[0][w], pg.v[1][w]), pack_lo16(pg.v[2][w], pg.v[3][w]));
-      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a_hi, b, acc[e], 0, 0, 0);
-      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a_lo, b, acc[e], 0, 0, 0);
+      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, p_hi, acc[e], 0, 0, 0);
+      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, p_lo, acc[e], 0, 0, 0);
     }
   }
 
-  // Pages 0..n-1 of this wave's share.  D = 2: a two-deep pipeline (the loads
-  // of page i+1 are issued before page i is consumed); D = 1: load then use
-  // (for 16-wave workgroups, where the other waves hide the latency and the
-  // register budget is 128).  page_tok(i): physical token row of page i's
-  // first row; rows_of(i): valid rows (0 past the end); lt_of(i): logical
-  // token of its first row.  All wave-uniform.
+  // Pages 0..n-1 of this wave's share through a D-deep pipeline: the loads of
+  // page i + D - 1 are issued before page i is consumed (loads past the end
+  // have no valid rows and move no bytes).  page_tok(i): physical token row
+  // of page i's first row; rows_of(i): valid rows (0 past the end); lt_of(i):
+  // logical token of its first row.  All wave-uniform.
   template <int D, class PageTok, class RowsOf, class LtOf>
   __device__ void stream(int n, PageTok page_tok, RowsOf rows_of, LtOf lt_of) {
-    if constexpr (D == 1) {
-      for (int i = 0; i < n; ++i) {
-        PrefillPage pg;
-        load_prefill_page(pg, a, page_tok(i), rows_of(i), lane, kvh);
-        process(pg, lt_of(i));
-      }
-    } else {
-      PrefillPage buf[2];
-      load_prefill_page(buf[0], a, page_tok(0), rows_of(0), lane, kvh);
-      int i = 0;
-      while (true) {
+    PrefillPage buf[D];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          load_prefill_page(buf[s ^ 1], a, page_tok(i + 1), rows_of(i + 1), lane, kvh);
-          process(buf[s], lt_of(i));
-          if (++i >= n) return;
-        }
+    for (int j = 0; j < D - 1; ++j) load_prefill_page(buf[j], a, page_tok(j), rows_of(j), lane, kvh);
+    int i = 0;
+    while (true) {
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        load_prefill_page(buf[(s + D - 1) % D], a, page_tok(i + D - 1), rows_of(i + D - 1), lane,
+                          kvh);
+        process(buf[s], lt_of(i));
+        if (++i >= n) return;
       }
     }
   }
@@ -220,12 +235,11 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   const int kvh = (int)(blockIdx.x % a.hkv);
   const int64_t tile = blockIdx.x / a.hkv;
 
-  // Global guards (prefill.rs:293-300), one round trip.
+  // Metadata in as few dependent round trips as possible: the global guard
+  // words and every request's qo range, page range and tail are loaded
+  // together; the guards are applied after the scan that locates this tile.
   const int32_t qo0 = a.qo[0], qoB = a.qo[a.batch];
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
-  const bool pages_ok = ipB >= 0 && (a.indices_capacity ? (int64_t)ipB <= a.n_indices
-                                                        : (int64_t)ipB == a.n_indices);
-  if (qo0 != 0 || qoB != a.nnz || ip0 != 0 || !pages_ok) return;
 
   // Locate the request owning this tile: prefix of the requests' tile counts.
   if (tid == 0) sm.req = -1;
@@ -233,8 +247,13 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   for (int base = 0; base < a.batch; base += W * 64) {
     const int r = base + tid;
     int64_t cnt = 0;
+    int32_t s0 = 0, s1 = 0, p0 = 0, p1 = 0, t1 = 0;
     if (r < a.batch) {
-      const int32_t s0 = a.qo[r], s1 = a.qo[r + 1];
+      s0 = a.qo[r];
+      s1 = a.qo[r + 1];
+      p0 = a.indptr[r];
+      p1 = a.indptr[r + 1];
+      t1 = a.last[r];
       cnt = (s0 >= 0 && s1 > s0 && s1 <= a.nnz) ? ((int64_t)(s1 - s0) * a.group + 15) / 16
                                                 : kNoTiles;
     }
@@ -252,18 +271,27 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
     if (r < a.batch && tile < incl && tile >= incl - cnt && cnt != kNoTiles) {
       sm.req = r;
       sm.tile0 = (int32_t)(tile - (incl - cnt));
+      sm.meta[0] = s0;
+      sm.meta[1] = s1;
+      sm.meta[2] = p0;
+      sm.meta[3] = p1;
+      sm.meta[4] = t1;
     }
     carry += tot;
     __syncthreads();
     if (carry > tile) break;
   }
+  // Global guards (prefill.rs:293-300).
+  const bool pages_ok = ipB >= 0 && (a.indices_capacity ? (int64_t)ipB <= a.n_indices
+                                                        : (int64_t)ipB == a.n_indices);
+  if (qo0 != 0 || qoB != a.nnz || ip0 != 0 || !pages_ok) return;
   const int r = uni(sm.req);
   if (r < 0) return;
   const int tile0 = uni(sm.tile0);
 
   // Per-request guards (prefill.rs:316-342).
-  const int32_t qs = uni(a.qo[r]), qe = uni(a.qo[r + 1]);
-  const int32_t ps = uni(a.indptr[r]), pe = uni(a.indptr[r + 1]), tl = uni(a.last[r]);
+  const int32_t qs = uni(sm.meta[0]), qe = uni(sm.meta[1]);
+  const int32_t ps = uni(sm.meta[2]), pe = uni(sm.meta[3]), tl = uni(sm.meta[4]);
   if (ps < 0 || pe <= ps || pe > ipB || tl < 1 || tl > 16) return;
   const int req_pages = pe - ps;
   const int64_t kv_len = (int64_t)(req_pages - 1) * 16 + tl;
@@ -271,38 +299,44 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   if ((int64_t)qo_len > kv_len) return;
 
   // This lane's column and the tile's page range.
-  const int64_t fcols = (int64_t)qo_len * a.group;
-  const int64_t f = (int64_t)tile0 * 16 + col;
+  // (fcols <= nnz_qo * Hq fits int32: the plan checks it)
+  const int fcols = qo_len * a.group;
+  const int f = tile0 * 16 + col;
   const bool colv = f < fcols;
-  const int qi = colv ? (int)(f / a.group) : 0;
-  const int gh = colv ? (int)(f - (int64_t)qi * a.group) : 0;
-  const int64_t f_last = min<int64_t>((int64_t)tile0 * 16 + 15, fcols - 1);
-  const int64_t tile_end = kv_len - qo_len + f_last / a.group + 1;
+  const int qi = colv ? (int)((uint32_t)f / (uint32_t)a.group) : 0;
+  const int gh = colv ? f - qi * a.group : 0;
+  const int f_last = min(tile0 * 16 + 15, fcols - 1);
+  const int64_t tile_end = kv_len - qo_len + (int)((uint32_t)f_last / (uint32_t)a.group) + 1;
   const int npages = (int)((tile_end + 15) / 16);
+  const int mine = npages > wave ? (npages - wave + W - 1) / W : 0;
 
-  // Every page index of the request is checked (the reference rejects the
-  // whole request), strided over the workgroup; the verdict is read after
-  // the stream.
+  // One round trip for: every page index of the request (the reference
+  // rejects the whole request; strided over the workgroup, the verdict is
+  // read after the stream), the query tile (wave 0, into LDS) and each wave's
+  // first block of page indices.
   bool bad = false;
   for (int i = tid; i < req_pages; i += W * 64) {
     const int32_t x = a.indices[ps + i];
     bad |= x < 0 || (int64_t)x >= a.pool;
   }
+  int idx = lane < min(mine, 64) ? a.indices[ps + wave + W * lane] : 0;
   if (wave == 0) {
     const uint16_t *qp = a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 +
                          quad * 8;
+    u32x4 qr[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) sm.qfrag[c][lane] = colv ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < 4; ++c) qr[c] = colv ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sm.qfrag[c][lane] = qr[c];
   }
   __syncthreads();
 
   PrefillWave w{a, sm.qfrag, lane, col, quad, kvh};
   w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
   w.reset();
-  const int mine = npages > wave ? (npages - wave + W - 1) / W : 0;
   for (int s0 = 0; s0 < mine; s0 += 64) {
     const int n = min(mine - s0, 64);
-    const int idx = lane < n ? a.indices[ps + wave + W * (s0 + lane)] : 0;
+    if (s0 > 0) idx = lane < n ? a.indices[ps + wave + W * (s0 + lane)] : 0;
     const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
     auto page_tok = [&](int i) {
       return (int64_t)__builtin_amdgcn_readlane(idx, min(i, n - 1)) * 16;
@@ -312,34 +346,31 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
       return wave + W * (s0 + i) == req_pages - 1 ? (int)tl : 16;
     };
     auto lt_of = [&](int i) { return (int64_t)(wave + W * (s0 + i)) * 16; };
-    w.template stream<(W >= 16 ? 1 : 2)>(n, page_tok, rows_of, lt_of);
+    w.template stream<prefill_depth(W)>(n, page_tok, rows_of, lt_of);
   }
 
   // Wave states -> LDS; an invalid page index anywhere in the request keeps
-  // its sentinels.
-  float l_tot = w.l_run + __shfl_xor(w.l_run, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  // its sentinels.  Every value below belongs to the lane's own column.
+  const float l_tot = quad_sum(w.l_run);
   if (quad == 0) {
     sm.m[wave][col] = w.m_run;
     sm.l[wave][col] = l_tot;
   }
   if (__syncthreads_or(bad)) return;
-
-  float M[4];
+  float M = -INFINITY;
 #pragma unroll
-  for (int r4 = 0; r4 < 4; ++r4) {
-    const int c = quad * 4 + r4;
-    float mm = -INFINITY;
+  for (int wv = 0; wv < W; ++wv) M = fmaxf(M, sm.m[wv][col]);
+  {
+    const float fac = M == -INFINITY ? 0.0f : fast_exp2(w.m_run - M);
 #pragma unroll
-    for (int wv = 0; wv < W; ++wv) mm = fmaxf(mm, sm.m[wv][c]);
-    M[r4] = mm;
-    const float fac = mm == -INFINITY ? 0.0f : fast_exp2(sm.m[wave][c] - mm);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) w.acc[e][r4] *= fac;
+    for (int e = 0; e < 8; ++e) w.acc[e] *= fac;
   }
-  // Deterministic tree sum of the W accumulators, half of them per pass.
+  // Deterministic tree sum of the accumulators of the waves that streamed
+  // pages (wave w streamed iff w < npages), half of them per pass.
+  const int active = min(npages, W);
 #pragma unroll
   for (int s = W / 2; s >= 1; s >>= 1) {
+    if (s >= active) continue;  // waves s.. hold nothing: skip the round (uniform)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       if (wave >= s && wave < 2 * s)
@@ -349,29 +380,26 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
       if (wave < s)
 #pragma unroll
         for (int e = 0; e < 4; ++e) w.acc[4 * h + e] += sm.red[wave][e][lane];
-      __syncthreads();
+      if (s > 1 || h == 0) __syncthreads();
     }
   }
-  if (wave != 0) return;
+  if (wave != 0 || !colv) return;
+  float L = 0.0f;
+#pragma unroll
+  for (int wv = 0; wv < W; ++wv) L = fmaf(sm.l[wv][col], fast_exp2(sm.m[wv][col] - M), L);
+  const float inv = 1.0f / L;
+  const int64_t row_head = (int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh;
+  uint16_t *orow = a.out + row_head * 128 + quad * 32;
 #pragma unroll
   for (int r4 = 0; r4 < 4; ++r4) {
-    const int c = quad * 4 + r4;
-    const int64_t fc = (int64_t)tile0 * 16 + c;
-    if (fc >= fcols) continue;
-    float L = 0.0f;
-#pragma unroll
-    for (int wv = 0; wv < W; ++wv) L = fmaf(sm.l[wv][c], fast_exp2(sm.m[wv][c] - M[r4]), L);
-    const int rq = (int)(fc / a.group);
-    const int hh = (int)(fc - (int64_t)rq * a.group);
-    const int64_t row_head = (int64_t)(qs + rq) * a.hq + (int64_t)kvh * a.group + hh;
     u32x4 o;
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2)
-      o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] / L) |
-              ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] / L) << 16);
-    *reinterpret_cast<u32x4 *>(a.out + row_head * 128 + col * 8) = o;
-    if (col == 0) a.lse[row_head] = M[r4] + __log2f(L);
+      o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv) |
+              ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv) << 16);
+    *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
   }
+  if (quad == 0) a.lse[row_head] = M + __log2f(L);
 }
 
 }  // namespace
@@ -389,10 +417,12 @@ namespace {
 // Waves per workgroup from the average page capacity per request (the
 // reference picks its kernel the same way, prefill.rs:2417-2426): short
 // tables are latency-bound (fewer waves, cheaper merge), long ones split the
-// causal range over more waves.
+// causal range over eight.  Sixteen waves (no register room for a prefetch)
+// measured slower on every shape of the reference's records; they stay
+// available as a plan option.
 uint32_t waves_for(const loom_paged_prefill_spec_t &s) {
   const uint64_t avg_pages = s.max_num_pages / s.batch_size;
-  return avg_pages <= 8 ? 4u : avg_pages <= 32 ? 8u : 16u;
+  return avg_pages <= 8 ? 4u : 8u;
 }
 
 loom_status_t require_aligned(const char *name, uintptr_t ptr, uintptr_t alignment,

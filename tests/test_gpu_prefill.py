@@ -260,3 +260,36 @@ def test_enqueue_rejections(L, oracle):
         r.run_dev(dq, dk, dv, dqo, dip, dix, dlast, out=big[4:4 + r.spec.output_numel])
     assert e.value.variant == "MisalignedBuffer" and e.value.operand == "O"
     torch.cuda.synchronize()
+
+
+def test_prefill_graph_replays_match_eager(L, oracle):
+    """gates/paged_prefill.rs:382-526: capture one prefill command, replay it
+    with eager work and host synchronization between replays, and compare
+    every replay with the eager result bit for bit."""
+    import torch
+    case = GOLDEN["paged_prefill"]["cases"][2]  # gqa4_reordered_reuse, as the reference's graph gate
+    log("prefill graph replay")
+    q, k, v = gate_inputs(oracle, case)
+    B, nnz, pool, hq, hkv = (case[x] for x in ("batch", "nnz_qo", "pool", "hq", "hkv"))
+    meta = (case["qo_indptr"], case["indptr"], case["indices"], case["last"])
+    ref_out, ref_lse = oracle.prefill(oracle.prefill_spec(B, nnz, pool, hq, hkv), q, k, v, *meta)
+    r = PrefillRunner(L, B, nnz, pool, hq, hkv)
+    eager_o, eager_l = r.run(q, k, v, *meta)
+    compare_decode(oracle, eager_o, eager_l, ref_out, ref_lse)
+    ins = [to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v)] + [to_dev_i32(m) for m in meta]
+    out = nan_bf16(r.spec.output_numel)
+    lse = torch.full((r.spec.lse_numel,), float("nan"), dtype=torch.float32, device="cuda")
+    gq = L.GraphQueue(0, 1)
+    b = gq.bindings(9)
+    h = [b.bind_read(x) for x in ins] + [b.bind_read_write(out), b.bind_read_write(lse)]
+    args = L.Bf16PagedPrefillArgs(*h[:7], h[7].write(), h[8].write())
+    exec_ = gq.capture(b, lambda scope: r.plan.enqueue_into(scope, args)).instantiate()
+    del ins
+    for i in range(1, 4):
+        out.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        exec_.launch().wait()
+        assert np.array_equal(bf16_host(out), eager_o), f"replay {i}"
+        assert np.array_equal(lse.cpu().numpy(), eager_l), f"replay {i}"
+    exec_.into_bindings()
