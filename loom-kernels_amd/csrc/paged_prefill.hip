@@ -178,8 +178,11 @@ struct PrefillWave {
     for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_use);
     l_run = l_run * al + ((p[0] + p[1]) + (p[2] + p[3]));
     m_run = m_new;
+    // Rescale only when some column's max moved (after the first pages of a
+    // stream it rarely does); the branch is wave-uniform.
+    if (__builtin_amdgcn_ballot_w64(al != 1.0f))
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= al;
+      for (int e = 0; e < 8; ++e) acc[e] *= al;
     // Pᵀ as the B fragment (lane: column col, tokens 4 quad + [0, 4)): BF16
     // high part and BF16 residual.
     uint32_t pb[4], rb[4];
@@ -307,8 +310,10 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   const int gh = colv ? f - qi * a.group : 0;
   const int f_last = min(tile0 * 16 + 15, fcols - 1);
   const int64_t tile_end = kv_len - qo_len + (int)((uint32_t)f_last / (uint32_t)a.group) + 1;
-  const int npages = (int)((tile_end + 15) / 16);
-  const int mine = npages > wave ? (npages - wave + W - 1) / W : 0;
+  // (the page counts are wave-uniform; pinning them to SGPRs keeps the buffer
+  // resources below scalar, with no waterfall loops around the loads)
+  const int npages = uni((int)((tile_end + 15) / 16));
+  const int mine = uni(npages > wave ? (npages - wave + W - 1) / W : 0);
 
   // One round trip for: every page index of the request (the reference
   // rejects the whole request; strided over the workgroup, the verdict is
@@ -335,15 +340,15 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
   w.reset();
   for (int s0 = 0; s0 < mine; s0 += 64) {
-    const int n = min(mine - s0, 64);
+    const int n = uni(min(mine - s0, 64));
     if (s0 > 0) idx = lane < n ? a.indices[ps + wave + W * (s0 + lane)] : 0;
     const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
     auto page_tok = [&](int i) {
-      return (int64_t)__builtin_amdgcn_readlane(idx, min(i, n - 1)) * 16;
+      return (int64_t)__builtin_amdgcn_readlane(idx, uni(min(i, n - 1))) * 16;
     };
     auto rows_of = [&](int i) {
       if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
-      return wave + W * (s0 + i) == req_pages - 1 ? (int)tl : 16;
+      return uni(wave + W * (s0 + i) == req_pages - 1 ? (int)tl : 16);
     };
     auto lt_of = [&](int i) { return (int64_t)(wave + W * (s0 + i)) * 16; };
     w.template stream<prefill_depth(W)>(n, page_tok, rows_of, lt_of);
@@ -414,16 +419,13 @@ struct loom_paged_prefill_plan {
 };
 
 namespace {
-// Waves per workgroup from the average page capacity per request (the
-// reference picks its kernel the same way, prefill.rs:2417-2426): short
-// tables are latency-bound (fewer waves, cheaper merge), long ones split the
-// causal range over eight.  Sixteen waves (no register room for a prefetch)
-// measured slower on every shape of the reference's records; they stay
-// available as a plan option.
-uint32_t waves_for(const loom_paged_prefill_spec_t &s) {
-  const uint64_t avg_pages = s.max_num_pages / s.batch_size;
-  return avg_pages <= 8 ? 4u : 8u;
-}
+// Waves per workgroup.  The reference picks its kernel from the average page
+// capacity per request (prefill.rs:2417-2426); here four waves measured
+// fastest on every shape of the reference's records, short and long (the
+// per-page dependency chain, not load latency, bounds a wave, and deeper
+// prefetch or more waves per tile did not shorten it), so the default is
+// four whatever the spec; 8 and 16 stay available as plan options.
+uint32_t waves_for(const loom_paged_prefill_spec_t &) { return 4u; }
 
 loom_status_t require_aligned(const char *name, uintptr_t ptr, uintptr_t alignment,
                               loom_error_t *err) {
