@@ -531,7 +531,7 @@ typedef enum loom_paged_prefill_algorithm {
 } loom_paged_prefill_algorithm_t;
 
 typedef struct loom_paged_prefill_plan_options {
-  uint32_t waves; /* waves per workgroup: 0 (chosen from the spec), 4, 8 or 16 */
+  uint32_t waves; /* waves per workgroup: 0 (the default, four), 4, 8 or 16 */
   uint32_t flags; /* 0 or LOOM_PLAN_PAGE_INDICES_CAPACITY */
 } loom_paged_prefill_plan_options_t;
 
