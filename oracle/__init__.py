@@ -61,6 +61,12 @@ class PrefillSpec(C.Structure):
                 ("num_kv_heads", C.c_size_t), ("softmax_scale", C.c_float)]
 
 
+class RaggedSpec(C.Structure):
+    _fields_ = [("batch_size", C.c_size_t), ("nnz_qo", C.c_size_t), ("nnz_kv", C.c_size_t),
+                ("num_query_heads", C.c_size_t), ("num_kv_heads", C.c_size_t),
+                ("softmax_scale", C.c_float)]
+
+
 class SingleSpec(C.Structure):
     _fields_ = [("kv_len", C.c_size_t), ("num_query_heads", C.c_size_t),
                 ("num_kv_heads", C.c_size_t), ("softmax_scale", C.c_float)]
@@ -88,6 +94,7 @@ def lib():
         _lib.lo_deterministic_bf16.argtypes = [C.c_size_t, C.c_uint64, C.c_void_p]
         _lib.lo_paged_request_kv_len.restype = C.c_int64
         _lib.lo_prefill_causal_kv_end.restype = C.c_int64
+        _lib.lo_ragged_causal_kv_end.restype = C.c_int64
     return _lib
 
 
@@ -243,6 +250,53 @@ def prefill_requests(spec, q, k, v, qo_indptr, indptr, indices, last, r0, r1, ou
     lib().lo_prefill_requests(C.byref(spec), _p(q), _p(k), _p(v), _p(qo_indptr), _p(indptr),
                               _p(indices), _p(last), C.c_size_t(r0), C.c_size_t(r1),
                               _p(out), _p(lse))
+
+
+# ---- ragged causal prefill -------------------------------------------------
+def ragged_spec(batch, nnz_qo, nnz_kv, hq, hkv, head_dim=128) -> RaggedSpec:
+    s, e = RaggedSpec(), _Err()
+    _check(lib().lo_ragged_spec_new(*(C.c_size_t(x) for x in (batch, nnz_qo, nnz_kv, hq, hkv,
+                                                                head_dim)),
+                                    C.byref(s), C.byref(e)), e)
+    return s
+
+
+def ragged_validate(spec, qo_indptr, kv_indptr):
+    qo_indptr, kv_indptr = _i32(qo_indptr), _i32(kv_indptr)
+    e = _Err()
+    _check(lib().lo_ragged_validate(C.byref(spec), _p(qo_indptr), C.c_size_t(qo_indptr.size),
+                                    _p(kv_indptr), C.c_size_t(kv_indptr.size), C.byref(e)), e)
+
+
+def ragged_causal_kv_end(spec, qo_indptr, kv_indptr, request, query_index):
+    qo_indptr, kv_indptr = _i32(qo_indptr), _i32(kv_indptr)
+    r = lib().lo_ragged_causal_kv_end(C.byref(spec), _p(qo_indptr), _p(kv_indptr),
+                                      C.c_size_t(request), C.c_size_t(query_index))
+    return None if r < 0 else int(r)
+
+
+def ragged(spec, q, k, v, qo_indptr, kv_indptr, out_len=None, lse_len=None):
+    """Returns (out bf16 bits [nnz_qo,Hq,128], lse f32 [nnz_qo,Hq]); raises OracleError."""
+    qo_indptr, kv_indptr = _i32(qo_indptr), _i32(kv_indptr)
+    q, k, v = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v))
+    nq = spec.nnz_qo * spec.num_query_heads * HEAD_DIM
+    out = np.full(nq if out_len is None else out_len, 0x7FC0, dtype=np.uint16)
+    n_l = spec.nnz_qo * spec.num_query_heads if lse_len is None else lse_len
+    lse = np.full(max(n_l, 1), np.nan, dtype=np.float32)
+    e = _Err()
+    _check(lib().lo_ragged_reference(
+        C.byref(spec), _p(q), C.c_size_t(q.size), _p(k), C.c_size_t(k.size), _p(v),
+        C.c_size_t(v.size), _p(qo_indptr), C.c_size_t(qo_indptr.size), _p(kv_indptr),
+        C.c_size_t(kv_indptr.size), _p(out), C.c_size_t(out.size), _p(lse), C.c_size_t(n_l),
+        C.byref(e)), e)
+    return out, lse
+
+
+def ragged_requests(spec, q, k, v, qo_indptr, kv_indptr, r0, r1, out, lse):
+    """Restated loop over requests [r0, r1) (bounded CPU-baseline sample)."""
+    qo_indptr, kv_indptr = _i32(qo_indptr), _i32(kv_indptr)
+    lib().lo_ragged_requests(C.byref(spec), _p(q), _p(k), _p(v), _p(qo_indptr), _p(kv_indptr),
+                             C.c_size_t(r0), C.c_size_t(r1), _p(out), _p(lse))
 
 
 # ---- single decode / split-K ----------------------------------------------

@@ -709,3 +709,126 @@ int lo_prefill_reference(const lo_prefill_spec *s, const uint16_t *q, size_t nq,
   lo_prefill_requests(s, q, k, v, qo, indptr, indices, last, 0, s->batch_size, out, lse);
   return LO_OK;
 }
+
+/* ------------------------------------------------------------------------ */
+/* ragged_prefill/mod.rs:27-79 Bf16RaggedPrefillSpec::new. */
+int lo_ragged_spec_new(size_t batch, size_t nnz_qo, size_t nnz_kv, size_t hq, size_t hkv,
+                       size_t head_dim, lo_ragged_spec *out, lo_error *err) {
+  if (batch == 0 || nnz_qo == 0 || nnz_kv == 0 || hq == 0 || hkv == 0 || head_dim == 0)
+    return fail(err, LO_ZERO_DIMENSION, NULL, 0, 0, 0, 0);
+  if (head_dim != HEAD_DIM)
+    return fail(err, LO_UNSUPPORTED_HEAD_DIMENSION, NULL, HEAD_DIM, (int64_t)head_dim, 0, 0);
+  if (hq % hkv != 0)
+    return fail(err, LO_INVALID_HEAD_MAPPING, NULL, (int64_t)hq, (int64_t)hkv, 0, 0);
+  if (nnz_qo > (size_t)INT32_MAX || nnz_kv > (size_t)INT32_MAX)
+    return fail(err, LO_ELEMENT_COUNT_OVERFLOW, NULL, 0, 0, 0, 0);
+  size_t t;
+  if (batch == SIZE_MAX || mul_overflows(nnz_qo, hq, &t) || mul_overflows(t, head_dim, &t) ||
+      mul_overflows(nnz_kv, hkv, &t) || mul_overflows(t, head_dim, &t))
+    return fail(err, LO_ELEMENT_COUNT_OVERFLOW, NULL, 0, 0, 0, 0);
+  out->batch_size = batch;
+  out->nnz_qo = nnz_qo;
+  out->nnz_kv = nnz_kv;
+  out->num_query_heads = hq;
+  out->num_kv_heads = hkv;
+  out->softmax_scale = 1.0f / sqrtf((float)head_dim);
+  return LO_OK;
+}
+
+/* ragged_prefill/mod.rs:169-193 validate_indptr. */
+static int ragged_indptr(lo_error *err, const char *buffer, const int32_t *p, size_t B,
+                         size_t total) {
+  if (p[0] != 0) return fail(err, LO_INVALID_INDPTR_START, buffer, p[0], 0, 0, 0);
+  for (size_t r = 0; r < B; ++r) {
+    if (p[r + 1] < p[r]) return fail(err, LO_NON_MONOTONIC_INDPTR, buffer, (int64_t)r, p[r],
+                                     p[r + 1], 0);
+    if (p[r + 1] == p[r]) return fail(err, LO_EMPTY_RAGGED_REQUEST, buffer, (int64_t)r, 0, 0, 0);
+  }
+  return require_len(err, buffer, (size_t)p[B], total);
+}
+
+/* ragged_prefill/mod.rs:140-167 validate_metadata. */
+int lo_ragged_validate(const lo_ragged_spec *s, const int32_t *qo, size_t n_qo,
+                       const int32_t *kv, size_t n_kv, lo_error *err) {
+  int rc;
+  const size_t B = s->batch_size;
+  if ((rc = require_len(err, "qo_indptr", n_qo, B + 1))) return rc;
+  if ((rc = require_len(err, "kv_indptr", n_kv, B + 1))) return rc;
+  if ((rc = ragged_indptr(err, "qo_indptr", qo, B, s->nnz_qo))) return rc;
+  if ((rc = ragged_indptr(err, "kv_indptr", kv, B, s->nnz_kv))) return rc;
+  for (size_t r = 0; r < B; ++r) {
+    int64_t qo_len = (int64_t)qo[r + 1] - qo[r], kv_len = (int64_t)kv[r + 1] - kv[r];
+    if (qo_len > kv_len)
+      return fail(err, LO_RAGGED_QUERY_LONGER_THAN_KV, NULL, (int64_t)r, qo_len, kv_len, 0);
+  }
+  return LO_OK;
+}
+
+/* ragged_prefill/mod.rs:233-242: kv_start + kv_len - qo_len + query_index + 1. */
+int64_t lo_ragged_causal_kv_end(const lo_ragged_spec *s, const int32_t *qo, const int32_t *kv,
+                                size_t request, size_t query_index) {
+  if (request >= s->batch_size) return -1;
+  int64_t qo_len = (int64_t)qo[request + 1] - qo[request];
+  int64_t kv_len = (int64_t)kv[request + 1] - kv[request];
+  if ((int64_t)query_index >= qo_len) return -1;
+  return (int64_t)kv[request] + kv_len - qo_len + (int64_t)query_index + 1;
+}
+
+/* ragged_prefill/mod.rs:262-329: the per-(query row, query head) loop. */
+void lo_ragged_requests(const lo_ragged_spec *s, const uint16_t *q, const uint16_t *k,
+                        const uint16_t *v, const int32_t *qo, const int32_t *kv, size_t r0,
+                        size_t r1, uint16_t *out, float *lse) {
+  const size_t hq = s->num_query_heads, hkv = s->num_kv_heads, group = hq / hkv;
+  float state[HEAD_DIM];
+  for (size_t r = r0; r < r1; ++r) {
+    const int64_t kv_start = kv[r];
+    for (size_t row = (size_t)qo[r]; row < (size_t)qo[r + 1]; ++row) {
+      const int64_t end = lo_ragged_causal_kv_end(s, qo, kv, r, row - (size_t)qo[r]);
+      for (size_t h = 0; h < hq; ++h) {
+        const uint16_t *qrow = q + (row * hq + h) * HEAD_DIM;
+        const size_t kvh = h / group;
+        float max_score = 0.0f, normalizer = 0.0f;
+        memset(state, 0, sizeof(state));
+        for (int64_t t = kv_start; t < end; ++t) {
+          size_t kv_off = ((size_t)t * hkv + kvh) * HEAD_DIM;
+          float score = dot_bf16(qrow, k + kv_off) * s->softmax_scale;
+          if (t == kv_start) {
+            max_score = score;
+            normalizer = 1.0f;
+            for (unsigned c = 0; c < HEAD_DIM; ++c) state[c] = lo_bf16_to_f32(v[kv_off + c]);
+            continue;
+          }
+          float next_max = fmaxf(max_score, score);
+          float prev_w = expf(max_score - next_max);
+          float cur_w = expf(score - next_max);
+          normalizer = normalizer * prev_w + cur_w;
+          for (unsigned c = 0; c < HEAD_DIM; ++c)
+            state[c] = state[c] * prev_w + lo_bf16_to_f32(v[kv_off + c]) * cur_w;
+          max_score = next_max;
+        }
+        uint16_t *orow = out + (row * hq + h) * HEAD_DIM;
+        for (unsigned c = 0; c < HEAD_DIM; ++c)
+          orow[c] = lo_bf16_from_f32(state[c] / normalizer);
+        lse[row * hq + h] = (max_score + logf(normalizer)) * LOG2E_F32;
+      }
+    }
+  }
+}
+
+/* ragged_prefill/mod.rs:246-329 ragged_prefill_bf16_reference. */
+int lo_ragged_reference(const lo_ragged_spec *s, const uint16_t *q, size_t nq,
+                        const uint16_t *k, size_t nk, const uint16_t *v, size_t nv,
+                        const int32_t *qo, size_t n_qo, const int32_t *kv, size_t n_kv,
+                        uint16_t *out, size_t nout, float *lse, size_t nlse, lo_error *err) {
+  const size_t qn = s->nnz_qo * s->num_query_heads * HEAD_DIM;
+  const size_t kvn = s->nnz_kv * s->num_kv_heads * HEAD_DIM;
+  int rc;
+  if ((rc = require_len(err, "Q", nq, qn))) return rc;
+  if ((rc = require_len(err, "K", nk, kvn))) return rc;
+  if ((rc = require_len(err, "V", nv, kvn))) return rc;
+  if ((rc = require_len(err, "O", nout, qn))) return rc;
+  if ((rc = require_len(err, "LSE", nlse, s->nnz_qo * s->num_query_heads))) return rc;
+  if ((rc = lo_ragged_validate(s, qo, n_qo, kv, n_kv, err))) return rc;
+  lo_ragged_requests(s, q, k, v, qo, kv, 0, s->batch_size, out, lse);
+  return LO_OK;
+}

@@ -25,6 +25,9 @@
  *     has one query row, the fixture digests of its evidence records, and the
  *     f64 brute force (its recorded output digests come from GPU runs with
  *     bit mismatches, so they are not oracle pins);
+ *   - ragged prefill: output digests of the reference's ragged correctness
+ *     records with 0 GPU mismatches (mha_equal_lengths, mqa_append_mixed,
+ *     gqa4_mixed), its unit tests' known answers and error matrices;
  *   - validation: the known-answer mapping tables and error matrices of the
  *     reference's unit tests;
  *   - closed forms (Q=0 => mean(V), LSE=log2(L); RoPE pos 0 = identity) and
@@ -170,6 +173,28 @@ void lo_prefill_requests(const lo_prefill_spec *s, const uint16_t *q, const uint
                          const int32_t *page_indptr, const int32_t *indices,
                          const int32_t *last, size_t r0, size_t r1, uint16_t *out,
                          float *lse);
+
+/* ---- ragged causal prefill (ragged_prefill/mod.rs) ---- */
+typedef struct lo_ragged_spec {
+  size_t batch_size, nnz_qo, nnz_kv, num_query_heads, num_kv_heads;
+  float softmax_scale;
+} lo_ragged_spec;
+int lo_ragged_spec_new(size_t batch, size_t nnz_qo, size_t nnz_kv, size_t hq, size_t hkv,
+                       size_t head_dim, lo_ragged_spec *out, lo_error *err);
+int lo_ragged_validate(const lo_ragged_spec *s, const int32_t *qo_indptr, size_t n_qo,
+                       const int32_t *kv_indptr, size_t n_kv, lo_error *err);
+/* causal_kv_end (ragged_prefill/mod.rs:233-242): an absolute KV row; -1 for None. */
+int64_t lo_ragged_causal_kv_end(const lo_ragged_spec *s, const int32_t *qo_indptr,
+                                const int32_t *kv_indptr, size_t request, size_t query_index);
+int lo_ragged_reference(const lo_ragged_spec *s, const uint16_t *q, size_t nq,
+                        const uint16_t *k, size_t nk, const uint16_t *v, size_t nv,
+                        const int32_t *qo_indptr, size_t n_qo, const int32_t *kv_indptr,
+                        size_t n_kv, uint16_t *out, size_t nout, float *lse, size_t nlse,
+                        lo_error *err);
+/* Requests [r0, r1) only (bounded CPU-baseline sample; metadata valid). */
+void lo_ragged_requests(const lo_ragged_spec *s, const uint16_t *q, const uint16_t *k,
+                        const uint16_t *v, const int32_t *qo_indptr, const int32_t *kv_indptr,
+                        size_t r0, size_t r1, uint16_t *out, float *lse);
 
 /* ---- RoPE (rope/mod.rs) ---- */
 int lo_rope_pos_ids_reference(size_t tokens, size_t qh, size_t kh, size_t head_dim,
