@@ -474,6 +474,47 @@ def prefill_shapes(L, stream, samples=30):
     return out
 
 
+def ragged_shapes(L, stream, samples=30):
+    """Ragged (contiguous K/V) causal prefill at the three shapes the reference
+    times on H20 (benchmarks/matched.rs:1436-1465; its cp-async eager record),
+    measured as prefill_shapes."""
+    import torch
+    g = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_digests.json")))
+    dev = "cuda"
+    out = {}
+    for c in g["ragged_prefill"]["timing_cases"]:
+        B, nnz, nkv, hq, hkv = c["batch"], c["nnz_qo"], c["nnz_kv"], c["hq"], c["hkv"]
+        spec = L.Bf16RaggedPrefillSpec(B, nnz, nkv, hq, hkv)
+        plan = L.PrefillProvider.load(0).plan_bf16_ragged(spec)
+        t = [torch.randn(n, device=dev).to(torch.bfloat16) for n in
+             (nnz * hq * 128, nkv * hkv * 128, nkv * hkv * 128)]
+        qo, kv = (torch.tensor(c[k], dtype=torch.int32, device=dev)
+                  for k in ("qo_indptr", "kv_indptr"))
+        o = torch.empty(nnz * hq * 128, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(nnz * hq, dtype=torch.float32, device=dev)
+
+        def bind(b):
+            return L.Bf16RaggedPrefillArgs(
+                b.bind_read(t[0]), b.bind_read(t[1]), b.bind_read(t[2]), b.bind_read(qo),
+                b.bind_read(kv), b.bind_read_write(o).write(), b.bind_read_write(lse).write())
+        eg = sorted(_timed_enqueues(L, stream, 7, bind, plan.enqueue_into, 100,
+                                    10 if i == 0 else 2) for i in range(samples))
+        gr = _graph_replay(L, 7, 1, bind, plan.enqueue_into, replays=samples)
+        flops = 0
+        for r in range(B):
+            kvl = c["kv_indptr"][r + 1] - c["kv_indptr"][r]
+            n = c["qo_indptr"][r + 1] - c["qo_indptr"][r]
+            flops += sum(kvl - n + i + 1 for i in range(n)) * hq * 128 * 4
+        e = eg[len(eg) // 2]
+        out[c["name"]] = {
+            "eager_us": round(e, 3), "graph_replay_us": round(gr, 3),
+            "waves": plan.info.waves, "grid_blocks": plan.info.grid_blocks,
+            "causal_gflop": round(flops / 1e9, 4), "TFLOPs": round(flops / (e * 1e-6) / 1e12, 3),
+            "h20_loom_eager_us": c["loom_h20_eager_median_us"],
+            "h20_flashinfer_eager_us": c["flashinfer_h20_eager_median_us"]}
+    return out
+
+
 def cpu_append_baseline(app, min_s=3.0):
     """The oracle's explicit-token append (rope/mod.rs + paged_append/mod.rs:
     429-489, single thread) on the config-2 command, repeated for at least
@@ -637,6 +678,8 @@ def main():
         log("[bench] paged prefill at the reference's shapes")
         detail["paged_prefill"] = prefill_shapes(L, stream)
         log(f"[bench] {detail['paged_prefill']}")
+        detail["ragged_prefill"] = ragged_shapes(L, stream)
+        log(f"[bench] {detail['ragged_prefill']}")
     if a.only:
         print(json.dumps(detail), flush=True)
         return

@@ -586,6 +586,84 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
                                          loom_error_t *err);
 
 /* ------------------------------------------------------------------------ */
+/* Ragged causal prefill, crates/loom-infer/src/attention/ragged_prefill/     */
+/* mod.rs: Q/O [nnz_qo, Hq, 128], K/V [nnz_kv, Hkv, 128] contiguous NHD rows,  */
+/* both ragged by i32 indptr arrays; same bottom-right causal mask.          */
+typedef struct loom_ragged_prefill_spec {
+  uint64_t batch_size;
+  uint64_t nnz_qo;
+  uint64_t nnz_kv;
+  uint64_t num_query_heads;
+  uint64_t num_kv_heads;
+  float softmax_scale;
+} loom_ragged_prefill_spec_t;
+
+/* Bf16RaggedPrefillSpec::new, ragged_prefill/mod.rs:27-79. */
+loom_status_t loom_ragged_prefill_spec_new(uint64_t batch_size, uint64_t nnz_qo,
+                                           uint64_t nnz_kv, uint64_t num_query_heads,
+                                           uint64_t num_kv_heads, uint64_t head_dim,
+                                           loom_ragged_prefill_spec_t *out, loom_error_t *err);
+/* validate_metadata, ragged_prefill/mod.rs:140-193. */
+loom_status_t loom_ragged_prefill_validate_metadata(const loom_ragged_prefill_spec_t *spec,
+                                                    const int32_t *qo_indptr, uint64_t n_qo,
+                                                    const int32_t *kv_indptr, uint64_t n_kv,
+                                                    loom_error_t *err);
+/* causal_kv_end, ragged_prefill/mod.rs:233-242 (an absolute KV row) on
+ * validated metadata: LOOM_OK, or LOOM_EMPTY_RAGGED_REQUEST for None. */
+loom_status_t loom_ragged_prefill_causal_kv_end(const loom_ragged_prefill_spec_t *spec,
+                                                const int32_t *qo_indptr,
+                                                const int32_t *kv_indptr, uint64_t request,
+                                                uint64_t query_index, uint64_t *end);
+
+typedef struct loom_ragged_prefill_plan loom_ragged_prefill_plan_t;
+
+typedef struct loom_ragged_prefill_plan_info {
+  loom_ragged_prefill_spec_t spec;
+  int32_t algorithm;          /* LOOM_PAGED_PREFILL_ROW_TILE: the same kernel design */
+  uint32_t waves;
+  uint64_t row_tiles;
+  uint32_t block_threads;
+  uint64_t grid_blocks;
+  uint64_t workspace_numel;   /* 0: this plan needs no workspace */
+} loom_ragged_prefill_plan_info_t;
+
+/* PrefillProvider::plan_bf16_ragged, prefill.rs:2331-2410.  `options` may be
+ * NULL; its `flags` must be 0 (no page table). */
+loom_status_t loom_prefill_provider_plan_bf16_ragged(const loom_prefill_provider_t *provider,
+                                                     const loom_ragged_prefill_spec_t *spec,
+                                                     const loom_paged_prefill_plan_options_t *options,
+                                                     loom_ragged_prefill_plan_t **out,
+                                                     loom_error_t *err);
+void loom_ragged_prefill_plan_free(loom_ragged_prefill_plan_t *plan);
+void loom_ragged_prefill_plan_get_info(const loom_ragged_prefill_plan_t *plan,
+                                       loom_ragged_prefill_plan_info_t *info);
+/* workspace_required_numel, prefill.rs:2640-2646: 0 for this plan. */
+uint64_t loom_ragged_prefill_workspace_numel(const loom_ragged_prefill_plan_t *plan);
+
+/* Bf16RaggedPrefillArgs, prefill.rs:2893-2931.  `workspace` is the optional
+ * with_workspace operand ({0, 0} when absent); this plan needs none and
+ * ignores it. */
+typedef struct loom_ragged_prefill_args {
+  loom_handle_t query;     /* Read<bf16>  [nnz_qo, Hq, 128] */
+  loom_handle_t key;       /* Read<bf16>  [nnz_kv, Hkv, 128] */
+  loom_handle_t value;     /* Read<bf16>  [nnz_kv, Hkv, 128] */
+  loom_handle_t qo_indptr; /* Read<i32>   [B+1] */
+  loom_handle_t kv_indptr; /* Read<i32>   [B+1] */
+  loom_handle_t output;    /* Write<bf16> [nnz_qo, Hq, 128] */
+  loom_handle_t lse;       /* Write<f32>  [nnz_qo, Hq], log2 domain */
+  loom_handle_t workspace; /* optional ReadWrite<f32> */
+} loom_ragged_prefill_args_t;
+
+/* Bf16RaggedPrefillPlan::enqueue_into, prefill.rs:2648-2760: one command, one
+ * kernel.  Device guards as prefill.rs:102-138: invalid global indptr words
+ * write nothing; a row belongs to the first request whose qo range ends after
+ * it, and keeps its sentinels when that request fails its guards. */
+loom_status_t loom_ragged_prefill_enqueue(const loom_ragged_prefill_plan_t *plan,
+                                          loom_command_scope_t *scope,
+                                          const loom_ragged_prefill_args_t *args,
+                                          loom_error_t *err);
+
+/* ------------------------------------------------------------------------ */
 /* Fused RoPE + paged append provider, crates/loom-infer-cuda/src/rope/mod.rs */
 typedef struct loom_rope_provider loom_rope_provider_t;
 typedef struct loom_rope_append_plan loom_rope_append_plan_t;

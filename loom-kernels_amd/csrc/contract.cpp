@@ -660,4 +660,75 @@ loom_status_t loom_paged_prefill_causal_kv_end(const loom_paged_prefill_spec_t *
   return LOOM_OK;
 }
 
+// ---- ragged causal prefill (ragged_prefill/mod.rs) -----------------------------
+// Bf16RaggedPrefillSpec::new, ragged_prefill/mod.rs:27-79.
+loom_status_t loom_ragged_prefill_spec_new(uint64_t batch, uint64_t nnz_qo, uint64_t nnz_kv,
+                                           uint64_t hq, uint64_t hkv, uint64_t head_dim,
+                                           loom_ragged_prefill_spec_t *out, loom_error_t *err) {
+  if (!out) return fail(err, LOOM_NULL_ARGUMENT, "out");
+  if (batch == 0 || nnz_qo == 0 || nnz_kv == 0 || hq == 0 || hkv == 0 || head_dim == 0)
+    return fail(err, LOOM_ZERO_DIMENSION);
+  if (head_dim != loom::kHeadDim)
+    return fail(err, LOOM_UNSUPPORTED_HEAD_DIMENSION, nullptr, loom::kHeadDim, head_dim);
+  if (hq % hkv != 0) return fail(err, LOOM_INVALID_HEAD_MAPPING, nullptr, hq, hkv);
+  if (nnz_qo > (uint64_t)INT32_MAX || nnz_kv > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  uint64_t t;
+  if (batch == UINT64_MAX || mul_ovf(nnz_qo, hq, &t) || mul_ovf(t, head_dim, &t) ||
+      mul_ovf(nnz_kv, hkv, &t) || mul_ovf(t, head_dim, &t))
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  out->batch_size = batch;
+  out->nnz_qo = nnz_qo;
+  out->nnz_kv = nnz_kv;
+  out->num_query_heads = hq;
+  out->num_kv_heads = hkv;
+  out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
+  return loom::ok(err);
+}
+
+namespace {
+// ragged_prefill/mod.rs:169-193 validate_indptr.
+loom_status_t ragged_indptr(loom_error_t *err, const char *buffer, const int32_t *p,
+                            uint64_t B, uint64_t total) {
+  if (p[0] != 0) return fail(err, LOOM_INVALID_INDPTR_START, buffer, p[0]);
+  for (uint64_t r = 0; r < B; ++r) {
+    if (p[r + 1] < p[r]) return fail(err, LOOM_NON_MONOTONIC_INDPTR, buffer, r, p[r], p[r + 1]);
+    if (p[r + 1] == p[r]) return fail(err, LOOM_EMPTY_RAGGED_REQUEST, buffer, r);
+  }
+  return require_len(err, buffer, (uint64_t)p[B], total);
+}
+}  // namespace
+
+// validate_metadata, ragged_prefill/mod.rs:140-167.
+loom_status_t loom_ragged_prefill_validate_metadata(const loom_ragged_prefill_spec_t *s,
+                                                    const int32_t *qo, uint64_t n_qo,
+                                                    const int32_t *kv, uint64_t n_kv,
+                                                    loom_error_t *err) {
+  if (!s) return fail(err, LOOM_NULL_ARGUMENT, "spec");
+  const uint64_t B = s->batch_size;
+  loom_status_t rc;
+  if ((rc = require_len(err, "qo_indptr", n_qo, B + 1))) return rc;
+  if ((rc = require_len(err, "kv_indptr", n_kv, B + 1))) return rc;
+  if ((rc = ragged_indptr(err, "qo_indptr", qo, B, s->nnz_qo))) return rc;
+  if ((rc = ragged_indptr(err, "kv_indptr", kv, B, s->nnz_kv))) return rc;
+  for (uint64_t r = 0; r < B; ++r) {
+    const int64_t ql = (int64_t)qo[r + 1] - qo[r], kl = (int64_t)kv[r + 1] - kv[r];
+    if (ql > kl) return fail(err, LOOM_RAGGED_QUERY_LONGER_THAN_KV, nullptr, r, ql, kl);
+  }
+  return loom::ok(err);
+}
+
+// causal_kv_end, ragged_prefill/mod.rs:233-242.
+loom_status_t loom_ragged_prefill_causal_kv_end(const loom_ragged_prefill_spec_t *s,
+                                                const int32_t *qo, const int32_t *kv,
+                                                uint64_t request, uint64_t query_index,
+                                                uint64_t *end) {
+  if (!s || !end || request >= s->batch_size) return LOOM_EMPTY_RAGGED_REQUEST;
+  const int64_t ql = (int64_t)qo[request + 1] - qo[request];
+  const int64_t kl = (int64_t)kv[request + 1] - kv[request];
+  if ((int64_t)query_index >= ql) return LOOM_EMPTY_RAGGED_REQUEST;
+  *end = (uint64_t)((int64_t)kv[request] + kl - ql + (int64_t)query_index + 1);
+  return LOOM_OK;
+}
+
 }  // extern "C"

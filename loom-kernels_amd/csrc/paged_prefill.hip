@@ -62,6 +62,9 @@ struct PrefillArgs {
   int64_t n_indices;
   float scale_log2;
   int32_t indices_capacity;
+  // Ragged (contiguous) K/V: `indptr` is kv_indptr over [nnz_kv, Hkv, 128]
+  // rows; `indices` and `last` are unused.
+  int32_t nnz_kv;
 };
 
 // Tile count given to a request whose qo range is malformed: larger than any
@@ -80,9 +83,12 @@ constexpr int prefill_depth(int w) { return w >= 16 ? 1 : LOOM_PREFILL_DEPTH; }
 template <int W>
 struct PrefillSmem {
   int64_t wave_tot[W];
+  int32_t wave_max[W];
   int32_t req;
   int32_t tile0;
-  int32_t meta[5];     // the located request's qo_indptr pair, page_indptr pair, tail
+  // the located request's qo_indptr pair, page (or kv) indptr pair, tail, and
+  // the first flattened column it owns
+  int32_t meta[6];
   u32x4 qfrag[4][64];  // MFMA B fragments of the tile's 16 query columns
   float m[W][16];      // per-wave running max (log2 domain) per column
   float l[W][16];      // per-wave normalizer per column
@@ -229,8 +235,8 @@ struct PrefillWave {
   }
 };
 
-template <int W>
-__global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
+template <int W, bool RAGGED>
+__device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
   __shared__ PrefillSmem<W> sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -239,26 +245,63 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   const int64_t tile = blockIdx.x / a.hkv;
 
   // Metadata in as few dependent round trips as possible: the global guard
-  // words and every request's qo range, page range and tail are loaded
+  // words and every request's qo range, page (kv) range and tail are loaded
   // together; the guards are applied after the scan that locates this tile.
   const int32_t qo0 = a.qo[0], qoB = a.qo[a.batch];
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
 
   // Locate the request owning this tile: prefix of the requests' tile counts.
+  // Paged (prefill.rs:303-313): rows belong to the requests before the first
+  // malformed qo range.  Ragged (prefill.rs:111-137): row q belongs to the
+  // first request r with q < qo_indptr[r+1], i.e. r owns the rows from
+  // max(qo_indptr[r], max(qo_indptr[1..r])) to qo_indptr[r+1], and a request
+  // failing its guards keeps its rows' sentinels.
   if (tid == 0) sm.req = -1;
   int64_t carry = 0;
+  int32_t carry_max = 0;
   for (int base = 0; base < a.batch; base += W * 64) {
     const int r = base + tid;
     int64_t cnt = 0;
-    int32_t s0 = 0, s1 = 0, p0 = 0, p1 = 0, t1 = 0;
+    int32_t s0 = 0, s1 = 0, p0 = 0, p1 = 0, t1 = 0, fbeg = 0;
     if (r < a.batch) {
       s0 = a.qo[r];
       s1 = a.qo[r + 1];
       p0 = a.indptr[r];
       p1 = a.indptr[r + 1];
-      t1 = a.last[r];
-      cnt = (s0 >= 0 && s1 > s0 && s1 <= a.nnz) ? ((int64_t)(s1 - s0) * a.group + 15) / 16
-                                                : kNoTiles;
+      if constexpr (!RAGGED) t1 = a.last[r];
+    }
+    if constexpr (RAGGED) {
+      // exclusive running max of the qo ends before r
+      int32_t x = r < a.batch ? s1 : INT32_MIN;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x = max(x, y);
+      }
+      if (lane == 63) sm.wave_max[wave] = x;
+      __syncthreads();
+      int32_t before = carry_max, blk = carry_max;
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        before = i < wave ? max(before, sm.wave_max[i]) : before;
+        blk = max(blk, sm.wave_max[i]);
+      }
+      const int32_t up = __shfl_up(x, 1, 64);
+      const int32_t excl = lane > 0 ? max(before, up) : before;
+      carry_max = blk;
+      if (r < a.batch) {
+        const bool ok = s0 >= 0 && s1 > s0 && s1 <= a.nnz && p0 >= 0 && p1 > p0 &&
+                        p1 <= a.nnz_kv && s1 - s0 <= p1 - p0;
+        const int32_t lo = max(s0, excl);
+        if (ok && s1 > lo) {
+          cnt = ((int64_t)(s1 - lo) * a.group + 15) / 16;
+          fbeg = (lo - s0) * a.group;
+        }
+      }
+    } else {
+      if (r < a.batch)
+        cnt = (s0 >= 0 && s1 > s0 && s1 <= a.nnz) ? ((int64_t)(s1 - s0) * a.group + 15) / 16
+                                                  : kNoTiles;
     }
     const int64_t x = wave_incl_scan64(cnt, lane);
     if (lane == 63) sm.wave_tot[wave] = x;
@@ -279,36 +322,53 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
       sm.meta[2] = p0;
       sm.meta[3] = p1;
       sm.meta[4] = t1;
+      sm.meta[5] = fbeg;
     }
     carry += tot;
     __syncthreads();
     if (carry > tile) break;
   }
-  // Global guards (prefill.rs:293-300).
-  const bool pages_ok = ipB >= 0 && (a.indices_capacity ? (int64_t)ipB <= a.n_indices
-                                                        : (int64_t)ipB == a.n_indices);
-  if (qo0 != 0 || qoB != a.nnz || ip0 != 0 || !pages_ok) return;
+  // Global guards (prefill.rs:293-300 paged, :102-108 ragged).
+  if constexpr (RAGGED) {
+    if (qo0 != 0 || qoB != a.nnz || ip0 != 0 || ipB != a.nnz_kv) return;
+  } else {
+    const bool pages_ok = ipB >= 0 && (a.indices_capacity ? (int64_t)ipB <= a.n_indices
+                                                          : (int64_t)ipB == a.n_indices);
+    if (qo0 != 0 || qoB != a.nnz || ip0 != 0 || !pages_ok) return;
+  }
   const int r = uni(sm.req);
   if (r < 0) return;
   const int tile0 = uni(sm.tile0);
+  const int fbeg = uni(sm.meta[5]);
 
-  // Per-request guards (prefill.rs:316-342).
+  // Per-request guards (paged: prefill.rs:316-342; ragged: applied in the
+  // scan above, a failing request owns no tile).
   const int32_t qs = uni(sm.meta[0]), qe = uni(sm.meta[1]);
-  const int32_t ps = uni(sm.meta[2]), pe = uni(sm.meta[3]), tl = uni(sm.meta[4]);
-  if (ps < 0 || pe <= ps || pe > ipB || tl < 1 || tl > 16) return;
-  const int req_pages = pe - ps;
-  const int64_t kv_len = (int64_t)(req_pages - 1) * 16 + tl;
+  const int32_t ps = uni(sm.meta[2]), pe = uni(sm.meta[3]);
+  int req_pages;
+  int32_t tl;
+  int64_t kv_len;
+  if constexpr (RAGGED) {
+    kv_len = pe - ps;
+    req_pages = (int)((kv_len + 15) / 16);
+    tl = (int32_t)(kv_len - (int64_t)(req_pages - 1) * 16);
+  } else {
+    tl = uni(sm.meta[4]);
+    if (ps < 0 || pe <= ps || pe > ipB || tl < 1 || tl > 16) return;
+    req_pages = pe - ps;
+    kv_len = (int64_t)(req_pages - 1) * 16 + tl;
+  }
   const int qo_len = qe - qs;
   if ((int64_t)qo_len > kv_len) return;
 
   // This lane's column and the tile's page range.
   // (fcols <= nnz_qo * Hq fits int32: the plan checks it)
   const int fcols = qo_len * a.group;
-  const int f = tile0 * 16 + col;
+  const int f = fbeg + tile0 * 16 + col;
   const bool colv = f < fcols;
   const int qi = colv ? (int)((uint32_t)f / (uint32_t)a.group) : 0;
   const int gh = colv ? f - qi * a.group : 0;
-  const int f_last = min(tile0 * 16 + 15, fcols - 1);
+  const int f_last = min(fbeg + tile0 * 16 + 15, fcols - 1);
   const int64_t tile_end = kv_len - qo_len + (int)((uint32_t)f_last / (uint32_t)a.group) + 1;
   // (the page counts are wave-uniform; pinning them to SGPRs keeps the buffer
   // resources below scalar, with no waterfall loops around the loads)
@@ -320,11 +380,14 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   // read after the stream), the query tile (wave 0, into LDS) and each wave's
   // first block of page indices.
   bool bad = false;
-  for (int i = tid; i < req_pages; i += W * 64) {
-    const int32_t x = a.indices[ps + i];
-    bad |= x < 0 || (int64_t)x >= a.pool;
+  int idx = 0;
+  if constexpr (!RAGGED) {
+    for (int i = tid; i < req_pages; i += W * 64) {
+      const int32_t x = a.indices[ps + i];
+      bad |= x < 0 || (int64_t)x >= a.pool;
+    }
+    idx = lane < min(mine, 64) ? a.indices[ps + wave + W * lane] : 0;
   }
-  int idx = lane < min(mine, 64) ? a.indices[ps + wave + W * lane] : 0;
   if (wave == 0) {
     const uint16_t *qp = a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 +
                          quad * 8;
@@ -341,9 +404,10 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   w.reset();
   for (int s0 = 0; s0 < mine; s0 += 64) {
     const int n = uni(min(mine - s0, 64));
-    if (s0 > 0) idx = lane < n ? a.indices[ps + wave + W * (s0 + lane)] : 0;
-    const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
+    if (!RAGGED && s0 > 0) idx = lane < n ? a.indices[ps + wave + W * (s0 + lane)] : 0;
+    const int ok = (RAGGED || (idx >= 0 && (int64_t)idx < a.pool)) ? 1 : 0;
     auto page_tok = [&](int i) {
+      if constexpr (RAGGED) return (int64_t)ps + (int64_t)(wave + W * (s0 + i)) * 16;
       return (int64_t)__builtin_amdgcn_readlane(idx, uni(min(i, n - 1))) * 16;
     };
     auto rows_of = [&](int i) {
@@ -407,6 +471,19 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
   if (quad == 0) a.lse[row_head] = M + __log2f(L);
 }
 
+template <int W>
+__global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
+  prefill_body<W, false>(a);
+}
+
+// Ragged prefill: contiguous K/V rows [nnz_kv, Hkv, 128]; any 16 consecutive
+// rows of a request form a block with the paged layout's row stride, so the
+// same page step and range-limited loads serve it.
+template <int W>
+__global__ __launch_bounds__(W * 64) void ragged_prefill_kernel(PrefillArgs a) {
+  prefill_body<W, true>(a);
+}
+
 }  // namespace
 
 // ---- provider / plan / enqueue -----------------------------------------------
@@ -418,6 +495,10 @@ struct loom_paged_prefill_plan {
   loom_paged_prefill_plan_info_t info;
 };
 
+struct loom_ragged_prefill_plan {
+  loom_ragged_prefill_plan_info_t info;
+};
+
 namespace {
 // Waves per workgroup.  The reference picks its kernel from the average page
 // capacity per request (prefill.rs:2417-2426); here four waves measured
@@ -425,7 +506,24 @@ namespace {
 // per-page dependency chain, not load latency, bounds a wave, and deeper
 // prefetch or more waves per tile did not shorten it), so the default is
 // four whatever the spec; 8 and 16 stay available as plan options.
-uint32_t waves_for(const loom_paged_prefill_spec_t &) { return 4u; }
+uint32_t waves_for() { return 4u; }
+
+// Grid of a prefill plan: the most 16-column tiles any valid qo_indptr can
+// produce (every request wastes less than one tile), times the kv-heads.
+// prefill.rs:2293-2298 / :2335-2340: the (row, head) states must fit the
+// launch range; the kernel indexes columns with int32.
+loom_status_t prefill_grid(uint64_t batch, uint64_t nnz_qo, uint64_t hq, uint64_t hkv,
+                           uint64_t *tiles, uint64_t *grid, loom_error_t *err) {
+  const uint64_t states = nnz_qo * hq;
+  if (states > (uint64_t)INT32_MAX || batch > (uint64_t)INT32_MAX - 1)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "prefill", states);
+  const uint64_t cols = nnz_qo * (hq / hkv);
+  *tiles = std::min(cols, (cols + 15 * batch) / 16);
+  *grid = *tiles * hkv;
+  if (*grid > (uint64_t)INT32_MAX)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "prefill", states);
+  return LOOM_OK;
+}
 
 loom_status_t require_aligned(const char *name, uintptr_t ptr, uintptr_t alignment,
                               loom_error_t *err) {
@@ -463,21 +561,14 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
   if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
-  // prefill.rs:2293-2298: the (row, head) states must fit the launch range;
-  // here the grid is tiles x kv-heads and the kernel indexes with int32.
-  const uint64_t group = spec->num_query_heads / spec->num_kv_heads;
-  const uint64_t states = spec->nnz_qo * spec->num_query_heads;
-  if (states > (uint64_t)INT32_MAX || spec->batch_size > (uint64_t)INT32_MAX - 1)
-    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged prefill", states);
-  const uint64_t cols = spec->nnz_qo * group;
-  const uint64_t tiles = std::min(cols, (cols + 15 * spec->batch_size) / 16);
-  const uint64_t grid = tiles * spec->num_kv_heads;
-  if (grid > (uint64_t)INT32_MAX)
-    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged prefill", states);
+  uint64_t tiles = 0, grid = 0;
+  loom_status_t rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads,
+                                  spec->num_kv_heads, &tiles, &grid, err);
+  if (rc) return rc;
   auto *p = new loom_paged_prefill_plan;
   p->info.spec = *spec;
   p->info.algorithm = LOOM_PAGED_PREFILL_ROW_TILE;
-  p->info.waves = opt.waves ? opt.waves : waves_for(*spec);
+  p->info.waves = opt.waves ? opt.waves : waves_for();
   p->info.row_tiles = tiles;
   p->info.block_threads = p->info.waves * 64;
   p->info.grid_blocks = grid;
@@ -561,6 +652,97 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
     case 4: hipLaunchKernelGGL(paged_prefill_kernel<4>, grid, block, 0, stream, a); break;
     case 8: hipLaunchKernelGGL(paged_prefill_kernel<8>, grid, block, 0, stream, a); break;
     default: hipLaunchKernelGGL(paged_prefill_kernel<16>, grid, block, 0, stream, a); break;
+  }
+  return loom::record_launch(scope, hipGetLastError(), err);
+}
+
+// ---- ragged prefill: plan and enqueue ------------------------------------------
+loom_status_t loom_prefill_provider_plan_bf16_ragged(
+    const loom_prefill_provider_t *provider, const loom_ragged_prefill_spec_t *spec,
+    const loom_paged_prefill_plan_options_t *options, loom_ragged_prefill_plan_t **out,
+    loom_error_t *err) {
+  if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
+  const loom_paged_prefill_plan_options_t opt =
+      options ? *options : loom_paged_prefill_plan_options_t{0, 0};
+  if (opt.flags != 0) return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
+  if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
+  uint64_t tiles = 0, grid = 0;
+  loom_status_t rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads,
+                                  spec->num_kv_heads, &tiles, &grid, err);
+  if (rc) return rc;
+  auto *p = new loom_ragged_prefill_plan;
+  p->info.spec = *spec;
+  p->info.algorithm = LOOM_PAGED_PREFILL_ROW_TILE;
+  p->info.waves = opt.waves ? opt.waves : waves_for();
+  p->info.row_tiles = tiles;
+  p->info.block_threads = p->info.waves * 64;
+  p->info.grid_blocks = grid;
+  p->info.workspace_numel = 0;
+  *out = p;
+  return loom::ok(err);
+}
+
+void loom_ragged_prefill_plan_free(loom_ragged_prefill_plan_t *p) { delete p; }
+
+void loom_ragged_prefill_plan_get_info(const loom_ragged_prefill_plan_t *p,
+                                       loom_ragged_prefill_plan_info_t *info) {
+  if (p && info) *info = p->info;
+}
+
+uint64_t loom_ragged_prefill_workspace_numel(const loom_ragged_prefill_plan_t *p) {
+  return p ? p->info.workspace_numel : 0;
+}
+
+// Bf16RaggedPrefillPlan::enqueue_into, prefill.rs:2648-2760 (the one-kernel
+// algorithms: the optional workspace operand is not used).
+loom_status_t loom_ragged_prefill_enqueue(const loom_ragged_prefill_plan_t *plan,
+                                          loom_command_scope_t *scope,
+                                          const loom_ragged_prefill_args_t *args,
+                                          loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_ragged_prefill_spec_t &s = plan->info.spec;
+  static const loom::OperandSpec ops[7] = {
+      {"Q", LOOM_DTYPE_BF16, false},         {"K", LOOM_DTYPE_BF16, false},
+      {"V", LOOM_DTYPE_BF16, false},         {"qo_indptr", LOOM_DTYPE_I32, false},
+      {"kv_indptr", LOOM_DTYPE_I32, false},  {"O", LOOM_DTYPE_BF16, true},
+      {"LSE", LOOM_DTYPE_F32, true}};
+  const loom_handle_t hs[7] = {args->query,     args->key,    args->value, args->qo_indptr,
+                               args->kv_indptr, args->output, args->lse};
+  const loom::Lease *l[7];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, 7, l, err);
+  if (rc) return rc;
+  // prefill.rs:2700-2712: exact spans.
+  const uint64_t qn = s.nnz_qo * s.num_query_heads * loom::kHeadDim;
+  const uint64_t kvn = s.nnz_kv * s.num_kv_heads * loom::kHeadDim;
+  const uint64_t want[7] = {qn, kvn, kvn, s.batch_size + 1, s.batch_size + 1, qn,
+                            s.nnz_qo * s.num_query_heads};
+  for (int i = 0; i < 7; ++i)
+    if (l[i]->numel != want[i])
+      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
+  for (int i : {0, 1, 2, 5})
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+  PrefillArgs a{};
+  a.q = (const uint16_t *)l[0]->ptr;
+  a.k = (const uint16_t *)l[1]->ptr;
+  a.v = (const uint16_t *)l[2]->ptr;
+  a.qo = (const int32_t *)l[3]->ptr;
+  a.indptr = (const int32_t *)l[4]->ptr;
+  a.out = (uint16_t *)l[5]->ptr;
+  a.lse = (float *)l[6]->ptr;
+  a.batch = (int32_t)s.batch_size;
+  a.nnz = (int32_t)s.nnz_qo;
+  a.nnz_kv = (int32_t)s.nnz_kv;
+  a.hq = (int32_t)s.num_query_heads;
+  a.hkv = (int32_t)s.num_kv_heads;
+  a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
+  a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
+  hipStream_t stream = scope->queue->stream;
+  const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
+  switch (plan->info.waves) {
+    case 4: hipLaunchKernelGGL(ragged_prefill_kernel<4>, grid, block, 0, stream, a); break;
+    case 8: hipLaunchKernelGGL(ragged_prefill_kernel<8>, grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL(ragged_prefill_kernel<16>, grid, block, 0, stream, a); break;
   }
   return loom::record_launch(scope, hipGetLastError(), err);
 }

@@ -866,8 +866,122 @@ class Bf16PagedPrefillPlan:
             pass
 
 
+class RaggedPrefillMetadata:
+    """Validated metadata view (ragged_prefill/mod.rs:196-243)."""
+
+    def __init__(self, spec: "Bf16RaggedPrefillSpec", qo_indptr, kv_indptr):
+        self.spec = spec
+        self.qo_indptr = list(qo_indptr)
+        self.kv_indptr = list(kv_indptr)
+
+    def request_row_ranges(self, request: int):
+        if request >= self.spec.batch_size:
+            return None
+        return ((self.qo_indptr[request], self.qo_indptr[request + 1]),
+                (self.kv_indptr[request], self.kv_indptr[request + 1]))
+
+    def causal_kv_end(self, request: int, query_index: int):
+        qo, _ = _i32_array(self.qo_indptr)
+        kv, _ = _i32_array(self.kv_indptr)
+        out = C.c_uint64()
+        rc = lib().loom_ragged_prefill_causal_kv_end(C.byref(self.spec._c), qo, kv, request,
+                                                     query_index, C.byref(out))
+        return None if rc else out.value
+
+
+class Bf16RaggedPrefillSpec:
+    """ragged_prefill/mod.rs:8-167."""
+
+    def __init__(self, batch_size, nnz_qo, nnz_kv, num_query_heads, num_kv_heads,
+                 head_dim=HEAD_DIM):
+        self._c = _ffi.RaggedPrefillSpec()
+        _call(lib().loom_ragged_prefill_spec_new, batch_size, nnz_qo, nnz_kv, num_query_heads,
+              num_kv_heads, head_dim, C.byref(self._c))
+
+    batch_size = property(lambda s: s._c.batch_size)
+    nnz_qo = property(lambda s: s._c.nnz_qo)
+    nnz_kv = property(lambda s: s._c.nnz_kv)
+    num_query_heads = property(lambda s: s._c.num_query_heads)
+    num_kv_heads = property(lambda s: s._c.num_kv_heads)
+    softmax_scale = property(lambda s: s._c.softmax_scale)
+    head_dim = property(lambda s: HEAD_DIM)
+    gqa_group_size = property(lambda s: s.num_query_heads // s.num_kv_heads)
+    query_numel = property(lambda s: s.nnz_qo * s.num_query_heads * HEAD_DIM)
+    kv_numel = property(lambda s: s.nnz_kv * s.num_kv_heads * HEAD_DIM)
+    output_numel = property(lambda s: s.query_numel)
+    lse_numel = property(lambda s: s.nnz_qo * s.num_query_heads)
+    indptr_numel = property(lambda s: s.batch_size + 1)
+
+    def kv_head_for_query_head(self, query_head: int):
+        return query_head // self.gqa_group_size if query_head < self.num_query_heads else None
+
+    def validate_metadata(self, qo_indptr, kv_indptr) -> RaggedPrefillMetadata:
+        qo, nqo = _i32_array(qo_indptr)
+        kv, nkv = _i32_array(kv_indptr)
+        _call(lib().loom_ragged_prefill_validate_metadata, C.byref(self._c), qo, nqo, kv, nkv)
+        return RaggedPrefillMetadata(self, qo_indptr, kv_indptr)
+
+
+@dataclass(frozen=True)
+class Bf16RaggedPrefillArgs:
+    """prefill.rs:2893-2931 (`workspace`: the optional with_workspace operand)."""
+    query: Read
+    key: Read
+    value: Read
+    qo_indptr: Read
+    kv_indptr: Read
+    output: Write
+    lse: Write
+    workspace: Optional["ReadWrite"] = None
+
+    def with_workspace(self, workspace: "ReadWrite") -> "Bf16RaggedPrefillArgs":
+        return Bf16RaggedPrefillArgs(self.query, self.key, self.value, self.qo_indptr,
+                                     self.kv_indptr, self.output, self.lse, workspace)
+
+    def __post_init__(self):
+        c = _ffi.RaggedPrefillArgs(*[_h(getattr(self, f)) for f in (
+            "query", "key", "value", "qo_indptr", "kv_indptr", "output", "lse")],
+            _h(self.workspace) if self.workspace is not None else _ffi.Handle(0, 0))
+        object.__setattr__(self, "_struct", c)
+        object.__setattr__(self, "_ref", C.byref(c))
+
+
+class Bf16RaggedPrefillPlan:
+    def __init__(self, ptr, spec):
+        self._p = ptr
+        self._spec = spec
+        self.info = _ffi.RaggedPrefillPlanInfo()
+        lib().loom_ragged_prefill_plan_get_info(self._p, C.byref(self.info))
+
+    def spec(self):
+        return self._spec
+
+    @property
+    def algorithm(self) -> str:
+        return {1: "row_tile"}[self.info.algorithm]
+
+    @property
+    def workspace_required_numel(self) -> int:
+        return lib().loom_ragged_prefill_workspace_numel(self._p)
+
+    @property
+    def workspace_required_bytes(self) -> int:
+        return self.workspace_required_numel * 4
+
+    def enqueue_into(self, scope: CommandScope, args: Bf16RaggedPrefillArgs):
+        _enqueue(_ffi.load().loom_ragged_prefill_enqueue, self._p, scope._p, args._ref)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_p", None):
+                lib().loom_ragged_prefill_plan_free(self._p)
+                self._p = None
+        except Exception:  # interpreter shutdown: module globals are gone
+            pass
+
+
 class PrefillProvider:
-    """prefill.rs:2278-2330 (the paged plan)."""
+    """prefill.rs:2278-2410 (the paged and ragged plans)."""
 
     def __init__(self, ptr, device):
         self._p = ptr
@@ -889,6 +1003,15 @@ class PrefillProvider:
         _call(lib().loom_prefill_provider_plan_bf16_paged_options, self._p, C.byref(spec._c),
               C.byref(opt), C.byref(out))
         return Bf16PagedPrefillPlan(out.value, spec)
+
+    def plan_bf16_ragged(self, spec: Bf16RaggedPrefillSpec,
+                         waves: int = 0) -> Bf16RaggedPrefillPlan:
+        """prefill.rs:2331-2410; `waves` per workgroup (0: four; 4, 8 or 16)."""
+        opt = _ffi.PagedPrefillPlanOptions(waves, 0)
+        out = C.c_void_p()
+        _call(lib().loom_prefill_provider_plan_bf16_ragged, self._p, C.byref(spec._c),
+              C.byref(opt), C.byref(out))
+        return Bf16RaggedPrefillPlan(out.value, spec)
 
     def __del__(self):
         try:

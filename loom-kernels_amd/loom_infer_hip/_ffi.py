@@ -91,6 +91,22 @@ class PagedPrefillArgs(C.Structure):
                                       "output", "lse")]
 
 
+class RaggedPrefillSpec(C.Structure):
+    _fields_ = [("batch_size", u64), ("nnz_qo", u64), ("nnz_kv", u64), ("num_query_heads", u64),
+                ("num_kv_heads", u64), ("softmax_scale", f32)]
+
+
+class RaggedPrefillPlanInfo(C.Structure):
+    _fields_ = [("spec", RaggedPrefillSpec), ("algorithm", i32), ("waves", u32),
+                ("row_tiles", u64), ("block_threads", u32), ("grid_blocks", u64),
+                ("workspace_numel", u64)]
+
+
+class RaggedPrefillArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key", "value", "qo_indptr", "kv_indptr",
+                                      "output", "lse", "workspace")]
+
+
 class RopeAppendPlanInfo(C.Structure):
     _fields_ = [("tokens", u64), ("batch_size", u64), ("num_query_heads", u64),
                 ("num_kv_heads", u64), ("explicit_tokens", i32), ("workspace_bytes", u64),
@@ -176,6 +192,15 @@ SIGNATURES = {
     "loom_paged_prefill_plan_free": (None, [vp]),
     "loom_paged_prefill_plan_get_info": (None, [vp, P(PagedPrefillPlanInfo)]),
     "loom_paged_prefill_enqueue": (i32, [vp, vp, P(PagedPrefillArgs), E]),
+    "loom_ragged_prefill_spec_new": (i32, [u64] * 6 + [P(RaggedPrefillSpec), E]),
+    "loom_ragged_prefill_validate_metadata": (i32, [P(RaggedPrefillSpec), pi32, u64, pi32, u64, E]),
+    "loom_ragged_prefill_causal_kv_end": (i32, [P(RaggedPrefillSpec), pi32, pi32, u64, u64, P(u64)]),
+    "loom_prefill_provider_plan_bf16_ragged": (
+        i32, [vp, P(RaggedPrefillSpec), P(PagedPrefillPlanOptions), P(vp), E]),
+    "loom_ragged_prefill_plan_free": (None, [vp]),
+    "loom_ragged_prefill_plan_get_info": (None, [vp, P(RaggedPrefillPlanInfo)]),
+    "loom_ragged_prefill_workspace_numel": (u64, [vp]),
+    "loom_ragged_prefill_enqueue": (i32, [vp, vp, P(RaggedPrefillArgs), E]),
     "loom_rope_provider_load": (i32, [C.c_int, P(vp), E]),
     "loom_rope_provider_free": (None, [vp]),
     "loom_rope_provider_plan_bf16_paged_append": (i32, [vp, P(RopeAppendSpec), P(vp), E]),

@@ -144,3 +144,40 @@ class PrefillRunner:
                                 to_dev_i32(qo), to_dev_i32(indptr), to_dev_i32(indices),
                                 to_dev_i32(last))
         return bf16_host(out), lse.cpu().numpy()
+
+
+class RaggedRunner:
+    """Plans once and runs ragged prefill via the C ABI on torch's current stream."""
+
+    def __init__(self, L, batch, nnz_qo, nnz_kv, hq, hkv, **plan_opts):
+        torch = torch_dev()
+        self.L = L
+        self.spec = L.Bf16RaggedPrefillSpec(batch, nnz_qo, nnz_kv, hq, hkv, 128)
+        self.plan = L.PrefillProvider.load(0).plan_bf16_ragged(self.spec, **plan_opts)
+        self.queue = L.CommandQueue(torch.cuda.current_stream(), 4)
+
+    def run_dev(self, q, k, v, qo, kv, out=None, lse=None, workspace=None):
+        torch = torch_dev()
+        s = self.spec
+        if out is None:
+            out = nan_bf16(s.output_numel)
+        if lse is None:
+            lse = torch.full((s.lse_numel,), float("nan"), dtype=torch.float32, device="cuda")
+        b = self.queue.bindings(8)
+        h = [b.bind_read(x) for x in (q, k, v, qo, kv)]
+        h += [b.bind_read_write(out), b.bind_read_write(lse)]
+        args = self.L.Bf16RaggedPrefillArgs(h[0], h[1], h[2], h[3], h[4], h[5].write(),
+                                            h[6].write())
+        if workspace is not None:
+            args = args.with_workspace(b.bind_read_write(workspace))
+        scope = self.queue.begin(b)
+        self.plan.enqueue_into(scope, args)
+        comp = scope.finish()
+        assert comp.submitted() == 1
+        b = comp.wait()
+        return b.take_read_write(h[5]), b.take_read_write(h[6])
+
+    def run(self, q_u16, k_u16, v_u16, qo, kv):
+        out, lse = self.run_dev(to_dev_bf16(q_u16), to_dev_bf16(k_u16), to_dev_bf16(v_u16),
+                                to_dev_i32(qo), to_dev_i32(kv))
+        return bf16_host(out), lse.cpu().numpy()

@@ -243,3 +243,31 @@ def test_paged_prefill_contracts_match_oracle(L, oracle):
         with pytest.raises(L.ContractError) as e:
             L.Bf16PagedPrefillSpec(*dims)
         assert e.value.variant == variant
+
+
+def test_ragged_prefill_contracts_match_oracle(L, oracle):
+    # crates/loom-infer/src/attention/ragged_prefill/mod.rs:27-243 through the
+    # C ABI, against the oracle (pinned by the reference's unit tests).
+    import test_oracle_ragged as R
+    s = L.Bf16RaggedPrefillSpec(2, 3, 6, 4, 2)
+    assert (s.nnz_qo, s.nnz_kv, s.query_numel, s.kv_numel, s.lse_numel) == (3, 6, 1536, 1536, 12)
+    m = s.validate_metadata([0, 2, 3], [0, 4, 6])
+    os_ = oracle.ragged_spec(2, 3, 6, 4, 2)
+    for r in range(3):
+        for i in range(3):
+            assert m.causal_kv_end(r, i) == oracle.ragged_causal_kv_end(os_, [0, 2, 3],
+                                                                        [0, 4, 6], r, i)
+    assert m.request_row_ranges(1) == ((2, 3), (4, 6)) and m.request_row_ranges(2) is None
+    s2 = L.Bf16RaggedPrefillSpec(2, 3, 5, 4, 2)
+    for args, (variant, buf, fields) in R.MALFORMED:
+        with pytest.raises(L.ContractError) as e:
+            s2.validate_metadata(*args)
+        assert (e.value.variant, e.value.fields) == (variant, fields), args
+        if buf:
+            assert e.value.operand == buf
+    for dims, variant in [((0, 1, 1, 1, 1), "ZeroDimension"), ((1, 1, 1, 6, 4), "InvalidHeadMapping"),
+                          ((1, 2 ** 31, 1, 1, 1), "ElementCountOverflow"),
+                          ((1, 1, 2 ** 31, 1, 1), "ElementCountOverflow")]:
+        with pytest.raises(L.ContractError) as e:
+            L.Bf16RaggedPrefillSpec(*dims)
+        assert e.value.variant == variant
