@@ -607,6 +607,17 @@ def main():
                         "algorithmic_bytes": case.bytes,
                         "teams": case.plan.info.teams,
                         "mean_kv_len": float(case.lens.mean())}
+        if name.startswith("c3"):
+            # the same command on HND pages (same bytes, head-major pages: one
+            # kv-head's 16 rows are 4 KiB contiguous); the pool contents are
+            # reinterpreted, which does not change the work
+            hspec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, 128, 16, kv_layout="HND")
+            hplan = L.DecodeProvider.load(0).plan_bf16_paged_batch(
+                hspec, max_total_pages=int(case.indptr_h[-1]))
+            h_us = _timed_enqueues(L, stream, 9, case.bind, hplan.enqueue_into, a.steps, a.warmup)
+            detail[name].update({"hnd_us_per_call": round(h_us, 3),
+                                 "hnd_GBps": round(case.bytes / (h_us * 1e-6) / 1e9, 1)})
+            del hplan
         if name.startswith("c1"):
             # cold: 16 copies of the workload (537 MB) used round-robin
             copies = [case] + [DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name) + i)

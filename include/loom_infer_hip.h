@@ -159,6 +159,18 @@ typedef enum loom_dtype {
 } loom_dtype_t;
 
 /* ------------------------------------------------------------------------ */
+/* K/V page layout (no reference counterpart: the reference supports NHD only
+ * and lists HND as unsupported, docs/results/h20-bf16-rope-paged-kv-append-
+ * tokens-correctness-20260806.json contract.unsupported).  NHD pages are
+ * [16, Hkv, 128] (token-major); HND pages are [Hkv, 16, 128] (head-major: one
+ * kv-head's 16 rows are 4 KiB contiguous).  Every paged operation (decode,
+ * append, paged prefill) reads and writes the layout its spec names. */
+typedef enum loom_kv_layout {
+  LOOM_KV_LAYOUT_NHD = 0,
+  LOOM_KV_LAYOUT_HND = 1
+} loom_kv_layout_t;
+
+/* ------------------------------------------------------------------------ */
 /* Paged batch-decode contract, crates/loom-infer/src/attention/paged_decode/mod.rs */
 typedef struct loom_paged_decode_spec {
   uint64_t batch_size;
@@ -166,6 +178,7 @@ typedef struct loom_paged_decode_spec {
   uint64_t num_query_heads;
   uint64_t num_kv_heads;
   float softmax_scale;
+  uint32_t kv_layout; /* loom_kv_layout_t; LOOM_KV_LAYOUT_NHD from spec_new */
 } loom_paged_decode_spec_t;
 
 /* Bf16PagedBatchDecodeSpec::new, paged_decode/mod.rs:28-82. */
@@ -173,6 +186,13 @@ loom_status_t loom_paged_decode_spec_new(uint64_t batch_size, uint64_t max_num_p
                                          uint64_t num_query_heads, uint64_t num_kv_heads,
                                          uint64_t head_dim, uint64_t page_size,
                                          loom_paged_decode_spec_t *out, loom_error_t *err);
+/* The same spec with another K/V page layout (no reference counterpart; the
+ * paged append specs embed this spec and take their layout from it).
+ * LOOM_PLAN_INVALID_OPTION for an unknown layout. */
+loom_status_t loom_paged_decode_spec_with_kv_layout(const loom_paged_decode_spec_t *spec,
+                                                    uint32_t kv_layout,
+                                                    loom_paged_decode_spec_t *out,
+                                                    loom_error_t *err);
 /* validate_page_table, paged_decode/mod.rs:152-213 (host metadata). */
 loom_status_t loom_paged_decode_validate_page_table(const loom_paged_decode_spec_t *spec,
                                                     const int32_t *page_indptr, uint64_t n_indptr,
@@ -489,6 +509,7 @@ typedef struct loom_paged_prefill_spec {
   uint64_t num_query_heads;
   uint64_t num_kv_heads;
   float softmax_scale;
+  uint32_t kv_layout; /* loom_kv_layout_t; LOOM_KV_LAYOUT_NHD from spec_new */
 } loom_paged_prefill_spec_t;
 
 /* Bf16PagedPrefillSpec::new, paged_prefill/mod.rs:30-91. */
@@ -497,6 +518,11 @@ loom_status_t loom_paged_prefill_spec_new(uint64_t batch_size, uint64_t nnz_qo,
                                           uint64_t num_kv_heads, uint64_t head_dim,
                                           uint64_t page_size, loom_paged_prefill_spec_t *out,
                                           loom_error_t *err);
+/* The same spec with another K/V page layout (no reference counterpart). */
+loom_status_t loom_paged_prefill_spec_with_kv_layout(const loom_paged_prefill_spec_t *spec,
+                                                     uint32_t kv_layout,
+                                                     loom_paged_prefill_spec_t *out,
+                                                     loom_error_t *err);
 /* validate_metadata, paged_prefill/mod.rs:161-264 (host metadata). */
 loom_status_t loom_paged_prefill_validate_metadata(const loom_paged_prefill_spec_t *spec,
                                                    const int32_t *qo_indptr, uint64_t n_qo,

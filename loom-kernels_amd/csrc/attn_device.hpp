@@ -48,10 +48,12 @@ __device__ __forceinline__ u32x4 load16_rows(__amdgpu_buffer_rsrc_t r, int byte_
       u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, NT ? 2 : 0));
 }
 
+// `row_elems`: elements between consecutive token rows of one kv-head
+// (Hkv * 128 in NHD storage, 128 in HND pages).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rows_rsrc(const uint16_t *base,
-                                                                int valid_rows, int hkv) {
+                                                                int valid_rows, int row_elems) {
   // gfx9 word 3: 32-bit data format, no swizzle; stride 0 (raw addressing)
-  const int bytes = valid_rows > 0 ? ((valid_rows - 1) * hkv + 1) * 256 : 0;
+  const int bytes = valid_rows > 0 ? ((valid_rows - 1) * row_elems + 128) * 2 : 0;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
 }
 

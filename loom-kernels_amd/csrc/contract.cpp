@@ -344,6 +344,19 @@ loom_status_t loom_paged_decode_spec_new(uint64_t batch, uint64_t pool, uint64_t
   out->num_query_heads = hq;
   out->num_kv_heads = hkv;
   out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
+  out->kv_layout = LOOM_KV_LAYOUT_NHD;
+  return loom::ok(err);
+}
+
+loom_status_t loom_paged_decode_spec_with_kv_layout(const loom_paged_decode_spec_t *spec,
+                                                    uint32_t kv_layout,
+                                                    loom_paged_decode_spec_t *out,
+                                                    loom_error_t *err) {
+  if (!spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "spec");
+  if (kv_layout != LOOM_KV_LAYOUT_NHD && kv_layout != LOOM_KV_LAYOUT_HND)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", kv_layout);
+  *out = *spec;
+  out->kv_layout = kv_layout;
   return loom::ok(err);
 }
 
@@ -606,6 +619,19 @@ loom_status_t loom_paged_prefill_spec_new(uint64_t batch, uint64_t nnz_qo, uint6
   out->num_query_heads = hq;
   out->num_kv_heads = hkv;
   out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
+  out->kv_layout = LOOM_KV_LAYOUT_NHD;
+  return loom::ok(err);
+}
+
+loom_status_t loom_paged_prefill_spec_with_kv_layout(const loom_paged_prefill_spec_t *spec,
+                                                     uint32_t kv_layout,
+                                                     loom_paged_prefill_spec_t *out,
+                                                     loom_error_t *err) {
+  if (!spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "spec");
+  if (kv_layout != LOOM_KV_LAYOUT_NHD && kv_layout != LOOM_KV_LAYOUT_HND)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", kv_layout);
+  *out = *spec;
+  out->kv_layout = kv_layout;
   return loom::ok(err);
 }
 

@@ -107,6 +107,12 @@ struct DecodeArgs {
   // length instead of requiring equality (fixed-address graphs replayed over
   // changing page tables).
   int32_t indices_capacity;
+  // K/V row geometry: row t of kv-head h starts at element
+  // t * Hkv * 128 + h * head_elems + (t % 16) * (row_elems - Hkv * 128), i.e.
+  // NHD: head_elems 128, row_elems Hkv * 128; HND pages: head_elems 16 * 128,
+  // row_elems 128 (t is a multiple of 16 for pages).  Contiguous K/V is NHD.
+  int32_t head_elems;
+  int32_t row_elems;
 };
 
 // decode.rs:233-246: indptr[B] is the page_indices length (or, for plans made
@@ -143,18 +149,19 @@ struct PageRegs {
   u32x4 v[4];
 };
 
-// 16 consecutive token rows starting at token row `token0` of the NHD K/V
-// buffers (a page of a paged cache, or any 16 tokens of a contiguous one).
-// `token0` and `valid_rows` are wave-uniform (the resource lives in SGPRs).
+// 16 consecutive token rows starting at token row `token0` of the K/V
+// buffers (a page of a paged cache, NHD or HND, or any 16 tokens of a
+// contiguous NHD one).  `token0` and `valid_rows` are wave-uniform (the
+// resource lives in SGPRs).
 __device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int64_t token0,
                                           int valid_rows, int lane, int kvh) {
   const int col = lane & 15, quad = lane >> 4;
-  const int64_t first = (token0 * a.hkv + kvh) * 128;
-  const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, valid_rows, a.hkv);
-  const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, valid_rows, a.hkv);
+  const int64_t first = token0 * a.hkv * 128 + (int64_t)kvh * a.head_elems;
+  const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, valid_rows, a.row_elems);
+  const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, valid_rows, a.row_elems);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int off = (quad * 4 + j) * a.hkv * 256 + col * 16;
+    const int off = (quad * 4 + j) * a.row_elems * 2 + col * 16;
     r.k[j] = load16_rows<LOOM_DECODE_NT_K>(rk, off);
     r.v[j] = load16_rows<LOOM_DECODE_NT_V>(rv, off);
   }
@@ -1045,6 +1052,8 @@ DecodeArgs single_args(const loom_single_decode_spec_t &s, uint32_t gtiles, uint
   a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
   a.members = (int32_t)(s.num_kv_heads * gtiles);
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
+  a.head_elems = 128;  // contiguous K/V: NHD rows
+  a.row_elems = a.hkv * 128;
   return a;
 }
 }  // namespace
@@ -1081,6 +1090,8 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   const uint64_t gtiles = (group + gtile - 1) / gtile;
   if (opt.flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
+  if (spec->kv_layout != LOOM_KV_LAYOUT_NHD && spec->kv_layout != LOOM_KV_LAYOUT_HND)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", spec->kv_layout);
   const uint64_t max_pages = opt.max_total_pages ? opt.max_total_pages : spec->max_num_pages;
   if (max_pages < B) return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
   if (max_pages > (uint64_t)INT32_MAX)
@@ -1224,6 +1235,9 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.n_indices = (int64_t)l[4]->numel;
   a.indices_capacity = (pi.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
+  const bool hnd = s.kv_layout == LOOM_KV_LAYOUT_HND;
+  a.head_elems = hnd ? 16 * 128 : 128;
+  a.row_elems = hnd ? 128 : a.hkv * 128;
 
   const uint64_t grid = pi.grid_blocks;
   hipStream_t stream = scope->queue->stream;

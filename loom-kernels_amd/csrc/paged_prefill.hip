@@ -65,6 +65,11 @@ struct PrefillArgs {
   // Ragged (contiguous) K/V: `indptr` is kv_indptr over [nnz_kv, Hkv, 128]
   // rows; `indices` and `last` are unused.
   int32_t nnz_kv;
+  // K/V row geometry (NHD: head_elems 128, row_elems Hkv * 128; HND pages:
+  // head_elems 16 * 128, row_elems 128): token row t of kv-head h, t a
+  // multiple of 16 for pages, starts at t * Hkv * 128 + h * head_elems.
+  int32_t head_elems;
+  int32_t row_elems;
 };
 
 // Tile count given to a request whose qo range is malformed: larger than any
@@ -106,10 +111,10 @@ struct PrefillPage {
 __device__ __forceinline__ void load_prefill_page(PrefillPage &p, const PrefillArgs &a,
                                                   int64_t token0, int rows, int lane, int kvh) {
   const int col = lane & 15, quad = lane >> 4;
-  const int64_t first = (token0 * a.hkv + kvh) * 128;
-  const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, rows, a.hkv);
-  const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, rows, a.hkv);
-  const int row_bytes = a.hkv * 256;
+  const int64_t first = token0 * a.hkv * 128 + (int64_t)kvh * a.head_elems;
+  const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, rows, a.row_elems);
+  const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, rows, a.row_elems);
+  const int row_bytes = a.row_elems * 2;
 #pragma unroll
   for (int c = 0; c < 4; ++c) p.k[c] = load16_rows<false>(rk, col * row_bytes + (32 * c + 8 * quad) * 2);
 #pragma unroll
@@ -559,6 +564,8 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
       options ? *options : loom_paged_prefill_plan_options_t{0, 0};
   if (opt.flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
+  if (spec->kv_layout != LOOM_KV_LAYOUT_NHD && spec->kv_layout != LOOM_KV_LAYOUT_HND)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", spec->kv_layout);
   if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
   uint64_t tiles = 0, grid = 0;
@@ -646,6 +653,9 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   a.n_indices = (int64_t)l[5]->numel;
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
   a.indices_capacity = (plan->info.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
+  const bool hnd = s.kv_layout == LOOM_KV_LAYOUT_HND;
+  a.head_elems = hnd ? 16 * 128 : 128;
+  a.row_elems = hnd ? 128 : a.hkv * 128;
   hipStream_t stream = scope->queue->stream;
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
   switch (plan->info.waves) {
@@ -737,6 +747,8 @@ loom_status_t loom_ragged_prefill_enqueue(const loom_ragged_prefill_plan_t *plan
   a.hkv = (int32_t)s.num_kv_heads;
   a.group = (int32_t)(s.num_query_heads / s.num_kv_heads);
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
+  a.head_elems = 128;  // contiguous K/V: NHD rows
+  a.row_elems = a.hkv * 128;
   hipStream_t stream = scope->queue->stream;
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
   switch (plan->info.waves) {

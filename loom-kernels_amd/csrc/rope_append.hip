@@ -77,6 +77,11 @@ struct AppendArgs {
   // page_indices is a capacity (LOOM_PLAN_PAGE_INDICES_CAPACITY): only the
   // first indptr[B] entries are part of the page table.
   int32_t indices_capacity;
+  // Page slot geometry: slot (page, off) of kv-head h starts at element
+  // page * 16 * Hkv * 128 + h * head_elems + off * row_elems (NHD: 128,
+  // Hkv * 128; HND pages: 16 * 128, 128).
+  int32_t head_elems;
+  int32_t row_elems;
   float inv_freq[64];
 };
 
@@ -262,7 +267,8 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
     const int kh = row - a.hq;
     const uint16_t *src = is_kv ? a.k + ((int64_t)t * a.hkv + kh) * 128
                                 : a.q + ((int64_t)t * a.hq + row) * 128;
-    const int64_t kv_dst = ((page * 16 + off) * a.hkv + kh) * 128;
+    const int64_t kv_dst =
+        page * 16 * a.hkv * 128 + (int64_t)kh * a.head_elems + (int64_t)off * a.row_elems;
     uint16_t *dst = is_kv ? a.k_pages + kv_dst : a.q_out + ((int64_t)t * a.hq + row) * 128;
     const u32x4 x = first ? first_slice.x : *reinterpret_cast<const u32x4 *>(src + c * 8);
     const u32x4 xp = first ? first_slice.xp : *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
@@ -381,6 +387,7 @@ struct loom_rope_append_plan {
   loom_rope_append_plan_info_t info;
   uint64_t max_num_pages = 0;
   uint32_t flags = 0;
+  uint32_t kv_layout = LOOM_KV_LAYOUT_NHD;
   float inv_freq[64];
 };
 
@@ -405,6 +412,8 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
                                loom_rope_append_plan_t **out, loom_error_t *err) {
   if (flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
+  if (s.kv_layout != LOOM_KV_LAYOUT_NHD && s.kv_layout != LOOM_KV_LAYOUT_HND)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", s.kv_layout);
   // rope/mod.rs:628-682: states = tokens * (Hq + Hkv) must fit the grid.
   uint64_t rows = s.num_query_heads + s.num_kv_heads, states;
   if (rows < s.num_query_heads || __builtin_mul_overflow(tokens, rows, &states))
@@ -424,6 +433,7 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
   p->info.validate_blocks = 0;  // depends on the bound page_indices length
   p->max_num_pages = s.max_num_pages;
   p->flags = flags;
+  p->kv_layout = s.kv_layout;
   // rope/mod.rs:148-149 with rope_scale = 1, rope_theta = 1e4, rotary_dim = 128
   // (paged_append/mod.rs:395-403): the reference's exact FP32 inverse frequencies.
   for (int i = 0; i < 64; ++i) {
@@ -547,6 +557,8 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   a.pool = (int64_t)plan->max_num_pages;
   a.n_indices = (int64_t)L(6)->numel;
   a.indices_capacity = (plan->flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
+  a.head_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? 16 * 128 : 128;
+  a.row_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? 128 : (int32_t)hkv * 128;
   for (int i = 0; i < 64; ++i) a.inv_freq[i] = plan->inv_freq[i];
 
   const uint64_t vblocks = std::max<uint64_t>(

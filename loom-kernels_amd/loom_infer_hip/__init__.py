@@ -34,6 +34,26 @@ HEAD_DIM = 128
 PAGE_SIZE = 16
 PARTIAL_STATE_WIDTH = 130
 PLAN_PAGE_INDICES_CAPACITY = 1
+# K/V page layouts (loom_kv_layout_t): NHD pages [16, Hkv, 128], HND pages
+# [Hkv, 16, 128].  The reference supports NHD only.
+KV_LAYOUTS = {"NHD": 0, "HND": 1}
+
+
+def _layout_code(kv_layout) -> int:
+    if kv_layout in KV_LAYOUTS.values():
+        return int(kv_layout)
+    if kv_layout not in KV_LAYOUTS:
+        raise ValueError(f"kv_layout must be one of {sorted(KV_LAYOUTS)}, got {kv_layout!r}")
+    return KV_LAYOUTS[kv_layout]
+
+
+def _set_paged_layout(c_paged, kv_layout):
+    """Applies loom_paged_decode_spec_with_kv_layout to an embedded paged spec."""
+    code = _layout_code(kv_layout)
+    if code != 0:
+        out = _ffi.PagedDecodeSpec()
+        _call(lib().loom_paged_decode_spec_with_kv_layout, C.byref(c_paged), code, C.byref(out))
+        c_paged.kv_layout = out.kv_layout
 ROPE_PAGED_KV_APPEND_MAX_TOKENS = 64
 ROPE_PAGED_KV_APPEND_MAX_TOKENS_EXTENDED = 8192
 
@@ -193,10 +213,13 @@ class Bf16PagedBatchDecodeSpec:
     """paged_decode/mod.rs:17-149."""
 
     def __init__(self, batch_size, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD"):
         self._c = _ffi.PagedDecodeSpec()
         _call(lib().loom_paged_decode_spec_new, batch_size, max_num_pages, num_query_heads,
               num_kv_heads, head_dim, page_size, C.byref(self._c))
+        _set_paged_layout(self._c, kv_layout)
+
+    kv_layout = property(lambda s: {v: k for k, v in KV_LAYOUTS.items()}[s._c.kv_layout])
 
     batch_size = property(lambda s: s._c.batch_size)
     max_num_pages = property(lambda s: s._c.max_num_pages)
@@ -229,10 +252,11 @@ class Bf16RopePagedKvAppendSpec:
     """paged_append/mod.rs:14-131 (one token per request at kv_len-1)."""
 
     def __init__(self, batch_size, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD"):
         self._c = _ffi.RopeAppendSpec()
         _call(lib().loom_rope_append_spec_new, batch_size, max_num_pages, num_query_heads,
               num_kv_heads, head_dim, page_size, C.byref(self._c))
+        _set_paged_layout(self._c.paged, kv_layout)
         self.paged = _wrap_paged(self._c.paged)
 
     batch_size = property(lambda s: s._c.paged.batch_size)
@@ -259,12 +283,14 @@ class Bf16RopePagedKvAppendTokensSpec:
     """paged_append/mod.rs:134-317 (explicit tokens; T <= 64, or the extended bound)."""
 
     def __init__(self, tokens, batch_size, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, extended: bool = False):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, extended: bool = False,
+                 kv_layout="NHD"):
         self._c = _ffi.RopeAppendTokensSpec()
         fn = (lib().loom_rope_append_tokens_spec_new_extended if extended
               else lib().loom_rope_append_tokens_spec_new)
         _call(fn, tokens, batch_size, max_num_pages, num_query_heads, num_kv_heads, head_dim,
               page_size, C.byref(self._c))
+        _set_paged_layout(self._c.paged, kv_layout)
         self.paged = _wrap_paged(self._c.paged)
 
     @classmethod
@@ -785,10 +811,18 @@ class Bf16PagedPrefillSpec:
     """paged_prefill/mod.rs:11-159."""
 
     def __init__(self, batch_size, nnz_qo, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD"):
         self._c = _ffi.PagedPrefillSpec()
         _call(lib().loom_paged_prefill_spec_new, batch_size, nnz_qo, max_num_pages,
               num_query_heads, num_kv_heads, head_dim, page_size, C.byref(self._c))
+        code = _layout_code(kv_layout)
+        if code != 0:
+            out = _ffi.PagedPrefillSpec()
+            _call(lib().loom_paged_prefill_spec_with_kv_layout, C.byref(self._c), code,
+                  C.byref(out))
+            self._c = out
+
+    kv_layout = property(lambda s: {v: k for k, v in KV_LAYOUTS.items()}[s._c.kv_layout])
 
     batch_size = property(lambda s: s._c.batch_size)
     nnz_qo = property(lambda s: s._c.nnz_qo)

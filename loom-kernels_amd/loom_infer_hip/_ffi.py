@@ -20,7 +20,7 @@ class Error(C.Structure):
 
 class PagedDecodeSpec(C.Structure):
     _fields_ = [("batch_size", u64), ("max_num_pages", u64), ("num_query_heads", u64),
-                ("num_kv_heads", u64), ("softmax_scale", f32)]
+                ("num_kv_heads", u64), ("softmax_scale", f32), ("kv_layout", u32)]
 
 
 class RopeAppendSpec(C.Structure):
@@ -72,7 +72,8 @@ class SingleDecodeSplitKArgs(C.Structure):
 
 class PagedPrefillSpec(C.Structure):
     _fields_ = [("batch_size", u64), ("nnz_qo", u64), ("max_num_pages", u64),
-                ("num_query_heads", u64), ("num_kv_heads", u64), ("softmax_scale", f32)]
+                ("num_query_heads", u64), ("num_kv_heads", u64), ("softmax_scale", f32),
+                ("kv_layout", u32)]
 
 
 class PagedPrefillPlanOptions(C.Structure):
@@ -128,6 +129,10 @@ SIGNATURES = {
     "loom_abi_version": (u32, []),
     "loom_status_name": (C.c_char_p, [i32]),
     "loom_paged_decode_spec_new": (i32, [u64] * 6 + [P(PagedDecodeSpec), E]),
+    "loom_paged_decode_spec_with_kv_layout": (
+        i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
+    "loom_paged_prefill_spec_with_kv_layout": (
+        i32, [P(PagedPrefillSpec), u32, P(PagedPrefillSpec), E]),
     "loom_paged_decode_validate_page_table": (
         i32, [P(PagedDecodeSpec), pi32, u64, pi32, u64, pi32, u64, E]),
     "loom_paged_decode_request_kv_len": (i32, [P(PagedDecodeSpec), pi32, pi32, u64, P(u64)]),

@@ -271,3 +271,22 @@ def test_ragged_prefill_contracts_match_oracle(L, oracle):
         with pytest.raises(L.ContractError) as e:
             L.Bf16RaggedPrefillSpec(*dims)
         assert e.value.variant == variant
+
+
+def test_kv_layout_specs(L):
+    # HND pages (no reference counterpart): the spec setters keep every other
+    # field and reject unknown layouts.
+    s = L.Bf16PagedBatchDecodeSpec(2, 8, 16, 4, kv_layout="HND")
+    assert s.kv_layout == "HND" and (s.batch_size, s.max_num_pages, s.num_kv_heads) == (2, 8, 4)
+    assert L.Bf16PagedBatchDecodeSpec(2, 8, 16, 4).kv_layout == "NHD"
+    p = L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, kv_layout="HND")
+    assert p.kv_layout == "HND" and p.nnz_qo == 5
+    a = L.Bf16RopePagedKvAppendTokensSpec(3, 2, 8, 16, 4, kv_layout="HND")
+    assert a.paged.kv_layout == "HND" and a.tokens == 3
+    import ctypes as C
+    out = L._ffi.PagedDecodeSpec()
+    e = L._ffi.Error()
+    rc = L.lib().loom_paged_decode_spec_with_kv_layout(C.byref(s._c), 2, C.byref(out), C.byref(e))
+    assert rc == 75 and e.operand == b"kv_layout"
+    with pytest.raises(ValueError):
+        L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, kv_layout="bad")
