@@ -95,6 +95,10 @@ def lib():
         _lib.lo_paged_request_kv_len.restype = C.c_int64
         _lib.lo_prefill_causal_kv_end.restype = C.c_int64
         _lib.lo_ragged_causal_kv_end.restype = C.c_int64
+        _lib.lo_fp8_e4m3_from_f32.restype = C.c_uint8
+        _lib.lo_fp8_e4m3_from_f32.argtypes = [C.c_float]
+        _lib.lo_fp8_e4m3_to_f32.restype = C.c_float
+        _lib.lo_fp8_e4m3_to_f32.argtypes = [C.c_uint8]
     return _lib
 
 
@@ -392,3 +396,49 @@ def append_tokens(spec, tokens, q, k, v, batch_indices, positions, indptr, indic
         C.c_size_t(indices.size), _p(last), C.c_size_t(last.size), _p(qo), _p(k_pages),
         _p(v_pages), C.byref(e)), e)
     return qo
+
+
+# ---- FP8 E4M3 KV storage (no reference counterpart) ---------------------------
+def fp8_from_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size, dtype=np.uint8)
+    lib().lo_fp8_e4m3_from_f32_array(_p(x), _p(out), C.c_size_t(x.size))
+    return out
+
+
+def fp8_to_f32(b) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(b.size, dtype=np.float32)
+    lib().lo_fp8_e4m3_to_f32_array(_p(b), _p(out), C.c_size_t(b.size))
+    return out
+
+
+def paged_decode_fp8(spec, q, k8, v8, indptr, indices, last, k_scale, v_scale):
+    """Paged decode over FP8 pages (metadata must be valid: checked here with the
+    BF16 contract's page-table validation)."""
+    paged_validate(spec, indptr, indices, last)
+    indptr, indices, last = _i32(indptr), _i32(indices), _i32(last)
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k8, v8 = (np.ascontiguousarray(x, dtype=np.uint8) for x in (k8, v8))
+    out = np.empty(spec.batch_size * spec.num_query_heads * HEAD_DIM, dtype=np.uint16)
+    lse = np.empty(spec.batch_size * spec.num_query_heads, dtype=np.float32)
+    lib().lo_paged_decode_fp8_requests(C.byref(spec), _p(q), _p(k8), _p(v8), _p(indptr),
+                                       _p(indices), _p(last), C.c_size_t(0),
+                                       C.c_size_t(spec.batch_size), C.c_float(k_scale),
+                                       C.c_float(v_scale), _p(out), _p(lse))
+    return out, lse
+
+
+def append_tokens_fp8(spec, tokens, q, k, v, batch_indices, positions, indptr, indices, last,
+                      k_pages, v_pages, k_scale, v_scale, max_tokens=APPEND_MAX_TOKENS):
+    """Explicit-token append writing FP8 pages in place; returns the BF16 query output."""
+    bi, pos = _i32(batch_indices), _i32(positions)
+    indptr, indices, last = _i32(indptr), _i32(indices), _i32(last)
+    q_out = np.empty(tokens * spec.num_query_heads * HEAD_DIM, dtype=np.uint16)
+    e = _Err()
+    _check(lib().lo_append_tokens_fp8_reference(
+        C.byref(spec), C.c_size_t(tokens), C.c_size_t(max_tokens), _p(q), _p(k), _p(v),
+        _p(bi), _p(pos), _p(indptr), C.c_size_t(indptr.size), _p(indices),
+        C.c_size_t(indices.size), _p(last), C.c_size_t(last.size), C.c_float(k_scale),
+        C.c_float(v_scale), _p(q_out), _p(k_pages), _p(v_pages), C.byref(e)), e)
+    return q_out

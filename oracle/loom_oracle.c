@@ -393,23 +393,33 @@ int lo_split_k_merge_reference(const lo_single_spec *s, size_t partitions,
 
 /* ------------------------------------------------------------------------ */
 /* rope/mod.rs:136-161 rotate_tensor (NeoX split-half). */
+/* One head row rotated in FP32 (the values rotate_tensor rounds to BF16). */
+static void rotate_row_f32(const uint16_t *in, int32_t pos, size_t head_dim, size_t rotary_dim,
+                           float scale, float theta, float *out) {
+  size_t half = rotary_dim / 2;
+  for (size_t p = 0; p < half; ++p) {
+    float exponent = 2.0f * (float)p / (float)rotary_dim;
+    float inv_freq = powf(theta, -exponent) / scale;
+    float angle = (float)pos * inv_freq;
+    float sn = sinf(angle), cs = cosf(angle);
+    float first = lo_bf16_to_f32(in[p]);
+    float second = lo_bf16_to_f32(in[half + p]);
+    out[p] = first * cs - second * sn;
+    out[half + p] = second * cs + first * sn;
+  }
+  for (size_t c = rotary_dim; c < head_dim; ++c) out[c] = lo_bf16_to_f32(in[c]);
+}
+
+/* rope/mod.rs:136-161 rotate_tensor (NeoX split-half). */
 static void rotate_tensor(const uint16_t *in, const int32_t *pos, size_t tokens,
                           uint16_t *out, size_t heads, size_t head_dim, size_t rotary_dim,
                           float scale, float theta) {
-  size_t half = rotary_dim / 2;
+  float row[HEAD_DIM];
   for (size_t t = 0; t < tokens; ++t) {
     for (size_t h = 0; h < heads; ++h) {
       size_t base = (t * heads + h) * head_dim;
-      for (size_t p = 0; p < half; ++p) {
-        float exponent = 2.0f * (float)p / (float)rotary_dim;
-        float inv_freq = powf(theta, -exponent) / scale;
-        float angle = (float)pos[t] * inv_freq;
-        float sn = sinf(angle), cs = cosf(angle);
-        float first = lo_bf16_to_f32(in[base + p]);
-        float second = lo_bf16_to_f32(in[base + half + p]);
-        out[base + p] = lo_bf16_from_f32(first * cs - second * sn);
-        out[base + half + p] = lo_bf16_from_f32(second * cs + first * sn);
-      }
+      rotate_row_f32(in + base, pos[t], head_dim, rotary_dim, scale, theta, row);
+      for (size_t c = 0; c < rotary_dim; ++c) out[base + c] = lo_bf16_from_f32(row[c]);
       for (size_t c = rotary_dim; c < head_dim; ++c) out[base + c] = in[base + c];
     }
   }
@@ -831,4 +841,135 @@ int lo_ragged_reference(const lo_ragged_spec *s, const uint16_t *q, size_t nq,
   if ((rc = lo_ragged_validate(s, qo, n_qo, kv, n_kv, err))) return rc;
   lo_ragged_requests(s, q, k, v, qo, kv, 0, s->batch_size, out, lse);
   return LO_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* FP8 E4M3 KV storage (no reference counterpart: the reference lists FP8 KV
+ * as unsupported).  OCP E4M3 ("fn": bias 7, no infinities, 0x7F/0xFF NaN,
+ * largest finite 448).  Encoding saturates finite values to +-448 and rounds
+ * to nearest even; subnormals are m * 2^-9. */
+uint8_t lo_fp8_e4m3_from_f32(float x) {
+  if (isnan(x)) return 0x7F;
+  const uint8_t s = signbit(x) ? 0x80 : 0x00;
+  const float a = fabsf(x);
+  if (a >= 448.0f) return s | 0x7E;
+  if (a < 0.015625f) { /* below 2^-6: subnormal grid m * 2^-9 (m = 8 is 2^-6) */
+    const float m = nearbyintf(a * 512.0f);
+    return s | (uint8_t)m;
+  }
+  int e;
+  const float fr = frexpf(a, &e); /* a = fr * 2^e, fr in [0.5, 1) */
+  int exp = e - 1;                 /* a = (2 fr) * 2^exp, 2 fr in [1, 2) */
+  int m = (int)nearbyintf((2.0f * fr - 1.0f) * 8.0f);
+  if (m == 8) {
+    m = 0;
+    ++exp;
+  }
+  int code = ((exp + 7) << 3) | m;
+  if (code > 0x7E) code = 0x7E;
+  return s | (uint8_t)code;
+}
+
+float lo_fp8_e4m3_to_f32(uint8_t b) {
+  const int e = (b >> 3) & 0xF, m = b & 7;
+  float v;
+  if (e == 15 && m == 7) v = NAN;
+  else if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return (b & 0x80) ? -v : v;
+}
+
+void lo_fp8_e4m3_from_f32_array(const float *src, uint8_t *dst, size_t n) {
+  for (size_t i = 0; i < n; ++i) dst[i] = lo_fp8_e4m3_from_f32(src[i]);
+}
+
+void lo_fp8_e4m3_to_f32_array(const uint8_t *src, float *dst, size_t n) {
+  for (size_t i = 0; i < n; ++i) dst[i] = lo_fp8_e4m3_to_f32(src[i]);
+}
+
+/* The paged decode loop of lo_paged_decode_requests over FP8 pages: K and V
+ * elements are fp8 * k_scale and fp8 * v_scale in FP32. */
+void lo_paged_decode_fp8_requests(const lo_paged_spec *s, const uint16_t *q, const uint8_t *k,
+                                  const uint8_t *v, const int32_t *indptr,
+                                  const int32_t *indices, const int32_t *last, size_t r0,
+                                  size_t r1, float k_scale, float v_scale, uint16_t *out,
+                                  float *lse) {
+  const size_t hq = s->num_query_heads, hkv = s->num_kv_heads, group = hq / hkv;
+  float state[HEAD_DIM];
+  for (size_t r = r0; r < r1; ++r) {
+    int64_t kv_len = lo_paged_request_kv_len(indptr, last, s->batch_size, r);
+    size_t page_start = (size_t)indptr[r];
+    for (size_t h = 0; h < hq; ++h) {
+      const uint16_t *qrow = q + (r * hq + h) * HEAD_DIM;
+      size_t kvh = h / group;
+      float max_score = 0.0f, normalizer = 0.0f;
+      memset(state, 0, sizeof(state));
+      for (int64_t t = 0; t < kv_len; ++t) {
+        size_t page = (size_t)indices[page_start + (size_t)t / PAGE_SIZE];
+        size_t off = (size_t)t % PAGE_SIZE;
+        size_t kv_off = ((page * PAGE_SIZE + off) * hkv + kvh) * HEAD_DIM;
+        float dot = 0.0f;
+        for (unsigned c = 0; c < HEAD_DIM; ++c)
+          dot = fmaf(lo_bf16_to_f32(qrow[c]), lo_fp8_e4m3_to_f32(k[kv_off + c]) * k_scale, dot);
+        float score = dot * s->softmax_scale;
+        if (t == 0) {
+          max_score = score;
+          normalizer = 1.0f;
+          for (unsigned c = 0; c < HEAD_DIM; ++c)
+            state[c] = lo_fp8_e4m3_to_f32(v[kv_off + c]) * v_scale;
+          continue;
+        }
+        float next_max = fmaxf(max_score, score);
+        float prev_w = expf(max_score - next_max);
+        float cur_w = expf(score - next_max);
+        normalizer = normalizer * prev_w + cur_w;
+        for (unsigned c = 0; c < HEAD_DIM; ++c)
+          state[c] = state[c] * prev_w + lo_fp8_e4m3_to_f32(v[kv_off + c]) * v_scale * cur_w;
+        max_score = next_max;
+      }
+      uint16_t *orow = out + (r * hq + h) * HEAD_DIM;
+      for (unsigned c = 0; c < HEAD_DIM; ++c) orow[c] = lo_bf16_from_f32(state[c] / normalizer);
+      lse[r * hq + h] = (max_score + logf(normalizer)) * LOG2E_F32;
+    }
+  }
+}
+
+/* The explicit-token append of lo_append_tokens_reference writing FP8 pages:
+ * the FP32 rotated K row divided by k_scale and the V row divided by v_scale,
+ * each encoded with lo_fp8_e4m3_from_f32.  The query output stays BF16. */
+int lo_append_tokens_fp8_reference(const lo_paged_spec *s, size_t tokens, size_t max_tokens,
+                                   const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                   const int32_t *batch_indices, const int32_t *positions,
+                                   const int32_t *indptr, size_t n_indptr,
+                                   const int32_t *indices, size_t n_indices,
+                                   const int32_t *last, size_t n_last, float k_scale,
+                                   float v_scale, uint16_t *q_out, uint8_t *k_pages,
+                                   uint8_t *v_pages, lo_error *err) {
+  int64_t *slots = malloc(2 * (tokens ? tokens : 1) * sizeof(int64_t));
+  int rc = lo_append_tokens_validate(s, tokens, max_tokens, batch_indices, positions, indptr,
+                                     n_indptr, indices, n_indices, last, n_last, slots, err);
+  if (rc == LO_OK) {
+    uint16_t *rot_k = malloc(tokens * s->num_kv_heads * HEAD_DIM * 2);
+    rc = lo_rope_pos_ids_reference(tokens, s->num_query_heads, s->num_kv_heads, HEAD_DIM,
+                                   HEAD_DIM, 1.0f, 10000.0f, q, k, positions, q_out, rot_k,
+                                   err);
+    free(rot_k);
+    if (rc == LO_OK) {
+      const size_t hkv = s->num_kv_heads;
+      float row[HEAD_DIM];
+      for (size_t t = 0; t < tokens; ++t)
+        for (size_t h = 0; h < hkv; ++h) {
+          const size_t src = (t * hkv + h) * HEAD_DIM;
+          const size_t dst = (((size_t)slots[2 * t] * PAGE_SIZE + (size_t)slots[2 * t + 1]) * hkv +
+                              h) * HEAD_DIM;
+          rotate_row_f32(k + src, positions[t], HEAD_DIM, HEAD_DIM, 1.0f, 10000.0f, row);
+          for (unsigned c = 0; c < HEAD_DIM; ++c) {
+            k_pages[dst + c] = lo_fp8_e4m3_from_f32(row[c] / k_scale);
+            v_pages[dst + c] = lo_fp8_e4m3_from_f32(lo_bf16_to_f32(v[src + c]) / v_scale);
+          }
+        }
+    }
+  }
+  free(slots);
+  return rc;
 }

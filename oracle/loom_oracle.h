@@ -25,6 +25,10 @@
  *     has one query row, the fixture digests of its evidence records, and the
  *     f64 brute force (its recorded output digests come from GPU runs with
  *     bit mismatches, so they are not oracle pins);
+ *   - FP8 E4M3 KV storage (no reference counterpart): the codec against
+ *     torch.float8_e4m3fn (every code decoded, saturating encode of a dense
+ *     sweep), the FP8 decode loop against the BF16 one on exactly
+ *     representable values;
  *   - ragged prefill: output digests of the reference's ragged correctness
  *     records with 0 GPU mismatches (mha_equal_lengths, mqa_append_mixed,
  *     gqa4_mixed), its unit tests' known answers and error matrices;
@@ -227,6 +231,25 @@ int lo_append_tokens_reference(const lo_paged_spec *s, size_t tokens, size_t max
                                const int32_t *indices, size_t n_indices,
                                const int32_t *last, size_t n_last, uint16_t *q_out,
                                uint16_t *k_pages, uint16_t *v_pages, lo_error *err);
+
+/* ---- FP8 E4M3 KV storage (no reference counterpart) ---- */
+uint8_t lo_fp8_e4m3_from_f32(float x);
+float lo_fp8_e4m3_to_f32(uint8_t b);
+void lo_fp8_e4m3_from_f32_array(const float *src, uint8_t *dst, size_t n);
+void lo_fp8_e4m3_to_f32_array(const uint8_t *src, float *dst, size_t n);
+void lo_paged_decode_fp8_requests(const lo_paged_spec *s, const uint16_t *q, const uint8_t *k,
+                                  const uint8_t *v, const int32_t *indptr,
+                                  const int32_t *indices, const int32_t *last, size_t r0,
+                                  size_t r1, float k_scale, float v_scale, uint16_t *out,
+                                  float *lse);
+int lo_append_tokens_fp8_reference(const lo_paged_spec *s, size_t tokens, size_t max_tokens,
+                                   const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                   const int32_t *batch_indices, const int32_t *positions,
+                                   const int32_t *indptr, size_t n_indptr,
+                                   const int32_t *indices, size_t n_indices,
+                                   const int32_t *last, size_t n_last, float k_scale,
+                                   float v_scale, uint16_t *q_out, uint8_t *k_pages,
+                                   uint8_t *v_pages, lo_error *err);
 
 #ifdef __cplusplus
 }
