@@ -618,6 +618,30 @@ def main():
             detail[name].update({"hnd_us_per_call": round(h_us, 3),
                                  "hnd_GBps": round(case.bytes / (h_us * 1e-6) / 1e9, 1)})
             del hplan
+            # and on FP8 E4M3 pages (half the K/V bytes; finite random codes,
+            # per-tensor scales): the K/V bytes per call and their rate
+            n8 = pool * 16 * hkv * 128
+            k8 = torch.randint(0, 0x60, (n8,), dtype=torch.uint8, device="cuda")
+            v8 = torch.randint(0, 0x60, (n8,), dtype=torch.uint8, device="cuda")
+            sc = torch.tensor([0.05, 0.05], dtype=torch.float32, device="cuda")
+            fspec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, 128, 16, kv_dtype="fp8_e4m3")
+            fplan = L.DecodeProvider.load(0).plan_bf16_paged_batch(
+                fspec, max_total_pages=int(case.indptr_h[-1]))
+
+            def bind8(b):
+                h = [b.bind_read(case.q), b.bind_read(k8), b.bind_read(v8),
+                     b.bind_read(case.indptr), b.bind_read(case.indices), b.bind_read(case.last),
+                     b.bind_read_write(case.out), b.bind_read_write(case.lse),
+                     b.bind_read_write(case.ws), b.bind_read(sc)]
+                return L.Bf16PagedBatchDecodeArgs(h[0], h[1], h[2], h[3], h[4], h[5],
+                                                  h[6].write(), h[7].write(), h[8].write(), h[9])
+            f_us = _timed_enqueues(L, stream, 10, bind8, fplan.enqueue_into, a.steps, a.warmup)
+            kv8 = int(2 * 128 * hkv * case.lens.sum())
+            f_bytes = case.bytes - kv8  # the K/V half of the BF16 bytes
+            detail[name].update({"fp8_us_per_call": round(f_us, 3),
+                                 "fp8_algorithmic_bytes": f_bytes,
+                                 "fp8_GBps": round(f_bytes / (f_us * 1e-6) / 1e9, 1)})
+            del fplan, k8, v8
         if name.startswith("c1"):
             # cold: 16 copies of the workload (537 MB) used round-robin
             copies = [case] + [DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name) + i)

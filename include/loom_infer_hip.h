@@ -170,6 +170,18 @@ typedef enum loom_kv_layout {
   LOOM_KV_LAYOUT_HND = 1
 } loom_kv_layout_t;
 
+/* K/V page element type (no reference counterpart: the reference lists FP8 KV
+ * storage as unsupported, same record).  FP8 pages hold OCP E4M3 bytes with
+ * per-tensor scales passed at enqueue as a device f32 [2] operand
+ * (k_scale, v_scale): K = fp8 * k_scale, V = fp8 * v_scale.  Append encodes
+ * K (after RoPE, from FP32) and V as fp8(x / scale): saturating to +-448,
+ * round to nearest even.  Decode reads them; the query, output and LSE stay
+ * BF16 / FP32. */
+typedef enum loom_kv_dtype {
+  LOOM_KV_DTYPE_BF16 = 0,
+  LOOM_KV_DTYPE_FP8_E4M3 = 1
+} loom_kv_dtype_t;
+
 /* ------------------------------------------------------------------------ */
 /* Paged batch-decode contract, crates/loom-infer/src/attention/paged_decode/mod.rs */
 typedef struct loom_paged_decode_spec {
@@ -179,6 +191,7 @@ typedef struct loom_paged_decode_spec {
   uint64_t num_kv_heads;
   float softmax_scale;
   uint32_t kv_layout; /* loom_kv_layout_t; LOOM_KV_LAYOUT_NHD from spec_new */
+  uint32_t kv_dtype;  /* loom_kv_dtype_t; LOOM_KV_DTYPE_BF16 from spec_new */
 } loom_paged_decode_spec_t;
 
 /* Bf16PagedBatchDecodeSpec::new, paged_decode/mod.rs:28-82. */
@@ -193,6 +206,12 @@ loom_status_t loom_paged_decode_spec_with_kv_layout(const loom_paged_decode_spec
                                                     uint32_t kv_layout,
                                                     loom_paged_decode_spec_t *out,
                                                     loom_error_t *err);
+/* The same spec with another K/V page element type (no reference
+ * counterpart; append specs take it from their embedded decode spec). */
+loom_status_t loom_paged_decode_spec_with_kv_dtype(const loom_paged_decode_spec_t *spec,
+                                                   uint32_t kv_dtype,
+                                                   loom_paged_decode_spec_t *out,
+                                                   loom_error_t *err);
 /* validate_page_table, paged_decode/mod.rs:152-213 (host metadata). */
 loom_status_t loom_paged_decode_validate_page_table(const loom_paged_decode_spec_t *spec,
                                                     const int32_t *page_indptr, uint64_t n_indptr,
@@ -402,6 +421,8 @@ typedef struct loom_paged_decode_args {
   loom_handle_t output;        /* Write<bf16> [B, Hq, 128] */
   loom_handle_t lse;           /* Write<f32>  [B, Hq], log2 domain */
   loom_handle_t workspace;     /* Write<u8>   [workspace_bytes] */
+  loom_handle_t kv_scales;     /* Read<f32> [2] for FP8 pages (K/V pages are then
+                                  Read<u8>); {0, 0} for BF16 pages */
 } loom_paged_decode_args_t;
 
 /* Bf16PagedBatchDecodePlan::enqueue_into, decode.rs:1199-1296: one command of
@@ -746,6 +767,8 @@ typedef struct loom_rope_append_args {
   loom_handle_t key_pages;     /* Write<bf16> [pool, 16, Hkv, 128] */
   loom_handle_t value_pages;   /* Write<bf16> [pool, 16, Hkv, 128] */
   loom_handle_t workspace;     /* Write<u8> */
+  loom_handle_t kv_scales;     /* Read<f32> [2] for FP8 pages (K/V pages are then
+                                  Write<u8>); {0, 0} for BF16 pages */
 } loom_rope_append_args_t;
 
 /* enqueue_into, rope/mod.rs:758-830 / :846-934: a metadata-validation kernel

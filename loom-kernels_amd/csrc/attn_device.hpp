@@ -12,6 +12,7 @@ namespace loom_dev {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -55,6 +56,52 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rows_rsrc(const uint16_t 
   // gfx9 word 3: 32-bit data format, no swizzle; stride 0 (raw addressing)
   const int bytes = valid_rows > 0 ? ((valid_rows - 1) * row_elems + 128) * 2 : 0;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
+}
+
+// 8-byte raw buffer load (FP8 rows: 8 elements per lane).
+template <bool NT>
+__device__ __forceinline__ u32x2 load8_rows(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_offset, 0, NT ? 2 : 0));
+}
+
+// FP8 E4M3 (OCP) storage.  Every E4M3 value is exact in BF16 (3 mantissa bits,
+// exponents 2^-9 .. 2^8), so the decode conversion is lossless: the hardware
+// v_cvt_pk_f32_fp8 widens two bytes to FP32, whose top half is the BF16.
+__device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 w) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  u32x4 o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[h], false);
+    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[h], true);
+    o[2 * h] = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u);
+    o[2 * h + 1] =
+        __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u);
+  }
+  return o;
+}
+
+// FP32 -> E4M3: finite values saturate to +-448, round to nearest even (the
+// subnormal grid is m * 2^-9), NaN -> 0x7F.
+__device__ __forceinline__ uint32_t fp8_e4m3_from_f32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t s = (u >> 24) & 0x80u;
+  const uint32_t au = u & 0x7fffffffu;
+  if (au > 0x7f800000u) return 0x7Fu;
+  const float a = __uint_as_float(au);
+  if (a >= 448.0f) return s | 0x7Eu;
+  if (a < 0.015625f) return s | (uint32_t)__builtin_rintf(a * 512.0f);
+  int exp = (int)(au >> 23) - 127;
+  uint32_t top = (au >> 20) & 7u;
+  const uint32_t rem = au & 0xFFFFFu;
+  top += (rem > 0x80000u || (rem == 0x80000u && (top & 1u))) ? 1u : 0u;
+  if (top == 8u) {
+    top = 0u;
+    ++exp;
+  }
+  const uint32_t code = min((uint32_t)((exp + 7) << 3) | top, 0x7Eu);
+  return s | code;
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }

@@ -34,6 +34,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 
 #include "attn_device.hpp"
@@ -113,6 +114,9 @@ struct DecodeArgs {
   // row_elems 128 (t is a multiple of 16 for pages).  Contiguous K/V is NHD.
   int32_t head_elems;
   int32_t row_elems;
+  // FP8 E4M3 pages: device [k_scale, v_scale] (K = fp8 * k_scale, V = fp8 *
+  // v_scale); null for BF16 pages.
+  const float *__restrict__ kv_scales;
 };
 
 // decode.rs:233-246: indptr[B] is the page_indices length (or, for plans made
@@ -170,6 +174,53 @@ __device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int6
 __device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page,
                                           int valid_rows, int lane, int kvh) {
   load_rows(r, a, (int64_t)page * 16, valid_rows, lane, kvh);
+}
+
+// The same 16 rows stored as FP8 E4M3 (one byte per element, so a row of one
+// kv-head is 128 bytes): lane (col, quad) holds 8 bytes of each of rows
+// 4*quad + j.  Half the registers of a BF16 page in flight; widened to the
+// BF16 PageRegs layout (exactly) when the page is consumed.
+struct PageRegs8 {
+  u32x2 k[4];
+  u32x2 v[4];
+};
+
+template <bool FP8>
+using PageBuf = typename std::conditional<FP8, PageRegs8, PageRegs>::type;
+
+__device__ __forceinline__ void load_rows(PageRegs8 &r, const DecodeArgs &a, int64_t token0,
+                                          int valid_rows, int lane, int kvh) {
+  const int col = lane & 15, quad = lane >> 4;
+  const int64_t first = token0 * a.hkv * 128 + (int64_t)kvh * a.head_elems;
+  const uint8_t *k8 = reinterpret_cast<const uint8_t *>(a.k) + first;
+  const uint8_t *v8 = reinterpret_cast<const uint8_t *>(a.v) + first;
+  const int bytes = valid_rows > 0 ? (valid_rows - 1) * a.row_elems + 128 : 0;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(k8), 0, bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(v8), 0, bytes, 0x00020000);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int off = (quad * 4 + j) * a.row_elems + col * 8;
+    r.k[j] = load8_rows<LOOM_DECODE_NT_K>(rk, off);
+    r.v[j] = load8_rows<LOOM_DECODE_NT_V>(rv, off);
+  }
+}
+
+__device__ __forceinline__ void load_page(PageRegs8 &r, const DecodeArgs &a, int page,
+                                          int valid_rows, int lane, int kvh) {
+  load_rows(r, a, (int64_t)page * 16, valid_rows, lane, kvh);
+}
+
+__device__ __forceinline__ const PageRegs &expand(const PageRegs &r) { return r; }
+__device__ __forceinline__ PageRegs expand(const PageRegs8 &r) {
+  PageRegs o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    o.k[j] = fp8x8_to_bf16x8(r.k[j]);
+    o.v[j] = fp8x8_to_bf16x8(r.v[j]);
+  }
+  return o;
 }
 
 
@@ -308,9 +359,9 @@ struct WaveDecoder {
   // touch no memory; the unrolled buffer rotation lets the compiler wait for
   // exactly the oldest block's loads.  tok_of(i) (first token row of block i)
   // and rows_of(i) must be wave-uniform.
-  template <class TokOf, class RowsOf>
+  template <bool FP8 = false, class TokOf, class RowsOf>
   __device__ void stream(int n, TokOf tok_of, RowsOf rows_of) {
-    PageRegs buf[kDepth];
+    PageBuf<FP8> buf[kDepth];
 #pragma unroll
     for (int j = 0; j < kDepth - 1; ++j) load_rows(buf[j], a, tok_of(j), rows_of(j), lane, kvh);
     int i = 0;
@@ -319,7 +370,7 @@ struct WaveDecoder {
       for (int s = 0; s < kDepth; ++s) {
         load_rows(buf[(s + kDepth - 1) % kDepth], a, tok_of(i + kDepth - 1),
                   rows_of(i + kDepth - 1), lane, kvh);
-        process(buf[s], rows_of(i));
+        process(expand(buf[s]), rows_of(i));
         if (++i >= n) return;
       }
     }
@@ -355,10 +406,16 @@ __device__ __forceinline__ int active_teams(int64_t total, int teams) {
   return (int)max<int64_t>(1, min<int64_t>(teams, by_pages));
 }
 
-template <int GT>
+template <int GT, bool FP8 = false>
 __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_split_kv_kernel(
     DecodeArgs a) {
   __shared__ Smem<GT> sm;
+  // FP8 pages: K's scale folds into the score scale, V's into the output.
+  float v_scale = 1.0f;
+  if constexpr (FP8) {
+    a.scale_log2 *= a.kv_scales[0];
+    v_scale = a.kv_scales[1];
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps team state in SGPRs
   const int col = lane & 15, quad = lane >> 4;
@@ -604,9 +661,14 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
           if (quad == 0) {
             uint32_t o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              o[e] = (uint32_t)f32_to_bf16(acc[g][2 * e] / Lg) |
-                     ((uint32_t)f32_to_bf16(acc[g][2 * e + 1] / Lg) << 16);
+            for (int e = 0; e < 4; ++e) {
+              float x0 = acc[g][2 * e] / Lg, x1 = acc[g][2 * e + 1] / Lg;
+              if constexpr (FP8) {
+                x0 *= v_scale;
+                x1 *= v_scale;
+              }
+              o[e] = (uint32_t)f32_to_bf16(x0) | ((uint32_t)f32_to_bf16(x1) << 16);
+            }
             *reinterpret_cast<u32x4 *>(a.out + ((int64_t)rr * a.hq + qh_base + g) * 128 +
                                        col * 8) = u32x4{o[0], o[1], o[2], o[3]};
           }
@@ -643,7 +705,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
   // Pipeline: page v+kDepth-1 is issued before page v is consumed; the
   // unrolled buffer rotation lets the compiler wait for exactly the oldest
   // page's loads.
-  PageRegs buf[kDepth];
+  PageBuf<FP8> buf[kDepth];
   int brows[kDepth];
 #pragma unroll
   for (int j = 0; j < kDepth - 1; ++j) {
@@ -671,7 +733,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
         begin_piece();
       }
       bad |= brows[s] == 0;
-      w.process(buf[s], brows[s]);
+      w.process(expand(buf[s]), brows[s]);
       ++v;
       if (++i >= n) goto stream_done;
       // Waves ahead of schedule yield issue priority to the ones behind: all
@@ -709,10 +771,15 @@ struct DirectSmem {
 
 // W waves per workgroup (4 for the tiniest tables; 8 when a request may hold
 // more pages, so each wave streams fewer of them).
-template <int GT, int W>
+template <int GT, int W, bool FP8 = false>
 __global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direct_kernel(
     DecodeArgs a) {
   __shared__ DirectSmem<GT, W> sm;
+  float v_scale = 1.0f;
+  if constexpr (FP8) {
+    a.scale_log2 *= a.kv_scales[0];
+    v_scale = a.kv_scales[1];
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, quad = lane >> 4;
@@ -754,7 +821,7 @@ __global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direc
         if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
         return wave + W * (s0 + i) == cnt - 1 ? tl : 16;
       };
-      w.stream(n, tok_of, rows_of);
+      w.template stream<FP8>(n, tok_of, rows_of);
     }
   }
   const float l_tot = w.reduce();
@@ -787,7 +854,9 @@ __global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direc
       L = fmaf(sm.wl[wv][g], f, L);
       O = fmaf(sm.wacc[wv][g][d], f, O);
     }
-    a.out[((int64_t)r * a.hq + qh_base + g) * 128 + d] = f32_to_bf16(O / L);
+    float o = O / L;
+    if constexpr (FP8) o *= v_scale;
+    a.out[((int64_t)r * a.hq + qh_base + g) * 128 + d] = f32_to_bf16(o);
     if (d == 0) a.lse[(int64_t)r * a.hq + qh_base + g] = M + __log2f(L);
   }
 }
@@ -845,7 +914,9 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
     M = mb;
   }
   if (poisoned) return;
-  a.out[((int64_t)r * a.hq + qh) * 128 + tid] = f32_to_bf16(o / l);
+  float ov = o / l;
+  if (a.kv_scales) ov *= a.kv_scales[1];  // FP8 pages: V's scale
+  a.out[((int64_t)r * a.hq + qh) * 128 + tid] = f32_to_bf16(ov);
   if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(l);
 }
 
@@ -1058,6 +1129,44 @@ DecodeArgs single_args(const loom_single_decode_spec_t &s, uint32_t gtiles, uint
 }
 }  // namespace
 
+namespace {
+template <bool FP8>
+void launch_direct(const loom_paged_decode_plan_info_t &pi, dim3 g3, dim3 bd, hipStream_t stream,
+                   const DecodeArgs &a) {
+  if (pi.block_threads == 4 * 64) {
+    switch (pi.group_tile) {
+      case 1: hipLaunchKernelGGL((paged_decode_direct_kernel<1, 4, FP8>), g3, bd, 0, stream, a); break;
+      case 2: hipLaunchKernelGGL((paged_decode_direct_kernel<2, 4, FP8>), g3, bd, 0, stream, a); break;
+      case 4: hipLaunchKernelGGL((paged_decode_direct_kernel<4, 4, FP8>), g3, bd, 0, stream, a); break;
+      default: hipLaunchKernelGGL((paged_decode_direct_kernel<8, 4, FP8>), g3, bd, 0, stream, a); break;
+    }
+  } else if (pi.block_threads == 16 * 64) {
+    if (pi.group_tile == 1)
+      hipLaunchKernelGGL((paged_decode_direct_kernel<1, 16, FP8>), g3, bd, 0, stream, a);
+    else
+      hipLaunchKernelGGL((paged_decode_direct_kernel<2, 16, FP8>), g3, bd, 0, stream, a);
+  } else {
+    switch (pi.group_tile) {
+      case 1: hipLaunchKernelGGL((paged_decode_direct_kernel<1, 8, FP8>), g3, bd, 0, stream, a); break;
+      case 2: hipLaunchKernelGGL((paged_decode_direct_kernel<2, 8, FP8>), g3, bd, 0, stream, a); break;
+      case 4: hipLaunchKernelGGL((paged_decode_direct_kernel<4, 8, FP8>), g3, bd, 0, stream, a); break;
+      default: hipLaunchKernelGGL((paged_decode_direct_kernel<8, 8, FP8>), g3, bd, 0, stream, a); break;
+    }
+  }
+}
+
+template <bool FP8>
+void launch_split(const loom_paged_decode_plan_info_t &pi, dim3 g3, dim3 b3, hipStream_t stream,
+                  const DecodeArgs &a) {
+  switch (pi.group_tile) {
+    case 1: hipLaunchKernelGGL((paged_decode_split_kv_kernel<1, FP8>), g3, b3, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((paged_decode_split_kv_kernel<2, FP8>), g3, b3, 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((paged_decode_split_kv_kernel<4, FP8>), g3, b3, 0, stream, a); break;
+    default: hipLaunchKernelGGL((paged_decode_split_kv_kernel<8, FP8>), g3, b3, 0, stream, a); break;
+  }
+}
+}  // namespace
+
 extern "C" {
 
 loom_status_t loom_decode_provider_load(int device, loom_decode_provider_t **out,
@@ -1092,6 +1201,8 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
   if (spec->kv_layout != LOOM_KV_LAYOUT_NHD && spec->kv_layout != LOOM_KV_LAYOUT_HND)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", spec->kv_layout);
+  if (spec->kv_dtype != LOOM_KV_DTYPE_BF16 && spec->kv_dtype != LOOM_KV_DTYPE_FP8_E4M3)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", spec->kv_dtype);
   const uint64_t max_pages = opt.max_total_pages ? opt.max_total_pages : spec->max_num_pages;
   if (max_pages < B) return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
   if (max_pages > (uint64_t)INT32_MAX)
@@ -1176,18 +1287,25 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
   const loom_paged_decode_plan_info_t &pi = plan->info;
   const loom_paged_decode_spec_t &s = pi.spec;
-  static const loom::OperandSpec ops[9] = {
-      {"Q", LOOM_DTYPE_BF16, false},           {"K_pages", LOOM_DTYPE_BF16, false},
-      {"V_pages", LOOM_DTYPE_BF16, false},     {"page_indptr", LOOM_DTYPE_I32, false},
+  // FP8 pages are u8 operands plus the [k_scale, v_scale] operand.
+  const bool fp8 = s.kv_dtype == LOOM_KV_DTYPE_FP8_E4M3;
+  const loom_dtype_t kv_t = fp8 ? LOOM_DTYPE_U8 : LOOM_DTYPE_BF16;
+  const loom::OperandSpec ops[10] = {
+      {"Q", LOOM_DTYPE_BF16, false},           {"K_pages", kv_t, false},
+      {"V_pages", kv_t, false},                {"page_indptr", LOOM_DTYPE_I32, false},
       {"page_indices", LOOM_DTYPE_I32, false}, {"last_page_len", LOOM_DTYPE_I32, false},
       {"O", LOOM_DTYPE_BF16, true},            {"LSE", LOOM_DTYPE_F32, true},
-      {"workspace", LOOM_DTYPE_U8, true}};
-  const loom_handle_t hs[9] = {args->query,       args->key_pages,     args->value_pages,
-                               args->page_indptr, args->page_indices,  args->last_page_len,
-                               args->output,      args->lse,           args->workspace};
-  const loom::Lease *l[9];
-  loom_status_t rc = loom::resolve_command(scope, hs, ops, 9, l, err);
+      {"workspace", LOOM_DTYPE_U8, true},      {"kv_scales", LOOM_DTYPE_F32, false}};
+  const loom_handle_t hs[10] = {args->query,       args->key_pages,    args->value_pages,
+                                args->page_indptr, args->page_indices, args->last_page_len,
+                                args->output,      args->lse,          args->workspace,
+                                args->kv_scales};
+  const int nops = fp8 ? 10 : 9;
+  const loom::Lease *l[10];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, nops, l, err);
   if (rc) return rc;
+  if (fp8 && l[9]->numel != 2)
+    return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, l[9]->numel);
   // decode.rs:1216-1242: exact lengths before submission.
   const uint64_t qn = s.batch_size * s.num_query_heads * loom::kHeadDim;
   const uint64_t kvn = s.max_num_pages * loom::kPageSize * s.num_kv_heads * loom::kHeadDim;
@@ -1211,8 +1329,11 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   for (int i : align_ops)
     if (l[i]->ptr % 16 != 0)
       return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, ops[i].name, (int64_t)l[i]->ptr, 16);
+  if (fp8 && l[9]->ptr % 4 != 0)
+    return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, "kv_scales", (int64_t)l[9]->ptr, 4);
 
-  DecodeArgs a;
+  DecodeArgs a{};
+  a.kv_scales = fp8 ? (const float *)l[9]->ptr : nullptr;
   a.q = (const uint16_t *)l[0]->ptr;
   a.k = (const uint16_t *)l[1]->ptr;
   a.v = (const uint16_t *)l[2]->ptr;
@@ -1244,34 +1365,16 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   const dim3 g3((unsigned)grid), b3(kThreads);
   if (direct) {
     const dim3 bd(pi.block_threads);
-    if (pi.block_threads == 4 * 64) {
-      switch (pi.group_tile) {
-        case 1: hipLaunchKernelGGL((paged_decode_direct_kernel<1, 4>), g3, bd, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((paged_decode_direct_kernel<2, 4>), g3, bd, 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((paged_decode_direct_kernel<4, 4>), g3, bd, 0, stream, a); break;
-        default: hipLaunchKernelGGL((paged_decode_direct_kernel<8, 4>), g3, bd, 0, stream, a); break;
-      }
-    } else if (pi.block_threads == 16 * 64) {
-      if (pi.group_tile == 1)
-        hipLaunchKernelGGL((paged_decode_direct_kernel<1, 16>), g3, bd, 0, stream, a);
-      else
-        hipLaunchKernelGGL((paged_decode_direct_kernel<2, 16>), g3, bd, 0, stream, a);
-    } else {
-      switch (pi.group_tile) {
-        case 1: hipLaunchKernelGGL((paged_decode_direct_kernel<1, 8>), g3, bd, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((paged_decode_direct_kernel<2, 8>), g3, bd, 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((paged_decode_direct_kernel<4, 8>), g3, bd, 0, stream, a); break;
-        default: hipLaunchKernelGGL((paged_decode_direct_kernel<8, 8>), g3, bd, 0, stream, a); break;
-      }
-    }
+    if (fp8)
+      launch_direct<true>(pi, g3, bd, stream, a);
+    else
+      launch_direct<false>(pi, g3, bd, stream, a);
     return loom::record_launch(scope, hipGetLastError(), err);
   }
-  switch (pi.group_tile) {
-    case 1: hipLaunchKernelGGL(paged_decode_split_kv_kernel<1>, g3, b3, 0, stream, a); break;
-    case 2: hipLaunchKernelGGL(paged_decode_split_kv_kernel<2>, g3, b3, 0, stream, a); break;
-    case 4: hipLaunchKernelGGL(paged_decode_split_kv_kernel<4>, g3, b3, 0, stream, a); break;
-    default: hipLaunchKernelGGL(paged_decode_split_kv_kernel<8>, g3, b3, 0, stream, a); break;
-  }
+  if (fp8)
+    launch_split<true>(pi, g3, b3, stream, a);
+  else
+    launch_split<false>(pi, g3, b3, stream, a);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
     // One command: the partial kernel, then the merge of split requests.

@@ -28,6 +28,7 @@
 
 #include <cmath>
 
+#include "attn_device.hpp"
 #include "loom_internal.hpp"
 
 using loom::fail;
@@ -82,6 +83,9 @@ struct AppendArgs {
   // Hkv * 128; HND pages: 16 * 128, 128).
   int32_t head_elems;
   int32_t row_elems;
+  // FP8 E4M3 pages: device [k_scale, v_scale]; the pages hold fp8(x / scale)
+  // bytes.  Null for BF16 pages.
+  const float *kv_scales;
   float inv_freq[64];
 };
 
@@ -272,12 +276,12 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
     uint16_t *dst = is_kv ? a.k_pages + kv_dst : a.q_out + ((int64_t)t * a.hq + row) * 128;
     const u32x4 x = first ? first_slice.x : *reinterpret_cast<const u32x4 *>(src + c * 8);
     const u32x4 xp = first ? first_slice.xp : *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
-    u32x4 o;
+    const bool fp8 = is_kv && a.kv_scales != nullptr;
+    float y[8];
     {
 #pragma clang fp contract(off)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        uint32_t packed = 0;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int elem = c * 8 + e * 2 + h;
@@ -286,19 +290,37 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
           const float other = __uint_as_float(h ? (xp[e] & 0xffff0000u) : (xp[e] << 16));
           const float cs = s_cos[pair], sn = s_sin[pair];
           // first half: first*cos - second*sin; second half: second*cos + first*sin
-          const float y = (c < 8) ? (self * cs - other * sn) : (self * cs + other * sn);
-          packed |= (uint32_t)f32_to_bf16(y) << (16 * h);
+          y[2 * e + h] = (c < 8) ? (self * cs - other * sn) : (self * cs + other * sn);
         }
-        o[e] = packed;
       }
     }
-    *reinterpret_cast<u32x4 *>(dst + c * 8) = o;
-    if (is_kv) {
-      const u32x4 vv = first ? first_slice.v
+    const u32x4 vv = !is_kv ? u32x4{0, 0, 0, 0}
+                     : first ? first_slice.v
                              : *reinterpret_cast<const u32x4 *>(
                                    a.v + ((int64_t)t * a.hkv + kh) * 128 + c * 8);
-      *reinterpret_cast<u32x4 *>(a.v_pages + kv_dst + c * 8) = vv;
+    if (fp8) {
+      // FP8 pages: the FP32 rotated K and the V row, divided by their scales
+      // (correctly rounded) and encoded; 8 bytes per lane.
+      const float ks = a.kv_scales[0], vs = a.kv_scales[1];
+      loom_dev::u32x2 k8 = {0, 0}, v8 = {0, 0};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float vf = __uint_as_float((i & 1) ? (vv[i >> 1] & 0xffff0000u) : (vv[i >> 1] << 16));
+        k8[i >> 2] |= loom_dev::fp8_e4m3_from_f32(y[i] / ks) << (8 * (i & 3));
+        v8[i >> 2] |= loom_dev::fp8_e4m3_from_f32(vf / vs) << (8 * (i & 3));
+      }
+      uint8_t *kp = reinterpret_cast<uint8_t *>(a.k_pages) + kv_dst + c * 8;
+      uint8_t *vp = reinterpret_cast<uint8_t *>(a.v_pages) + kv_dst + c * 8;
+      *reinterpret_cast<loom_dev::u32x2 *>(kp) = k8;
+      *reinterpret_cast<loom_dev::u32x2 *>(vp) = v8;
+      continue;
     }
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = (uint32_t)f32_to_bf16(y[2 * e]) | ((uint32_t)f32_to_bf16(y[2 * e + 1]) << 16);
+    *reinterpret_cast<u32x4 *>(dst + c * 8) = o;
+    if (is_kv) *reinterpret_cast<u32x4 *>(a.v_pages + kv_dst + c * 8) = vv;
   }
 }
 
@@ -388,6 +410,7 @@ struct loom_rope_append_plan {
   uint64_t max_num_pages = 0;
   uint32_t flags = 0;
   uint32_t kv_layout = LOOM_KV_LAYOUT_NHD;
+  uint32_t kv_dtype = LOOM_KV_DTYPE_BF16;
   float inv_freq[64];
 };
 
@@ -414,6 +437,8 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
   if (s.kv_layout != LOOM_KV_LAYOUT_NHD && s.kv_layout != LOOM_KV_LAYOUT_HND)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", s.kv_layout);
+  if (s.kv_dtype != LOOM_KV_DTYPE_BF16 && s.kv_dtype != LOOM_KV_DTYPE_FP8_E4M3)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", s.kv_dtype);
   // rope/mod.rs:628-682: states = tokens * (Hq + Hkv) must fit the grid.
   uint64_t rows = s.num_query_heads + s.num_kv_heads, states;
   if (rows < s.num_query_heads || __builtin_mul_overflow(tokens, rows, &states))
@@ -434,6 +459,7 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
   p->max_num_pages = s.max_num_pages;
   p->flags = flags;
   p->kv_layout = s.kv_layout;
+  p->kv_dtype = s.kv_dtype;
   // rope/mod.rs:148-149 with rope_scale = 1, rope_theta = 1e4, rotary_dim = 128
   // (paged_append/mod.rs:395-403): the reference's exact FP32 inverse frequencies.
   for (int i = 0; i < 64; ++i) {
@@ -487,31 +513,39 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   const loom_rope_append_plan_info_t &pi = plan->info;
   const bool ex = pi.explicit_tokens != 0;
   // Operand order of Bf16RopePagedKvAppend{,Tokens}Args (rope/mod.rs:963-1047).
-  loom::OperandSpec ops[12] = {
+  const bool fp8 = plan->kv_dtype == LOOM_KV_DTYPE_FP8_E4M3;
+  const loom_dtype_t kv_t = fp8 ? LOOM_DTYPE_U8 : LOOM_DTYPE_BF16;
+  loom::OperandSpec ops[13] = {
       {"query", LOOM_DTYPE_BF16, false},        {"key", LOOM_DTYPE_BF16, false},
       {"value", LOOM_DTYPE_BF16, false},        {"batch_indices", LOOM_DTYPE_I32, false},
       {"positions", LOOM_DTYPE_I32, false},     {"page_indptr", LOOM_DTYPE_I32, false},
       {"page_indices", LOOM_DTYPE_I32, false},  {"last_page_len", LOOM_DTYPE_I32, false},
-      {"query_output", LOOM_DTYPE_BF16, true},  {"key_pages", LOOM_DTYPE_BF16, true},
-      {"value_pages", LOOM_DTYPE_BF16, true},   {"workspace", LOOM_DTYPE_U8, true}};
-  loom_handle_t hs_all[12] = {args->query,        args->key,           args->value,
+      {"query_output", LOOM_DTYPE_BF16, true},  {"key_pages", kv_t, true},
+      {"value_pages", kv_t, true},              {"workspace", LOOM_DTYPE_U8, true},
+      {"kv_scales", LOOM_DTYPE_F32, false}};
+  loom_handle_t hs_all[13] = {args->query,        args->key,           args->value,
                               args->batch_indices, args->positions,    args->page_indptr,
                               args->page_indices, args->last_page_len, args->query_output,
-                              args->key_pages,    args->value_pages,   args->workspace};
-  // The one-token form has no batch_indices/positions operands.
-  loom::OperandSpec sel_ops[12];
-  loom_handle_t sel[12];
-  int map[12];
+                              args->key_pages,    args->value_pages,   args->workspace,
+                              args->kv_scales};
+  // The one-token form has no batch_indices/positions operands; only FP8
+  // plans take kv_scales.
+  loom::OperandSpec sel_ops[13];
+  loom_handle_t sel[13];
+  int map[13];
   int n = 0;
-  for (int i = 0; i < 12; ++i) {
+  for (int i = 0; i < 13; ++i) {
     if (!ex && (i == 3 || i == 4)) continue;
+    if (!fp8 && i == 12) continue;
     sel_ops[n] = ops[i];
     sel[n] = hs_all[i];
     map[i] = n++;
   }
-  const loom::Lease *l[12];
+  const loom::Lease *l[13];
   loom_status_t rc = loom::resolve_command(scope, sel, sel_ops, n, l, err);
   if (rc) return rc;
+  if (fp8 && l[map[12]]->numel != 2)
+    return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, l[map[12]]->numel);
   auto L = [&](int i) { return l[map[i]]; };
   const uint64_t T = pi.tokens, B = pi.batch_size, hq = pi.num_query_heads,
                  hkv = pi.num_kv_heads;
@@ -537,7 +571,7 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
     if (L(i)->ptr % 16 != 0)
       return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, ops[i].name, (int64_t)L(i)->ptr, 16);
 
-  AppendArgs a;
+  AppendArgs a{};
   a.q = (const uint16_t *)L(0)->ptr;
   a.k = (const uint16_t *)L(1)->ptr;
   a.v = (const uint16_t *)L(2)->ptr;
@@ -557,6 +591,7 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   a.pool = (int64_t)plan->max_num_pages;
   a.n_indices = (int64_t)L(6)->numel;
   a.indices_capacity = (plan->flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
+  a.kv_scales = fp8 ? (const float *)l[map[12]]->ptr : nullptr;
   a.head_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? 16 * 128 : 128;
   a.row_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? 128 : (int32_t)hkv * 128;
   for (int i = 0; i < 64; ++i) a.inv_freq[i] = plan->inv_freq[i];

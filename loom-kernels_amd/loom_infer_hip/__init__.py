@@ -47,13 +47,25 @@ def _layout_code(kv_layout) -> int:
     return KV_LAYOUTS[kv_layout]
 
 
-def _set_paged_layout(c_paged, kv_layout):
-    """Applies loom_paged_decode_spec_with_kv_layout to an embedded paged spec."""
+# K/V page element types (loom_kv_dtype_t): BF16, or OCP FP8 E4M3 bytes with
+# per-tensor [k_scale, v_scale] (no reference counterpart).
+KV_DTYPES = {"bf16": 0, "fp8_e4m3": 1}
+
+
+def _set_paged_layout(c_paged, kv_layout, kv_dtype="bf16"):
+    """Applies loom_paged_decode_spec_with_kv_{layout,dtype} to an embedded paged spec."""
     code = _layout_code(kv_layout)
     if code != 0:
         out = _ffi.PagedDecodeSpec()
         _call(lib().loom_paged_decode_spec_with_kv_layout, C.byref(c_paged), code, C.byref(out))
         c_paged.kv_layout = out.kv_layout
+    if kv_dtype not in KV_DTYPES:
+        raise ValueError(f"kv_dtype must be one of {sorted(KV_DTYPES)}, got {kv_dtype!r}")
+    if KV_DTYPES[kv_dtype] != 0:
+        out = _ffi.PagedDecodeSpec()
+        _call(lib().loom_paged_decode_spec_with_kv_dtype, C.byref(c_paged), KV_DTYPES[kv_dtype],
+              C.byref(out))
+        c_paged.kv_dtype = out.kv_dtype
 ROPE_PAGED_KV_APPEND_MAX_TOKENS = 64
 ROPE_PAGED_KV_APPEND_MAX_TOKENS_EXTENDED = 8192
 
@@ -213,13 +225,14 @@ class Bf16PagedBatchDecodeSpec:
     """paged_decode/mod.rs:17-149."""
 
     def __init__(self, batch_size, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD"):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_dtype="bf16"):
         self._c = _ffi.PagedDecodeSpec()
         _call(lib().loom_paged_decode_spec_new, batch_size, max_num_pages, num_query_heads,
               num_kv_heads, head_dim, page_size, C.byref(self._c))
-        _set_paged_layout(self._c, kv_layout)
+        _set_paged_layout(self._c, kv_layout, kv_dtype)
 
     kv_layout = property(lambda s: {v: k for k, v in KV_LAYOUTS.items()}[s._c.kv_layout])
+    kv_dtype = property(lambda s: {v: k for k, v in KV_DTYPES.items()}[s._c.kv_dtype])
 
     batch_size = property(lambda s: s._c.batch_size)
     max_num_pages = property(lambda s: s._c.max_num_pages)
@@ -252,11 +265,11 @@ class Bf16RopePagedKvAppendSpec:
     """paged_append/mod.rs:14-131 (one token per request at kv_len-1)."""
 
     def __init__(self, batch_size, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD"):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_dtype="bf16"):
         self._c = _ffi.RopeAppendSpec()
         _call(lib().loom_rope_append_spec_new, batch_size, max_num_pages, num_query_heads,
               num_kv_heads, head_dim, page_size, C.byref(self._c))
-        _set_paged_layout(self._c.paged, kv_layout)
+        _set_paged_layout(self._c.paged, kv_layout, kv_dtype)
         self.paged = _wrap_paged(self._c.paged)
 
     batch_size = property(lambda s: s._c.paged.batch_size)
@@ -284,13 +297,13 @@ class Bf16RopePagedKvAppendTokensSpec:
 
     def __init__(self, tokens, batch_size, max_num_pages, num_query_heads, num_kv_heads,
                  head_dim=HEAD_DIM, page_size=PAGE_SIZE, extended: bool = False,
-                 kv_layout="NHD"):
+                 kv_layout="NHD", kv_dtype="bf16"):
         self._c = _ffi.RopeAppendTokensSpec()
         fn = (lib().loom_rope_append_tokens_spec_new_extended if extended
               else lib().loom_rope_append_tokens_spec_new)
         _call(fn, tokens, batch_size, max_num_pages, num_query_heads, num_kv_heads, head_dim,
               page_size, C.byref(self._c))
-        _set_paged_layout(self._c.paged, kv_layout)
+        _set_paged_layout(self._c.paged, kv_layout, kv_dtype)
         self.paged = _wrap_paged(self._c.paged)
 
     @classmethod
@@ -556,11 +569,12 @@ class Bf16PagedBatchDecodeArgs:
     output: Write
     lse: Write
     workspace: Write
+    kv_scales: Optional[Read] = None  # FP8 pages: Read<f32> [k_scale, v_scale]
 
     def _c(self):
         return _ffi.PagedDecodeArgs(*[_h(getattr(self, f)) for f in (
             "query", "key_pages", "value_pages", "page_indptr", "page_indices",
-            "last_page_len", "output", "lse", "workspace")])
+            "last_page_len", "output", "lse", "workspace", "kv_scales")])
 
     def __post_init__(self):
         c = self._c()
@@ -1072,12 +1086,13 @@ class Bf16RopePagedKvAppendArgs:
     workspace: Write
     batch_indices: Optional[Read] = None
     positions: Optional[Read] = None
+    kv_scales: Optional[Read] = None  # FP8 pages: Read<f32> [k_scale, v_scale]
 
     def _c(self):
         return _ffi.RopeAppendArgs(*[_h(getattr(self, f)) for f in (
             "query", "key", "value", "batch_indices", "positions", "page_indptr",
             "page_indices", "last_page_len", "query_output", "key_pages", "value_pages",
-            "workspace")])
+            "workspace", "kv_scales")])
 
     def __post_init__(self):
         c = self._c()
@@ -1087,11 +1102,11 @@ class Bf16RopePagedKvAppendArgs:
 
 def Bf16RopePagedKvAppendTokensArgs(query, key, value, batch_indices, positions, page_indptr,
                                     page_indices, last_page_len, query_output, key_pages,
-                                    value_pages, workspace):
+                                    value_pages, workspace, kv_scales=None):
     """rope/mod.rs:1005-1047 (same operand order as the reference)."""
     return Bf16RopePagedKvAppendArgs(query, key, value, page_indptr, page_indices,
                                      last_page_len, query_output, key_pages, value_pages,
-                                     workspace, batch_indices, positions)
+                                     workspace, batch_indices, positions, kv_scales)
 
 
 class Bf16RopePagedKvAppendPlan:

@@ -20,7 +20,8 @@ class Error(C.Structure):
 
 class PagedDecodeSpec(C.Structure):
     _fields_ = [("batch_size", u64), ("max_num_pages", u64), ("num_query_heads", u64),
-                ("num_kv_heads", u64), ("softmax_scale", f32), ("kv_layout", u32)]
+                ("num_kv_heads", u64), ("softmax_scale", f32), ("kv_layout", u32),
+                ("kv_dtype", u32)]
 
 
 class RopeAppendSpec(C.Structure):
@@ -50,7 +51,7 @@ class PagedDecodePlanInfo(C.Structure):
 class PagedDecodeArgs(C.Structure):
     _fields_ = [(n, Handle) for n in ("query", "key_pages", "value_pages", "page_indptr",
                                       "page_indices", "last_page_len", "output", "lse",
-                                      "workspace")]
+                                      "workspace", "kv_scales")]
 
 
 class SingleDecodeSpec(C.Structure):
@@ -117,7 +118,8 @@ class RopeAppendPlanInfo(C.Structure):
 class RopeAppendArgs(C.Structure):
     _fields_ = [(n, Handle) for n in ("query", "key", "value", "batch_indices", "positions",
                                       "page_indptr", "page_indices", "last_page_len",
-                                      "query_output", "key_pages", "value_pages", "workspace")]
+                                      "query_output", "key_pages", "value_pages", "workspace",
+                                      "kv_scales")]
 
 
 P = C.POINTER
@@ -129,6 +131,8 @@ SIGNATURES = {
     "loom_abi_version": (u32, []),
     "loom_status_name": (C.c_char_p, [i32]),
     "loom_paged_decode_spec_new": (i32, [u64] * 6 + [P(PagedDecodeSpec), E]),
+    "loom_paged_decode_spec_with_kv_dtype": (
+        i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
     "loom_paged_decode_spec_with_kv_layout": (
         i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
     "loom_paged_prefill_spec_with_kv_layout": (
