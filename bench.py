@@ -570,6 +570,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="configs 1 and 3 only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="skip the HND and FP8 page timings of config 3 (profiling runs)")
     ap.add_argument("--only", default=None,
                     help="run one config (prefix match, e.g. c3) and print its detail")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -607,7 +609,7 @@ def main():
                         "algorithmic_bytes": case.bytes,
                         "teams": case.plan.info.teams,
                         "mean_kv_len": float(case.lens.mean())}
-        if name.startswith("c3"):
+        if name.startswith("c3") and not a.no_variants:
             # the same command on HND pages (same bytes, head-major pages: one
             # kv-head's 16 rows are 4 KiB contiguous); the pool contents are
             # reinterpreted, which does not change the work
