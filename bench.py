@@ -571,7 +571,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="configs 1 and 3 only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-variants", action="store_true",
-                    help="skip the HND and FP8 page timings of config 3 (profiling runs)")
+                    help="skip the HND, FP8 and 64-row page timings of config 3 (profiling runs)")
     ap.add_argument("--only", default=None,
                     help="run one config (prefix match, e.g. c3) and print its detail")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -644,6 +644,33 @@ def main():
                                  "fp8_algorithmic_bytes": f_bytes,
                                  "fp8_GBps": round(f_bytes / (f_us * 1e-6) / 1e9, 1)})
             del fplan, k8, v8
+            # and on 64-row pages (the same pool bytes as pool / 4 pages; the
+            # same request lengths, so the same algorithmic bytes)
+            import numpy as np
+            P = 64
+            pages64 = (case.lens + P - 1) // P
+            ip64 = np.concatenate([[0], np.cumsum(pages64)]).astype(np.int32)
+            ix64 = np.random.default_rng(64).permutation(pool // (P // 16))[: int(ip64[-1])]
+            last64 = (case.lens - (pages64 - 1) * P).astype(np.int32)
+            d_ip = torch.from_numpy(ip64).to("cuda")
+            d_ix = torch.from_numpy(ix64.astype(np.int32)).to("cuda")
+            d_last = torch.from_numpy(last64).to("cuda")
+            pspec = L.Bf16PagedBatchDecodeSpec(B, pool // (P // 16), hq, hkv, kv_page_size=P)
+            pplan = L.DecodeProvider.load(0).plan_bf16_paged_batch(
+                pspec, max_total_pages=int(ip64[-1]))
+
+            def bind64(b):
+                h = [b.bind_read(case.q), b.bind_read(case.k), b.bind_read(case.v),
+                     b.bind_read(d_ip), b.bind_read(d_ix), b.bind_read(d_last),
+                     b.bind_read_write(case.out), b.bind_read_write(case.lse),
+                     b.bind_read_write(case.ws)]
+                return L.Bf16PagedBatchDecodeArgs(h[0], h[1], h[2], h[3], h[4], h[5],
+                                                  h[6].write(), h[7].write(), h[8].write())
+            assert pplan.workspace_bytes <= case.plan.workspace_bytes
+            p_us = _timed_enqueues(L, stream, 9, bind64, pplan.enqueue_into, a.steps, a.warmup)
+            detail[name].update({"page64_us_per_call": round(p_us, 3),
+                                 "page64_GBps": round(case.bytes / (p_us * 1e-6) / 1e9, 1)})
+            del pplan
         if name.startswith("c1"):
             # cold: 16 copies of the workload (537 MB) used round-robin
             copies = [case] + [DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name) + i)

@@ -192,6 +192,8 @@ typedef struct loom_paged_decode_spec {
   float softmax_scale;
   uint32_t kv_layout; /* loom_kv_layout_t; LOOM_KV_LAYOUT_NHD from spec_new */
   uint32_t kv_dtype;  /* loom_kv_dtype_t; LOOM_KV_DTYPE_BF16 from spec_new */
+  uint32_t page_size; /* token rows per page: 16 from spec_new; 32 or 64 through
+                         loom_paged_decode_spec_with_page_size */
 } loom_paged_decode_spec_t;
 
 /* Bf16PagedBatchDecodeSpec::new, paged_decode/mod.rs:28-82. */
@@ -212,6 +214,18 @@ loom_status_t loom_paged_decode_spec_with_kv_dtype(const loom_paged_decode_spec_
                                                    uint32_t kv_dtype,
                                                    loom_paged_decode_spec_t *out,
                                                    loom_error_t *err);
+/* The same spec with another page size (no reference counterpart: the
+ * reference's spec_new accepts 16 only, and so does this library's).  32 and 64
+ * rows per page are accepted for paged decode and paged append (each page is
+ * streamed as page_size / 16 blocks of 16 rows); LOOM_UNSUPPORTED_PAGE_SIZE
+ * otherwise, LOOM_ELEMENT_COUNT_OVERFLOW when pool * page_size does not fit
+ * 31 bits.  The page-table contract scales with it: last_page_len lies in
+ * 1..page_size and token t of a request sits in page t / page_size, row
+ * t % page_size. */
+loom_status_t loom_paged_decode_spec_with_page_size(const loom_paged_decode_spec_t *spec,
+                                                    uint32_t page_size,
+                                                    loom_paged_decode_spec_t *out,
+                                                    loom_error_t *err);
 /* validate_page_table, paged_decode/mod.rs:152-213 (host metadata). */
 loom_status_t loom_paged_decode_validate_page_table(const loom_paged_decode_spec_t *spec,
                                                     const int32_t *page_indptr, uint64_t n_indptr,

@@ -305,9 +305,14 @@ loom_status_t require_len(loom_error_t *err, const char *buffer, uint64_t actual
 
 bool mul_ovf(uint64_t a, uint64_t b, uint64_t *o) { return __builtin_mul_overflow(a, b, o); }
 
+// Token rows per page of a paged spec (16 unless set by spec_with_page_size).
+uint64_t page_rows(const loom_paged_decode_spec_t *s) {
+  return s->page_size ? s->page_size : loom::kPageSize;
+}
+
 // Request geometry on a validated table (paged_decode/mod.rs:242-278).
-int64_t kv_len_of(const int32_t *indptr, const int32_t *last, uint64_t r) {
-  return ((int64_t)indptr[r + 1] - indptr[r] - 1) * (int64_t)loom::kPageSize + last[r];
+int64_t kv_len_of(const int32_t *indptr, const int32_t *last, uint64_t r, uint64_t page) {
+  return ((int64_t)indptr[r + 1] - indptr[r] - 1) * (int64_t)page + last[r];
 }
 
 }  // namespace
@@ -346,6 +351,23 @@ loom_status_t loom_paged_decode_spec_new(uint64_t batch, uint64_t pool, uint64_t
   out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
   out->kv_layout = LOOM_KV_LAYOUT_NHD;
   out->kv_dtype = LOOM_KV_DTYPE_BF16;
+  out->page_size = (uint32_t)loom::kPageSize;
+  return loom::ok(err);
+}
+
+loom_status_t loom_paged_decode_spec_with_page_size(const loom_paged_decode_spec_t *spec,
+                                                    uint32_t page_size,
+                                                    loom_paged_decode_spec_t *out,
+                                                    loom_error_t *err) {
+  if (!spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "spec");
+  if (page_size != 16 && page_size != 32 && page_size != 64)
+    return fail(err, LOOM_UNSUPPORTED_PAGE_SIZE, nullptr, loom::kPageSize, page_size);
+  uint64_t t;
+  if (mul_ovf(spec->max_num_pages, page_size, &t) || t > (uint64_t)INT32_MAX ||
+      mul_ovf(t, spec->num_kv_heads, &t) || mul_ovf(t, loom::kHeadDim, &t))
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  *out = *spec;
+  out->page_size = page_size;
   return loom::ok(err);
 }
 
@@ -439,8 +461,8 @@ loom_status_t loom_paged_decode_validate_page_table(const loom_paged_decode_spec
     int32_t a = indptr[r], b = indptr[r + 1];
     if (b < a) return fail(err, LOOM_NON_MONOTONIC_PAGE_INDPTR, nullptr, r, a, b);
     if (b == a) return fail(err, LOOM_EMPTY_PAGED_REQUEST, nullptr, r);
-    if (last[r] < 1 || last[r] > (int32_t)loom::kPageSize)
-      return fail(err, LOOM_INVALID_LAST_PAGE_LENGTH, nullptr, r, last[r], loom::kPageSize);
+    if (last[r] < 1 || last[r] > (int32_t)page_rows(s))
+      return fail(err, LOOM_INVALID_LAST_PAGE_LENGTH, nullptr, r, last[r], page_rows(s));
   }
   if (indptr[s->batch_size] < 0) return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
   if ((rc = require_len(err, "page_indices", n_indices, (uint64_t)indptr[s->batch_size])))
@@ -455,7 +477,7 @@ loom_status_t loom_paged_decode_request_kv_len(const loom_paged_decode_spec_t *s
                                                const int32_t *indptr, const int32_t *last,
                                                uint64_t request, uint64_t *kv_len) {
   if (!s || request >= s->batch_size) return LOOM_PAGE_INDEX_OUT_OF_RANGE;
-  *kv_len = (uint64_t)kv_len_of(indptr, last, request);
+  *kv_len = (uint64_t)kv_len_of(indptr, last, request, page_rows(s));
   return LOOM_OK;
 }
 
@@ -466,9 +488,9 @@ loom_status_t loom_paged_decode_physical_page_for_token(const loom_paged_decode_
                                                         uint64_t token, uint64_t *page,
                                                         uint64_t *offset) {
   if (!s || request >= s->batch_size) return LOOM_PAGE_INDEX_OUT_OF_RANGE;
-  if ((int64_t)token >= kv_len_of(indptr, last, request)) return LOOM_PAGE_INDEX_OUT_OF_RANGE;
-  *page = (uint64_t)indices[(uint64_t)indptr[request] + token / loom::kPageSize];
-  *offset = token % loom::kPageSize;
+  if ((int64_t)token >= kv_len_of(indptr, last, request, page_rows(s))) return LOOM_PAGE_INDEX_OUT_OF_RANGE;
+  *page = (uint64_t)indices[(uint64_t)indptr[request] + token / page_rows(s)];
+  *offset = token % page_rows(s);
   return LOOM_OK;
 }
 
@@ -498,9 +520,9 @@ loom_status_t loom_rope_append_validate_page_table(const loom_rope_append_spec_t
   std::unordered_map<uint64_t, std::pair<int64_t, int64_t>> seen;
   seen.reserve(s->batch_size * 2);
   for (uint64_t r = 0; r < s->batch_size; ++r) {
-    int64_t pos = kv_len_of(indptr, last, r) - 1;
-    uint64_t page = (uint64_t)indices[(uint64_t)indptr[r] + (uint64_t)pos / loom::kPageSize];
-    uint64_t key = page * loom::kPageSize + (uint64_t)pos % loom::kPageSize;
+    int64_t pos = kv_len_of(indptr, last, r, page_rows(s)) - 1;
+    uint64_t page = (uint64_t)indices[(uint64_t)indptr[r] + (uint64_t)pos / page_rows(s)];
+    uint64_t key = page * page_rows(s) + (uint64_t)pos % page_rows(s);
     auto it = seen.find(key);
     if (it == seen.end())
       seen.emplace(key, std::make_pair((int64_t)r, (int64_t)-1));
@@ -519,7 +541,7 @@ loom_status_t loom_rope_append_validate_page_table(const loom_rope_append_spec_t
   }
   if (best_first >= 0)
     return fail(err, LOOM_DUPLICATE_PAGE_APPEND_SLOT, nullptr, best_first, best_second,
-                (int64_t)(best_key / loom::kPageSize), (int64_t)(best_key % loom::kPageSize));
+                (int64_t)(best_key / page_rows(s)), (int64_t)(best_key % page_rows(s)));
   return loom::ok(err);
 }
 
@@ -585,13 +607,13 @@ loom_status_t loom_rope_append_tokens_validate_metadata(
     int32_t bi = batch_indices[t];
     if (bi < 0 || (uint64_t)bi >= s->batch_size)
       return fail(err, LOOM_APPEND_BATCH_INDEX_OUT_OF_RANGE, nullptr, t, bi, s->batch_size);
-    int64_t kv_len = kv_len_of(indptr, last, (uint64_t)bi);
+    int64_t kv_len = kv_len_of(indptr, last, (uint64_t)bi, page_rows(s));
     int32_t p = positions[t];
     if (p < 0 || p >= kv_len)
       return fail(err, LOOM_APPEND_POSITION_OUT_OF_RANGE, nullptr, t, bi, p, kv_len);
-    uint64_t page = (uint64_t)indices[(uint64_t)indptr[bi] + (uint64_t)p / loom::kPageSize];
-    uint64_t off = (uint64_t)p % loom::kPageSize;
-    uint64_t key = page * loom::kPageSize + off;
+    uint64_t page = (uint64_t)indices[(uint64_t)indptr[bi] + (uint64_t)p / page_rows(s)];
+    uint64_t off = (uint64_t)p % page_rows(s);
+    uint64_t key = page * page_rows(s) + off;
     auto it = seen.find(key);
     if (it != seen.end())
       return fail(err, LOOM_DUPLICATE_PAGE_APPEND_TOKEN_SLOT, nullptr, (int64_t)it->second, t,
@@ -676,7 +698,7 @@ loom_status_t loom_paged_prefill_validate_metadata(const loom_paged_prefill_spec
     if (last[r] < 1 || last[r] > (int32_t)loom::kPageSize)
       return fail(err, LOOM_INVALID_LAST_PAGE_LENGTH, nullptr, r, last[r], loom::kPageSize);
     const int64_t qo_len = (int64_t)qo[r + 1] - qo[r];
-    const int64_t kv_len = kv_len_of(indptr, last, r);
+    const int64_t kv_len = kv_len_of(indptr, last, r, loom::kPageSize);
     if (qo_len > kv_len)
       return fail(err, LOOM_RAGGED_QUERY_LONGER_THAN_KV, nullptr, r, qo_len, kv_len);
   }
@@ -695,7 +717,7 @@ loom_status_t loom_paged_prefill_causal_kv_end(const loom_paged_prefill_spec_t *
   if (!s || !end || request >= s->batch_size) return LOOM_EMPTY_RAGGED_REQUEST;
   const int64_t qo_len = (int64_t)qo[request + 1] - qo[request];
   if ((int64_t)query_index >= qo_len) return LOOM_EMPTY_RAGGED_REQUEST;
-  *end = (uint64_t)(kv_len_of(indptr, last, request) - qo_len + (int64_t)query_index + 1);
+  *end = (uint64_t)(kv_len_of(indptr, last, request, loom::kPageSize) - qo_len + (int64_t)query_index + 1);
   return LOOM_OK;
 }
 

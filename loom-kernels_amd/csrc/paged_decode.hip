@@ -114,6 +114,11 @@ struct DecodeArgs {
   // row_elems 128 (t is a multiple of 16 for pages).  Contiguous K/V is NHD.
   int32_t head_elems;
   int32_t row_elems;
+  // Token rows per page (16, 32 or 64) and log2 of the 16-row blocks per page:
+  // the kernels stream 16-row blocks, block j of page p starting at token row
+  // p * page_rows + 16 * j.
+  int32_t page_rows;
+  int32_t blocks_lg;
   // FP8 E4M3 pages: device [k_scale, v_scale] (K = fp8 * k_scale, V = fp8 *
   // v_scale); null for BF16 pages.
   const float *__restrict__ kv_scales;
@@ -157,10 +162,10 @@ struct PageRegs {
 // buffers (a page of a paged cache, NHD or HND, or any 16 tokens of a
 // contiguous NHD one).  `token0` and `valid_rows` are wave-uniform (the
 // resource lives in SGPRs).
-__device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int64_t token0,
+__device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int64_t elem0,
                                           int valid_rows, int lane, int kvh) {
   const int col = lane & 15, quad = lane >> 4;
-  const int64_t first = token0 * a.hkv * 128 + (int64_t)kvh * a.head_elems;
+  const int64_t first = elem0 + (int64_t)kvh * a.head_elems;
   const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, valid_rows, a.row_elems);
   const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, valid_rows, a.row_elems);
 #pragma unroll
@@ -171,9 +176,18 @@ __device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int6
   }
 }
 
-__device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page,
+// Element offset (kv-head 0) of block `sub` of page `page`.
+__device__ __forceinline__ int64_t block_elem(const DecodeArgs &a, int page, int sub) {
+  return (int64_t)page * a.page_rows * a.hkv * 128 + (int64_t)(sub * 16) * a.row_elems;
+}
+// Element offset (kv-head 0) of token row `token` of contiguous NHD K/V.
+__device__ __forceinline__ int64_t token_elem(const DecodeArgs &a, int64_t token) {
+  return token * a.hkv * 128;
+}
+
+__device__ __forceinline__ void load_page(PageRegs &r, const DecodeArgs &a, int page, int sub,
                                           int valid_rows, int lane, int kvh) {
-  load_rows(r, a, (int64_t)page * 16, valid_rows, lane, kvh);
+  load_rows(r, a, block_elem(a, page, sub), valid_rows, lane, kvh);
 }
 
 // The same 16 rows stored as FP8 E4M3 (one byte per element, so a row of one
@@ -188,10 +202,10 @@ struct PageRegs8 {
 template <bool FP8>
 using PageBuf = typename std::conditional<FP8, PageRegs8, PageRegs>::type;
 
-__device__ __forceinline__ void load_rows(PageRegs8 &r, const DecodeArgs &a, int64_t token0,
+__device__ __forceinline__ void load_rows(PageRegs8 &r, const DecodeArgs &a, int64_t elem0,
                                           int valid_rows, int lane, int kvh) {
   const int col = lane & 15, quad = lane >> 4;
-  const int64_t first = token0 * a.hkv * 128 + (int64_t)kvh * a.head_elems;
+  const int64_t first = elem0 + (int64_t)kvh * a.head_elems;
   const uint8_t *k8 = reinterpret_cast<const uint8_t *>(a.k) + first;
   const uint8_t *v8 = reinterpret_cast<const uint8_t *>(a.v) + first;
   const int bytes = valid_rows > 0 ? (valid_rows - 1) * a.row_elems + 128 : 0;
@@ -207,9 +221,9 @@ __device__ __forceinline__ void load_rows(PageRegs8 &r, const DecodeArgs &a, int
   }
 }
 
-__device__ __forceinline__ void load_page(PageRegs8 &r, const DecodeArgs &a, int page,
+__device__ __forceinline__ void load_page(PageRegs8 &r, const DecodeArgs &a, int page, int sub,
                                           int valid_rows, int lane, int kvh) {
-  load_rows(r, a, (int64_t)page * 16, valid_rows, lane, kvh);
+  load_rows(r, a, block_elem(a, page, sub), valid_rows, lane, kvh);
 }
 
 __device__ __forceinline__ const PageRegs &expand(const PageRegs &r) { return r; }
@@ -225,12 +239,17 @@ __device__ __forceinline__ PageRegs expand(const PageRegs8 &r) {
 
 
 
-// Pages request r contributes to the virtual page list (0 if the request fails
-// the per-request guard of decode.rs:430-478).
-__device__ __forceinline__ int request_pages(int32_t st, int32_t en, int32_t tl, int32_t ipB) {
-  const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= 16;
-  return valid ? en - st : 0;
+// 16-row blocks request r contributes to the virtual block list (0 if the
+// request fails the per-request guard of decode.rs:430-478, last_page_len in
+// 1..page_rows): page_rows / 16 per page, ceil(last / 16) on its last page.
+// With 16-row pages a block is a page.
+__device__ __forceinline__ int request_pages(const DecodeArgs &a, int32_t st, int32_t en,
+                                             int32_t tl, int32_t ipB) {
+  const bool valid = st >= 0 && en > st && en <= ipB && tl >= 1 && tl <= a.page_rows;
+  return valid ? ((en - st - 1) << a.blocks_lg) + ((tl + 15) >> 4) : 0;
 }
+// Valid rows of a request's last block.
+__device__ __forceinline__ int last_block_rows(int32_t tl) { return ((tl - 1) & 15) + 1; }
 
 // Teams split the virtual page list into equal ranges: team t owns
 // [team_start(t), team_start(t+1)).
@@ -357,7 +376,8 @@ struct WaveDecoder {
   // each step issues the loads of the block kDepth-1 steps ahead before
   // consuming the current one.  Loads past the end have no valid rows and
   // touch no memory; the unrolled buffer rotation lets the compiler wait for
-  // exactly the oldest block's loads.  tok_of(i) (first token row of block i)
+  // exactly the oldest block's loads.  tok_of(i) (element offset of block i's
+  // first row for kv-head 0)
   // and rows_of(i) must be wave-uniform.
   template <bool FP8 = false, class TokOf, class RowsOf>
   __device__ void stream(int n, TokOf tok_of, RowsOf rows_of) {
@@ -431,10 +451,10 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     int cnt = 0;
     if (r < a.batch) {
       const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
-      cnt = request_pages(st, en, tl, ipB);
+      cnt = request_pages(a, st, en, tl, ipB);
       if (r < kLdsPrefix) {
         sm.req_st[r] = st;
-        sm.req_tl[r] = tl;
+        sm.req_tl[r] = last_block_rows(tl);
       }
     }
     const int64_t x = wave_incl_scan64(cnt, lane);
@@ -511,7 +531,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
       for (int base = blk * kThreads; found < 0 && base < a.batch; base += 64) {
         const int rr = base + lane;
         int cnt = 0;
-        if (rr < a.batch) cnt = request_pages(a.indptr[rr], a.indptr[rr + 1], a.last[rr], ipB);
+        if (rr < a.batch) cnt = request_pages(a, a.indptr[rr], a.indptr[rr + 1], a.last[rr], ipB);
         const int64_t x = c + wave_incl_scan64(cnt, lane);
         const uint64_t m = __ballot(rr < a.batch && x > v_begin);
         if (m) {
@@ -528,7 +548,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     if (r < kLdsPrefix) {
       cnt0 = (int)(inc - (r > 0 ? sm.incl[r - 1] : 0));
     } else {
-      cnt0 = request_pages(a.indptr[r], a.indptr[r + 1], a.last[r], ipB);
+      cnt0 = request_pages(a, a.indptr[r], a.indptr[r + 1], a.last[r], ipB);
     }
     pre = uni64(inc - uni(cnt0));
   }
@@ -549,7 +569,8 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     } else {
       st_out = a.indptr[rr];
       tl_out = a.last[rr];
-      c = request_pages(st_out, a.indptr[rr + 1], tl_out, ipB);
+      c = request_pages(a, st_out, a.indptr[rr + 1], tl_out, ipB);
+      tl_out = last_block_rows(tl_out);
     }
     st_out = uni(st_out);
     tl_out = uni(tl_out);
@@ -601,18 +622,19 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
           cn = (int)(sm.incl[rr] - sm.incl[rr - 1]);
         } else {
           sto = a.indptr[rr];
-          cn = request_pages(sto, a.indptr[rr + 1], a.last[rr], ipB);
+          cn = request_pages(a, sto, a.indptr[rr + 1], a.last[rr], ipB);
         }
       } while (cn == 0);
     }
-    return a.indices[sto + (int)(vv - pr)];
+    return a.indices[sto + ((int)(vv - pr) >> a.blocks_lg)];
   };
   const int n = (int)(v_end - v_begin);
   int ib = 0, ib_next = 0;  // index blocks: current and next
-  // Page index and valid rows of virtual page vl (0 rows: past the range, or
-  // an index failing the guard of decode.rs:284-289).
-  auto describe = [&](Cursor &c, int64_t vl, int &page, int &rows) {
+  // Page index, block within the page and valid rows of virtual block vl (0
+  // rows: past the range, or an index failing the guard of decode.rs:284-289).
+  auto describe = [&](Cursor &c, int64_t vl, int &page, int &blk, int &rows) {
     page = 0;
+    blk = 0;
     rows = 0;
     if (vl >= v_end) return;
     advance(c, vl);
@@ -624,6 +646,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     const int32_t idx = __builtin_amdgcn_readlane(ib, k & 63);
     if (idx >= 0 && (int64_t)idx < a.pool) {
       page = idx;
+      blk = (int)(vl - c.pre) & ((1 << a.blocks_lg) - 1);
       rows = (int)(vl - c.pre) == c.cnt - 1 ? c.tl : 16;
     }
   };
@@ -709,9 +732,9 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
   int brows[kDepth];
 #pragma unroll
   for (int j = 0; j < kDepth - 1; ++j) {
-    int pg;
-    describe(lc, v_begin + j, pg, brows[j]);
-    load_page(buf[j], a, pg, brows[j], lane, kvh);
+    int pg, blk;
+    describe(lc, v_begin + j, pg, blk, brows[j]);
+    load_page(buf[j], a, pg, blk, brows[j], lane, kvh);
   }
   // Issue priority by progress (see the page loop): every wave starts high.
   __builtin_amdgcn_s_setprio(3);
@@ -723,9 +746,9 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     for (int s = 0; s < kDepth; ++s) {
       {
         const int nb = (s + kDepth - 1) % kDepth;
-        int pg;
-        describe(lc, v + kDepth - 1, pg, brows[nb]);
-        load_page(buf[nb], a, pg, brows[nb], lane, kvh);
+        int pg, blk;
+        describe(lc, v + kDepth - 1, pg, blk, brows[nb]);
+        load_page(buf[nb], a, pg, blk, brows[nb], lane, kvh);
       }
       if (v >= pc.pre + pc.cnt) {
         finish_piece();
@@ -792,34 +815,40 @@ __global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direc
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
   const int32_t st = uni(a.indptr[r]), en = uni(a.indptr[r + 1]), tl = uni(a.last[r]);
   if (ip0 != 0 || !batch_pages_ok(a, ipB)) return;
-  const int cnt = request_pages(st, en, tl, ipB);
+  const int cnt = request_pages(a, st, en, tl, ipB);
   if (cnt == 0) return;
 
   const int g_base = gt * GT;
   const int gcount = min(GT, a.group - g_base);
   WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
                     lane, col, quad, kvh};
-  // this wave's pages: request-local positions wave + W*i
+  // this wave's 16-row blocks: request-local positions wave + W*i (block b
+  // is block b % (page_rows / 16) of the request's page b / (page_rows / 16))
   const int mine = cnt > wave ? (cnt - wave + W - 1) / W : 0;
+  const int tl_rows = last_block_rows(tl);
+  const int bmask = (1 << a.blocks_lg) - 1;
   bool bad = false;
   {
     u32x4 qr[4];
     int idx = 0;
-    if (lane < min(mine, 64)) idx = a.indices[st + wave + W * lane];
+    if (lane < min(mine, 64)) idx = a.indices[st + ((wave + W * lane) >> a.blocks_lg)];
     w.load_q(r, kvh * a.group + g_base, gcount, qr);
     w.store_q(qr);
     w.reset();
     for (int s0 = 0; s0 < mine; s0 += 64) {
-      if (s0 > 0) idx = lane < min(mine - s0, 64) ? a.indices[st + wave + W * (s0 + lane)] : 0;
+      if (s0 > 0)
+        idx = lane < min(mine - s0, 64) ? a.indices[st + ((wave + W * (s0 + lane)) >> a.blocks_lg)]
+                                        : 0;
       const int n = min(mine - s0, 64);
       const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
       bad |= __ballot(lane < n && !ok) != 0;
       auto tok_of = [&](int i) {
-        return (int64_t)__builtin_amdgcn_readlane(idx, min(i, n - 1)) * 16;
+        const int j = min(i, n - 1);
+        return block_elem(a, __builtin_amdgcn_readlane(idx, j), (wave + W * (s0 + j)) & bmask);
       };
       auto rows_of = [&](int i) {
         if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
-        return wave + W * (s0 + i) == cnt - 1 ? tl : 16;
+        return wave + W * (s0 + i) == cnt - 1 ? tl_rows : 16;
       };
       w.template stream<FP8>(n, tok_of, rows_of);
     }
@@ -949,7 +978,9 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_ke
   }
   w.reset();
   if (mine > 0) {
-    auto tok_of = [&](int i) { return (int64_t)(wave + kWaves * min(i, mine - 1)) * 16; };
+    auto tok_of = [&](int i) {
+      return token_elem(a, (int64_t)(wave + kWaves * min(i, mine - 1)) * 16);
+    };
     auto rows_of = [&](int i) {
       if (i >= mine) return 0;
       return (int)min<int64_t>(16, kv_len - (int64_t)(wave + kWaves * i) * 16);
@@ -1016,7 +1047,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_sp
   }
   w.reset();
   const int nb = (int)((end - start + 15) / 16);
-  auto tok_of = [&](int i) { return start + (int64_t)min(i, nb - 1) * 16; };
+  auto tok_of = [&](int i) { return token_elem(a, start + (int64_t)min(i, nb - 1) * 16); };
   auto rows_of = [&](int i) {
     return i >= nb ? 0 : (int)min<int64_t>(16, end - start - (int64_t)i * 16);
   };
@@ -1125,6 +1156,8 @@ DecodeArgs single_args(const loom_single_decode_spec_t &s, uint32_t gtiles, uint
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
   a.head_elems = 128;  // contiguous K/V: NHD rows
   a.row_elems = a.hkv * 128;
+  a.page_rows = 16;
+  a.blocks_lg = 0;
   return a;
 }
 }  // namespace
@@ -1203,6 +1236,9 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", spec->kv_layout);
   if (spec->kv_dtype != LOOM_KV_DTYPE_BF16 && spec->kv_dtype != LOOM_KV_DTYPE_FP8_E4M3)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", spec->kv_dtype);
+  const uint32_t page_rows = spec->page_size ? spec->page_size : (uint32_t)loom::kPageSize;
+  if (page_rows != 16 && page_rows != 32 && page_rows != 64)
+    return fail(err, LOOM_UNSUPPORTED_PAGE_SIZE, nullptr, loom::kPageSize, page_rows);
   const uint64_t max_pages = opt.max_total_pages ? opt.max_total_pages : spec->max_num_pages;
   if (max_pages < B) return fail(err, LOOM_PLAN_INVALID_OPTION, "max_total_pages", max_pages);
   if (max_pages > (uint64_t)INT32_MAX)
@@ -1308,7 +1344,8 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
     return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, l[9]->numel);
   // decode.rs:1216-1242: exact lengths before submission.
   const uint64_t qn = s.batch_size * s.num_query_heads * loom::kHeadDim;
-  const uint64_t kvn = s.max_num_pages * loom::kPageSize * s.num_kv_heads * loom::kHeadDim;
+  const uint64_t page_rows = s.page_size ? s.page_size : loom::kPageSize;
+  const uint64_t kvn = s.max_num_pages * page_rows * s.num_kv_heads * loom::kHeadDim;
   const uint64_t want[9] = {qn, kvn, kvn, s.batch_size + 1, 0, s.batch_size, qn,
                             s.batch_size * s.num_query_heads, pi.workspace_bytes};
   for (int i = 0; i < 9; ++i) {
@@ -1357,8 +1394,10 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.indices_capacity = (pi.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
   const bool hnd = s.kv_layout == LOOM_KV_LAYOUT_HND;
-  a.head_elems = hnd ? 16 * 128 : 128;
+  a.head_elems = hnd ? (int32_t)page_rows * 128 : 128;
   a.row_elems = hnd ? 128 : a.hkv * 128;
+  a.page_rows = (int32_t)page_rows;
+  a.blocks_lg = page_rows == 64 ? 2 : page_rows == 32 ? 1 : 0;
 
   const uint64_t grid = pi.grid_blocks;
   hipStream_t stream = scope->queue->stream;

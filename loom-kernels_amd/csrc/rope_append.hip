@@ -1,4 +1,4 @@
-// Fused NeoX RoPE + paged K/V append for gfx950, BF16 NHD D128 page-16.
+// Fused NeoX RoPE + paged K/V append for gfx950, BF16 or FP8 pages, D128, 16-64 rows per page.
 //
 // Semantics: crates/loom-infer/src/attention/paged_append/mod.rs:360-489 (the
 // CPU reference, one-token and explicit-token forms) via
@@ -79,10 +79,11 @@ struct AppendArgs {
   // first indptr[B] entries are part of the page table.
   int32_t indices_capacity;
   // Page slot geometry: slot (page, off) of kv-head h starts at element
-  // page * 16 * Hkv * 128 + h * head_elems + off * row_elems (NHD: 128,
-  // Hkv * 128; HND pages: 16 * 128, 128).
+  // page * page_rows * Hkv * 128 + h * head_elems + off * row_elems (NHD: 128,
+  // Hkv * 128; HND pages: page_rows * 128, 128).
   int32_t head_elems;
   int32_t row_elems;
+  int32_t page_rows;  // 16, 32 or 64
   // FP8 E4M3 pages: device [k_scale, v_scale]; the pages hold fp8(x / scale)
   // bytes.  Null for BF16 pages.
   const float *kv_scales;
@@ -115,16 +116,16 @@ __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t p
   const int r = a.batch_indices ? a.batch_indices[t] : t;
   if (r < 0 || r >= a.batch) return false;
   const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
-  if (st < 0 || en <= st || (int64_t)en > pages || tl < 1 || tl > 16) return false;
-  const int kv_len = (en - st - 1) * 16 + tl;
+  if (st < 0 || en <= st || (int64_t)en > pages || tl < 1 || tl > a.page_rows) return false;
+  const int kv_len = (en - st - 1) * a.page_rows + tl;
   const int p = a.batch_indices ? a.positions[t] : kv_len - 1;
   if (p < 0 || p >= kv_len) return false;
-  const int32_t pg = a.indices[st + p / 16];
+  const int32_t pg = a.indices[st + p / a.page_rows];
   if (pg < 0 || (int64_t)pg >= a.pool) return false;
   *req = r;
   *pos = p;
   *page = pg;
-  *off = p % 16;
+  *off = p % a.page_rows;
   return true;
 }
 
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
     int64_t pg;
     uint32_t key = kEmptyKey;
     if (token_slot(a, t, pages, &r, &p, &pg, &off))
-      key = (uint32_t)(pg * 16 + off);
+      key = (uint32_t)(pg * a.page_rows + off);
     else
       bad = 1;
     keys[t] = key;
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
   if (tid == 0) bad |= table_bounds_bad(a, a.indptr[0], a.indptr[a.batch]) ? 1 : 0;
   for (int r = tid; r < a.batch; r += kValidateThreads) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
-    bad |= (en <= st || tl < 1 || tl > 16) ? 1 : 0;
+    bad |= (en <= st || tl < 1 || tl > a.page_rows) ? 1 : 0;
   }
   const int slots = hash_slots(a.tokens);
   for (int i = tid; i < slots; i += kValidateThreads) table[i] = kEmptyKey;
@@ -272,7 +273,7 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
     const uint16_t *src = is_kv ? a.k + ((int64_t)t * a.hkv + kh) * 128
                                 : a.q + ((int64_t)t * a.hq + row) * 128;
     const int64_t kv_dst =
-        page * 16 * a.hkv * 128 + (int64_t)kh * a.head_elems + (int64_t)off * a.row_elems;
+        page * a.page_rows * a.hkv * 128 + (int64_t)kh * a.head_elems + (int64_t)off * a.row_elems;
     uint16_t *dst = is_kv ? a.k_pages + kv_dst : a.q_out + ((int64_t)t * a.hq + row) * 128;
     const u32x4 x = first ? first_slice.x : *reinterpret_cast<const u32x4 *>(src + c * 8);
     const u32x4 xp = first ? first_slice.xp : *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
@@ -342,7 +343,9 @@ __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs 
   token_sincos(a, pos, tid, s_sin, s_cos);
   __syncthreads();
   if (!s_ok) return;
-  apply_token(a, t, key >> 4, key & 15, tid, s_sin, s_cos, first);
+  // key = page * page_rows + row
+  apply_token(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid, s_sin,
+              s_cos, first);
 }
 
 // Small commands (T <= 64 tokens, <= 4096 page indices): one launch.  Every
@@ -370,7 +373,7 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
   if (tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
   for (int r = tid; r < a.batch; r += kApplyThreads) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
-    bad |= (en <= st || tl < 1 || tl > 16) ? 1 : 0;
+    bad |= (en <= st || tl < 1 || tl > a.page_rows) ? 1 : 0;
   }
   // tokens (paged_append/mod.rs:262-309)
   if (tid < a.tokens) {
@@ -378,7 +381,7 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
     int64_t pg;
     uint32_t key = 0xffffffffu;
     if (token_slot(a, tid, pages, &r, &p, &pg, &off))
-      key = (uint32_t)(pg * 16 + off);
+      key = (uint32_t)(pg * a.page_rows + off);
     else
       bad = 1;
     s_keys[tid] = key;
@@ -396,7 +399,9 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
   token_sincos(a, pos, tid, s_sin, s_cos);
   if (__syncthreads_or(dup)) return;
   const uint32_t key = s_keys[t];
-  apply_token(a, t, key >> 4, key & 15, tid, s_sin, s_cos, first);
+  // key = page * page_rows + row
+  apply_token(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid, s_sin,
+              s_cos, first);
 }
 
 }  // namespace
@@ -411,6 +416,7 @@ struct loom_rope_append_plan {
   uint32_t flags = 0;
   uint32_t kv_layout = LOOM_KV_LAYOUT_NHD;
   uint32_t kv_dtype = LOOM_KV_DTYPE_BF16;
+  uint32_t page_rows = 16;
   float inv_freq[64];
 };
 
@@ -445,8 +451,11 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
     return fail(err, LOOM_PLAN_STATE_COUNT_OVERFLOW, "RoPE");
   if (states > (uint64_t)INT32_MAX || tokens > (uint64_t)kMaxTokens)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE", states);
-  // Slot keys are page*16+offset in 32 bits.
-  if (s.max_num_pages >= (1ull << 28))
+  // Slot keys are page*page_rows+offset in 32 bits.
+  const uint64_t page_rows = s.page_size ? s.page_size : loom::kPageSize;
+  if (page_rows != 16 && page_rows != 32 && page_rows != 64)
+    return fail(err, LOOM_UNSUPPORTED_PAGE_SIZE, nullptr, loom::kPageSize, page_rows);
+  if (s.max_num_pages >= (1ull << 32) / page_rows)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE page pool", s.max_num_pages);
   auto *p = new loom_rope_append_plan;
   p->info.tokens = tokens;
@@ -460,6 +469,7 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
   p->flags = flags;
   p->kv_layout = s.kv_layout;
   p->kv_dtype = s.kv_dtype;
+  p->page_rows = (uint32_t)page_rows;
   // rope/mod.rs:148-149 with rope_scale = 1, rope_theta = 1e4, rotary_dim = 128
   // (paged_append/mod.rs:395-403): the reference's exact FP32 inverse frequencies.
   for (int i = 0; i < 64; ++i) {
@@ -549,7 +559,7 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   auto L = [&](int i) { return l[map[i]]; };
   const uint64_t T = pi.tokens, B = pi.batch_size, hq = pi.num_query_heads,
                  hkv = pi.num_kv_heads;
-  const uint64_t kvn = plan->max_num_pages * loom::kPageSize * hkv * loom::kHeadDim;
+  const uint64_t kvn = plan->max_num_pages * plan->page_rows * hkv * loom::kHeadDim;
   struct Want {
     int i;
     uint64_t n;
@@ -592,7 +602,8 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   a.n_indices = (int64_t)L(6)->numel;
   a.indices_capacity = (plan->flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
   a.kv_scales = fp8 ? (const float *)l[map[12]]->ptr : nullptr;
-  a.head_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? 16 * 128 : 128;
+  a.page_rows = (int32_t)plan->page_rows;
+  a.head_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? a.page_rows * 128 : 128;
   a.row_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? 128 : (int32_t)hkv * 128;
   for (int i = 0; i < 64; ++i) a.inv_freq[i] = plan->inv_freq[i];
 

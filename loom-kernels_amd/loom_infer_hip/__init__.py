@@ -52,8 +52,15 @@ def _layout_code(kv_layout) -> int:
 KV_DTYPES = {"bf16": 0, "fp8_e4m3": 1}
 
 
-def _set_paged_layout(c_paged, kv_layout, kv_dtype="bf16"):
-    """Applies loom_paged_decode_spec_with_kv_{layout,dtype} to an embedded paged spec."""
+def _set_paged_layout(c_paged, kv_layout, kv_dtype="bf16", kv_page_size=None):
+    """Applies loom_paged_decode_spec_with_kv_{layout,dtype} and, when
+    kv_page_size is given, loom_paged_decode_spec_with_page_size (16, 32 or 64
+    rows per page; no reference counterpart) to an embedded paged spec."""
+    if kv_page_size is not None:
+        out = _ffi.PagedDecodeSpec()
+        _call(lib().loom_paged_decode_spec_with_page_size, C.byref(c_paged), int(kv_page_size),
+              C.byref(out))
+        c_paged.page_size = out.page_size
     code = _layout_code(kv_layout)
     if code != 0:
         out = _ffi.PagedDecodeSpec()
@@ -225,11 +232,12 @@ class Bf16PagedBatchDecodeSpec:
     """paged_decode/mod.rs:17-149."""
 
     def __init__(self, batch_size, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_dtype="bf16"):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_dtype="bf16",
+                 kv_page_size=None):
         self._c = _ffi.PagedDecodeSpec()
         _call(lib().loom_paged_decode_spec_new, batch_size, max_num_pages, num_query_heads,
               num_kv_heads, head_dim, page_size, C.byref(self._c))
-        _set_paged_layout(self._c, kv_layout, kv_dtype)
+        _set_paged_layout(self._c, kv_layout, kv_dtype, kv_page_size)
 
     kv_layout = property(lambda s: {v: k for k, v in KV_LAYOUTS.items()}[s._c.kv_layout])
     kv_dtype = property(lambda s: {v: k for k, v in KV_DTYPES.items()}[s._c.kv_dtype])
@@ -240,10 +248,10 @@ class Bf16PagedBatchDecodeSpec:
     num_kv_heads = property(lambda s: s._c.num_kv_heads)
     softmax_scale = property(lambda s: s._c.softmax_scale)
     head_dim = property(lambda s: HEAD_DIM)
-    page_size = property(lambda s: PAGE_SIZE)
+    page_size = property(lambda s: s._c.page_size or PAGE_SIZE)
     gqa_group_size = property(lambda s: s.num_query_heads // s.num_kv_heads)
     query_numel = property(lambda s: s.batch_size * s.num_query_heads * HEAD_DIM)
-    kv_pages_numel = property(lambda s: s.max_num_pages * PAGE_SIZE * s.num_kv_heads * HEAD_DIM)
+    kv_pages_numel = property(lambda s: s.max_num_pages * s.page_size * s.num_kv_heads * HEAD_DIM)
     output_numel = property(lambda s: s.query_numel)
     lse_numel = property(lambda s: s.batch_size * s.num_query_heads)
     page_indptr_numel = property(lambda s: s.batch_size + 1)
@@ -265,11 +273,12 @@ class Bf16RopePagedKvAppendSpec:
     """paged_append/mod.rs:14-131 (one token per request at kv_len-1)."""
 
     def __init__(self, batch_size, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_dtype="bf16"):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_dtype="bf16",
+                 kv_page_size=None):
         self._c = _ffi.RopeAppendSpec()
         _call(lib().loom_rope_append_spec_new, batch_size, max_num_pages, num_query_heads,
               num_kv_heads, head_dim, page_size, C.byref(self._c))
-        _set_paged_layout(self._c.paged, kv_layout, kv_dtype)
+        _set_paged_layout(self._c.paged, kv_layout, kv_dtype, kv_page_size)
         self.paged = _wrap_paged(self._c.paged)
 
     batch_size = property(lambda s: s._c.paged.batch_size)
@@ -281,7 +290,7 @@ class Bf16RopePagedKvAppendSpec:
     key_numel = property(lambda s: s.batch_size * s.num_kv_heads * HEAD_DIM)
     value_numel = key_numel
     query_output_numel = query_numel
-    kv_pages_numel = property(lambda s: s.max_num_pages * PAGE_SIZE * s.num_kv_heads * HEAD_DIM)
+    kv_pages_numel = property(lambda s: s.paged.kv_pages_numel)
 
     def validate_page_table(self, indptr, indices, last) -> PagedBatchDecodePageTable:
         ip, nip = _i32_array(indptr)
@@ -297,13 +306,13 @@ class Bf16RopePagedKvAppendTokensSpec:
 
     def __init__(self, tokens, batch_size, max_num_pages, num_query_heads, num_kv_heads,
                  head_dim=HEAD_DIM, page_size=PAGE_SIZE, extended: bool = False,
-                 kv_layout="NHD", kv_dtype="bf16"):
+                 kv_layout="NHD", kv_dtype="bf16", kv_page_size=None):
         self._c = _ffi.RopeAppendTokensSpec()
         fn = (lib().loom_rope_append_tokens_spec_new_extended if extended
               else lib().loom_rope_append_tokens_spec_new)
         _call(fn, tokens, batch_size, max_num_pages, num_query_heads, num_kv_heads, head_dim,
               page_size, C.byref(self._c))
-        _set_paged_layout(self._c.paged, kv_layout, kv_dtype)
+        _set_paged_layout(self._c.paged, kv_layout, kv_dtype, kv_page_size)
         self.paged = _wrap_paged(self._c.paged)
 
     @classmethod
@@ -319,7 +328,7 @@ class Bf16RopePagedKvAppendTokensSpec:
     key_numel = property(lambda s: s.tokens * s.num_kv_heads * HEAD_DIM)
     value_numel = key_numel
     query_output_numel = query_numel
-    kv_pages_numel = property(lambda s: s.max_num_pages * PAGE_SIZE * s.num_kv_heads * HEAD_DIM)
+    kv_pages_numel = property(lambda s: s.paged.kv_pages_numel)
 
     def validate_metadata(self, batch_indices, positions, indptr, indices, last):
         bi, nbi = _i32_array(batch_indices)

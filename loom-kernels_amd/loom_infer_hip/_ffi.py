@@ -21,7 +21,7 @@ class Error(C.Structure):
 class PagedDecodeSpec(C.Structure):
     _fields_ = [("batch_size", u64), ("max_num_pages", u64), ("num_query_heads", u64),
                 ("num_kv_heads", u64), ("softmax_scale", f32), ("kv_layout", u32),
-                ("kv_dtype", u32)]
+                ("kv_dtype", u32), ("page_size", u32)]
 
 
 class RopeAppendSpec(C.Structure):
@@ -131,6 +131,8 @@ SIGNATURES = {
     "loom_abi_version": (u32, []),
     "loom_status_name": (C.c_char_p, [i32]),
     "loom_paged_decode_spec_new": (i32, [u64] * 6 + [P(PagedDecodeSpec), E]),
+    "loom_paged_decode_spec_with_page_size": (
+        i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
     "loom_paged_decode_spec_with_kv_dtype": (
         i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
     "loom_paged_decode_spec_with_kv_layout": (

@@ -290,3 +290,46 @@ def test_kv_layout_specs(L):
     assert rc == 75 and e.operand == b"kv_layout"
     with pytest.raises(ValueError):
         L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, kv_layout="bad")
+
+
+def test_page_size_specs(L):
+    """Pages of 32 and 64 rows (no reference counterpart: the reference's
+    spec_new, like this library's, accepts 16 only).  The page-table contract
+    scales with the page size: last_page_len in 1..page_size, token t of a
+    request in page t // page_size, row t % page_size."""
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16PagedBatchDecodeSpec(2, 8, 16, 4, 128, 32)
+    assert e.value.variant == "UnsupportedPageSize" and e.value.fields[:2] == (16, 32)
+    for bad in (8, 48, 128):
+        with pytest.raises(L.ContractError) as e:
+            L.Bf16PagedBatchDecodeSpec(2, 8, 16, 4, kv_page_size=bad)
+        assert e.value.variant == "UnsupportedPageSize"
+    s = L.Bf16PagedBatchDecodeSpec(2, 8, 16, 4, kv_page_size=32, kv_layout="HND")
+    assert (s.page_size, s.kv_layout, s.max_num_pages) == (32, "HND", 8)
+    assert s.kv_pages_numel == 8 * 32 * 4 * 128
+    assert L.Bf16PagedBatchDecodeSpec(2, 8, 16, 4).page_size == 16
+    t = s.validate_page_table([0, 2, 3], [5, 1, 7], [20, 32])
+    assert (t.request_kv_len(0), t.request_kv_len(1)) == (52, 32)
+    assert t.physical_page_for_token(0, 40) == (1, 8)
+    assert t.physical_page_for_token(0, 31) == (5, 31)
+    assert t.physical_page_for_token(0, 52) is None
+    with pytest.raises(L.ContractError) as e:
+        s.validate_page_table([0, 2, 3], [5, 1, 7], [20, 33])
+    assert (e.value.variant, e.value.fields[:3]) == ("InvalidLastPageLength", (1, 33, 32))
+    # a pool whose slot count does not fit 31 bits
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16PagedBatchDecodeSpec(1, 1 << 26, 1, 1, kv_page_size=64)
+    assert e.value.variant == "ElementCountOverflow"
+    # append: one-token slots at kv_len - 1, explicit-token slots (page, row)
+    a = L.Bf16RopePagedKvAppendSpec(2, 8, 2, 1, kv_page_size=64)
+    assert a.paged.page_size == 64 and a.kv_pages_numel == 8 * 64 * 128
+    with pytest.raises(L.ContractError) as e:
+        a.validate_page_table([0, 1, 2], [3, 3], [10, 10])
+    assert (e.value.variant, e.value.fields) == ("DuplicatePageAppendSlot", (0, 1, 3, 9))
+    ts = L.Bf16RopePagedKvAppendTokensSpec(3, 2, 8, 2, 1, kv_page_size=32)
+    slots = ts.validate_metadata([0, 1, 0], [33, 5, 0], [0, 2, 3], [4, 6, 2], [10, 32])
+    assert slots == [(6, 1), (2, 5), (4, 0)]
+    # paged prefill keeps 16-row pages
+    with pytest.raises(L.ContractError) as e:
+        L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, 128, 32)
+    assert e.value.variant == "UnsupportedPageSize"
