@@ -545,6 +545,8 @@ typedef struct loom_paged_prefill_spec {
   uint64_t num_kv_heads;
   float softmax_scale;
   uint32_t kv_layout; /* loom_kv_layout_t; LOOM_KV_LAYOUT_NHD from spec_new */
+  uint32_t page_size; /* 16 from spec_new; 32 or 64 through
+                         loom_paged_prefill_spec_with_page_size */
 } loom_paged_prefill_spec_t;
 
 /* Bf16PagedPrefillSpec::new, paged_prefill/mod.rs:30-91. */
@@ -556,6 +558,12 @@ loom_status_t loom_paged_prefill_spec_new(uint64_t batch_size, uint64_t nnz_qo,
 /* The same spec with another K/V page layout (no reference counterpart). */
 loom_status_t loom_paged_prefill_spec_with_kv_layout(const loom_paged_prefill_spec_t *spec,
                                                      uint32_t kv_layout,
+                                                     loom_paged_prefill_spec_t *out,
+                                                     loom_error_t *err);
+/* The same spec with 32- or 64-row pages (no reference counterpart; the same
+ * contract as loom_paged_decode_spec_with_page_size). */
+loom_status_t loom_paged_prefill_spec_with_page_size(const loom_paged_prefill_spec_t *spec,
+                                                     uint32_t page_size,
                                                      loom_paged_prefill_spec_t *out,
                                                      loom_error_t *err);
 /* validate_metadata, paged_prefill/mod.rs:161-264 (host metadata). */

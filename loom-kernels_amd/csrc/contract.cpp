@@ -309,6 +309,9 @@ bool mul_ovf(uint64_t a, uint64_t b, uint64_t *o) { return __builtin_mul_overflo
 uint64_t page_rows(const loom_paged_decode_spec_t *s) {
   return s->page_size ? s->page_size : loom::kPageSize;
 }
+uint64_t prefill_page_rows(const loom_paged_prefill_spec_t *s) {
+  return s->page_size ? s->page_size : loom::kPageSize;
+}
 
 // Request geometry on a validated table (paged_decode/mod.rs:242-278).
 int64_t kv_len_of(const int32_t *indptr, const int32_t *last, uint64_t r, uint64_t page) {
@@ -488,7 +491,8 @@ loom_status_t loom_paged_decode_physical_page_for_token(const loom_paged_decode_
                                                         uint64_t token, uint64_t *page,
                                                         uint64_t *offset) {
   if (!s || request >= s->batch_size) return LOOM_PAGE_INDEX_OUT_OF_RANGE;
-  if ((int64_t)token >= kv_len_of(indptr, last, request, page_rows(s))) return LOOM_PAGE_INDEX_OUT_OF_RANGE;
+  if ((int64_t)token >= kv_len_of(indptr, last, request, page_rows(s)))
+    return LOOM_PAGE_INDEX_OUT_OF_RANGE;
   *page = (uint64_t)indices[(uint64_t)indptr[request] + token / page_rows(s)];
   *offset = token % page_rows(s);
   return LOOM_OK;
@@ -655,6 +659,23 @@ loom_status_t loom_paged_prefill_spec_new(uint64_t batch, uint64_t nnz_qo, uint6
   out->num_kv_heads = hkv;
   out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
   out->kv_layout = LOOM_KV_LAYOUT_NHD;
+  out->page_size = (uint32_t)loom::kPageSize;
+  return loom::ok(err);
+}
+
+loom_status_t loom_paged_prefill_spec_with_page_size(const loom_paged_prefill_spec_t *spec,
+                                                     uint32_t page_size,
+                                                     loom_paged_prefill_spec_t *out,
+                                                     loom_error_t *err) {
+  if (!spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "spec");
+  if (page_size != 16 && page_size != 32 && page_size != 64)
+    return fail(err, LOOM_UNSUPPORTED_PAGE_SIZE, nullptr, loom::kPageSize, page_size);
+  uint64_t t;
+  if (mul_ovf(spec->max_num_pages, page_size, &t) || t > (uint64_t)INT32_MAX ||
+      mul_ovf(t, spec->num_kv_heads, &t) || mul_ovf(t, loom::kHeadDim, &t))
+    return fail(err, LOOM_ELEMENT_COUNT_OVERFLOW);
+  *out = *spec;
+  out->page_size = page_size;
   return loom::ok(err);
 }
 
@@ -695,10 +716,10 @@ loom_status_t loom_paged_prefill_validate_metadata(const loom_paged_prefill_spec
     const int32_t a = indptr[r], b = indptr[r + 1];
     if (b < a) return fail(err, LOOM_NON_MONOTONIC_PAGE_INDPTR, nullptr, r, a, b);
     if (b == a) return fail(err, LOOM_EMPTY_PAGED_REQUEST, nullptr, r);
-    if (last[r] < 1 || last[r] > (int32_t)loom::kPageSize)
-      return fail(err, LOOM_INVALID_LAST_PAGE_LENGTH, nullptr, r, last[r], loom::kPageSize);
+    if (last[r] < 1 || last[r] > (int32_t)prefill_page_rows(s))
+      return fail(err, LOOM_INVALID_LAST_PAGE_LENGTH, nullptr, r, last[r], prefill_page_rows(s));
     const int64_t qo_len = (int64_t)qo[r + 1] - qo[r];
-    const int64_t kv_len = kv_len_of(indptr, last, r, loom::kPageSize);
+    const int64_t kv_len = kv_len_of(indptr, last, r, prefill_page_rows(s));
     if (qo_len > kv_len)
       return fail(err, LOOM_RAGGED_QUERY_LONGER_THAN_KV, nullptr, r, qo_len, kv_len);
   }
@@ -717,7 +738,8 @@ loom_status_t loom_paged_prefill_causal_kv_end(const loom_paged_prefill_spec_t *
   if (!s || !end || request >= s->batch_size) return LOOM_EMPTY_RAGGED_REQUEST;
   const int64_t qo_len = (int64_t)qo[request + 1] - qo[request];
   if ((int64_t)query_index >= qo_len) return LOOM_EMPTY_RAGGED_REQUEST;
-  *end = (uint64_t)(kv_len_of(indptr, last, request, loom::kPageSize) - qo_len + (int64_t)query_index + 1);
+  *end = (uint64_t)(kv_len_of(indptr, last, request, prefill_page_rows(s)) - qo_len +
+                    (int64_t)query_index + 1);
   return LOOM_OK;
 }
 

@@ -1,4 +1,4 @@
-// Paged causal prefill attention for gfx950 (MI355X), BF16 NHD D128 page-16
+// Paged causal prefill attention for gfx950 (MI355X), BF16 D128, NHD or HND pages of 16-64 rows
 // caches, ragged query rows.
 //
 // Semantics: crates/loom-infer/src/attention/paged_prefill/mod.rs:386-446 (the
@@ -70,6 +70,11 @@ struct PrefillArgs {
   // multiple of 16 for pages, starts at t * Hkv * 128 + h * head_elems.
   int32_t head_elems;
   int32_t row_elems;
+  // Paged K/V: token rows per page (16, 32 or 64) and log2 of the 16-row
+  // blocks per page; the kernel streams 16-row blocks, block j of page p
+  // starting at token row p * page_rows + 16 * j.
+  int32_t page_rows;
+  int32_t blocks_lg;
 };
 
 // Tile count given to a request whose qo range is malformed: larger than any
@@ -108,10 +113,11 @@ struct PrefillPage {
   u32x4 v[4];
 };
 
+// elem0: element offset of the block's first row for kv-head 0.
 __device__ __forceinline__ void load_prefill_page(PrefillPage &p, const PrefillArgs &a,
-                                                  int64_t token0, int rows, int lane, int kvh) {
+                                                  int64_t elem0, int rows, int lane, int kvh) {
   const int col = lane & 15, quad = lane >> 4;
-  const int64_t first = token0 * a.hkv * 128 + (int64_t)kvh * a.head_elems;
+  const int64_t first = elem0 + (int64_t)kvh * a.head_elems;
   const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(a.k + first, rows, a.row_elems);
   const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(a.v + first, rows, a.row_elems);
   const int row_bytes = a.row_elems * 2;
@@ -219,9 +225,9 @@ struct PrefillWave {
 
   // Pages 0..n-1 of this wave's share through a D-deep pipeline: the loads of
   // page i + D - 1 are issued before page i is consumed (loads past the end
-  // have no valid rows and move no bytes).  page_tok(i): physical token row
-  // of page i's first row; rows_of(i): valid rows (0 past the end); lt_of(i):
-  // logical token of its first row.  All wave-uniform.
+  // have no valid rows and move no bytes).  page_tok(i): element offset of
+  // block i's first row (kv-head 0); rows_of(i): valid rows (0 past the end);
+  // lt_of(i): logical token of its first row.  All wave-uniform.
   template <int D, class PageTok, class RowsOf, class LtOf>
   __device__ void stream(int n, PageTok page_tok, RowsOf rows_of, LtOf lt_of) {
     PrefillPage buf[D];
@@ -359,9 +365,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     tl = (int32_t)(kv_len - (int64_t)(req_pages - 1) * 16);
   } else {
     tl = uni(sm.meta[4]);
-    if (ps < 0 || pe <= ps || pe > ipB || tl < 1 || tl > 16) return;
-    req_pages = pe - ps;
-    kv_len = (int64_t)(req_pages - 1) * 16 + tl;
+    if (ps < 0 || pe <= ps || pe > ipB || tl < 1 || tl > a.page_rows) return;
+    kv_len = (int64_t)(pe - ps - 1) * a.page_rows + tl;
+    // 16-row blocks of the request and the valid rows of its last one
+    req_pages = (int)((kv_len + 15) / 16);
+    tl = (int32_t)(kv_len - (int64_t)(req_pages - 1) * 16);
   }
   const int qo_len = qe - qs;
   if ((int64_t)qo_len > kv_len) return;
@@ -387,11 +395,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
   bool bad = false;
   int idx = 0;
   if constexpr (!RAGGED) {
-    for (int i = tid; i < req_pages; i += W * 64) {
+    for (int i = tid; i < pe - ps; i += W * 64) {
       const int32_t x = a.indices[ps + i];
       bad |= x < 0 || (int64_t)x >= a.pool;
     }
-    idx = lane < min(mine, 64) ? a.indices[ps + wave + W * lane] : 0;
+    idx = lane < min(mine, 64) ? a.indices[ps + ((wave + W * lane) >> a.blocks_lg)] : 0;
   }
   if (wave == 0) {
     const uint16_t *qp = a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 +
@@ -409,11 +417,15 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
   w.reset();
   for (int s0 = 0; s0 < mine; s0 += 64) {
     const int n = uni(min(mine - s0, 64));
-    if (!RAGGED && s0 > 0) idx = lane < n ? a.indices[ps + wave + W * (s0 + lane)] : 0;
+    if (!RAGGED && s0 > 0)
+      idx = lane < n ? a.indices[ps + ((wave + W * (s0 + lane)) >> a.blocks_lg)] : 0;
     const int ok = (RAGGED || (idx >= 0 && (int64_t)idx < a.pool)) ? 1 : 0;
     auto page_tok = [&](int i) {
-      if constexpr (RAGGED) return (int64_t)ps + (int64_t)(wave + W * (s0 + i)) * 16;
-      return (int64_t)__builtin_amdgcn_readlane(idx, uni(min(i, n - 1))) * 16;
+      if constexpr (RAGGED) return ((int64_t)ps + (int64_t)(wave + W * (s0 + i)) * 16) * a.hkv * 128;
+      const int j = uni(min(i, n - 1));
+      const int b = wave + W * (s0 + j);
+      return (int64_t)__builtin_amdgcn_readlane(idx, j) * a.page_rows * a.hkv * 128 +
+             (int64_t)((b & ((1 << a.blocks_lg) - 1)) * 16) * a.row_elems;
     };
     auto rows_of = [&](int i) {
       if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
@@ -566,6 +578,9 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
   if (spec->kv_layout != LOOM_KV_LAYOUT_NHD && spec->kv_layout != LOOM_KV_LAYOUT_HND)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", spec->kv_layout);
+  if (spec->page_size != 0 && spec->page_size != 16 && spec->page_size != 32 &&
+      spec->page_size != 64)
+    return fail(err, LOOM_UNSUPPORTED_PAGE_SIZE, nullptr, loom::kPageSize, spec->page_size);
   if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
   uint64_t tiles = 0, grid = 0;
@@ -619,7 +634,8 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   if (rc) return rc;
   // prefill.rs:2474-2495: exact spans, page_indices at least B entries.
   const uint64_t qn = s.nnz_qo * s.num_query_heads * loom::kHeadDim;
-  const uint64_t kvn = s.max_num_pages * loom::kPageSize * s.num_kv_heads * loom::kHeadDim;
+  const uint64_t page_rows = s.page_size ? s.page_size : loom::kPageSize;
+  const uint64_t kvn = s.max_num_pages * page_rows * s.num_kv_heads * loom::kHeadDim;
   const uint64_t want[9] = {qn, kvn, kvn, s.batch_size + 1, s.batch_size + 1, 0,
                             s.batch_size, qn, s.nnz_qo * s.num_query_heads};
   for (int i = 0; i < 9; ++i) {
@@ -654,8 +670,10 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
   a.indices_capacity = (plan->info.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
   const bool hnd = s.kv_layout == LOOM_KV_LAYOUT_HND;
-  a.head_elems = hnd ? 16 * 128 : 128;
+  a.head_elems = hnd ? (int32_t)page_rows * 128 : 128;
   a.row_elems = hnd ? 128 : a.hkv * 128;
+  a.page_rows = (int32_t)page_rows;
+  a.blocks_lg = page_rows == 64 ? 2 : page_rows == 32 ? 1 : 0;
   hipStream_t stream = scope->queue->stream;
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
   switch (plan->info.waves) {
@@ -749,6 +767,8 @@ loom_status_t loom_ragged_prefill_enqueue(const loom_ragged_prefill_plan_t *plan
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
   a.head_elems = 128;  // contiguous K/V: NHD rows
   a.row_elems = a.hkv * 128;
+  a.page_rows = 16;
+  a.blocks_lg = 0;
   hipStream_t stream = scope->queue->stream;
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
   switch (plan->info.waves) {

@@ -812,7 +812,7 @@ class PagedPrefillMetadata:
         if request >= self.spec.batch_size:
             return None
         st, en = self.request_page_range(request)
-        return (en - st - 1) * PAGE_SIZE + self.last_page_len[request]
+        return (en - st - 1) * self.spec.page_size + self.last_page_len[request]
 
     def causal_kv_end(self, request: int, query_index: int):
         qo, _ = _i32_array(self.qo_indptr)
@@ -827,14 +827,15 @@ class PagedPrefillMetadata:
         kv = self.request_kv_len(request)
         if kv is None or token >= kv:
             return None
-        return self.page_indices[self.page_indptr[request] + token // PAGE_SIZE], token % PAGE_SIZE
+        P = self.spec.page_size
+        return self.page_indices[self.page_indptr[request] + token // P], token % P
 
 
 class Bf16PagedPrefillSpec:
     """paged_prefill/mod.rs:11-159."""
 
     def __init__(self, batch_size, nnz_qo, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD"):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_page_size=None):
         self._c = _ffi.PagedPrefillSpec()
         _call(lib().loom_paged_prefill_spec_new, batch_size, nnz_qo, max_num_pages,
               num_query_heads, num_kv_heads, head_dim, page_size, C.byref(self._c))
@@ -843,6 +844,11 @@ class Bf16PagedPrefillSpec:
             out = _ffi.PagedPrefillSpec()
             _call(lib().loom_paged_prefill_spec_with_kv_layout, C.byref(self._c), code,
                   C.byref(out))
+            self._c = out
+        if kv_page_size is not None:
+            out = _ffi.PagedPrefillSpec()
+            _call(lib().loom_paged_prefill_spec_with_page_size, C.byref(self._c),
+                  int(kv_page_size), C.byref(out))
             self._c = out
 
     kv_layout = property(lambda s: {v: k for k, v in KV_LAYOUTS.items()}[s._c.kv_layout])
@@ -854,10 +860,10 @@ class Bf16PagedPrefillSpec:
     num_kv_heads = property(lambda s: s._c.num_kv_heads)
     softmax_scale = property(lambda s: s._c.softmax_scale)
     head_dim = property(lambda s: HEAD_DIM)
-    page_size = property(lambda s: PAGE_SIZE)
+    page_size = property(lambda s: s._c.page_size or PAGE_SIZE)
     gqa_group_size = property(lambda s: s.num_query_heads // s.num_kv_heads)
     query_numel = property(lambda s: s.nnz_qo * s.num_query_heads * HEAD_DIM)
-    kv_pages_numel = property(lambda s: s.max_num_pages * PAGE_SIZE * s.num_kv_heads * HEAD_DIM)
+    kv_pages_numel = property(lambda s: s.max_num_pages * s.page_size * s.num_kv_heads * HEAD_DIM)
     output_numel = property(lambda s: s.query_numel)
     lse_numel = property(lambda s: s.nnz_qo * s.num_query_heads)
     indptr_numel = property(lambda s: s.batch_size + 1)

@@ -74,7 +74,7 @@ class SingleDecodeSplitKArgs(C.Structure):
 class PagedPrefillSpec(C.Structure):
     _fields_ = [("batch_size", u64), ("nnz_qo", u64), ("max_num_pages", u64),
                 ("num_query_heads", u64), ("num_kv_heads", u64), ("softmax_scale", f32),
-                ("kv_layout", u32)]
+                ("kv_layout", u32), ("page_size", u32)]
 
 
 class PagedPrefillPlanOptions(C.Structure):
@@ -137,6 +137,8 @@ SIGNATURES = {
         i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
     "loom_paged_decode_spec_with_kv_layout": (
         i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
+    "loom_paged_prefill_spec_with_page_size": (
+        i32, [P(PagedPrefillSpec), u32, P(PagedPrefillSpec), E]),
     "loom_paged_prefill_spec_with_kv_layout": (
         i32, [P(PagedPrefillSpec), u32, P(PagedPrefillSpec), E]),
     "loom_paged_decode_validate_page_table": (

@@ -329,7 +329,16 @@ def test_page_size_specs(L):
     ts = L.Bf16RopePagedKvAppendTokensSpec(3, 2, 8, 2, 1, kv_page_size=32)
     slots = ts.validate_metadata([0, 1, 0], [33, 5, 0], [0, 2, 3], [4, 6, 2], [10, 32])
     assert slots == [(6, 1), (2, 5), (4, 0)]
-    # paged prefill keeps 16-row pages
+    # paged prefill: spec_new keeps the reference's 16; the setter takes 32/64
     with pytest.raises(L.ContractError) as e:
         L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, 128, 32)
     assert e.value.variant == "UnsupportedPageSize"
+    ps = L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, kv_page_size=64)
+    assert ps.page_size == 64 and ps.kv_pages_numel == 8 * 64 * 4 * 128
+    md = ps.validate_metadata([0, 2, 5], [0, 1, 3], [4, 2, 7], [60, 3])
+    assert md.request_kv_len(0) == 60 and md.request_kv_len(1) == 67
+    assert md.physical_page_for_token(1, 65) == (7, 1)
+    assert md.causal_kv_end(1, 0) == 65
+    with pytest.raises(L.ContractError) as e:
+        ps.validate_metadata([0, 2, 5], [0, 1, 3], [4, 2, 7], [65, 3])
+    assert (e.value.variant, e.value.fields[:3]) == ("InvalidLastPageLength", (0, 65, 64))

@@ -188,3 +188,41 @@ def test_fp8_decode_page_size_equals_16_row_table(L, oracle, opts):
     assert p1.info.algorithm == p2.info.algorithm
     assert not np.any(np.isnan(oracle.bf16_to_f32(o1)))
     assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
+
+
+@pytest.mark.parametrize("P", [32, 64])
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+def test_prefill_page_size_equals_16_row_table(L, oracle, P, layout):
+    """Paged causal prefill on P-row pages equals the 16-row command on the
+    table naming the same bytes (NHD), and HND P-row pages the NHD ones."""
+    from gpu_util import PrefillRunner
+    log(f"prefill page size {P} {layout}")
+    rng = np.random.default_rng(P + len(layout))
+    B, hq, hkv = 3, 16, 4
+    qo_lens, kv_lens = [3, 40, 1], [40, 300, P]
+    pool = sum((n + P - 1) // P for n in kv_lens) + 2
+    ip, ix, last = table(rng, kv_lens, pool, P)
+    ip16, ix16, last16 = to_rows16(ip, ix, last, P)
+    m = P // 16
+    qo = np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32)
+    nnz = int(qo[-1])
+    q = seeded_normal_bf16(oracle, rng, nnz * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * P * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * P * hkv * 128)
+    ref = oracle.prefill(oracle.prefill_spec(B, nnz, pool * m, hq, hkv), q, k, v, qo, ip16,
+                         ix16, last16)
+    r16 = PrefillRunner(L, B, nnz, pool * m, hq, hkv)
+    o1, l1 = r16.run(q, k, v, qo, ip16, ix16, last16)
+    compare_decode(oracle, o1, l1, *ref)
+    rp = PrefillRunner(L, B, nnz, pool, hq, hkv)
+    rp.spec = L.Bf16PagedPrefillSpec(B, nnz, pool, hq, hkv, kv_layout=layout, kv_page_size=P)
+    rp.plan = rp.provider.plan_bf16_paged(rp.spec)
+    if layout == "HND":
+        def conv(x):
+            return np.ascontiguousarray(
+                x.reshape(pool, P, hkv, 128).transpose(0, 2, 1, 3)).reshape(-1)
+        kk, vv = conv(k), conv(v)
+    else:
+        kk, vv = k, v
+    o2, l2 = rp.run(q, kk, vv, qo, ip, ix, last)
+    assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
