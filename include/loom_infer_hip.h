@@ -547,6 +547,7 @@ typedef struct loom_paged_prefill_spec {
   uint32_t kv_layout; /* loom_kv_layout_t; LOOM_KV_LAYOUT_NHD from spec_new */
   uint32_t page_size; /* 16 from spec_new; 32 or 64 through
                          loom_paged_prefill_spec_with_page_size */
+  uint32_t kv_dtype;  /* loom_kv_dtype_t; LOOM_KV_DTYPE_BF16 from spec_new */
 } loom_paged_prefill_spec_t;
 
 /* Bf16PagedPrefillSpec::new, paged_prefill/mod.rs:30-91. */
@@ -560,6 +561,12 @@ loom_status_t loom_paged_prefill_spec_with_kv_layout(const loom_paged_prefill_sp
                                                      uint32_t kv_layout,
                                                      loom_paged_prefill_spec_t *out,
                                                      loom_error_t *err);
+/* The same spec with FP8 E4M3 K/V pages (no reference counterpart; the pages
+ * and the kv_scales operand as for paged decode). */
+loom_status_t loom_paged_prefill_spec_with_kv_dtype(const loom_paged_prefill_spec_t *spec,
+                                                    uint32_t kv_dtype,
+                                                    loom_paged_prefill_spec_t *out,
+                                                    loom_error_t *err);
 /* The same spec with 32- or 64-row pages (no reference counterpart; the same
  * contract as loom_paged_decode_spec_with_page_size). */
 loom_status_t loom_paged_prefill_spec_with_page_size(const loom_paged_prefill_spec_t *spec,
@@ -641,6 +648,8 @@ typedef struct loom_paged_prefill_args {
   loom_handle_t last_page_len; /* Read<i32>   [B] */
   loom_handle_t output;        /* Write<bf16> [nnz_qo, Hq, 128] */
   loom_handle_t lse;           /* Write<f32>  [nnz_qo, Hq], log2 domain */
+  loom_handle_t kv_scales;     /* Read<f32> [2] for FP8 pages (K/V pages are then
+                                  Read<u8>); {0, 0} for BF16 pages */
 } loom_paged_prefill_args_t;
 
 /* Bf16PagedPrefillPlan::enqueue_into, prefill.rs:2447-2560: one command, one

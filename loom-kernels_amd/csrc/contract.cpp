@@ -660,6 +660,19 @@ loom_status_t loom_paged_prefill_spec_new(uint64_t batch, uint64_t nnz_qo, uint6
   out->softmax_scale = 1.0f / std::sqrt((float)head_dim);
   out->kv_layout = LOOM_KV_LAYOUT_NHD;
   out->page_size = (uint32_t)loom::kPageSize;
+  out->kv_dtype = LOOM_KV_DTYPE_BF16;
+  return loom::ok(err);
+}
+
+loom_status_t loom_paged_prefill_spec_with_kv_dtype(const loom_paged_prefill_spec_t *spec,
+                                                    uint32_t kv_dtype,
+                                                    loom_paged_prefill_spec_t *out,
+                                                    loom_error_t *err) {
+  if (!spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "spec");
+  if (kv_dtype != LOOM_KV_DTYPE_BF16 && kv_dtype != LOOM_KV_DTYPE_FP8_E4M3)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", kv_dtype);
+  *out = *spec;
+  out->kv_dtype = kv_dtype;
   return loom::ok(err);
 }
 

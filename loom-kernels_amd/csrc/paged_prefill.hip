@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "attn_device.hpp"
 #include "loom_internal.hpp"
@@ -75,6 +76,9 @@ struct PrefillArgs {
   // starting at token row p * page_rows + 16 * j.
   int32_t page_rows;
   int32_t blocks_lg;
+  // FP8 E4M3 pages: device [k_scale, v_scale] (K = fp8 * k_scale, V = fp8 *
+  // v_scale); null for BF16 pages.
+  const float *kv_scales;
 };
 
 // Tile count given to a request whose qo range is malformed: larger than any
@@ -126,6 +130,44 @@ __device__ __forceinline__ void load_prefill_page(PrefillPage &p, const PrefillA
 #pragma unroll
   for (int j = 0; j < 4; ++j) p.v[j] = load16_rows<false>(rv, (quad * 4 + j) * row_bytes + col * 16);
 }
+
+// The same block on FP8 E4M3 pages (one byte per element): 8 bytes per lane
+// per fragment, widened to the BF16 layout above (exactly) when consumed.
+struct PrefillPage8 {
+  u32x2 k[4];
+  u32x2 v[4];
+};
+
+__device__ __forceinline__ void load_prefill_page(PrefillPage8 &p, const PrefillArgs &a,
+                                                  int64_t elem0, int rows, int lane, int kvh) {
+  const int col = lane & 15, quad = lane >> 4;
+  const int64_t first = elem0 + (int64_t)kvh * a.head_elems;
+  const uint8_t *k8 = reinterpret_cast<const uint8_t *>(a.k) + first;
+  const uint8_t *v8 = reinterpret_cast<const uint8_t *>(a.v) + first;
+  const int bytes = rows > 0 ? (rows - 1) * a.row_elems + 128 : 0;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(k8), 0, bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(v8), 0, bytes, 0x00020000);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) p.k[c] = load8_rows<false>(rk, col * a.row_elems + 32 * c + 8 * quad);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p.v[j] = load8_rows<false>(rv, (quad * 4 + j) * a.row_elems + col * 8);
+}
+
+__device__ __forceinline__ const PrefillPage &expand(const PrefillPage &p) { return p; }
+__device__ __forceinline__ PrefillPage expand(const PrefillPage8 &p) {
+  PrefillPage o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    o.k[j] = fp8x8_to_bf16x8(p.k[j]);
+    o.v[j] = fp8x8_to_bf16x8(p.v[j]);
+  }
+  return o;
+}
+
+template <bool FP8>
+using PrefillBuf = typename std::conditional<FP8, PrefillPage8, PrefillPage>::type;
 
 // Upper 16 bits of two floats packed into one register (lo <- a, hi <- b).
 __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
@@ -228,9 +270,9 @@ struct PrefillWave {
   // have no valid rows and move no bytes).  page_tok(i): element offset of
   // block i's first row (kv-head 0); rows_of(i): valid rows (0 past the end);
   // lt_of(i): logical token of its first row.  All wave-uniform.
-  template <int D, class PageTok, class RowsOf, class LtOf>
+  template <int D, bool FP8, class PageTok, class RowsOf, class LtOf>
   __device__ void stream(int n, PageTok page_tok, RowsOf rows_of, LtOf lt_of) {
-    PrefillPage buf[D];
+    PrefillBuf<FP8> buf[D];
 #pragma unroll
     for (int j = 0; j < D - 1; ++j) load_prefill_page(buf[j], a, page_tok(j), rows_of(j), lane, kvh);
     int i = 0;
@@ -239,15 +281,22 @@ struct PrefillWave {
       for (int s = 0; s < D; ++s) {
         load_prefill_page(buf[(s + D - 1) % D], a, page_tok(i + D - 1), rows_of(i + D - 1), lane,
                           kvh);
-        process(buf[s], lt_of(i));
+        process(expand(buf[s]), lt_of(i));
         if (++i >= n) return;
       }
     }
   }
 };
 
-template <int W, bool RAGGED>
-__device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
+template <int W, bool RAGGED, bool FP8 = false>
+__device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
+  // FP8 pages: K's scale folds into the score scale, V's into the output.
+  PrefillArgs a = args;
+  float v_scale = 1.0f;
+  if constexpr (FP8) {
+    a.scale_log2 *= a.kv_scales[0];
+    v_scale = a.kv_scales[1];
+  }
   __shared__ PrefillSmem<W> sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -432,7 +481,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
       return uni(wave + W * (s0 + i) == req_pages - 1 ? (int)tl : 16);
     };
     auto lt_of = [&](int i) { return (int64_t)(wave + W * (s0 + i)) * 16; };
-    w.template stream<prefill_depth(W)>(n, page_tok, rows_of, lt_of);
+    w.template stream<prefill_depth(W), FP8>(n, page_tok, rows_of, lt_of);
   }
 
   // Wave states -> LDS; an invalid page index anywhere in the request keeps
@@ -481,16 +530,16 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a) {
     u32x4 o;
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2)
-      o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv) |
-              ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv) << 16);
+      o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv * v_scale) |
+              ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv * v_scale) << 16);
     *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
   }
   if (quad == 0) a.lse[row_head] = M + __log2f(L);
 }
 
-template <int W>
+template <int W, bool FP8>
 __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
-  prefill_body<W, false>(a);
+  prefill_body<W, false, FP8>(a);
 }
 
 // Ragged prefill: contiguous K/V rows [nnz_kv, Hkv, 128]; any 16 consecutive
@@ -581,6 +630,8 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   if (spec->page_size != 0 && spec->page_size != 16 && spec->page_size != 32 &&
       spec->page_size != 64)
     return fail(err, LOOM_UNSUPPORTED_PAGE_SIZE, nullptr, loom::kPageSize, spec->page_size);
+  if (spec->kv_dtype != LOOM_KV_DTYPE_BF16 && spec->kv_dtype != LOOM_KV_DTYPE_FP8_E4M3)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", spec->kv_dtype);
   if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
   uint64_t tiles = 0, grid = 0;
@@ -620,18 +671,26 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
                                          loom_error_t *err) {
   if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
   const loom_paged_prefill_spec_t &s = plan->info.spec;
-  static const loom::OperandSpec ops[9] = {
-      {"Q", LOOM_DTYPE_BF16, false},           {"K_pages", LOOM_DTYPE_BF16, false},
-      {"V_pages", LOOM_DTYPE_BF16, false},     {"qo_indptr", LOOM_DTYPE_I32, false},
+  // FP8 pages are u8 operands plus the [k_scale, v_scale] operand.
+  const bool fp8 = s.kv_dtype == LOOM_KV_DTYPE_FP8_E4M3;
+  const loom_dtype_t kv_t = fp8 ? LOOM_DTYPE_U8 : LOOM_DTYPE_BF16;
+  const loom::OperandSpec ops[10] = {
+      {"Q", LOOM_DTYPE_BF16, false},           {"K_pages", kv_t, false},
+      {"V_pages", kv_t, false},                {"qo_indptr", LOOM_DTYPE_I32, false},
       {"page_indptr", LOOM_DTYPE_I32, false},  {"page_indices", LOOM_DTYPE_I32, false},
       {"last_page_len", LOOM_DTYPE_I32, false}, {"O", LOOM_DTYPE_BF16, true},
-      {"LSE", LOOM_DTYPE_F32, true}};
-  const loom_handle_t hs[9] = {args->query,       args->key_pages,   args->value_pages,
-                               args->qo_indptr,   args->page_indptr, args->page_indices,
-                               args->last_page_len, args->output,    args->lse};
-  const loom::Lease *l[9];
-  loom_status_t rc = loom::resolve_command(scope, hs, ops, 9, l, err);
+      {"LSE", LOOM_DTYPE_F32, true},           {"kv_scales", LOOM_DTYPE_F32, false}};
+  const loom_handle_t hs[10] = {args->query,       args->key_pages,   args->value_pages,
+                                args->qo_indptr,   args->page_indptr, args->page_indices,
+                                args->last_page_len, args->output,    args->lse,
+                                args->kv_scales};
+  const loom::Lease *l[10];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, fp8 ? 10 : 9, l, err);
   if (rc) return rc;
+  if (fp8 && l[9]->numel != 2)
+    return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, l[9]->numel);
+  if (fp8 && l[9]->ptr % 4 != 0)
+    return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, "kv_scales", (int64_t)l[9]->ptr, 4);
   // prefill.rs:2474-2495: exact spans, page_indices at least B entries.
   const uint64_t qn = s.nnz_qo * s.num_query_heads * loom::kHeadDim;
   const uint64_t page_rows = s.page_size ? s.page_size : loom::kPageSize;
@@ -651,6 +710,7 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   for (int i : {0, 1, 2, 7})
     if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
   PrefillArgs a{};
+  a.kv_scales = fp8 ? (const float *)l[9]->ptr : nullptr;
   a.q = (const uint16_t *)l[0]->ptr;
   a.k = (const uint16_t *)l[1]->ptr;
   a.v = (const uint16_t *)l[2]->ptr;
@@ -676,10 +736,22 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   a.blocks_lg = page_rows == 64 ? 2 : page_rows == 32 ? 1 : 0;
   hipStream_t stream = scope->queue->stream;
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
-  switch (plan->info.waves) {
-    case 4: hipLaunchKernelGGL(paged_prefill_kernel<4>, grid, block, 0, stream, a); break;
-    case 8: hipLaunchKernelGGL(paged_prefill_kernel<8>, grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL(paged_prefill_kernel<16>, grid, block, 0, stream, a); break;
+  if (fp8) {
+    switch (plan->info.waves) {
+      case 4: hipLaunchKernelGGL((paged_prefill_kernel<4, true>), grid, block, 0, stream, a); break;
+      case 8: hipLaunchKernelGGL((paged_prefill_kernel<8, true>), grid, block, 0, stream, a); break;
+      default:
+        hipLaunchKernelGGL((paged_prefill_kernel<16, true>), grid, block, 0, stream, a);
+        break;
+    }
+  } else {
+    switch (plan->info.waves) {
+      case 4: hipLaunchKernelGGL((paged_prefill_kernel<4, false>), grid, block, 0, stream, a); break;
+      case 8: hipLaunchKernelGGL((paged_prefill_kernel<8, false>), grid, block, 0, stream, a); break;
+      default:
+        hipLaunchKernelGGL((paged_prefill_kernel<16, false>), grid, block, 0, stream, a);
+        break;
+    }
   }
   return loom::record_launch(scope, hipGetLastError(), err);
 }

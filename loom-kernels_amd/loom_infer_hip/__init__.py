@@ -835,7 +835,8 @@ class Bf16PagedPrefillSpec:
     """paged_prefill/mod.rs:11-159."""
 
     def __init__(self, batch_size, nnz_qo, max_num_pages, num_query_heads, num_kv_heads,
-                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_page_size=None):
+                 head_dim=HEAD_DIM, page_size=PAGE_SIZE, kv_layout="NHD", kv_page_size=None,
+                 kv_dtype="bf16"):
         self._c = _ffi.PagedPrefillSpec()
         _call(lib().loom_paged_prefill_spec_new, batch_size, nnz_qo, max_num_pages,
               num_query_heads, num_kv_heads, head_dim, page_size, C.byref(self._c))
@@ -850,6 +851,15 @@ class Bf16PagedPrefillSpec:
             _call(lib().loom_paged_prefill_spec_with_page_size, C.byref(self._c),
                   int(kv_page_size), C.byref(out))
             self._c = out
+        if kv_dtype not in KV_DTYPES:
+            raise ValueError(f"kv_dtype must be one of {sorted(KV_DTYPES)}, got {kv_dtype!r}")
+        if KV_DTYPES[kv_dtype] != 0:
+            out = _ffi.PagedPrefillSpec()
+            _call(lib().loom_paged_prefill_spec_with_kv_dtype, C.byref(self._c),
+                  KV_DTYPES[kv_dtype], C.byref(out))
+            self._c = out
+
+    kv_dtype = property(lambda s: {v: k for k, v in KV_DTYPES.items()}[s._c.kv_dtype])
 
     kv_layout = property(lambda s: {v: k for k, v in KV_LAYOUTS.items()}[s._c.kv_layout])
 
@@ -894,11 +904,12 @@ class Bf16PagedPrefillArgs:
     last_page_len: Read
     output: Write
     lse: Write
+    kv_scales: Optional[Read] = None  # FP8 pages: Read<f32> [k_scale, v_scale]
 
     def __post_init__(self):
         c = _ffi.PagedPrefillArgs(*[_h(getattr(self, f)) for f in (
             "query", "key_pages", "value_pages", "qo_indptr", "page_indptr", "page_indices",
-            "last_page_len", "output", "lse")])
+            "last_page_len", "output", "lse", "kv_scales")])
         object.__setattr__(self, "_struct", c)
         object.__setattr__(self, "_ref", C.byref(c))
 

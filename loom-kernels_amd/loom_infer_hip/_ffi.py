@@ -74,7 +74,7 @@ class SingleDecodeSplitKArgs(C.Structure):
 class PagedPrefillSpec(C.Structure):
     _fields_ = [("batch_size", u64), ("nnz_qo", u64), ("max_num_pages", u64),
                 ("num_query_heads", u64), ("num_kv_heads", u64), ("softmax_scale", f32),
-                ("kv_layout", u32), ("page_size", u32)]
+                ("kv_layout", u32), ("page_size", u32), ("kv_dtype", u32)]
 
 
 class PagedPrefillPlanOptions(C.Structure):
@@ -90,7 +90,7 @@ class PagedPrefillPlanInfo(C.Structure):
 class PagedPrefillArgs(C.Structure):
     _fields_ = [(n, Handle) for n in ("query", "key_pages", "value_pages", "qo_indptr",
                                       "page_indptr", "page_indices", "last_page_len",
-                                      "output", "lse")]
+                                      "output", "lse", "kv_scales")]
 
 
 class RaggedPrefillSpec(C.Structure):
@@ -138,6 +138,8 @@ SIGNATURES = {
     "loom_paged_decode_spec_with_kv_layout": (
         i32, [P(PagedDecodeSpec), u32, P(PagedDecodeSpec), E]),
     "loom_paged_prefill_spec_with_page_size": (
+        i32, [P(PagedPrefillSpec), u32, P(PagedPrefillSpec), E]),
+    "loom_paged_prefill_spec_with_kv_dtype": (
         i32, [P(PagedPrefillSpec), u32, P(PagedPrefillSpec), E]),
     "loom_paged_prefill_spec_with_kv_layout": (
         i32, [P(PagedPrefillSpec), u32, P(PagedPrefillSpec), E]),

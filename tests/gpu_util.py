@@ -121,19 +121,20 @@ class PrefillRunner:
         self.plan = self.provider.plan_bf16_paged(self.spec, **plan_opts)
         self.queue = L.CommandQueue(torch.cuda.current_stream(), 4)
 
-    def run_dev(self, q, k, v, qo, indptr, indices, last, out=None, lse=None):
+    def run_dev(self, q, k, v, qo, indptr, indices, last, out=None, lse=None, scales=None):
         torch = torch_dev()
         s = self.spec
         if out is None:
             out = nan_bf16(s.output_numel)
         if lse is None:
             lse = torch.full((s.lse_numel,), float("nan"), dtype=torch.float32, device="cuda")
-        b = self.queue.bindings(9)
+        b = self.queue.bindings(10)
         h = [b.bind_read(x) for x in (q, k, v, qo, indptr, indices, last)]
         h += [b.bind_read_write(out), b.bind_read_write(lse)]
+        sc = b.bind_read(scales) if scales is not None else None
         scope = self.queue.begin(b)
         self.plan.enqueue_into(scope, self.L.Bf16PagedPrefillArgs(
-            h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7].write(), h[8].write()))
+            h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7].write(), h[8].write(), sc))
         comp = scope.finish()
         assert comp.submitted() == 1
         b = comp.wait()

@@ -226,3 +226,60 @@ def test_prefill_page_size_equals_16_row_table(L, oracle, P, layout):
         kk, vv = k, v
     o2, l2 = rp.run(q, kk, vv, qo, ip, ix, last)
     assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
+
+
+@pytest.mark.parametrize("P", [16, 32])
+def test_fp8_prefill_equals_bf16_on_widened_pages(L, oracle, P):
+    """FP8 E4M3 paged prefill (no reference counterpart).  E4M3 is exact in
+    BF16 and power-of-two scales are exact, so with scales (0.5, 0.25) the FP8
+    command must equal the BF16 command on the widened, scaled pages bit for
+    bit; a non-power-of-two scale is checked against the oracle's prefill on
+    the same values within the decode tolerance."""
+    import torch
+    from gpu_util import PrefillRunner, bf16_host, to_dev_bf16, to_dev_i32
+    from test_gpu_fp8 import random_fp8
+    log(f"fp8 prefill page size {P}")
+    rng = np.random.default_rng(300 + P)
+    B, hq, hkv = 3, 16, 4
+    qo_lens, kv_lens = [5, 33, 1], [40, 200, 17]
+    pool = sum((n + P - 1) // P for n in kv_lens) + 2
+    ip, ix, last = table(rng, kv_lens, pool, P)
+    qo = np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32)
+    nnz = int(qo[-1])
+    q = seeded_normal_bf16(oracle, rng, nnz * hq * 128)
+    k8 = random_fp8(rng, pool * P * hkv * 128)
+    v8 = random_fp8(rng, pool * P * hkv * 128)
+    kw = {} if P == 16 else {"kv_page_size": P}
+
+    def fp8_run(scales, k8=k8, v8=v8):
+        r = PrefillRunner(L, B, nnz, pool, hq, hkv)
+        r.spec = L.Bf16PagedPrefillSpec(B, nnz, pool, hq, hkv, kv_dtype="fp8_e4m3", **kw)
+        r.plan = r.provider.plan_bf16_paged(r.spec)
+        out, lse = r.run_dev(to_dev_bf16(q), torch.from_numpy(k8).to("cuda"),
+                             torch.from_numpy(v8).to("cuda"), to_dev_i32(qo), to_dev_i32(ip),
+                             to_dev_i32(ix), to_dev_i32(last),
+                             scales=torch.tensor(scales, dtype=torch.float32, device="cuda"))
+        return bf16_host(out), lse.cpu().numpy()
+
+    def widened(x8, scale):
+        return oracle.bf16_from_f32((oracle.fp8_to_f32(x8) * np.float32(scale)).astype(np.float32))
+
+    rb = PrefillRunner(L, B, nnz, pool, hq, hkv)
+    rb.spec = L.Bf16PagedPrefillSpec(B, nnz, pool, hq, hkv, **kw)
+    rb.plan = rb.provider.plan_bf16_paged(rb.spec)
+    o_b, l_b = rb.run(q, widened(k8, 0.5), widened(v8, 0.25), qo, ip, ix, last)
+    o_f, l_f = fp8_run([0.5, 0.25])
+    assert not np.any(np.isnan(oracle.bf16_to_f32(o_f)))
+    assert np.array_equal(o_b, o_f) and np.array_equal(l_b, l_f)
+    # a scale that is not a power of two: the oracle on the dequantized values
+    # (codes up to 0x44, |x| <= 3, so the BF16 rounding of x * scale moves the
+    # scores by far less than the tolerance)
+    if P == 16:
+        ks = random_fp8(rng, pool * P * hkv * 128, max_code=0x44)
+        vs = random_fp8(rng, pool * P * hkv * 128, max_code=0x44)
+        o3, l3 = fp8_run([0.3, 0.7], ks, vs)
+        kd = (oracle.fp8_to_f32(ks) * np.float32(0.3)).astype(np.float32)
+        vd = (oracle.fp8_to_f32(vs) * np.float32(0.7)).astype(np.float32)
+        ref = oracle.prefill(oracle.prefill_spec(B, nnz, pool, hq, hkv), q,
+                             oracle.bf16_from_f32(kd), oracle.bf16_from_f32(vd), qo, ip, ix, last)
+        compare_decode(oracle, o3, l3, *ref)
