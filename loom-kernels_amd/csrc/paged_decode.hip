@@ -226,15 +226,31 @@ __device__ __forceinline__ void load_page(PageRegs8 &r, const DecodeArgs &a, int
   load_rows(r, a, block_elem(a, page, sub), valid_rows, lane, kvh);
 }
 
-__device__ __forceinline__ const PageRegs &expand(const PageRegs &r) { return r; }
-__device__ __forceinline__ PageRegs expand(const PageRegs8 &r) {
-  PageRegs o;
+// K row words (BF16 pairs) and V row values (FP32) of a page in either form;
+// FP8 V bytes widen straight to FP32 (v_cvt_pk_f32_fp8), skipping BF16.
+__device__ __forceinline__ u32x4 k_words(const PageRegs &r, int j) { return r.k[j]; }
+__device__ __forceinline__ u32x4 k_words(const PageRegs8 &r, int j) {
+  return fp8x8_to_bf16x8(r.k[j]);
+}
+__device__ __forceinline__ void v_values(const PageRegs &r, int j, float (&vf)[8]) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    o.k[j] = fp8x8_to_bf16x8(r.k[j]);
-    o.v[j] = fp8x8_to_bf16x8(r.v[j]);
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t wv = r.v[j][e];
+    vf[2 * e] = bf16_lo(wv);
+    vf[2 * e + 1] = bf16_hi(wv);
   }
-  return o;
+}
+__device__ __forceinline__ void v_values(const PageRegs8 &r, int j, float (&vf)[8]) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)r.v[j][h], false);
+    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)r.v[j][h], true);
+    vf[4 * h] = lo[0];
+    vf[4 * h + 1] = lo[1];
+    vf[4 * h + 2] = hi[0];
+    vf[4 * h + 3] = hi[1];
+  }
 }
 
 
@@ -310,12 +326,13 @@ struct WaveDecoder {
   // One page: S = K·Qᵀ on MFMA, online softmax, P·V on the VALU.  `rows` is
   // the number of valid token rows (16, the request's tail on its last page,
   // 0 for a page index that failed the guard).
-  __device__ void process(const PageRegs &pr, int rows) {
+  template <class Page>
+  __device__ void process(const Page &pr, int rows) {
     // K rows -> LDS tile -> MFMA A fragments (lane: token row `col`, dims
     // 32c + 8*quad + [0, 8)).
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<u32x4 *>(kt + (quad * 4 + j) * kKRowBytes + col * 16) = pr.k[j];
+      *reinterpret_cast<u32x4 *>(kt + (quad * 4 + j) * kKRowBytes + col * 16) = k_words(pr, j);
     wave_lds_fence();
     u32x4 kf[4];
 #pragma unroll
@@ -358,12 +375,7 @@ struct WaveDecoder {
     for (int j = 0; j < 4; ++j) {
       // rows past the valid ones were loaded as zeros and have zero weight
       float vf[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t wv = pr.v[j][e];
-        vf[2 * e] = bf16_lo(wv);
-        vf[2 * e + 1] = bf16_hi(wv);
-      }
+      v_values(pr, j, vf);
 #pragma unroll
       for (int g = 0; g < GT; ++g)
 #pragma unroll
@@ -390,7 +402,7 @@ struct WaveDecoder {
       for (int s = 0; s < kDepth; ++s) {
         load_rows(buf[(s + kDepth - 1) % kDepth], a, tok_of(i + kDepth - 1),
                   rows_of(i + kDepth - 1), lane, kvh);
-        process(expand(buf[s]), rows_of(i));
+        process(buf[s], rows_of(i));
         if (++i >= n) return;
       }
     }
@@ -756,7 +768,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
         begin_piece();
       }
       bad |= brows[s] == 0;
-      w.process(expand(buf[s]), brows[s]);
+      w.process(buf[s], brows[s]);
       ++v;
       if (++i >= n) goto stream_done;
       // Waves ahead of schedule yield issue priority to the ones behind: all
