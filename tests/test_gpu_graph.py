@@ -229,3 +229,50 @@ def test_serving_loop_replays_one_graph_over_changing_page_tables(L, oracle, cap
         log(f"  step {step}: lens {lens.tolist()} pages {len(indices)} {st}")
     assert np.array_equal(bf16_host(t_vp), vp_h)
     exec_.into_bindings()
+
+
+def test_fp8_decode_graph_replays_with_new_scales(L, oracle):
+    """FP8 E4M3 decode on 32-row pages captured once; the per-tensor scales
+    are a device operand, so replays after the caller rewrites them in place
+    follow the new scales (each replay equals the eager command with the same
+    scales, bit for bit)."""
+    import torch
+    from test_gpu_fp8 import dev_u8, random_fp8, run_decode
+    log("graph fp8 decode replay")
+    rng = np.random.default_rng(33)
+    B, hq, hkv, P = 4, 16, 4, 32
+    lens = [40, 700, 17, 300]
+    pool = sum((x + P - 1) // P for x in lens) + 4
+    pages = [(x + P - 1) // P for x in lens]
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
+    last = np.array([x - (p - 1) * P for x, p in zip(lens, pages)], np.int32)
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k8 = random_fp8(rng, pool * P * hkv * 128, max_code=0x50)
+    v8 = random_fp8(rng, pool * P * hkv * 128, max_code=0x50)
+    spec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, kv_dtype="fp8_e4m3", kv_page_size=P)
+    opts = {"teams": 5}
+    eager = [run_decode(L, spec, opts, q, k8, v8, indptr, indices, last, s)[:2]
+             for s in ([0.5, 0.25], [0.125, 2.0])]
+    plan = L.DecodeProvider.load(0).plan_bf16_paged_batch(spec, **opts)
+    ws = torch.zeros(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    scales = torch.tensor([0.5, 0.25], dtype=torch.float32, device="cuda")
+    out = torch.full((B * hq * 128,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    lse = torch.full((B * hq,), float("nan"), dtype=torch.float32, device="cuda")
+    gq = L.GraphQueue(0, 1)
+    b = gq.bindings(10)
+    h = [b.bind_read(to_dev_bf16(q)), b.bind_read(dev_u8(k8)), b.bind_read(dev_u8(v8)),
+         b.bind_read(to_dev_i32(indptr)), b.bind_read(to_dev_i32(indices)),
+         b.bind_read(to_dev_i32(last)), b.bind_read_write(out), b.bind_read_write(lse),
+         b.bind_read_write(ws), b.bind_read(scales)]
+    args = L.Bf16PagedBatchDecodeArgs(h[0], h[1], h[2], h[3], h[4], h[5], h[6].write(),
+                                      h[7].write(), h[8].write(), h[9])
+    exec_ = gq.capture(b, lambda scope: plan.enqueue_into(scope, args)).instantiate()
+    for i, (sc, (eo, el)) in enumerate(zip(([0.5, 0.25], [0.125, 2.0], [0.5, 0.25]),
+                                           eager + eager[:1])):
+        scales.copy_(torch.tensor(sc, dtype=torch.float32))  # eager work between replays
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        exec_.launch().wait()
+        assert np.array_equal(bf16_host(out), eo), f"replay {i}"
+        assert np.array_equal(lse.cpu().numpy(), el), f"replay {i}"
