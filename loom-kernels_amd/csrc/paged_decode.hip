@@ -119,6 +119,8 @@ struct DecodeArgs {
   // p * page_rows + 16 * j.
   int32_t page_rows;
   int32_t blocks_lg;
+  int64_t page_elems;   // page_rows * Hkv * 128: elements per page (all kv-heads)
+  int32_t block_elems;  // 16 * row_elems: element step between a page's blocks
   // FP8 E4M3 pages: device [k_scale, v_scale] (K = fp8 * k_scale, V = fp8 *
   // v_scale); null for BF16 pages.
   const float *__restrict__ kv_scales;
@@ -178,7 +180,7 @@ __device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int6
 
 // Element offset (kv-head 0) of block `sub` of page `page`.
 __device__ __forceinline__ int64_t block_elem(const DecodeArgs &a, int page, int sub) {
-  return (int64_t)page * a.page_rows * a.hkv * 128 + (int64_t)(sub * 16) * a.row_elems;
+  return (int64_t)page * a.page_elems + (int64_t)(sub * a.block_elems);
 }
 // Element offset (kv-head 0) of token row `token` of contiguous NHD K/V.
 __device__ __forceinline__ int64_t token_elem(const DecodeArgs &a, int64_t token) {
@@ -1170,6 +1172,8 @@ DecodeArgs single_args(const loom_single_decode_spec_t &s, uint32_t gtiles, uint
   a.row_elems = a.hkv * 128;
   a.page_rows = 16;
   a.blocks_lg = 0;
+  a.page_elems = (int64_t)16 * a.hkv * 128;
+  a.block_elems = 16 * a.row_elems;
   return a;
 }
 }  // namespace
@@ -1410,6 +1414,8 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.row_elems = hnd ? 128 : a.hkv * 128;
   a.page_rows = (int32_t)page_rows;
   a.blocks_lg = page_rows == 64 ? 2 : page_rows == 32 ? 1 : 0;
+  a.page_elems = (int64_t)page_rows * a.hkv * 128;
+  a.block_elems = 16 * a.row_elems;
 
   const uint64_t grid = pi.grid_blocks;
   hipStream_t stream = scope->queue->stream;
