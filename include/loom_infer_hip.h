@@ -427,8 +427,8 @@ void loom_paged_decode_plan_get_info(const loom_paged_decode_plan_t *plan,
  * initialization needed, contents are scratch between commands). */
 typedef struct loom_paged_decode_args {
   loom_handle_t query;         /* Read<bf16>  [B, Hq, 128] */
-  loom_handle_t key_pages;     /* Read<bf16>  [pool, 16, Hkv, 128] */
-  loom_handle_t value_pages;   /* Read<bf16>  [pool, 16, Hkv, 128] */
+  loom_handle_t key_pages;     /* Read<bf16>  [pool, P, Hkv, 128]; P = page_size */
+  loom_handle_t value_pages;   /* Read<bf16>  [pool, P, Hkv, 128]; P = page_size */
   loom_handle_t page_indptr;   /* Read<i32>   [B+1] */
   loom_handle_t page_indices;  /* Read<i32>   [>= B] */
   loom_handle_t last_page_len; /* Read<i32>   [B] */
@@ -533,7 +533,7 @@ loom_status_t loom_single_decode_split_k_enqueue(const loom_single_decode_split_
 
 /* ------------------------------------------------------------------------ */
 /* Paged causal prefill, crates/loom-infer/src/attention/paged_prefill/mod.rs  */
-/* Q/O [nnz_qo, Hq, 128] ragged by qo_indptr; K/V pages [pool, 16, Hkv, 128]  */
+/* Q/O [nnz_qo, Hq, 128] ragged by qo_indptr; K/V pages [pool, P, Hkv, 128] (NHD) */
 /* (NHD) by page_indptr / page_indices / last_page_len; LSE [nnz_qo, Hq]       */
 /* log2.  Bottom-right causal mask: row i of a request with qo_len rows sees   */
 /* KV tokens 0 .. kv_len - qo_len + i.                                         */
@@ -640,8 +640,8 @@ void loom_paged_prefill_plan_get_info(const loom_paged_prefill_plan_t *plan,
 /* Bf16PagedPrefillArgs, prefill.rs:2852-2890. */
 typedef struct loom_paged_prefill_args {
   loom_handle_t query;         /* Read<bf16>  [nnz_qo, Hq, 128] */
-  loom_handle_t key_pages;     /* Read<bf16>  [pool, 16, Hkv, 128] */
-  loom_handle_t value_pages;   /* Read<bf16>  [pool, 16, Hkv, 128] */
+  loom_handle_t key_pages;     /* Read<bf16>  [pool, P, Hkv, 128]; P = page_size */
+  loom_handle_t value_pages;   /* Read<bf16>  [pool, P, Hkv, 128]; P = page_size */
   loom_handle_t qo_indptr;     /* Read<i32>   [B+1] */
   loom_handle_t page_indptr;   /* Read<i32>   [B+1] */
   loom_handle_t page_indices;  /* Read<i32>   [>= B] */
@@ -795,8 +795,8 @@ typedef struct loom_rope_append_args {
   loom_handle_t page_indices;  /* Read<i32>  [>= B] */
   loom_handle_t last_page_len; /* Read<i32>  [B] */
   loom_handle_t query_output;  /* Write<bf16> [T, Hq, 128] */
-  loom_handle_t key_pages;     /* Write<bf16> [pool, 16, Hkv, 128] */
-  loom_handle_t value_pages;   /* Write<bf16> [pool, 16, Hkv, 128] */
+  loom_handle_t key_pages;     /* Write<bf16> [pool, P, Hkv, 128]; P = page_size */
+  loom_handle_t value_pages;   /* Write<bf16> [pool, P, Hkv, 128]; P = page_size */
   loom_handle_t workspace;     /* Write<u8> */
   loom_handle_t kv_scales;     /* Read<f32> [2] for FP8 pages (K/V pages are then
                                   Write<u8>); {0, 0} for BF16 pages */

@@ -1,4 +1,4 @@
-// Paged decode attention for gfx950 (MI355X), BF16 NHD D128 page-16 caches.
+// Paged decode attention for gfx950 (MI355X), D128, BF16 or FP8 pages of 16-64 rows, NHD or HND.
 //
 // Semantics: crates/loom-infer/src/attention/paged_decode/mod.rs:287-366 (the
 // CPU reference), with the device metadata guards of
