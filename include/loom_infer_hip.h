@@ -533,7 +533,7 @@ loom_status_t loom_single_decode_split_k_enqueue(const loom_single_decode_split_
 
 /* ------------------------------------------------------------------------ */
 /* Paged causal prefill, crates/loom-infer/src/attention/paged_prefill/mod.rs  */
-/* Q/O [nnz_qo, Hq, 128] ragged by qo_indptr; K/V pages [pool, P, Hkv, 128] (NHD) */
+/* Q/O [nnz_qo, Hq, 128] ragged by qo_indptr; K/V pages [pool, P, Hkv, 128]      */
 /* (NHD) by page_indptr / page_indices / last_page_len; LSE [nnz_qo, Hq]       */
 /* log2.  Bottom-right causal mask: row i of a request with qo_len rows sees   */
 /* KV tokens 0 .. kv_len - qo_len + i.                                         */
