@@ -342,3 +342,21 @@ def test_page_size_specs(L):
     with pytest.raises(L.ContractError) as e:
         ps.validate_metadata([0, 2, 5], [0, 1, 3], [4, 2, 7], [65, 3])
     assert (e.value.variant, e.value.fields[:3]) == ("InvalidLastPageLength", (0, 65, 64))
+
+
+def test_fp8_prefill_spec_and_args(L):
+    """FP8 E4M3 pages for paged prefill (no reference counterpart): the spec
+    setter keeps every other field, rejects unknown element types, and the
+    args carry the optional kv_scales operand."""
+    s = L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, kv_dtype="fp8_e4m3", kv_page_size=32,
+                               kv_layout="HND")
+    assert (s.kv_dtype, s.page_size, s.kv_layout, s.nnz_qo) == ("fp8_e4m3", 32, "HND", 5)
+    assert L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4).kv_dtype == "bf16"
+    with pytest.raises(ValueError):
+        L.Bf16PagedPrefillSpec(2, 5, 8, 16, 4, kv_dtype="fp4")
+    import ctypes as C
+    out = L._ffi.PagedPrefillSpec()
+    e = L._ffi.Error()
+    rc = L.lib().loom_paged_prefill_spec_with_kv_dtype(C.byref(s._c), 9, C.byref(out), C.byref(e))
+    assert rc == 75 and e.operand == b"kv_dtype"
+    assert "kv_scales" in [f for f, _ in L._ffi.PagedPrefillArgs._fields_]
