@@ -537,8 +537,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   if (quad == 0) a.lse[row_head] = M + __log2f(L);
 }
 
+// At least three waves per SIMD: the per-block chain (MFMA, softmax, MFMA)
+// leaves a wave waiting most of the time, and a third wave per SIMD fills
+// those gaps (the four-wave BF16 kernel would otherwise settle at two).
+constexpr int kPrefillWavesPerEu = 3;
+
 template <int W, bool FP8>
-__global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(W * 64, kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
   prefill_body<W, false, FP8>(a);
 }
 
@@ -546,7 +551,7 @@ __global__ __launch_bounds__(W * 64) void paged_prefill_kernel(PrefillArgs a) {
 // rows of a request form a block with the paged layout's row stride, so the
 // same page step and range-limited loads serve it.
 template <int W>
-__global__ __launch_bounds__(W * 64) void ragged_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(W * 64, kPrefillWavesPerEu) void ragged_prefill_kernel(PrefillArgs a) {
   prefill_body<W, true>(a);
 }
 
