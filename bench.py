@@ -515,6 +515,44 @@ def ragged_shapes(L, stream, samples=30):
     return out
 
 
+def long_prefill_shapes(L, stream, samples=5):
+    """Paged causal prefill on long prompts (no reference counterpart: its
+    timed shapes stop at 64 query rows): GQA4 Hq 32 / Hkv 8, qo_len = kv_len per
+    request, a seeded permutation page table; eager µs (median of `samples`
+    batches of 5 enqueues) and causal TFLOP/s."""
+    import torch
+    dev = "cuda"
+    out = {}
+    for B, n in ((1, 512), (1, 1024), (1, 4096), (1, 8192), (4, 2048), (8, 256)):
+        hq, hkv = 32, 8
+        nnz, pages = B * n, (n + 15) // 16
+        pool = B * pages
+        spec = L.Bf16PagedPrefillSpec(B, nnz, pool, hq, hkv)
+        plan = L.PrefillProvider.load(0).plan_bf16_paged(spec)
+        g = torch.Generator(device=dev).manual_seed(B * 100000 + n)
+        t = [torch.randn(x, device=dev, generator=g).to(torch.bfloat16)
+             for x in (nnz * hq * 128, pool * 16 * hkv * 128, pool * 16 * hkv * 128)]
+        qo = torch.arange(0, nnz + 1, n, dtype=torch.int32, device=dev)
+        ip = torch.arange(0, pool + 1, pages, dtype=torch.int32, device=dev)
+        ix = torch.randperm(pool, device=dev, generator=g).to(torch.int32)
+        ln = torch.full((B,), n - (pages - 1) * 16, dtype=torch.int32, device=dev)
+        o = torch.empty(nnz * hq * 128, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(nnz * hq, dtype=torch.float32, device=dev)
+
+        def bind(b):
+            return L.Bf16PagedPrefillArgs(
+                b.bind_read(t[0]), b.bind_read(t[1]), b.bind_read(t[2]), b.bind_read(qo),
+                b.bind_read(ip), b.bind_read(ix), b.bind_read(ln), b.bind_read_write(o).write(),
+                b.bind_read_write(lse).write())
+        us = sorted(_timed_enqueues(L, stream, 9, bind, plan.enqueue_into, 5, 2)
+                    for _ in range(samples))[samples // 2]
+        flops = B * (n * (n + 1) // 2) * hq * 128 * 4
+        out[f"gqa4_b{B}_q{n}_kv{n}"] = {"eager_us": round(us, 2), "causal_gflop": round(flops / 1e9, 2),
+                                       "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1),
+                                       "grid_blocks": plan.info.grid_blocks}
+    return out
+
+
 def cpu_append_baseline(app, min_s=3.0):
     """The oracle's explicit-token append (rope/mod.rs + paged_append/mod.rs:
     429-489, single thread) on the config-2 command, repeated for at least
@@ -744,6 +782,8 @@ def main():
         log(f"[bench] {detail['paged_prefill']}")
         detail["ragged_prefill"] = ragged_shapes(L, stream)
         log(f"[bench] {detail['ragged_prefill']}")
+        detail["long_prefill"] = long_prefill_shapes(L, stream)
+        log(f"[bench] {detail['long_prefill']}")
     if a.only:
         print(json.dumps(detail), flush=True)
         return
