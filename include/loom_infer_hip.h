@@ -603,12 +603,25 @@ typedef enum loom_paged_prefill_algorithm {
    * flattened (query row, group head) pairs).  The waves split the tile's
    * causal page range; per page, S = K·Qᵀ and O += P·V both run on MFMA, and
    * the wave states merge in LDS.  No workspace. */
-  LOOM_PAGED_PREFILL_ROW_TILE = 1
+  LOOM_PAGED_PREFILL_ROW_TILE = 1,
+  /* For long prompts: one workgroup of four waves per (request, kv-head, tile
+   * of 64 flattened pairs), one 16-column tile per wave.  Every wave walks the
+   * whole causal page range; each K/V block is loaded once per workgroup,
+   * staged through LDS and read by all four waves, so a workgroup reads a
+   * quarter of the L2 bytes per column that ROW_TILE reads.  No cross-wave
+   * merge.  BF16 pages only.  No workspace. */
+  LOOM_PAGED_PREFILL_WIDE_TILE = 2
 } loom_paged_prefill_algorithm_t;
+
+/* Prefill plan flags (no reference counterpart): force ROW_TILE or WIDE_TILE;
+ * with neither, the plan picks one from the spec. */
+#define LOOM_PLAN_PREFILL_TILE_16 2u
+#define LOOM_PLAN_PREFILL_TILE_64 4u
 
 typedef struct loom_paged_prefill_plan_options {
   uint32_t waves; /* waves per workgroup: 0 (the default, four), 4, 8 or 16 */
-  uint32_t flags; /* 0 or LOOM_PLAN_PAGE_INDICES_CAPACITY */
+  uint32_t flags; /* LOOM_PLAN_PAGE_INDICES_CAPACITY (paged only) and at most one of
+                     LOOM_PLAN_PREFILL_TILE_16 / LOOM_PLAN_PREFILL_TILE_64 (four waves) */
 } loom_paged_prefill_plan_options_t;
 
 typedef struct loom_paged_prefill_plan_info {
@@ -616,7 +629,8 @@ typedef struct loom_paged_prefill_plan_info {
   int32_t algorithm;
   uint32_t waves;
   uint64_t row_tiles;  /* upper bound of tiles over any valid qo_indptr:
-                          floor((nnz_qo * group + 15 * batch) / 16) */
+                          min(C, floor((C + (t - 1) * batch) / t)), C = nnz_qo * group,
+                          t = 16 (ROW_TILE) or 64 (WIDE_TILE) columns per tile */
   uint32_t block_threads;
   uint64_t grid_blocks; /* row_tiles * Hkv */
   uint32_t flags;
@@ -697,7 +711,8 @@ typedef struct loom_ragged_prefill_plan loom_ragged_prefill_plan_t;
 
 typedef struct loom_ragged_prefill_plan_info {
   loom_ragged_prefill_spec_t spec;
-  int32_t algorithm;          /* LOOM_PAGED_PREFILL_ROW_TILE: the same kernel design */
+  int32_t algorithm;          /* LOOM_PAGED_PREFILL_ROW_TILE or _WIDE_TILE: the same
+                                 kernel designs */
   uint32_t waves;
   uint64_t row_tiles;
   uint32_t block_threads;

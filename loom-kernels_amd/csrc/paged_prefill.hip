@@ -27,6 +27,11 @@
 //     2^-15 against FP32 weights);
 //   * the W wave states merge in LDS (max, rescale, deterministic tree sum)
 //     and wave 0 writes O and the log2 LSE.
+// Wide tiles (long prompts; LOOM_PAGED_PREFILL_WIDE_TILE): a workgroup of
+// four waves owns 64 columns, one 16-column tile per wave; every wave walks
+// the whole causal block range, each block loaded once per workgroup (a
+// quarter per wave) into an LDS ring and read back by all four, so the L2
+// bytes per column fall fourfold; each wave finishes its own tile (no merge).
 // No workspace and one launch; the grid depends only on the plan.
 #include <hip/hip_runtime.h>
 
@@ -94,7 +99,7 @@ constexpr int64_t kNoTiles = (int64_t)1 << 50;
 #endif
 constexpr int prefill_depth(int w) { return w >= 16 ? 1 : LOOM_PREFILL_DEPTH; }
 
-template <int W>
+template <int W, bool SH>
 struct PrefillSmem {
   int64_t wave_tot[W];
   int32_t wave_max[W];
@@ -103,7 +108,7 @@ struct PrefillSmem {
   // the located request's qo_indptr pair, page (or kv) indptr pair, tail, and
   // the first flattened column it owns
   int32_t meta[6];
-  u32x4 qfrag[4][64];  // MFMA B fragments of the tile's 16 query columns
+  u32x4 qfrag[SH ? W : 1][4][64];  // MFMA B fragments of 16 query columns (per wave: SH)
   float m[W][16];      // per-wave running max (log2 domain) per column
   float l[W][16];      // per-wave normalizer per column
   f32x4 red[W / 2 > 0 ? W / 2 : 1][4][64];  // tree-sum staging, half the accumulators
@@ -286,10 +291,68 @@ struct PrefillWave {
       }
     }
   }
+
+  // Wide tiles (four waves, BF16): blocks 0..n-1 are loaded once per
+  // workgroup, each wave fetching one quarter (wave w: K for w < 2, V
+  // otherwise, rows 8 (w & 1) .. +8, two 16-byte loads per lane) two blocks
+  // ahead, stored into a two-slot LDS ring of 272-byte rows (fragment reads
+  // conflict free) and read back by every wave in the register layout of
+  // load_prefill_page.  One barrier per block: a slot is rewritten two blocks
+  // later, after every wave has passed the barrier that follows its reads.
+  // `own_end`: causal end of this wave's last column; blocks at or past it
+  // are staged but not computed.
+  template <class PageTok, class RowsOf, class LtOf>
+  __device__ void stream_shared(int n, PageTok page_tok, RowsOf rows_of, LtOf lt_of,
+                                u32x4 (*ring)[2][16][17], int wave, int64_t own_end) {
+    const int mat = wave >> 1, row0 = 8 * (wave & 1);
+    const uint16_t *src = mat ? a.v : a.k;
+    const int row_bytes = a.row_elems * 2;
+    auto fetch = [&](int i, u32x4 (&d)[2]) {
+      const __amdgpu_buffer_rsrc_t r = page_rows_rsrc(
+          src + page_tok(i) + (int64_t)kvh * a.head_elems, rows_of(i), a.row_elems);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ch = lane + 64 * j;
+        d[j] = load16_rows<false>(r, (row0 + (ch >> 4)) * row_bytes + (ch & 15) * 16);
+      }
+    };
+    auto step = [&](int i, u32x4 (&d)[2]) {
+      u32x4 (*slot)[16][17] = ring[i & 1];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ch = lane + 64 * j;
+        slot[mat][row0 + (ch >> 4)][ch & 15] = d[j];
+      }
+      fetch(i + 2, d);  // past the end: no valid rows, no traffic
+      __syncthreads();
+      const int64_t lt0 = lt_of(i);
+      if (lt0 < own_end) {
+        PrefillPage pg;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) pg.k[c] = slot[0][col][4 * c + quad];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pg.v[j] = slot[1][4 * quad + j][col];
+        process(pg, lt0);
+      }
+    };
+    u32x4 d0[2], d1[2];
+    fetch(0, d0);
+    fetch(1, d1);
+    for (int i = 0;;) {
+      step(i, d0);
+      if (++i >= n) return;
+      step(i, d1);
+      if (++i >= n) return;
+    }
+  }
 };
 
-template <int W, bool RAGGED, bool FP8 = false>
+// SH: the wide-tile algorithm (W = 4, BF16): 16 * W columns per workgroup,
+// one 16-column tile per wave, every wave over the whole page range.
+template <int W, bool RAGGED, bool FP8, bool SH>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
+  static_assert(!SH || (W == 4 && !FP8), "wide tiles: four waves, BF16 pages");
+  constexpr int TC = SH ? 16 * W : 16;  // flattened columns per workgroup
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   PrefillArgs a = args;
   float v_scale = 1.0f;
@@ -297,7 +360,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     a.scale_log2 *= a.kv_scales[0];
     v_scale = a.kv_scales[1];
   }
-  __shared__ PrefillSmem<W> sm;
+  __shared__ PrefillSmem<W, SH> sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, quad = lane >> 4;
@@ -354,13 +417,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
                         p1 <= a.nnz_kv && s1 - s0 <= p1 - p0;
         const int32_t lo = max(s0, excl);
         if (ok && s1 > lo) {
-          cnt = ((int64_t)(s1 - lo) * a.group + 15) / 16;
+          cnt = ((int64_t)(s1 - lo) * a.group + TC - 1) / TC;
           fbeg = (lo - s0) * a.group;
         }
       }
     } else {
       if (r < a.batch)
-        cnt = (s0 >= 0 && s1 > s0 && s1 <= a.nnz) ? ((int64_t)(s1 - s0) * a.group + 15) / 16
+        cnt = (s0 >= 0 && s1 > s0 && s1 <= a.nnz) ? ((int64_t)(s1 - s0) * a.group + TC - 1) / TC
                                                   : kNoTiles;
     }
     const int64_t x = wave_incl_scan64(cnt, lane);
@@ -426,16 +489,19 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   // This lane's column and the tile's page range.
   // (fcols <= nnz_qo * Hq fits int32: the plan checks it)
   const int fcols = qo_len * a.group;
-  const int f = fbeg + tile0 * 16 + col;
+  const int own0 = fbeg + tile0 * TC + (SH ? 16 * wave : 0);  // first column of this wave's tile
+  const int f = own0 + col;
   const bool colv = f < fcols;
   const int qi = colv ? (int)((uint32_t)f / (uint32_t)a.group) : 0;
   const int gh = colv ? f - qi * a.group : 0;
-  const int f_last = min(fbeg + tile0 * 16 + 15, fcols - 1);
+  const int f_last = min(fbeg + tile0 * TC + TC - 1, fcols - 1);
   const int64_t tile_end = kv_len - qo_len + (int)((uint32_t)f_last / (uint32_t)a.group) + 1;
   // (the page counts are wave-uniform; pinning them to SGPRs keeps the buffer
   // resources below scalar, with no waterfall loops around the loads)
   const int npages = uni((int)((tile_end + 15) / 16));
-  const int mine = uni(npages > wave ? (npages - wave + W - 1) / W : 0);
+  // (SH: every wave walks every block; otherwise wave w takes blocks w, w + W, ...)
+  const int mine = SH ? npages : uni(npages > wave ? (npages - wave + W - 1) / W : 0);
+  auto blk = [&](int i) { return SH ? i : wave + W * i; };
 
   // One round trip for: every page index of the request (the reference
   // rejects the whole request; strided over the workgroup, the verdict is
@@ -448,40 +514,70 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
       const int32_t x = a.indices[ps + i];
       bad |= x < 0 || (int64_t)x >= a.pool;
     }
-    idx = lane < min(mine, 64) ? a.indices[ps + ((wave + W * lane) >> a.blocks_lg)] : 0;
+    idx = lane < min(mine, 64) ? a.indices[ps + (blk(lane) >> a.blocks_lg)] : 0;
   }
-  if (wave == 0) {
+  if (SH || wave == 0) {
     const uint16_t *qp = a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 +
                          quad * 8;
     u32x4 qr[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) qr[c] = colv ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) sm.qfrag[c][lane] = qr[c];
+    for (int c = 0; c < 4; ++c) sm.qfrag[SH ? wave : 0][c][lane] = qr[c];
   }
   __syncthreads();
 
-  PrefillWave w{a, sm.qfrag, lane, col, quad, kvh};
+  PrefillWave w{a, sm.qfrag[SH ? wave : 0], lane, col, quad, kvh};
   w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
   w.reset();
   for (int s0 = 0; s0 < mine; s0 += 64) {
     const int n = uni(min(mine - s0, 64));
     if (!RAGGED && s0 > 0)
-      idx = lane < n ? a.indices[ps + ((wave + W * (s0 + lane)) >> a.blocks_lg)] : 0;
+      idx = lane < n ? a.indices[ps + (blk(s0 + lane) >> a.blocks_lg)] : 0;
     const int ok = (RAGGED || (idx >= 0 && (int64_t)idx < a.pool)) ? 1 : 0;
     auto page_tok = [&](int i) {
-      if constexpr (RAGGED) return ((int64_t)ps + (int64_t)(wave + W * (s0 + i)) * 16) * a.hkv * 128;
+      if constexpr (RAGGED) return ((int64_t)ps + (int64_t)blk(s0 + i) * 16) * a.hkv * 128;
       const int j = uni(min(i, n - 1));
-      const int b = wave + W * (s0 + j);
+      const int b = blk(s0 + j);
       return (int64_t)__builtin_amdgcn_readlane(idx, j) * a.page_rows * a.hkv * 128 +
              (int64_t)((b & ((1 << a.blocks_lg) - 1)) * 16) * a.row_elems;
     };
     auto rows_of = [&](int i) {
       if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
-      return uni(wave + W * (s0 + i) == req_pages - 1 ? (int)tl : 16);
+      return uni(blk(s0 + i) == req_pages - 1 ? (int)tl : 16);
     };
-    auto lt_of = [&](int i) { return (int64_t)(wave + W * (s0 + i)) * 16; };
-    w.template stream<prefill_depth(W), FP8>(n, page_tok, rows_of, lt_of);
+    auto lt_of = [&](int i) { return (int64_t)blk(s0 + i) * 16; };
+    if constexpr (SH) {
+      __shared__ u32x4 ring[2][2][16][17];
+      // causal end of this wave's last column (0: the wave's tile is empty)
+      const int64_t own_end =
+          own0 < fcols
+              ? kv_len - qo_len + (int)((uint32_t)min(own0 + 15, fcols - 1) / (uint32_t)a.group) + 1
+              : 0;
+      w.stream_shared(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
+    } else {
+      w.template stream<prefill_depth(W), FP8>(n, page_tok, rows_of, lt_of);
+    }
+  }
+
+  if constexpr (SH) {
+    // No cross-wave merge: each wave finishes its own tile.
+    const float L = quad_sum(w.l_run);
+    if (__syncthreads_or(bad) || !colv) return;
+    const float inv = 1.0f / L;
+    const int64_t row_head = (int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh;
+    uint16_t *orow = a.out + row_head * 128 + quad * 32;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      u32x4 o;
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2)
+        o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv) |
+                ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv) << 16);
+      *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
+    }
+    if (quad == 0) a.lse[row_head] = w.m_run + __log2f(L);
+    return;
   }
 
   // Wave states -> LDS; an invalid page index anywhere in the request keeps
@@ -542,17 +638,17 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
 // those gaps (the four-wave BF16 kernel would otherwise settle at two).
 constexpr int kPrefillWavesPerEu = 3;
 
-template <int W, bool FP8>
+template <int W, bool FP8, bool SH = false>
 __global__ __launch_bounds__(W * 64, kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
-  prefill_body<W, false, FP8>(a);
+  prefill_body<W, false, FP8, SH>(a);
 }
 
 // Ragged prefill: contiguous K/V rows [nnz_kv, Hkv, 128]; any 16 consecutive
 // rows of a request form a block with the paged layout's row stride, so the
 // same page step and range-limited loads serve it.
-template <int W>
+template <int W, bool SH = false>
 __global__ __launch_bounds__(W * 64, kPrefillWavesPerEu) void ragged_prefill_kernel(PrefillArgs a) {
-  prefill_body<W, true>(a);
+  prefill_body<W, true, false, SH>(a);
 }
 
 }  // namespace
@@ -584,15 +680,50 @@ uint32_t waves_for() { return 4u; }
 // prefill.rs:2293-2298 / :2335-2340: the (row, head) states must fit the
 // launch range; the kernel indexes columns with int32.
 loom_status_t prefill_grid(uint64_t batch, uint64_t nnz_qo, uint64_t hq, uint64_t hkv,
-                           uint64_t *tiles, uint64_t *grid, loom_error_t *err) {
+                           uint64_t tile_cols, uint64_t *tiles, uint64_t *grid,
+                           loom_error_t *err) {
   const uint64_t states = nnz_qo * hq;
   if (states > (uint64_t)INT32_MAX || batch > (uint64_t)INT32_MAX - 1)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "prefill", states);
   const uint64_t cols = nnz_qo * (hq / hkv);
-  *tiles = std::min(cols, (cols + 15 * batch) / 16);
+  *tiles = std::min(cols, (cols + (tile_cols - 1) * batch) / tile_cols);
   *grid = *tiles * hkv;
   if (*grid > (uint64_t)INT32_MAX)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "prefill", states);
+  return LOOM_OK;
+}
+
+// Columns per workgroup of a prefill plan: 64 (wide tiles) or 16.  Forced by
+// the plan flags; otherwise wide for BF16 pages when the average request has
+// at least LOOM_PREFILL_WIDE_MIN_COLS flattened columns and the wide grid
+// still holds LOOM_PREFILL_WIDE_MIN_GRID workgroups.  Measured on GQA4
+// 32/8 prompts (qo = kv): wide 1.5-1.7x faster from 4 x 2048 and 8 x 256
+// rows up, even at 1 x 1024 rows (512 workgroups), slower at 1 x 512 (256).
+#ifndef LOOM_PREFILL_WIDE_MIN_COLS
+#define LOOM_PREFILL_WIDE_MIN_COLS 256
+#endif
+#ifndef LOOM_PREFILL_WIDE_MIN_GRID
+#define LOOM_PREFILL_WIDE_MIN_GRID 512
+#endif
+loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, bool fp8, uint64_t batch,
+                                uint64_t nnz_qo, uint64_t hq, uint64_t hkv, uint32_t *tile_cols,
+                                loom_error_t *err) {
+  const uint32_t t = flags & (LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64);
+  if (t == (LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64))
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
+  if (t == LOOM_PLAN_PREFILL_TILE_64 && waves != 4)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", waves);
+  if (t == LOOM_PLAN_PREFILL_TILE_64 && fp8)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", LOOM_KV_DTYPE_FP8_E4M3);
+  if (t) {
+    *tile_cols = t == LOOM_PLAN_PREFILL_TILE_64 ? 64 : 16;
+    return LOOM_OK;
+  }
+  const uint64_t cols = nnz_qo * (hq / hkv);
+  *tile_cols = (waves == 4 && !fp8 && batch > 0 && cols >= LOOM_PREFILL_WIDE_MIN_COLS * batch &&
+                (cols / 64) * hkv >= LOOM_PREFILL_WIDE_MIN_GRID)
+                   ? 64
+                   : 16;
   return LOOM_OK;
 }
 
@@ -628,7 +759,8 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
   const loom_paged_prefill_plan_options_t opt =
       options ? *options : loom_paged_prefill_plan_options_t{0, 0};
-  if (opt.flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
+  if (opt.flags & ~(LOOM_PLAN_PAGE_INDICES_CAPACITY | LOOM_PLAN_PREFILL_TILE_16 |
+                    LOOM_PLAN_PREFILL_TILE_64))
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
   if (spec->kv_layout != LOOM_KV_LAYOUT_NHD && spec->kv_layout != LOOM_KV_LAYOUT_HND)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", spec->kv_layout);
@@ -639,14 +771,20 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", spec->kv_dtype);
   if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
+  const uint32_t waves = opt.waves ? opt.waves : waves_for();
+  uint32_t tile_cols = 16;
+  loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->kv_dtype == LOOM_KV_DTYPE_FP8_E4M3,
+                                       spec->batch_size, spec->nnz_qo, spec->num_query_heads,
+                                       spec->num_kv_heads, &tile_cols, err);
+  if (rc) return rc;
   uint64_t tiles = 0, grid = 0;
-  loom_status_t rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads,
-                                  spec->num_kv_heads, &tiles, &grid, err);
+  rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads, spec->num_kv_heads,
+                    tile_cols, &tiles, &grid, err);
   if (rc) return rc;
   auto *p = new loom_paged_prefill_plan;
   p->info.spec = *spec;
-  p->info.algorithm = LOOM_PAGED_PREFILL_ROW_TILE;
-  p->info.waves = opt.waves ? opt.waves : waves_for();
+  p->info.algorithm = tile_cols == 64 ? LOOM_PAGED_PREFILL_WIDE_TILE : LOOM_PAGED_PREFILL_ROW_TILE;
+  p->info.waves = waves;
   p->info.row_tiles = tiles;
   p->info.block_threads = p->info.waves * 64;
   p->info.grid_blocks = grid;
@@ -751,7 +889,12 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
     }
   } else {
     switch (plan->info.waves) {
-      case 4: hipLaunchKernelGGL((paged_prefill_kernel<4, false>), grid, block, 0, stream, a); break;
+      case 4:
+        if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
+          hipLaunchKernelGGL((paged_prefill_kernel<4, false, true>), grid, block, 0, stream, a);
+        else
+          hipLaunchKernelGGL((paged_prefill_kernel<4, false>), grid, block, 0, stream, a);
+        break;
       case 8: hipLaunchKernelGGL((paged_prefill_kernel<8, false>), grid, block, 0, stream, a); break;
       default:
         hipLaunchKernelGGL((paged_prefill_kernel<16, false>), grid, block, 0, stream, a);
@@ -769,17 +912,23 @@ loom_status_t loom_prefill_provider_plan_bf16_ragged(
   if (!provider || !spec || !out) return fail(err, LOOM_NULL_ARGUMENT, "provider");
   const loom_paged_prefill_plan_options_t opt =
       options ? *options : loom_paged_prefill_plan_options_t{0, 0};
-  if (opt.flags != 0) return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
+  if (opt.flags & ~(LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64))
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
   if (opt.waves != 0 && opt.waves != 4 && opt.waves != 8 && opt.waves != 16)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
+  const uint32_t waves = opt.waves ? opt.waves : waves_for();
+  uint32_t tile_cols = 16;
+  loom_status_t rc = prefill_tile_cols(opt.flags, waves, false, spec->batch_size, spec->nnz_qo,
+                                       spec->num_query_heads, spec->num_kv_heads, &tile_cols, err);
+  if (rc) return rc;
   uint64_t tiles = 0, grid = 0;
-  loom_status_t rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads,
-                                  spec->num_kv_heads, &tiles, &grid, err);
+  rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads, spec->num_kv_heads,
+                    tile_cols, &tiles, &grid, err);
   if (rc) return rc;
   auto *p = new loom_ragged_prefill_plan;
   p->info.spec = *spec;
-  p->info.algorithm = LOOM_PAGED_PREFILL_ROW_TILE;
-  p->info.waves = opt.waves ? opt.waves : waves_for();
+  p->info.algorithm = tile_cols == 64 ? LOOM_PAGED_PREFILL_WIDE_TILE : LOOM_PAGED_PREFILL_ROW_TILE;
+  p->info.waves = waves;
   p->info.row_tiles = tiles;
   p->info.block_threads = p->info.waves * 64;
   p->info.grid_blocks = grid;
@@ -849,7 +998,12 @@ loom_status_t loom_ragged_prefill_enqueue(const loom_ragged_prefill_plan_t *plan
   hipStream_t stream = scope->queue->stream;
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
   switch (plan->info.waves) {
-    case 4: hipLaunchKernelGGL(ragged_prefill_kernel<4>, grid, block, 0, stream, a); break;
+    case 4:
+      if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
+        hipLaunchKernelGGL((ragged_prefill_kernel<4, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL(ragged_prefill_kernel<4>, grid, block, 0, stream, a);
+      break;
     case 8: hipLaunchKernelGGL(ragged_prefill_kernel<8>, grid, block, 0, stream, a); break;
     default: hipLaunchKernelGGL(ragged_prefill_kernel<16>, grid, block, 0, stream, a); break;
   }

@@ -34,6 +34,14 @@ HEAD_DIM = 128
 PAGE_SIZE = 16
 PARTIAL_STATE_WIDTH = 130
 PLAN_PAGE_INDICES_CAPACITY = 1
+PLAN_PREFILL_TILE_16 = 2
+PLAN_PREFILL_TILE_64 = 4
+
+
+def _prefill_tile_flag(tile_cols: int) -> int:
+    if tile_cols not in (0, 16, 64):
+        raise ValueError(f"tile_cols must be 0, 16 or 64, got {tile_cols}")
+    return {0: 0, 16: PLAN_PREFILL_TILE_16, 64: PLAN_PREFILL_TILE_64}[tile_cols]
 # K/V page layouts (loom_kv_layout_t): NHD pages [16, Hkv, 128], HND pages
 # [Hkv, 16, 128].  The reference supports NHD only.
 KV_LAYOUTS = {"NHD": 0, "HND": 1}
@@ -926,7 +934,7 @@ class Bf16PagedPrefillPlan:
 
     @property
     def algorithm(self) -> str:
-        return {1: "row_tile"}[self.info.algorithm]
+        return {1: "row_tile", 2: "wide_tile"}[self.info.algorithm]
 
     def enqueue_into(self, scope: CommandScope, args: Bf16PagedPrefillArgs):
         _enqueue(_ffi.load().loom_paged_prefill_enqueue, self._p, scope._p, args._ref)
@@ -1032,7 +1040,7 @@ class Bf16RaggedPrefillPlan:
 
     @property
     def algorithm(self) -> str:
-        return {1: "row_tile"}[self.info.algorithm]
+        return {1: "row_tile", 2: "wide_tile"}[self.info.algorithm]
 
     @property
     def workspace_required_numel(self) -> int:
@@ -1068,20 +1076,25 @@ class PrefillProvider:
         return cls(out.value, device)
 
     def plan_bf16_paged(self, spec: Bf16PagedPrefillSpec, waves: int = 0,
-                        indices_capacity: bool = False) -> Bf16PagedPrefillPlan:
+                        indices_capacity: bool = False,
+                        tile_cols: int = 0) -> Bf16PagedPrefillPlan:
         """`waves` per workgroup (0: chosen from the spec; 4, 8 or 16);
-        `indices_capacity`: page_indices is a capacity (LOOM_PLAN_PAGE_INDICES_CAPACITY)."""
-        opt = _ffi.PagedPrefillPlanOptions(waves,
-                                           PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0)
+        `indices_capacity`: page_indices is a capacity (LOOM_PLAN_PAGE_INDICES_CAPACITY);
+        `tile_cols`: query columns per workgroup (0: chosen from the spec; 16 for
+        the row-tile algorithm, 64 for the wide-tile one)."""
+        opt = _ffi.PagedPrefillPlanOptions(
+            waves, (PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0)
+            | _prefill_tile_flag(tile_cols))
         out = C.c_void_p()
         _call(lib().loom_prefill_provider_plan_bf16_paged_options, self._p, C.byref(spec._c),
               C.byref(opt), C.byref(out))
         return Bf16PagedPrefillPlan(out.value, spec)
 
-    def plan_bf16_ragged(self, spec: Bf16RaggedPrefillSpec,
-                         waves: int = 0) -> Bf16RaggedPrefillPlan:
-        """prefill.rs:2331-2410; `waves` per workgroup (0: four; 4, 8 or 16)."""
-        opt = _ffi.PagedPrefillPlanOptions(waves, 0)
+    def plan_bf16_ragged(self, spec: Bf16RaggedPrefillSpec, waves: int = 0,
+                         tile_cols: int = 0) -> Bf16RaggedPrefillPlan:
+        """prefill.rs:2331-2410; `waves` per workgroup (0: four; 4, 8 or 16);
+        `tile_cols` as for the paged plan."""
+        opt = _ffi.PagedPrefillPlanOptions(waves, _prefill_tile_flag(tile_cols))
         out = C.c_void_p()
         _call(lib().loom_prefill_provider_plan_bf16_ragged, self._p, C.byref(spec._c),
               C.byref(opt), C.byref(out))
