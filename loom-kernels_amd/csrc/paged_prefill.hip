@@ -111,7 +111,7 @@ struct PrefillSmem {
   u32x4 qfrag[SH ? W : 1][4][64];  // MFMA B fragments of 16 query columns (per wave: SH)
   float m[W][16];      // per-wave running max (log2 domain) per column
   float l[W][16];      // per-wave normalizer per column
-  f32x4 red[W / 2 > 0 ? W / 2 : 1][4][64];  // tree-sum staging, half the accumulators
+  f32x4 red[SH ? 1 : (W / 2 > 0 ? W / 2 : 1)][4][64];  // tree-sum staging (row tiles only)
 };
 
 // One page of K (A-fragment layout) and V (row layout) for one wave.
