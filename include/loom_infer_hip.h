@@ -609,7 +609,7 @@ typedef enum loom_paged_prefill_algorithm {
    * whole causal page range; each K/V block is loaded once per workgroup,
    * staged through LDS and read by all four waves, so a workgroup reads a
    * quarter of the L2 bytes per column that ROW_TILE reads.  No cross-wave
-   * merge.  BF16 pages only.  No workspace. */
+   * merge.  No workspace. */
   LOOM_PAGED_PREFILL_WIDE_TILE = 2
 } loom_paged_prefill_algorithm_t;
 

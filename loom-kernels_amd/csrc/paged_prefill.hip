@@ -301,19 +301,34 @@ struct PrefillWave {
   // later, after every wave has passed the barrier that follows its reads.
   // `own_end`: causal end of this wave's last column; blocks at or past it
   // are staged but not computed.
-  template <class PageTok, class RowsOf, class LtOf>
+  // FP8 pages: each 16-byte chunk is loaded as its 8 E4M3 bytes and widened
+  // to BF16 (exactly) before it is stored, so the ring holds the BF16 layout.
+  template <bool FP8, class PageTok, class RowsOf, class LtOf>
   __device__ void stream_shared(int n, PageTok page_tok, RowsOf rows_of, LtOf lt_of,
                                 u32x4 (*ring)[2][16][17], int wave, int64_t own_end) {
     const int mat = wave >> 1, row0 = 8 * (wave & 1);
     const uint16_t *src = mat ? a.v : a.k;
-    const int row_bytes = a.row_elems * 2;
     auto fetch = [&](int i, u32x4 (&d)[2]) {
-      const __amdgpu_buffer_rsrc_t r = page_rows_rsrc(
-          src + page_tok(i) + (int64_t)kvh * a.head_elems, rows_of(i), a.row_elems);
+      const int64_t first = page_tok(i) + (int64_t)kvh * a.head_elems;
+      const int rows = rows_of(i);
+      if constexpr (FP8) {
+        const uint8_t *s8 = reinterpret_cast<const uint8_t *>(src) + first;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(s8), 0, rows > 0 ? (rows - 1) * a.row_elems + 128 : 0,
+            0x00020000);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int ch = lane + 64 * j;
-        d[j] = load16_rows<false>(r, (row0 + (ch >> 4)) * row_bytes + (ch & 15) * 16);
+        for (int j = 0; j < 2; ++j) {
+          const int ch = lane + 64 * j;
+          d[j] = fp8x8_to_bf16x8(
+              load8_rows<false>(r, (row0 + (ch >> 4)) * a.row_elems + (ch & 15) * 8));
+        }
+      } else {
+        const __amdgpu_buffer_rsrc_t r = page_rows_rsrc(src + first, rows, a.row_elems);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int ch = lane + 64 * j;
+          d[j] = load16_rows<false>(r, (row0 + (ch >> 4)) * a.row_elems * 2 + (ch & 15) * 16);
+        }
       }
     };
     auto step = [&](int i, u32x4 (&d)[2]) {
@@ -351,7 +366,7 @@ struct PrefillWave {
 // one 16-column tile per wave, every wave over the whole page range.
 template <int W, bool RAGGED, bool FP8, bool SH>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
-  static_assert(!SH || (W == 4 && !FP8), "wide tiles: four waves, BF16 pages");
+  static_assert(!SH || W == 4, "wide tiles: four waves");
   constexpr int TC = SH ? 16 * W : 16;  // flattened columns per workgroup
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   PrefillArgs a = args;
@@ -554,7 +569,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
           own0 < fcols
               ? kv_len - qo_len + (int)((uint32_t)min(own0 + 15, fcols - 1) / (uint32_t)a.group) + 1
               : 0;
-      w.stream_shared(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
+      w.template stream_shared<FP8>(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
     } else {
       w.template stream<prefill_depth(W), FP8>(n, page_tok, rows_of, lt_of);
     }
@@ -572,8 +587,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
       u32x4 o;
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2)
-        o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv) |
-                ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv) << 16);
+        o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv * v_scale) |
+                ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv * v_scale) << 16);
       *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
     }
     if (quad == 0) a.lse[row_head] = w.m_run + __log2f(L);
@@ -694,7 +709,7 @@ loom_status_t prefill_grid(uint64_t batch, uint64_t nnz_qo, uint64_t hq, uint64_
 }
 
 // Columns per workgroup of a prefill plan: 64 (wide tiles) or 16.  Forced by
-// the plan flags; otherwise wide for BF16 pages when the average request has
+// the plan flags; otherwise wide when the average request has
 // at least LOOM_PREFILL_WIDE_MIN_COLS flattened columns and the wide grid
 // still holds LOOM_PREFILL_WIDE_MIN_GRID workgroups.  Measured on GQA4
 // 32/8 prompts (qo = kv): wide 1.5-1.7x faster from 4 x 2048 and 8 x 256
@@ -705,7 +720,7 @@ loom_status_t prefill_grid(uint64_t batch, uint64_t nnz_qo, uint64_t hq, uint64_
 #ifndef LOOM_PREFILL_WIDE_MIN_GRID
 #define LOOM_PREFILL_WIDE_MIN_GRID 512
 #endif
-loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, bool fp8, uint64_t batch,
+loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
                                 uint64_t nnz_qo, uint64_t hq, uint64_t hkv, uint32_t *tile_cols,
                                 loom_error_t *err) {
   const uint32_t t = flags & (LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64);
@@ -713,14 +728,12 @@ loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, bool fp8, uint64
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
   if (t == LOOM_PLAN_PREFILL_TILE_64 && waves != 4)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", waves);
-  if (t == LOOM_PLAN_PREFILL_TILE_64 && fp8)
-    return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_dtype", LOOM_KV_DTYPE_FP8_E4M3);
   if (t) {
     *tile_cols = t == LOOM_PLAN_PREFILL_TILE_64 ? 64 : 16;
     return LOOM_OK;
   }
   const uint64_t cols = nnz_qo * (hq / hkv);
-  *tile_cols = (waves == 4 && !fp8 && batch > 0 && cols >= LOOM_PREFILL_WIDE_MIN_COLS * batch &&
+  *tile_cols = (waves == 4 && batch > 0 && cols >= LOOM_PREFILL_WIDE_MIN_COLS * batch &&
                 (cols / 64) * hkv >= LOOM_PREFILL_WIDE_MIN_GRID)
                    ? 64
                    : 16;
@@ -773,8 +786,8 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
   const uint32_t waves = opt.waves ? opt.waves : waves_for();
   uint32_t tile_cols = 16;
-  loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->kv_dtype == LOOM_KV_DTYPE_FP8_E4M3,
-                                       spec->batch_size, spec->nnz_qo, spec->num_query_heads,
+  loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->batch_size, spec->nnz_qo,
+                                       spec->num_query_heads,
                                        spec->num_kv_heads, &tile_cols, err);
   if (rc) return rc;
   uint64_t tiles = 0, grid = 0;
@@ -881,7 +894,12 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
   if (fp8) {
     switch (plan->info.waves) {
-      case 4: hipLaunchKernelGGL((paged_prefill_kernel<4, true>), grid, block, 0, stream, a); break;
+      case 4:
+        if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
+          hipLaunchKernelGGL((paged_prefill_kernel<4, true, true>), grid, block, 0, stream, a);
+        else
+          hipLaunchKernelGGL((paged_prefill_kernel<4, true>), grid, block, 0, stream, a);
+        break;
       case 8: hipLaunchKernelGGL((paged_prefill_kernel<8, true>), grid, block, 0, stream, a); break;
       default:
         hipLaunchKernelGGL((paged_prefill_kernel<16, true>), grid, block, 0, stream, a);
@@ -918,7 +936,7 @@ loom_status_t loom_prefill_provider_plan_bf16_ragged(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
   const uint32_t waves = opt.waves ? opt.waves : waves_for();
   uint32_t tile_cols = 16;
-  loom_status_t rc = prefill_tile_cols(opt.flags, waves, false, spec->batch_size, spec->nnz_qo,
+  loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->batch_size, spec->nnz_qo,
                                        spec->num_query_heads, spec->num_kv_heads, &tile_cols, err);
   if (rc) return rc;
   uint64_t tiles = 0, grid = 0;

@@ -262,18 +262,19 @@ def test_enqueue_rejections(L, oracle):
     torch.cuda.synchronize()
 
 
-def test_prefill_graph_replays_match_eager(L, oracle):
+@pytest.mark.parametrize("tile_cols", [16, 64])
+def test_prefill_graph_replays_match_eager(L, oracle, tile_cols):
     """gates/paged_prefill.rs:382-526: capture one prefill command, replay it
     with eager work and host synchronization between replays, and compare
     every replay with the eager result bit for bit."""
     import torch
     case = GOLDEN["paged_prefill"]["cases"][2]  # gqa4_reordered_reuse, as the reference's graph gate
-    log("prefill graph replay")
+    log(f"prefill graph replay tile_cols={tile_cols}")
     q, k, v = gate_inputs(oracle, case)
     B, nnz, pool, hq, hkv = (case[x] for x in ("batch", "nnz_qo", "pool", "hq", "hkv"))
     meta = (case["qo_indptr"], case["indptr"], case["indices"], case["last"])
     ref_out, ref_lse = oracle.prefill(oracle.prefill_spec(B, nnz, pool, hq, hkv), q, k, v, *meta)
-    r = PrefillRunner(L, B, nnz, pool, hq, hkv)
+    r = PrefillRunner(L, B, nnz, pool, hq, hkv, tile_cols=tile_cols)
     eager_o, eager_l = r.run(q, k, v, *meta)
     compare_decode(oracle, eager_o, eager_l, ref_out, ref_lse)
     ins = [to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v)] + [to_dev_i32(m) for m in meta]

@@ -3,8 +3,8 @@ K/V blocks staged through LDS for four waves), paged and ragged, through the
 C ABI.  It has no reference counterpart: the reference runs one warp per
 (row, head).  Checked against the oracle on the reference's fixtures and
 seeded shapes, and against the 16-column algorithm (itself pinned to the
-oracle) on long prompts, where the plan picks it by itself, on HND and
-64-row pages, and on every device-guard outcome: the same sentinel rows,
+oracle) on long prompts, where the plan picks it by itself, on FP8, HND
+and 64-row pages, and on every device-guard outcome: the same sentinel rows,
 byte for byte, and the other rows within the oracle tolerance (the two
 algorithms sum a column's blocks in different orders)."""
 import sys
@@ -147,16 +147,30 @@ def test_long_prompt_picks_wide_and_matches_row_tiles(L, oracle):
                                   l.view(np.float32)[(n - tail) * hq:], ref_out, ref_lse)))
 
 
-def test_fp8_stays_on_row_tiles(L):
-    """FP8 pages have no wide-tile kernel: the plan keeps 16-column tiles for
-    them and rejects the wide flag."""
-    spec = L.Bf16PagedPrefillSpec(1, 4096, 256, 32, 8, kv_dtype="fp8_e4m3")
+def test_fp8_pages_on_wide_tiles(L, oracle):
+    """FP8 E4M3 pages on wide tiles (widened to BF16 as they are staged):
+    the plan picks them for a long prompt as for BF16, and the result matches
+    the 16-column FP8 command within the oracle tolerance (codes up to 0x44,
+    |x| <= 3, so outputs stay below 4 and one BF16 ulp is at most 1/64)."""
+    import torch
+    from test_gpu_fp8 import random_fp8
+    log("wide prefill fp8")
     prov = L.PrefillProvider.load(0)
-    assert prov.plan_bf16_paged(spec).algorithm == "row_tile"
-    with pytest.raises(L.LoomError):
-        prov.plan_bf16_paged(spec, tile_cols=64)
-    assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 4096, 256, 32, 8)).algorithm == \
-        "wide_tile"
+    assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 4096, 256, 32, 8,
+                                                       kv_dtype="fp8_e4m3")).algorithm == "wide_tile"
+    rng = np.random.default_rng(88)
+    B, hq, hkv = 3, 16, 4
+    qo_lens, kv_lens = [70, 5, 130], [400, 90, 130]
+    pool = sum((x + 15) // 16 for x in kv_lens) + 2
+    qo, ip, ix, last = ragged_meta(rng, qo_lens, kv_lens, pool)
+    nnz = int(qo[-1])
+    q = seeded_normal_bf16(oracle, rng, nnz * hq * 128)
+    k = torch.from_numpy(random_fp8(rng, pool * 16 * hkv * 128, max_code=0x44)).to("cuda")
+    v = torch.from_numpy(random_fp8(rng, pool * 16 * hkv * 128, max_code=0x44)).to("cuda")
+    res = paged_pair(L, B, nnz, pool, hq, hkv, q, k, v, qo, ip, ix, last,
+                     spec_kw={"kv_dtype": "fp8_e4m3"}, scales=[0.3, 0.7])
+    assert not np.any(np.isnan(oracle.bf16_to_f32(res[0][0])))
+    log(f"  vs 16-column: {assert_close(oracle, res)}")
 
 
 @pytest.mark.parametrize("variant", ["hnd", "page64"])
