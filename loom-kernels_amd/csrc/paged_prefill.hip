@@ -301,6 +301,10 @@ struct PrefillWave {
   // later, after every wave has passed the barrier that follows its reads.
   // `own_end`: causal end of this wave's last column; blocks at or past it
   // are staged but not computed.
+#ifndef LOOM_PREFILL_WIDE_AHEAD
+#define LOOM_PREFILL_WIDE_AHEAD 2
+#endif
+  static constexpr int kWideAhead = LOOM_PREFILL_WIDE_AHEAD;  // blocks in flight per wave
   // FP8 pages: each 16-byte chunk is loaded as its 8 E4M3 bytes and widened
   // to BF16 (exactly) before it is stored, so the ring holds the BF16 layout.
   template <bool FP8, class PageTok, class RowsOf, class LtOf>
@@ -338,7 +342,7 @@ struct PrefillWave {
         const int ch = lane + 64 * j;
         slot[mat][row0 + (ch >> 4)][ch & 15] = d[j];
       }
-      fetch(i + 2, d);  // past the end: no valid rows, no traffic
+      fetch(i + kWideAhead, d);  // past the end: no valid rows, no traffic
       __syncthreads();
       const int64_t lt0 = lt_of(i);
       if (lt0 < own_end) {
@@ -350,14 +354,15 @@ struct PrefillWave {
         process(pg, lt0);
       }
     };
-    u32x4 d0[2], d1[2];
-    fetch(0, d0);
-    fetch(1, d1);
+    u32x4 d[kWideAhead][2];
+#pragma unroll
+    for (int j = 0; j < kWideAhead; ++j) fetch(j, d[j]);
     for (int i = 0;;) {
-      step(i, d0);
-      if (++i >= n) return;
-      step(i, d1);
-      if (++i >= n) return;
+#pragma unroll
+      for (int j = 0; j < kWideAhead; ++j) {
+        step(i, d[j]);
+        if (++i >= n) return;
+      }
     }
   }
 };
