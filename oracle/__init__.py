@@ -206,6 +206,29 @@ def paged_decode_requests(spec, q, k, v, indptr, indices, last, r0, r1, out, lse
                                    _p(out), _p(lse))
 
 
+def paged_decode_parallel(spec, q, k, v, indptr, indices, last, threads=None):
+    """paged_decode with the requests split over host threads (ctypes releases
+    the GIL); each request is the same single-threaded loop, so the result is
+    bit-identical to paged_decode."""
+    from concurrent.futures import ThreadPoolExecutor
+    paged_validate(spec, indptr, indices, last)
+    indptr, indices, last = _i32(indptr), _i32(indices), _i32(last)
+    q, k, v = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v))
+    B, hq = spec.batch_size, spec.num_query_heads
+    out = np.full(B * hq * HEAD_DIM, 0x7FC0, dtype=np.uint16)
+    lse = np.full(B * hq, np.nan, dtype=np.float32)
+    threads = threads or min(16, os.cpu_count() or 1)
+    # cut the requests into chunks of about equal token counts
+    lens = np.diff(indptr.astype(np.int64)) * PAGE_SIZE
+    bounds = np.searchsorted(np.cumsum(lens), np.linspace(0, lens.sum(), 4 * threads + 1)[1:-1])
+    cuts = sorted(set([0] + [int(b) + 1 for b in bounds if b + 1 < B] + [B]))
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(lambda r: paged_decode_requests(spec, q, k, v, indptr, indices, last,
+                                                    r[0], r[1], out, lse),
+                    zip(cuts[:-1], cuts[1:])))
+    return out, lse
+
+
 # ---- paged causal prefill --------------------------------------------------
 def prefill_spec(batch, nnz_qo, pool, hq, hkv, head_dim=128, page_size=16) -> PrefillSpec:
     s, e = PrefillSpec(), _Err()

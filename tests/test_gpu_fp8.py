@@ -4,7 +4,7 @@ in tests/test_oracle_fp8.py against torch.float8_e4m3fn and the BF16 paths).
 
 * Append: V bytes bit-exact (no RoPE in between); K bytes bit-exact except
   where the oracle's FP32 rotation differs from the device's by the sin/cos
-  rounding discussed in test_gpu_append.within_rope_tolerance, which can move
+  rounding discussed in test_gpu_append.check_rope, which can move
   a value across an FP8 rounding boundary: such bytes are adjacent codes, and
   rare.  Query output within the BF16 append's tolerance.
 * Decode: against the oracle's FP8 decode with the BF16 decode's tolerances

@@ -409,3 +409,23 @@ def test_append_known_slots_and_rejections(oracle):
         oracle.append_tokens_validate(oracle.paged_spec(1, 1, 1, 1), 65, [0] * 65, [0] * 65,
                                       [0, 1], [0], [16])
     assert e.value.name == "UnsupportedAppendTokenCount" and e.value.fields[:2] == (64, 65)
+
+
+def test_parallel_paged_decode_equals_serial(oracle):
+    """paged_decode_parallel (requests split over host threads, used by the
+    full-size GPU parity tests) is bit-identical to the serial oracle."""
+    rng = np.random.default_rng(17)
+    B, hq, hkv = 9, 16, 4
+    lens = rng.integers(1, 400, size=B)
+    pages = (lens + 15) // 16
+    pool = int(pages.sum()) + 5
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
+    last = (lens - (pages - 1) * 16).astype(np.int32)
+    q = oracle.bf16_from_f32(rng.standard_normal(B * hq * 128, dtype=np.float32))
+    k = oracle.bf16_from_f32(rng.standard_normal(pool * 16 * hkv * 128, dtype=np.float32))
+    v = oracle.bf16_from_f32(rng.standard_normal(pool * 16 * hkv * 128, dtype=np.float32))
+    s = oracle.paged_spec(B, pool, hq, hkv)
+    a = oracle.paged_decode(s, q, k, v, indptr, indices, last)
+    b = oracle.paged_decode_parallel(s, q, k, v, indptr, indices, last, threads=4)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
