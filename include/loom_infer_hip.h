@@ -25,8 +25,11 @@
  *   - Buffers are raw device pointers with an element count and dtype.
  *     Binding a buffer read-write transfers it to the binding set until the
  *     command completion that used it is settled and the caller takes it back.
- *   - No function here allocates device memory except *_new/_load and graph
- *     instantiation; enqueue paths never allocate.
+ *   - No function here allocates device memory except *_new/_load, graph
+ *     instantiation, loom_command_queue_reserve_workspace and the first
+ *     enqueue of a reference-shaped argument struct on a queue whose
+ *     workspace is too small (the *_enqueue_bf16 forms); enqueues that take
+ *     a caller-owned workspace never allocate.
  */
 #ifndef LOOM_INFER_HIP_H
 #define LOOM_INFER_HIP_H
@@ -312,6 +315,17 @@ loom_status_t loom_command_queue_new(void *hip_stream, uint64_t max_commands,
                                      loom_command_queue_t **out, loom_error_t *err);
 /* Drop: synchronizes the stream if commands are still retained. */
 void loom_command_queue_free(loom_command_queue_t *queue);
+/* No reference counterpart: the reference's plans need no workspace.  The
+ * enqueue forms that take the reference's argument structs keep their scratch
+ * in device buffers owned by the queue; this allocates them ahead of the
+ * first command (split-KV `scratch_bytes` = a decode plan's workspace_bytes,
+ * append `zeroed_bytes` = an append plan's workspace_bytes) so that those
+ * enqueues allocate nothing.  Buffers only grow; they are freed with the
+ * queue (or with the graph that captured its commands). */
+loom_status_t loom_command_queue_reserve_workspace(loom_command_queue_t *queue,
+                                                   uint64_t scratch_bytes, uint64_t zeroed_bytes,
+                                                   loom_error_t *err);
+uint64_t loom_command_queue_workspace_bytes(const loom_command_queue_t *queue);
 uint64_t loom_command_queue_max_commands(const loom_command_queue_t *queue);
 int loom_command_queue_is_poisoned(const loom_command_queue_t *queue);
 
@@ -446,6 +460,33 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
                                         loom_command_scope_t *scope,
                                         const loom_paged_decode_args_t *args,
                                         loom_error_t *err);
+
+/* Bf16PagedBatchDecodeArgs exactly as the reference declares it
+ * (decode.rs:1452-1487): eight operands, no workspace. */
+typedef struct loom_bf16_paged_batch_decode_args {
+  loom_handle_t query;         /* Read<bf16>  [B, Hq, 128] */
+  loom_handle_t key_pages;     /* Read<bf16>  [pool, P, Hkv, 128] */
+  loom_handle_t value_pages;   /* Read<bf16>  [pool, P, Hkv, 128] */
+  loom_handle_t page_indptr;   /* Read<i32>   [B+1] */
+  loom_handle_t page_indices;  /* Read<i32>   [>= B] */
+  loom_handle_t last_page_len; /* Read<i32>   [B] */
+  loom_handle_t output;        /* Write<bf16> [B, Hq, 128] */
+  loom_handle_t lse;           /* Write<f32>  [B, Hq], log2 domain */
+} loom_bf16_paged_batch_decode_args_t;
+
+/* Bf16PagedBatchDecodePlan::enqueue_into(scope, Bf16PagedBatchDecodeArgs),
+ * decode.rs:1199-1296, with the reference's argument struct.  The split-KV
+ * states live in a workspace owned by the scope's command queue: it is
+ * allocated (hipMalloc) the first time a command needs more than the queue
+ * holds, then reused by every later command on that queue (stream-ordered, so
+ * without races), and freed with the queue.  Callers that must not allocate
+ * here reserve it first (loom_command_queue_reserve_workspace with
+ * plan.workspace_bytes) or pass their own (loom_paged_decode_enqueue).  BF16
+ * pages only (the reference's args carry no FP8 scales). */
+loom_status_t loom_paged_decode_enqueue_bf16(const loom_paged_decode_plan_t *plan,
+                                             loom_command_scope_t *scope,
+                                             const loom_bf16_paged_batch_decode_args_t *args,
+                                             loom_error_t *err);
 
 /* ------------------------------------------------------------------------ */
 /* Contiguous single decode, crates/loom-infer/src/attention/single_decode/    */
@@ -826,6 +867,51 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
                                        loom_command_scope_t *scope,
                                        const loom_rope_append_args_t *args,
                                        loom_error_t *err);
+
+/* Bf16RopePagedKvAppendArgs and Bf16RopePagedKvAppendTokensArgs exactly as
+ * the reference declares them (rope/mod.rs:963-1047): no workspace, BF16
+ * pages. */
+typedef struct loom_bf16_rope_paged_kv_append_args {
+  loom_handle_t query;         /* Read<bf16>  [B, Hq, 128] */
+  loom_handle_t key;           /* Read<bf16>  [B, Hkv, 128] */
+  loom_handle_t value;         /* Read<bf16>  [B, Hkv, 128] */
+  loom_handle_t page_indptr;   /* Read<i32>   [B+1] */
+  loom_handle_t page_indices;  /* Read<i32>   [>= B] */
+  loom_handle_t last_page_len; /* Read<i32>   [B] */
+  loom_handle_t query_output;  /* Write<bf16> [B, Hq, 128] */
+  loom_handle_t key_pages;     /* Write<bf16> [pool, P, Hkv, 128] */
+  loom_handle_t value_pages;   /* Write<bf16> [pool, P, Hkv, 128] */
+} loom_bf16_rope_paged_kv_append_args_t;
+
+typedef struct loom_bf16_rope_paged_kv_append_tokens_args {
+  loom_handle_t query;         /* Read<bf16>  [T, Hq, 128] */
+  loom_handle_t key;           /* Read<bf16>  [T, Hkv, 128] */
+  loom_handle_t value;         /* Read<bf16>  [T, Hkv, 128] */
+  loom_handle_t batch_indices; /* Read<i32>   [T] */
+  loom_handle_t positions;     /* Read<i32>   [T] */
+  loom_handle_t page_indptr;   /* Read<i32>   [B+1] */
+  loom_handle_t page_indices;  /* Read<i32>   [>= B] */
+  loom_handle_t last_page_len; /* Read<i32>   [B] */
+  loom_handle_t query_output;  /* Write<bf16> [T, Hq, 128] */
+  loom_handle_t key_pages;     /* Write<bf16> [pool, P, Hkv, 128] */
+  loom_handle_t value_pages;   /* Write<bf16> [pool, P, Hkv, 128] */
+} loom_bf16_rope_paged_kv_append_tokens_args_t;
+
+/* Bf16RopePagedKvAppendPlan::enqueue_into (rope/mod.rs:758-830) and
+ * Bf16RopePagedKvAppendTokensPlan::enqueue_into (:846-934) with the
+ * reference's argument structs.  The validation words live in a
+ * zero-initialised workspace owned by the scope's command queue (allocated on
+ * the first command that needs more than the queue holds, or ahead of time by
+ * loom_command_queue_reserve_workspace; see loom_paged_decode_enqueue_bf16).
+ * A one-token plan takes the first form, an explicit-token plan the second
+ * (LOOM_NULL_ARGUMENT "args" otherwise). */
+loom_status_t loom_rope_append_enqueue_bf16(const loom_rope_append_plan_t *plan,
+                                            loom_command_scope_t *scope,
+                                            const loom_bf16_rope_paged_kv_append_args_t *args,
+                                            loom_error_t *err);
+loom_status_t loom_rope_append_tokens_enqueue_bf16(
+    const loom_rope_append_plan_t *plan, loom_command_scope_t *scope,
+    const loom_bf16_rope_paged_kv_append_tokens_args_t *args, loom_error_t *err);
 
 /* ------------------------------------------------------------------------ */
 /* Graph capture and replay, crates/loom-infer-cuda/src/graph/mod.rs           */

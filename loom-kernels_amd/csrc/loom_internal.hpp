@@ -62,6 +62,18 @@ struct loom_command_queue {
   bool poisoned = false;
   bool owns_stream = false;
   bool active = false;  // a scope or completion borrows the queue (Rust's &mut)
+  // Device workspaces owned by the queue for the enqueue forms that take the
+  // reference's argument structs (no workspace operand).  `scratch` holds
+  // split-KV states (no initialisation needed); `zeroed` holds append
+  // validation words (zero-filled when allocated; every command leaves them
+  // at zero).  Commands on one queue are ordered on its one stream, so they
+  // reuse the buffers without races.  A buffer that grows is retired, not
+  // freed, until the queue is dropped: commands already submitted may use it.
+  uint8_t *scratch = nullptr;
+  uint64_t scratch_bytes = 0;
+  uint8_t *zeroed = nullptr;
+  uint64_t zeroed_bytes = 0;
+  std::vector<void *> retired;
 };
 
 struct loom_command_scope {
@@ -97,6 +109,12 @@ loom_status_t record_launch(loom_command_scope *scope, hipError_t launch_status,
 // submission.rs / completion.rs:165-182: synchronize the stream, then the
 // device; abort when neither proves quiescence.
 hipError_t synchronize_stream_or_abort(hipStream_t stream);
+
+// The queue's workspace of at least `bytes` (allocated or grown on first
+// need; see loom_command_queue).  `zeroed` selects the zero-initialised
+// buffer.
+loom_status_t queue_workspace(loom_command_queue *queue, uint64_t bytes, bool zeroed,
+                              uint8_t **out, loom_error_t *err);
 
 // Device facts used by providers.
 struct DeviceInfo {

@@ -1332,32 +1332,54 @@ void loom_paged_decode_plan_get_info(const loom_paged_decode_plan_t *p,
   if (p && info) *info = p->info;
 }
 
-loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
-                                        loom_command_scope_t *scope,
-                                        const loom_paged_decode_args_t *args,
-                                        loom_error_t *err) {
-  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+}  // extern "C"
+
+namespace {
+
+// Where a paged-decode command finds its split-KV workspace.
+enum class DecodeWorkspace {
+  kOperand,  // the `workspace` handle of loom_paged_decode_args_t
+  kQueue,    // the command queue's own workspace (reference-shaped args)
+};
+
+// Bf16PagedBatchDecodePlan::enqueue_into, decode.rs:1199-1296.  `hs` holds
+// the ten handles of loom_paged_decode_args_t; with the queue's workspace the
+// workspace handle is not an operand.
+loom_status_t paged_decode_enqueue_impl(const loom_paged_decode_plan_t *plan,
+                                        loom_command_scope_t *scope, const loom_handle_t *hs_all,
+                                        DecodeWorkspace where, loom_error_t *err) {
   const loom_paged_decode_plan_info_t &pi = plan->info;
   const loom_paged_decode_spec_t &s = pi.spec;
   // FP8 pages are u8 operands plus the [k_scale, v_scale] operand.
   const bool fp8 = s.kv_dtype == LOOM_KV_DTYPE_FP8_E4M3;
   const loom_dtype_t kv_t = fp8 ? LOOM_DTYPE_U8 : LOOM_DTYPE_BF16;
-  const loom::OperandSpec ops[10] = {
+  const loom::OperandSpec ops_all[10] = {
       {"Q", LOOM_DTYPE_BF16, false},           {"K_pages", kv_t, false},
       {"V_pages", kv_t, false},                {"page_indptr", LOOM_DTYPE_I32, false},
       {"page_indices", LOOM_DTYPE_I32, false}, {"last_page_len", LOOM_DTYPE_I32, false},
       {"O", LOOM_DTYPE_BF16, true},            {"LSE", LOOM_DTYPE_F32, true},
       {"workspace", LOOM_DTYPE_U8, true},      {"kv_scales", LOOM_DTYPE_F32, false}};
-  const loom_handle_t hs[10] = {args->query,       args->key_pages,    args->value_pages,
-                                args->page_indptr, args->page_indices, args->last_page_len,
-                                args->output,      args->lse,          args->workspace,
-                                args->kv_scales};
-  const int nops = fp8 ? 10 : 9;
-  const loom::Lease *l[10];
-  loom_status_t rc = loom::resolve_command(scope, hs, ops, nops, l, err);
+  const bool ws_operand = where == DecodeWorkspace::kOperand;
+  if (fp8 && !ws_operand)  // the reference-shaped args carry no scales
+    return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, 0);
+  loom::OperandSpec ops[10];
+  loom_handle_t hs[10];
+  int map[10];
+  int nops = 0;
+  for (int i = 0; i < 10; ++i) {
+    map[i] = -1;
+    if (i == 8 && !ws_operand) continue;
+    if (i == 9 && !fp8) continue;
+    ops[nops] = ops_all[i];
+    hs[nops] = hs_all[i];
+    map[i] = nops++;
+  }
+  const loom::Lease *lr[10];
+  loom_status_t rc = loom::resolve_command(scope, hs, ops, nops, lr, err);
   if (rc) return rc;
-  if (fp8 && l[9]->numel != 2)
-    return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, l[9]->numel);
+  auto l = [&](int i) { return lr[map[i]]; };
+  if (fp8 && l(9)->numel != 2)
+    return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, l(9)->numel);
   // decode.rs:1216-1242: exact lengths before submission.
   const uint64_t qn = s.batch_size * s.num_query_heads * loom::kHeadDim;
   const uint64_t page_rows = s.page_size ? s.page_size : loom::kPageSize;
@@ -1365,38 +1387,49 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   const uint64_t want[9] = {qn, kvn, kvn, s.batch_size + 1, 0, s.batch_size, qn,
                             s.batch_size * s.num_query_heads, pi.workspace_bytes};
   for (int i = 0; i < 9; ++i) {
+    if (i == 8 && !ws_operand) continue;
     if (i == 4) {
-      if (l[4]->numel < s.batch_size)
-        return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_SHORT, nullptr, s.batch_size, l[4]->numel);
-      if (l[4]->numel > pi.max_total_pages)
+      if (l(4)->numel < s.batch_size)
+        return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_SHORT, nullptr, s.batch_size, l(4)->numel);
+      if (l(4)->numel > pi.max_total_pages)
         return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_LONG, nullptr, pi.max_total_pages,
-                    l[4]->numel);
+                    l(4)->numel);
       continue;
     }
-    if (l[i]->numel != want[i])
-      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
+    if (l(i)->numel != want[i])
+      return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops_all[i].name, want[i], l(i)->numel);
   }
-  // 16-byte vector loads and stores (decode.rs:1243-1251 checks 4 bytes for its
-  // packed pairs; this kernel moves 16 bytes per lane).
-  const int align_ops[5] = {0, 1, 2, 6, 8};
-  for (int i : align_ops)
-    if (l[i]->ptr % 16 != 0)
-      return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, ops[i].name, (int64_t)l[i]->ptr, 16);
-  if (fp8 && l[9]->ptr % 4 != 0)
-    return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, "kv_scales", (int64_t)l[9]->ptr, 4);
+  // decode.rs:1243-1251 / :1585-1600: Q, K/V pages and O on 4-byte
+  // boundaries (the kernels' 16-byte accesses do not need more: global and
+  // buffer accesses of gfx950 run in unaligned mode).  The caller-owned
+  // workspace takes 16-byte vector stores of the split states.
+  for (int i : {0, 1, 2, 6, 7})
+    if (l(i)->ptr % 4 != 0)
+      return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, ops_all[i].name, (int64_t)l(i)->ptr, 4);
+  if (ws_operand && l(8)->ptr % 16 != 0)
+    return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, "workspace", (int64_t)l(8)->ptr, 16);
+  if (fp8 && l(9)->ptr % 4 != 0)
+    return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, "kv_scales", (int64_t)l(9)->ptr, 4);
 
+  uint8_t *ws = nullptr;
+  if (where == DecodeWorkspace::kOperand) {
+    ws = (uint8_t *)l(8)->ptr;
+  } else {
+    rc = loom::queue_workspace(scope->queue, pi.workspace_bytes, false, &ws, err);
+    if (rc) return rc;
+  }
   DecodeArgs a{};
-  a.kv_scales = fp8 ? (const float *)l[9]->ptr : nullptr;
-  a.q = (const uint16_t *)l[0]->ptr;
-  a.k = (const uint16_t *)l[1]->ptr;
-  a.v = (const uint16_t *)l[2]->ptr;
-  a.indptr = (const int32_t *)l[3]->ptr;
-  a.indices = (const int32_t *)l[4]->ptr;
-  a.last = (const int32_t *)l[5]->ptr;
-  a.out = (uint16_t *)l[6]->ptr;
-  a.lse = (float *)l[7]->ptr;
-  a.header = (int64_t *)l[8]->ptr;
-  a.states = (float *)(l[8]->ptr + pi.header_bytes);
+  a.kv_scales = fp8 ? (const float *)l(9)->ptr : nullptr;
+  a.q = (const uint16_t *)l(0)->ptr;
+  a.k = (const uint16_t *)l(1)->ptr;
+  a.v = (const uint16_t *)l(2)->ptr;
+  a.indptr = (const int32_t *)l(3)->ptr;
+  a.indices = (const int32_t *)l(4)->ptr;
+  a.last = (const int32_t *)l(5)->ptr;
+  a.out = (uint16_t *)l(6)->ptr;
+  a.lse = (float *)l(7)->ptr;
+  a.header = (int64_t *)ws;
+  a.states = (float *)(ws + pi.header_bytes);
   a.batch = (int32_t)s.batch_size;
   a.hq = (int32_t)s.num_query_heads;
   a.hkv = (int32_t)s.num_kv_heads;
@@ -1406,7 +1439,7 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   a.members = (int32_t)(direct ? pi.group_tiles : s.num_kv_heads * pi.group_tiles);
   a.teams = (int32_t)pi.teams;
   a.pool = (int64_t)s.max_num_pages;
-  a.n_indices = (int64_t)l[4]->numel;
+  a.n_indices = (int64_t)l(4)->numel;
   a.indices_capacity = (pi.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
   a.scale_log2 = s.softmax_scale * 1.44269504088896340736f;
   const bool hnd = s.kv_layout == LOOM_KV_LAYOUT_HND;
@@ -1441,6 +1474,43 @@ loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
   }
   return loom::record_launch(scope, e, err);
 }
+
+}  // namespace
+
+extern "C" {
+
+loom_status_t loom_paged_decode_enqueue(const loom_paged_decode_plan_t *plan,
+                                        loom_command_scope_t *scope,
+                                        const loom_paged_decode_args_t *args,
+                                        loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_handle_t hs[10] = {args->query,       args->key_pages,    args->value_pages,
+                                args->page_indptr, args->page_indices, args->last_page_len,
+                                args->output,      args->lse,          args->workspace,
+                                args->kv_scales};
+  return paged_decode_enqueue_impl(plan, scope, hs, DecodeWorkspace::kOperand, err);
+}
+
+static void ref_handles(const loom_bf16_paged_batch_decode_args_t *a, loom_handle_t *hs) {
+  const loom_handle_t none{0, 0};
+  const loom_handle_t v[10] = {a->query,       a->key_pages,    a->value_pages,
+                               a->page_indptr, a->page_indices, a->last_page_len,
+                               a->output,      a->lse,          none,
+                               none};
+  for (int i = 0; i < 10; ++i) hs[i] = v[i];
+}
+
+loom_status_t loom_paged_decode_enqueue_bf16(const loom_paged_decode_plan_t *plan,
+                                             loom_command_scope_t *scope,
+                                             const loom_bf16_paged_batch_decode_args_t *args,
+                                             loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  loom_handle_t hs[10];
+  ref_handles(args, hs);
+  return paged_decode_enqueue_impl(plan, scope, hs, DecodeWorkspace::kQueue, err);
+}
+
+
 
 
 // ---- contiguous single decode: plans and enqueue -------------------------------
@@ -1494,8 +1564,9 @@ uint64_t loom_single_decode_split_k_workspace_bytes(const loom_single_decode_spl
 }
 
 namespace {
-// decode.rs:1683-1696 checks 4-byte alignment for its packed pairs; these
-// kernels move 16 bytes per lane (Q, K, V) and write 2-byte O elements.
+// decode.rs:1683-1696 checks 4-byte alignment for its packed pairs, and so
+// do these: their 16-byte accesses need no more on gfx950 (global and buffer
+// accesses run in unaligned mode).
 loom_status_t require_aligned(const char *name, uintptr_t ptr, uintptr_t alignment,
                               loom_error_t *err) {
   if (ptr % alignment != 0)
@@ -1526,7 +1597,7 @@ loom_status_t loom_single_decode_enqueue(const loom_single_decode_plan_t *plan,
     if (l[i]->numel != want[i])
       return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
   for (int i : {0, 1, 2})
-    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 4, err))) return rc;
   if ((rc = require_aligned("O", l[3]->ptr, 4, err))) return rc;
   DecodeArgs a = single_args(s, plan->group_tiles, l[0]->ptr, l[1]->ptr, l[2]->ptr, l[3]->ptr,
                              l[4]->ptr);
@@ -1568,7 +1639,7 @@ loom_status_t loom_single_decode_split_k_enqueue(const loom_single_decode_split_
     if (l[i]->numel != want[i])
       return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
   for (int i : {0, 1, 2})
-    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 4, err))) return rc;
   if ((rc = require_aligned("workspace", l[3]->ptr, 8, err))) return rc;
   if ((rc = require_aligned("O", l[4]->ptr, 4, err))) return rc;
   DecodeArgs a = single_args(s, plan->group_tiles, l[0]->ptr, l[1]->ptr, l[2]->ptr, l[4]->ptr,

@@ -869,7 +869,7 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
       return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
   }
   for (int i : {0, 1, 2, 7})
-    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 4, err))) return rc;
   PrefillArgs a{};
   a.kv_scales = fp8 ? (const float *)l[9]->ptr : nullptr;
   a.q = (const uint16_t *)l[0]->ptr;
@@ -998,7 +998,7 @@ loom_status_t loom_ragged_prefill_enqueue(const loom_ragged_prefill_plan_t *plan
     if (l[i]->numel != want[i])
       return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[i].name, want[i], l[i]->numel);
   for (int i : {0, 1, 2, 5})
-    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 16, err))) return rc;
+    if ((rc = require_aligned(ops[i].name, l[i]->ptr, 4, err))) return rc;
   PrefillArgs a{};
   a.q = (const uint16_t *)l[0]->ptr;
   a.k = (const uint16_t *)l[1]->ptr;

@@ -517,14 +517,23 @@ void loom_rope_append_plan_get_info(const loom_rope_append_plan_t *p,
   if (p && info) *info = p->info;
 }
 
-loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
-                                       loom_command_scope_t *scope,
-                                       const loom_rope_append_args_t *args, loom_error_t *err) {
-  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+}  // extern "C"
+
+namespace {
+
+// enqueue_into, rope/mod.rs:758-830 / :846-934.  `hs_all` holds the thirteen
+// handles of loom_rope_append_args_t; with `queue_ws` the validation words
+// live in the command queue's zero-initialised workspace and the workspace
+// handle is not an operand.
+loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
+                                       loom_command_scope_t *scope, const loom_handle_t *hs_all,
+                                       bool queue_ws, loom_error_t *err) {
   const loom_rope_append_plan_info_t &pi = plan->info;
   const bool ex = pi.explicit_tokens != 0;
   // Operand order of Bf16RopePagedKvAppend{,Tokens}Args (rope/mod.rs:963-1047).
   const bool fp8 = plan->kv_dtype == LOOM_KV_DTYPE_FP8_E4M3;
+  if (fp8 && queue_ws)  // the reference-shaped args carry no scales
+    return fail(err, LOOM_ENQ_LENGTH_MISMATCH, "kv_scales", 2, 0);
   const loom_dtype_t kv_t = fp8 ? LOOM_DTYPE_U8 : LOOM_DTYPE_BF16;
   loom::OperandSpec ops[13] = {
       {"query", LOOM_DTYPE_BF16, false},        {"key", LOOM_DTYPE_BF16, false},
@@ -534,11 +543,6 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
       {"query_output", LOOM_DTYPE_BF16, true},  {"key_pages", kv_t, true},
       {"value_pages", kv_t, true},              {"workspace", LOOM_DTYPE_U8, true},
       {"kv_scales", LOOM_DTYPE_F32, false}};
-  loom_handle_t hs_all[13] = {args->query,        args->key,           args->value,
-                              args->batch_indices, args->positions,    args->page_indptr,
-                              args->page_indices, args->last_page_len, args->query_output,
-                              args->key_pages,    args->value_pages,   args->workspace,
-                              args->kv_scales};
   // The one-token form has no batch_indices/positions operands; only FP8
   // plans take kv_scales.
   loom::OperandSpec sel_ops[13];
@@ -547,6 +551,7 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   int n = 0;
   for (int i = 0; i < 13; ++i) {
     if (!ex && (i == 3 || i == 4)) continue;
+    if (queue_ws && i == 11) continue;
     if (!fp8 && i == 12) continue;
     sel_ops[n] = ops[i];
     sel[n] = hs_all[i];
@@ -571,6 +576,7 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
                         {10, kvn},        {11, pi.workspace_bytes}};
   for (const Want &w : wants) {
     if (!ex && (w.i == 3 || w.i == 4)) continue;
+    if (queue_ws && w.i == 11) continue;
     if (w.i == 7) {  // page_indices precedes last_page_len in the reference order
       if (L(6)->numel < B)
         return fail(err, LOOM_ENQ_PAGE_INDICES_TOO_SHORT, nullptr, B, L(6)->numel);
@@ -578,9 +584,21 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
     if (L(w.i)->numel != w.n)
       return fail(err, LOOM_ENQ_LENGTH_MISMATCH, ops[w.i].name, w.n, L(w.i)->numel);
   }
-  for (int i : {0, 1, 2, 8, 9, 10})
-    if (L(i)->ptr % 16 != 0)
-      return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, ops[i].name, (int64_t)L(i)->ptr, 16);
+  // The reference's append checks no alignment (rope/mod.rs:1062-1077): the
+  // kernels' 16-byte row accesses need none on gfx950 (global and buffer
+  // accesses run in unaligned mode).  The caller-owned validation workspace
+  // takes 32-bit atomics and must be 16-byte aligned.
+  uint32_t *ws = nullptr;
+  if (queue_ws) {
+    uint8_t *p = nullptr;
+    rc = loom::queue_workspace(scope->queue, pi.workspace_bytes, true, &p, err);
+    if (rc) return rc;
+    ws = (uint32_t *)p;
+  } else {
+    if (L(11)->ptr % 16 != 0)
+      return fail(err, LOOM_ENQ_MISALIGNED_BUFFER, "workspace", (int64_t)L(11)->ptr, 16);
+    ws = (uint32_t *)L(11)->ptr;
+  }
 
   AppendArgs a{};
   a.q = (const uint16_t *)L(0)->ptr;
@@ -594,7 +612,7 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
   a.q_out = (uint16_t *)L(8)->ptr;
   a.k_pages = (uint16_t *)L(9)->ptr;
   a.v_pages = (uint16_t *)L(10)->ptr;
-  a.ws = (uint32_t *)L(11)->ptr;
+  a.ws = ws;
   a.tokens = (int32_t)T;
   a.batch = (int32_t)B;
   a.hq = (int32_t)hq;
@@ -626,6 +644,53 @@ loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
     e = hipGetLastError();
   }
   return loom::record_launch(scope, e, err);
+}
+
+}  // namespace
+
+extern "C" {
+
+loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
+                                       loom_command_scope_t *scope,
+                                       const loom_rope_append_args_t *args, loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  const loom_handle_t hs[13] = {args->query,        args->key,           args->value,
+                                args->batch_indices, args->positions,    args->page_indptr,
+                                args->page_indices, args->last_page_len, args->query_output,
+                                args->key_pages,    args->value_pages,   args->workspace,
+                                args->kv_scales};
+  return rope_append_enqueue_impl(plan, scope, hs, false, err);
+}
+
+loom_status_t loom_rope_append_enqueue_bf16(const loom_rope_append_plan_t *plan,
+                                            loom_command_scope_t *scope,
+                                            const loom_bf16_rope_paged_kv_append_args_t *args,
+                                            loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  if (plan->info.explicit_tokens)  // the tokens plan takes the tokens args
+    return fail(err, LOOM_NULL_ARGUMENT, "args");
+  const loom_handle_t none{0, 0};
+  const loom_handle_t hs[13] = {args->query,        args->key,           args->value,
+                                none,               none,                args->page_indptr,
+                                args->page_indices, args->last_page_len, args->query_output,
+                                args->key_pages,    args->value_pages,   none,
+                                none};
+  return rope_append_enqueue_impl(plan, scope, hs, true, err);
+}
+
+loom_status_t loom_rope_append_tokens_enqueue_bf16(
+    const loom_rope_append_plan_t *plan, loom_command_scope_t *scope,
+    const loom_bf16_rope_paged_kv_append_tokens_args_t *args, loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  if (!plan->info.explicit_tokens)  // the one-token plan takes the one-token args
+    return fail(err, LOOM_NULL_ARGUMENT, "args");
+  const loom_handle_t none{0, 0};
+  const loom_handle_t hs[13] = {args->query,        args->key,           args->value,
+                                args->batch_indices, args->positions,    args->page_indptr,
+                                args->page_indices, args->last_page_len, args->query_output,
+                                args->key_pages,    args->value_pages,   none,
+                                none};
+  return rope_append_enqueue_impl(plan, scope, hs, true, err);
 }
 
 }  // extern "C"

@@ -7,6 +7,7 @@
 // commands; a failed submission poisons the scope and the queue; settling
 // in-flight work synchronizes the stream, then the device, and aborts when
 // neither proves quiescence.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 
@@ -96,6 +97,52 @@ loom_status_t record_launch(loom_command_scope *scope, hipError_t launch_status,
   return LOOM_OK;
 }
 
+namespace {
+__global__ void zero_words_kernel(uint32_t *p, uint64_t n) {
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+}  // namespace
+
+loom_status_t queue_workspace(loom_command_queue *q, uint64_t bytes, bool zeroed,
+                              uint8_t **out, loom_error_t *err) {
+  uint8_t *&buf = zeroed ? q->zeroed : q->scratch;
+  uint64_t &have = zeroed ? q->zeroed_bytes : q->scratch_bytes;
+  if (bytes <= have && buf) {
+    *out = buf;
+    return LOOM_OK;
+  }
+  // Grow to the next 1 MiB multiple.  hipMalloc is not a stream operation; a
+  // capturing thread switches to relaxed capture mode around it so the
+  // allocation is legal while a graph queue records its commands.
+  const uint64_t want = std::max<uint64_t>(((bytes + (1u << 20) - 1) >> 20) << 20, 1u << 20);
+  int prev = 0;
+  hipGetDevice(&prev);
+  hipSetDevice(q->device);
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  hipThreadExchangeStreamCaptureMode(&mode);
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, want);
+  hipThreadExchangeStreamCaptureMode(&mode);
+  hipSetDevice(prev);
+  if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "queue workspace", 0, 0, 0, 0, 0.0, e);
+  if (buf) q->retired.push_back(buf);
+  buf = (uint8_t *)p;
+  have = want;
+  if (zeroed) {
+    // Stream-ordered fill kernel (a captured graph replays it harmlessly: the
+    // words it clears are zero again after every command).
+    const uint64_t words = want / 4;
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)std::min<uint64_t>((words + 255) / 256, 1024)),
+                       dim3(256), 0, q->stream, (uint32_t *)p, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "queue workspace", 0, 0, 0, 0, 0.0, e);
+  }
+  *out = buf;
+  return LOOM_OK;
+}
+
 }  // namespace loom
 
 struct loom_command_completion {
@@ -170,9 +217,38 @@ void loom_command_queue_free(loom_command_queue_t *q) {
               "loom-infer-hip command queue synchronized after a stream error during drop: %s\n",
               hipGetErrorString(e));
   }
+  if (q->scratch || q->zeroed || !q->retired.empty()) {
+    // Commands that used the workspaces may still run (their completion was
+    // dropped unsettled only after it synchronized, but a caller may free the
+    // queue with work outstanding on a stream it shares with others).
+    loom::synchronize_stream_or_abort(q->stream);
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(q->device);
+    if (q->scratch) hipFree(q->scratch);
+    if (q->zeroed) hipFree(q->zeroed);
+    for (void *p : q->retired) hipFree(p);
+    hipSetDevice(prev);
+  }
   hipEventDestroy(q->completion_event);
   if (q->owns_stream) hipStreamDestroy(q->stream);
   delete q;
+}
+
+loom_status_t loom_command_queue_reserve_workspace(loom_command_queue_t *q,
+                                                   uint64_t scratch_bytes, uint64_t zeroed_bytes,
+                                                   loom_error_t *err) {
+  if (!q) return fail(err, LOOM_NULL_ARGUMENT, "queue");
+  if (q->active) return fail(err, LOOM_CMD_SCOPE_ACTIVE);
+  uint8_t *p = nullptr;
+  loom_status_t rc = LOOM_OK;
+  if (scratch_bytes) rc = loom::queue_workspace(q, scratch_bytes, false, &p, err);
+  if (!rc && zeroed_bytes) rc = loom::queue_workspace(q, zeroed_bytes, true, &p, err);
+  return rc ? rc : loom::ok(err);
+}
+
+uint64_t loom_command_queue_workspace_bytes(const loom_command_queue_t *q) {
+  return q ? q->scratch_bytes + q->zeroed_bytes : 0;
 }
 
 uint64_t loom_command_queue_max_commands(const loom_command_queue_t *q) {

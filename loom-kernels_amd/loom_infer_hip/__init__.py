@@ -549,6 +549,16 @@ class CommandQueue:
     def stream(self):
         return self._stream
 
+    def reserve_workspace(self, scratch_bytes: int = 0, zeroed_bytes: int = 0):
+        """Allocates the queue-owned workspaces that the reference-shaped
+        enqueues use, so those enqueues allocate nothing (no reference
+        counterpart: the reference's plans need no workspace)."""
+        _call(lib().loom_command_queue_reserve_workspace, self._p, scratch_bytes, zeroed_bytes)
+
+    @property
+    def workspace_bytes(self) -> int:
+        return lib().loom_command_queue_workspace_bytes(self._p)
+
     def bindings(self, capacity: int) -> CheckedBindings:
         out = C.c_void_p()
         _call(lib().loom_command_queue_bindings, self._p, capacity, C.byref(out))
@@ -576,7 +586,9 @@ class CommandQueue:
 # ---- paged decode ---------------------------------------------------------------
 @dataclass(frozen=True)
 class Bf16PagedBatchDecodeArgs:
-    """decode.rs:1452-1487 plus the split-KV state workspace."""
+    """decode.rs:1452-1487.  With the reference's eight operands the split-KV
+    states live in the command queue's workspace; a caller-owned `workspace`
+    (and, for FP8 pages, `kv_scales`) selects the extended form."""
     query: Read
     key_pages: Read
     value_pages: Read
@@ -585,10 +597,18 @@ class Bf16PagedBatchDecodeArgs:
     last_page_len: Read
     output: Write
     lse: Write
-    workspace: Write
+    workspace: Optional[Write] = None
     kv_scales: Optional[Read] = None  # FP8 pages: Read<f32> [k_scale, v_scale]
 
+    @property
+    def reference_shaped(self) -> bool:
+        return self.workspace is None and self.kv_scales is None
+
     def _c(self):
+        if self.reference_shaped:
+            return _ffi.Bf16PagedBatchDecodeArgs(*[_h(getattr(self, f)) for f in (
+                "query", "key_pages", "value_pages", "page_indptr", "page_indices",
+                "last_page_len", "output", "lse")])
         return _ffi.PagedDecodeArgs(*[_h(getattr(self, f)) for f in (
             "query", "key_pages", "value_pages", "page_indptr", "page_indices",
             "last_page_len", "output", "lse", "workspace", "kv_scales")])
@@ -618,7 +638,9 @@ class Bf16PagedBatchDecodePlan:
         return self.info.workspace_bytes
 
     def enqueue_into(self, scope: CommandScope, args: Bf16PagedBatchDecodeArgs):
-        _enqueue(_ffi.load().loom_paged_decode_enqueue, self._p, scope._p, args._ref)
+        fn = (_ffi.load().loom_paged_decode_enqueue_bf16 if args.reference_shaped
+              else _ffi.load().loom_paged_decode_enqueue)
+        _enqueue(fn, self._p, scope._p, args._ref)
 
     def __del__(self):
         try:
@@ -1112,7 +1134,9 @@ class PrefillProvider:
 # ---- fused RoPE + append --------------------------------------------------------
 @dataclass(frozen=True)
 class Bf16RopePagedKvAppendArgs:
-    """rope/mod.rs:963-1003 plus the validation workspace."""
+    """rope/mod.rs:963-1003.  Without a `workspace` (and `kv_scales`) this is
+    the reference's struct and the validation words live in the command
+    queue's workspace; a caller-owned `workspace` selects the extended form."""
     query: Read
     key: Read
     value: Read
@@ -1122,12 +1146,24 @@ class Bf16RopePagedKvAppendArgs:
     query_output: Write
     key_pages: Write
     value_pages: Write
-    workspace: Write
+    workspace: Optional[Write] = None
     batch_indices: Optional[Read] = None
     positions: Optional[Read] = None
     kv_scales: Optional[Read] = None  # FP8 pages: Read<f32> [k_scale, v_scale]
 
+    @property
+    def reference_shaped(self) -> bool:
+        return self.workspace is None and self.kv_scales is None
+
     def _c(self):
+        if self.reference_shaped and self.batch_indices is None:
+            return _ffi.Bf16RopePagedKvAppendArgs(*[_h(getattr(self, f)) for f in (
+                "query", "key", "value", "page_indptr", "page_indices", "last_page_len",
+                "query_output", "key_pages", "value_pages")])
+        if self.reference_shaped:
+            return _ffi.Bf16RopePagedKvAppendTokensArgs(*[_h(getattr(self, f)) for f in (
+                "query", "key", "value", "batch_indices", "positions", "page_indptr",
+                "page_indices", "last_page_len", "query_output", "key_pages", "value_pages")])
         return _ffi.RopeAppendArgs(*[_h(getattr(self, f)) for f in (
             "query", "key", "value", "batch_indices", "positions", "page_indptr",
             "page_indices", "last_page_len", "query_output", "key_pages", "value_pages",
@@ -1141,7 +1177,7 @@ class Bf16RopePagedKvAppendArgs:
 
 def Bf16RopePagedKvAppendTokensArgs(query, key, value, batch_indices, positions, page_indptr,
                                     page_indices, last_page_len, query_output, key_pages,
-                                    value_pages, workspace, kv_scales=None):
+                                    value_pages, workspace=None, kv_scales=None):
     """rope/mod.rs:1005-1047 (same operand order as the reference)."""
     return Bf16RopePagedKvAppendArgs(query, key, value, page_indptr, page_indices,
                                      last_page_len, query_output, key_pages, value_pages,
@@ -1163,7 +1199,13 @@ class Bf16RopePagedKvAppendPlan:
         return self.info.workspace_bytes
 
     def enqueue_into(self, scope: CommandScope, args: Bf16RopePagedKvAppendArgs):
-        _enqueue(_ffi.load().loom_rope_append_enqueue, self._p, scope._p, args._ref)
+        if not args.reference_shaped:
+            fn = _ffi.load().loom_rope_append_enqueue
+        elif args.batch_indices is None:
+            fn = _ffi.load().loom_rope_append_enqueue_bf16
+        else:
+            fn = _ffi.load().loom_rope_append_tokens_enqueue_bf16
+        _enqueue(fn, self._p, scope._p, args._ref)
 
     def __del__(self):
         try:

@@ -54,6 +54,11 @@ class PagedDecodeArgs(C.Structure):
                                       "workspace", "kv_scales")]
 
 
+class Bf16PagedBatchDecodeArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key_pages", "value_pages", "page_indptr",
+                                      "page_indices", "last_page_len", "output", "lse")]
+
+
 class SingleDecodeSpec(C.Structure):
     _fields_ = [("kv_len", u64), ("num_query_heads", u64), ("num_kv_heads", u64),
                 ("softmax_scale", f32)]
@@ -122,6 +127,18 @@ class RopeAppendArgs(C.Structure):
                                       "kv_scales")]
 
 
+class Bf16RopePagedKvAppendArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key", "value", "page_indptr", "page_indices",
+                                      "last_page_len", "query_output", "key_pages",
+                                      "value_pages")]
+
+
+class Bf16RopePagedKvAppendTokensArgs(C.Structure):
+    _fields_ = [(n, Handle) for n in ("query", "key", "value", "batch_indices", "positions",
+                                      "page_indptr", "page_indices", "last_page_len",
+                                      "query_output", "key_pages", "value_pages")]
+
+
 P = C.POINTER
 pi32 = P(i32)
 E = P(Error)
@@ -159,6 +176,8 @@ SIGNATURES = {
     "loom_command_queue_new": (i32, [vp, u64, P(vp), E]),
     "loom_command_queue_free": (None, [vp]),
     "loom_command_queue_max_commands": (u64, [vp]),
+    "loom_command_queue_reserve_workspace": (i32, [vp, u64, u64, E]),
+    "loom_command_queue_workspace_bytes": (u64, [vp]),
     "loom_command_queue_is_poisoned": (C.c_int, [vp]),
     "loom_command_queue_bindings": (i32, [vp, u64, P(vp), E]),
     "loom_bindings_free": (None, [vp]),
@@ -182,6 +201,7 @@ SIGNATURES = {
     "loom_paged_decode_plan_free": (None, [vp]),
     "loom_paged_decode_plan_get_info": (None, [vp, P(PagedDecodePlanInfo)]),
     "loom_paged_decode_enqueue": (i32, [vp, vp, P(PagedDecodeArgs), E]),
+    "loom_paged_decode_enqueue_bf16": (i32, [vp, vp, P(Bf16PagedBatchDecodeArgs), E]),
     "loom_single_decode_spec_new": (i32, [u64] * 4 + [P(SingleDecodeSpec), E]),
     "loom_single_decode_split_k_spec_new": (
         i32, [P(SingleDecodeSpec), u64, P(SingleDecodeSplitKSpec), E]),
@@ -228,6 +248,9 @@ SIGNATURES = {
     "loom_rope_append_plan_free": (None, [vp]),
     "loom_rope_append_plan_get_info": (None, [vp, P(RopeAppendPlanInfo)]),
     "loom_rope_append_enqueue": (i32, [vp, vp, P(RopeAppendArgs), E]),
+    "loom_rope_append_enqueue_bf16": (i32, [vp, vp, P(Bf16RopePagedKvAppendArgs), E]),
+    "loom_rope_append_tokens_enqueue_bf16": (
+        i32, [vp, vp, P(Bf16RopePagedKvAppendTokensArgs), E]),
     "loom_graph_queue_new": (i32, [C.c_int, u64, P(vp), E]),
     "loom_graph_queue_free": (None, [vp]),
     "loom_graph_queue_bindings": (i32, [vp, u64, P(vp), E]),

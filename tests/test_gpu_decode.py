@@ -329,7 +329,7 @@ def test_plan_selection_and_rejections(L):
 
 @pytest.mark.parametrize("teams", [0, 4], ids=["direct", "balanced"])
 def test_enqueue_rejections_submit_nothing(L, teams):
-    """Exact operand lengths, page_indices bounds and 16-byte alignment are
+    """Exact operand lengths, page_indices bounds and 4-byte alignment are
     checked before anything is submitted (decode.rs:1216-1251)."""
     torch = pytest.importorskip("torch")
     B, pool, hq, hkv = 2, 8, 8, 2

@@ -240,7 +240,7 @@ def test_capacity_plan_accepts_longer_page_indices(L, oracle):
 
 
 def test_enqueue_rejections(L, oracle):
-    # prefill.rs:2474-2505 and the 16-byte alignment of this kernel's rows
+    # prefill.rs:2474-2505 (4-byte alignment, prefill.rs:3015-3029)
     import torch
     (hq, hkv, pool, nnz), (q, k, v), (qo, ip, ix, last), _ = _guard_setup(oracle)
     r = PrefillRunner(L, 3, nnz, pool, hq, hkv)
@@ -257,7 +257,7 @@ def test_enqueue_rejections(L, oracle):
     assert e.value.variant == "LengthMismatch" and e.value.operand == "qo_indptr"
     big = nan_bf16(r.spec.output_numel + 8)
     with pytest.raises(L.EnqueueError) as e:
-        r.run_dev(dq, dk, dv, dqo, dip, dix, dlast, out=big[4:4 + r.spec.output_numel])
+        r.run_dev(dq, dk, dv, dqo, dip, dix, dlast, out=big[1:1 + r.spec.output_numel])
     assert e.value.variant == "MisalignedBuffer" and e.value.operand == "O"
     torch.cuda.synchronize()
 

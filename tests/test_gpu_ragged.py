@@ -176,7 +176,7 @@ def test_enqueue_rejections(L, oracle):
     assert e.value.variant == "LengthMismatch" and e.value.operand == "kv_indptr"
     big = nan_bf16(r.spec.output_numel + 8)
     with pytest.raises(L.EnqueueError) as e:
-        r.run_dev(dq, dk, dv, dqo, dkv, out=big[4:4 + r.spec.output_numel])
+        r.run_dev(dq, dk, dv, dqo, dkv, out=big[1:1 + r.spec.output_numel])
     assert e.value.variant == "MisalignedBuffer" and e.value.operand == "O"
 
 
