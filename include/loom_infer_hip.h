@@ -122,6 +122,7 @@ enum {
   LOOM_ENQ_PAGE_INDICES_TOO_SHORT = 91,
   LOOM_ENQ_MISALIGNED_BUFFER = 92,
   LOOM_ENQ_PAGE_INDICES_TOO_LONG = 93, /* more pages than the plan's workspace covers */
+  LOOM_ENQ_STATIC_SCRATCH_TOO_SMALL = 94, /* plan workspace beyond the static scratch */
 
   /* GraphError, crates/loom-infer-cuda/src/graph/mod.rs:688-721. */
   LOOM_GRAPH_DEFAULT_STREAM_UNSUPPORTED = 110,
@@ -487,6 +488,22 @@ loom_status_t loom_paged_decode_enqueue_bf16(const loom_paged_decode_plan_t *pla
                                              loom_command_scope_t *scope,
                                              const loom_bf16_paged_batch_decode_args_t *args,
                                              loom_error_t *err);
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory at all (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): the same command as loom_paged_decode_enqueue_bf16,
+ * with the split-KV workspace in a static device array of this library
+ * (LOOM_PAGED_DECODE_STATIC_SCRATCH_BYTES per device, held until the process
+ * ends; its address is looked up when a decode provider is loaded on the
+ * device).  Allocates nothing.  Plans whose workspace_bytes exceed the array
+ * are rejected with LOOM_ENQ_STATIC_SCRATCH_TOO_SMALL (BASELINE-sized plans
+ * need at most ~11 MiB).  Every call on a device shares its one array: calls
+ * whose commands overlap in time on one device (two streams, two queues)
+ * race; calls ordered on one stream do not. */
+#define LOOM_PAGED_DECODE_STATIC_SCRATCH_BYTES (32u << 20)
+loom_status_t loom_paged_decode_enqueue_bf16_no_alloc(
+    const loom_paged_decode_plan_t *plan, loom_command_scope_t *scope,
+    const loom_bf16_paged_batch_decode_args_t *args, loom_error_t *err);
 
 /* ------------------------------------------------------------------------ */
 /* Contiguous single decode, crates/loom-infer/src/attention/single_decode/    */

@@ -237,6 +237,12 @@ void format_message(loom_error_t *e) {
       snprintf(m, n, "page_indices has %lld entries but the plan's workspace covers %lld",
                (long long)f[1], (long long)f[0]);
       break;
+    case LOOM_ENQ_STATIC_SCRATCH_TOO_SMALL:
+      snprintf(m, n,
+               "the plan's %s needs %lld bytes but the static scratch of the allocation-free "
+               "enqueue holds %lld",
+               op, (long long)f[1], (long long)f[0]);
+      break;
     case LOOM_GRAPH_DEFAULT_STREAM_UNSUPPORTED:
       snprintf(m, n, "HIP graph capture requires a non-default stream");
       break;

@@ -34,8 +34,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <type_traits>
 #include <cmath>
+#include <mutex>
+#include <type_traits>
 
 #include "attn_device.hpp"
 #include "loom_internal.hpp"
@@ -1216,6 +1217,10 @@ void launch_split(const loom_paged_decode_plan_info_t &pi, dim3 g3, dim3 b3, hip
 }
 }  // namespace
 
+namespace {
+loom_status_t bind_static_scratch(int device, loom_error_t *err);
+}  // namespace
+
 extern "C" {
 
 loom_status_t loom_decode_provider_load(int device, loom_decode_provider_t **out,
@@ -1225,6 +1230,9 @@ loom_status_t loom_decode_provider_load(int device, loom_decode_provider_t **out
   loom_status_t rc = loom::query_device(device, &dev, err);
   if (rc) return rc;
   if (!dev.gfx950) return fail(err, LOOM_PLAN_UNSUPPORTED_DEVICE, nullptr, device);
+  // set-up of the allocation-free enqueue: this device's scratch address
+  rc = bind_static_scratch(device, err);
+  if (rc) return rc;
   auto *p = new loom_decode_provider;
   p->dev = dev;
   *out = p;
@@ -1340,7 +1348,43 @@ namespace {
 enum class DecodeWorkspace {
   kOperand,  // the `workspace` handle of loom_paged_decode_args_t
   kQueue,    // the command queue's own workspace (reference-shaped args)
+  kStatic,   // this library's per-device static scratch (no allocation)
 };
+
+// The per-device address of `scratch` below, looked up once per device when
+// a decode provider is loaded there (hipGetSymbolAddress with the device
+// current).  Host code uses these addresses, never the array's name.
+constexpr int kMaxDevices = 64;
+uint8_t *g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+}  // namespace
+
+// Static scratch of loom_paged_decode_enqueue_bf16_no_alloc: the split-KV
+// header and states of one command.  Every command on a device shares that
+// device's copy and keeps the last command's contents (the partial kernel
+// rewrites the header and every state it reads, so nothing needs clearing);
+// commands that overlap in time on one device race.
+static __device__ __align__(256) uint8_t scratch[LOOM_PAGED_DECODE_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+loom_status_t bind_static_scratch(int device, loom_error_t *err) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(err, LOOM_PLAN_UNSUPPORTED_DEVICE, "device", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return LOOM_OK;
+  int prev = 0;
+  hipGetDevice(&prev);
+  hipError_t e = hipSetDevice(device);
+  void *ptr = nullptr;
+  if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  hipSetDevice(prev);
+  if (e != hipSuccess || !ptr)
+    return fail(err, LOOM_CMD_DRIVER, "static scratch", 0, 0, 0, 0, 0.0, e);
+  g_scratch_ptr[device] = (uint8_t *)ptr;
+  return LOOM_OK;
+}
 
 // Bf16PagedBatchDecodePlan::enqueue_into, decode.rs:1199-1296.  `hs` holds
 // the ten handles of loom_paged_decode_args_t; with the queue's workspace the
@@ -1414,9 +1458,17 @@ loom_status_t paged_decode_enqueue_impl(const loom_paged_decode_plan_t *plan,
   uint8_t *ws = nullptr;
   if (where == DecodeWorkspace::kOperand) {
     ws = (uint8_t *)l(8)->ptr;
-  } else {
+  } else if (where == DecodeWorkspace::kQueue) {
     rc = loom::queue_workspace(scope->queue, pi.workspace_bytes, false, &ws, err);
     if (rc) return rc;
+  } else {
+    if (pi.workspace_bytes > LOOM_PAGED_DECODE_STATIC_SCRATCH_BYTES)
+      return fail(err, LOOM_ENQ_STATIC_SCRATCH_TOO_SMALL, "workspace",
+                  LOOM_PAGED_DECODE_STATIC_SCRATCH_BYTES, pi.workspace_bytes);
+    const int dev = scope->queue->device;
+    ws = (dev >= 0 && dev < kMaxDevices) ? g_scratch_ptr[dev] : nullptr;
+    if (!ws)  // no decode provider was loaded on this device
+      return fail(err, LOOM_PLAN_UNSUPPORTED_DEVICE, "static scratch", dev);
   }
   DecodeArgs a{};
   a.kv_scales = fp8 ? (const float *)l(9)->ptr : nullptr;
@@ -1508,6 +1560,15 @@ loom_status_t loom_paged_decode_enqueue_bf16(const loom_paged_decode_plan_t *pla
   loom_handle_t hs[10];
   ref_handles(args, hs);
   return paged_decode_enqueue_impl(plan, scope, hs, DecodeWorkspace::kQueue, err);
+}
+
+loom_status_t loom_paged_decode_enqueue_bf16_no_alloc(
+    const loom_paged_decode_plan_t *plan, loom_command_scope_t *scope,
+    const loom_bf16_paged_batch_decode_args_t *args, loom_error_t *err) {
+  if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  loom_handle_t hs[10];
+  ref_handles(args, hs);
+  return paged_decode_enqueue_impl(plan, scope, hs, DecodeWorkspace::kStatic, err);
 }
 
 

@@ -110,7 +110,7 @@ PLAN_VARIANTS = {70: "StateCountOutOfRange", 71: "StateCountOverflow",
                  72: "UnsupportedHeadDimension", 73: "UnsupportedRotaryDimension",
                  74: "UnsupportedDevice", 75: "InvalidOption"}
 ENQUEUE_VARIANTS = {90: "LengthMismatch", 91: "PageIndicesTooShort", 92: "MisalignedBuffer",
-                    93: "PageIndicesTooLong"}
+                    93: "PageIndicesTooLong", 94: "StaticScratchTooSmall"}
 GRAPH_VARIANTS = {110: "DefaultStreamUnsupported", 111: "EmptyCapture",
                   112: "CaptureInvalidated", 113: "NullExecutableHandle",
                   114: "ExecutionPoisoned", 115: "ReplayInFlight", 116: "LaunchCountExhausted",
@@ -641,6 +641,15 @@ class Bf16PagedBatchDecodePlan:
         fn = (_ffi.load().loom_paged_decode_enqueue_bf16 if args.reference_shaped
               else _ffi.load().loom_paged_decode_enqueue)
         _enqueue(fn, self._p, scope._p, args._ref)
+
+    def enqueue_into_no_alloc(self, scope: CommandScope, args: Bf16PagedBatchDecodeArgs):
+        """The same command with the split-KV workspace in the library's static
+        per-device scratch: allocates nothing (no reference counterpart).
+        Commands that overlap in time on one device race."""
+        if not args.reference_shaped:
+            raise TypeError("the allocation-free enqueue takes the reference's eight operands")
+        _enqueue(_ffi.load().loom_paged_decode_enqueue_bf16_no_alloc, self._p, scope._p,
+                 args._ref)
 
     def __del__(self):
         try:

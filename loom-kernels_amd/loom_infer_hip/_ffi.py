@@ -202,6 +202,7 @@ SIGNATURES = {
     "loom_paged_decode_plan_get_info": (None, [vp, P(PagedDecodePlanInfo)]),
     "loom_paged_decode_enqueue": (i32, [vp, vp, P(PagedDecodeArgs), E]),
     "loom_paged_decode_enqueue_bf16": (i32, [vp, vp, P(Bf16PagedBatchDecodeArgs), E]),
+    "loom_paged_decode_enqueue_bf16_no_alloc": (i32, [vp, vp, P(Bf16PagedBatchDecodeArgs), E]),
     "loom_single_decode_spec_new": (i32, [u64] * 4 + [P(SingleDecodeSpec), E]),
     "loom_single_decode_split_k_spec_new": (
         i32, [P(SingleDecodeSpec), u64, P(SingleDecodeSplitKSpec), E]),
