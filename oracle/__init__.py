@@ -16,7 +16,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libloom_oracle.so")
+# LOOM_ORACLE_LIB selects another build of the oracle (the sanitizer build of
+# tests/run_sanitized.sh); the default is the in-tree build.
+LIB_PATH = os.environ.get("LOOM_ORACLE_LIB") or os.path.join(_HERE, "libloom_oracle.so")
 
 HEAD_DIM = 128
 PAGE_SIZE = 16
