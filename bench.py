@@ -118,6 +118,79 @@ def _timed_enqueues(L, stream, n_bind, bind, enqueue, steps, warmup):
     return start.elapsed_time(end) * 1000.0 / steps  # µs per call
 
 
+def _sampled_enqueues(L, stream, n_bind, bind, enqueue, samples, per_sample, warmup):
+    """`samples` hipEvent intervals, each around `per_sample` back-to-back
+    enqueues on the launch stream, divided by `per_sample`: µs per call per
+    sample (the reference's raw samples_us, validation support/benchmark.rs:24)."""
+    import torch
+    q = L.CommandQueue(stream, samples * per_sample + warmup + 1)
+    b = q.bindings(n_bind)
+    args = bind(b)
+    with torch.cuda.stream(stream):
+        scope = q.begin(b)
+        for _ in range(warmup):
+            enqueue(scope, args)
+        b = scope.finish().wait()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(samples)]
+        scope = q.begin(b)
+        torch.cuda.synchronize()
+        for st, en in ev:
+            st.record(stream)
+            for _ in range(per_sample):
+                enqueue(scope, args)
+            en.record(stream)
+        b = scope.finish().wait()
+        torch.cuda.synchronize()
+    return [st.elapsed_time(en) * 1000.0 / per_sample for st, en in ev]
+
+
+def _pct(xs, q):
+    xs = sorted(xs)
+    i = min(len(xs) - 1, max(0, int(round(q * (len(xs) - 1)))))
+    return xs[i]
+
+
+def draw_lens(name, seed):
+    """Request lengths of a config for one stats seed (configs 3 and 5 draw
+    theirs from the stated distributions; 1 and 4 are fixed)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    if name.startswith("c3"):
+        return list(rng.integers(512, 8193, size=64))
+    if name.startswith("c5"):
+        return list(np.clip(np.round(np.exp(np.log(2048) + 0.8 * rng.standard_normal(256))), 16,
+                            16384).astype(int))
+    if name.startswith("c4"):
+        return [32768] * 8
+    return [1024]
+
+
+def seed_stats(L, stream, name, B, hq, hkv, pool, seeds, samples, per_sample, warmup):
+    """Per-call µs over seeds 0..n-1 (each seed its own lengths, page table and
+    inputs): median / p10 / p90 over every sample, and each seed's median."""
+    import torch
+    us_all, gbs_all, per_seed = [], [], []
+    for sd in seeds:
+        case = DecodeCase(L, name, B, hq, hkv, pool, draw_lens(name, sd), seed=sd)
+        xs = _sampled_enqueues(L, stream, 9, case.bind, case.plan.enqueue_into, samples,
+                               per_sample, warmup)
+        us_all += xs
+        gbs_all += [case.bytes / (x * 1e-6) / 1e9 for x in xs]
+        per_seed.append({"seed": sd, "median_us": round(_pct(xs, 0.5), 3),
+                         "mean_kv_len": round(float(case.lens.mean()), 1),
+                         "algorithmic_bytes": case.bytes})
+        del case
+        torch.cuda.empty_cache()
+    return {"samples": len(us_all), "calls_per_sample": per_sample,
+            "median_us": round(_pct(us_all, 0.5), 3), "p10_us": round(_pct(us_all, 0.1), 3),
+            "p90_us": round(_pct(us_all, 0.9), 3),
+            "median_GBps": round(_pct(gbs_all, 0.5), 1),
+            "p10_GBps": round(_pct(gbs_all, 0.1), 1), "p90_GBps": round(_pct(gbs_all, 0.9), 1),
+            "median_frac_hbm_peak": round(_pct(gbs_all, 0.5) / HBM_PEAK_GBS, 4),
+            "per_seed": per_seed}
+
+
 def _timed_rotating(L, stream, n_bind, binders, enqueue, steps, warmup):
     """Like _timed_enqueues, but call i uses input set i % len(binders): with
     the sets together larger than the 256 MB Infinity Cache, every call reads
@@ -610,6 +683,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the HND, FP8 and 64-row page timings of config 3 (profiling runs)")
+    ap.add_argument("--no-stats", action="store_true",
+                    help="skip the seeds 0..4 sample statistics of the decode configs")
     ap.add_argument("--only", default=None,
                     help="run one config (prefix match, e.g. c3) and print its detail")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -667,12 +742,13 @@ def main():
             fspec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, 128, 16, kv_dtype="fp8_e4m3")
             fplan = L.DecodeProvider.load(0).plan_bf16_paged_batch(
                 fspec, max_total_pages=int(case.indptr_h[-1]))
+            ws8 = torch.zeros(fplan.workspace_bytes, dtype=torch.uint8, device="cuda")
 
             def bind8(b):
                 h = [b.bind_read(case.q), b.bind_read(k8), b.bind_read(v8),
                      b.bind_read(case.indptr), b.bind_read(case.indices), b.bind_read(case.last),
                      b.bind_read_write(case.out), b.bind_read_write(case.lse),
-                     b.bind_read_write(case.ws), b.bind_read(sc)]
+                     b.bind_read_write(ws8), b.bind_read(sc)]
                 return L.Bf16PagedBatchDecodeArgs(h[0], h[1], h[2], h[3], h[4], h[5],
                                                   h[6].write(), h[7].write(), h[8].write(), h[9])
             f_us = _timed_enqueues(L, stream, 10, bind8, fplan.enqueue_into, a.steps, a.warmup)
@@ -681,7 +757,7 @@ def main():
             detail[name].update({"fp8_us_per_call": round(f_us, 3),
                                  "fp8_algorithmic_bytes": f_bytes,
                                  "fp8_GBps": round(f_bytes / (f_us * 1e-6) / 1e9, 1)})
-            del fplan, k8, v8
+            del fplan, k8, v8, ws8
             # and on 64-row pages (the same pool bytes as pool / 4 pages; the
             # same request lengths, so the same algorithmic bytes)
             import numpy as np
@@ -727,6 +803,9 @@ def main():
                                  "append_graph_replay_us": round(ap_g, 3),
                                  "full_step_graph_replay_us": round(step_g, 3)})
             del app
+        if not a.no_stats:
+            detail[name]["seed_stats"] = seed_stats(L, stream, name, B, hq, hkv, pool,
+                                                    range(5), 10, 10, a.warmup)
         log(f"[bench] {name}: {detail[name]}")
         if name.startswith("c3"):
             head = case

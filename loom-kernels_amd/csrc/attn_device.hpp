@@ -138,4 +138,42 @@ __device__ __forceinline__ int64_t wave_incl_scan64(int64_t x, int lane) {
   return x;
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Upper 16 bits of two floats packed into one register (lo <- a, hi <- b).
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ s16x4 as_s16x4(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(s16x4, u32x2{lo, hi});
+}
+
+// Max / sum over the four 16-lane rows of a wave (the lanes l, l^16, l^32,
+// l^48 share a query column): v_permlane16_swap / v_permlane32_swap, no LDS.
+__device__ __forceinline__ float quad_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Two 16-bit halves packed into bf16x8 operands: four registers, low halves
+// first.
+__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(bf16x8, u32x4{a, b, c, d});
+}
+
 }  // namespace loom_dev

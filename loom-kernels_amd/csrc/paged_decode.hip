@@ -58,24 +58,52 @@ constexpr int kStateStride = 132;
 #define LOOM_DECODE_DIRECT_MAX_PAGES 128
 #endif
 constexpr int kKRowBytes = 256 + 16;
+// K loaded straight into MFMA fragments (64 bytes of each of 16 rows per
+// load) instead of whole rows transposed through LDS.
+#ifndef LOOM_DECODE_K_DIRECT
+#define LOOM_DECODE_K_DIRECT 0
+#endif
+constexpr int kKTileBytes = LOOM_DECODE_K_DIRECT ? 16 : 16 * kKRowBytes;
 #ifndef LOOM_DECODE_DEPTH
 #define LOOM_DECODE_DEPTH 2
 #endif
 // Waves per SIMD the register allocation must allow (HIP's second launch
-// bound); more resident waves hide HBM latency better than deeper per-wave
-// prefetch on this kernel.
-#ifndef LOOM_DECODE_WAVES_TILE4
-#define LOOM_DECODE_WAVES_TILE4 3
+// bound) for the direct and single-decode kernels.  The page step's registers
+// do not depend on the tile width (both products accumulate in MFMA tiles of
+// 16 query columns).
+#ifndef LOOM_DECODE_WAVES
+#define LOOM_DECODE_WAVES 3
 #endif
-constexpr int waves_per_eu_for(int gt) {
-  return gt <= 2 ? 3 : gt == 4 ? LOOM_DECODE_WAVES_TILE4 : 2;
-}
+constexpr int waves_per_eu_for(int) { return LOOM_DECODE_WAVES; }
 template <int GT>
 constexpr int waves_per_eu() {
   return waves_per_eu_for(GT);
 }
 // Pages in flight per wave (register buffers of 32 VGPRs each).
 constexpr int kDepth = LOOM_DECODE_DEPTH;
+// The balanced split kernel streams fewer, deeper page streams: a register
+// budget of two waves per SIMD and three pages in flight per wave, with the
+// grid sized to about 13 waves per 4 CUs (planner).  Measured on MI355X over
+// configs 3-5 (80..384 teams of 8 waves, depths 2-6, 1-3 waves per SIMD):
+// 96-104 teams of 8 waves with three pages in flight beat the full-occupancy
+// grid (384 teams, two pages) by 7-10%, and grids whose workgroups do not
+// spread evenly over an XCD's 32 CUs (160, 192, 320 teams) lose 5-20%.
+#ifndef LOOM_DECODE_SPLIT_DEPTH
+#define LOOM_DECODE_SPLIT_DEPTH 3
+#endif
+#ifndef LOOM_DECODE_SPLIT_WAVES
+#define LOOM_DECODE_SPLIT_WAVES 2
+#endif
+#ifndef LOOM_DECODE_SPLIT_WAVES_PER_4CU
+#define LOOM_DECODE_SPLIT_WAVES_PER_4CU 13
+#endif
+// FP8 pages carry half the bytes per page step, so the page step's
+// instructions, not HBM, bound a wave: the grid fills the register budget
+// (2 waves per SIMD).  Measured on config 3: 256 teams 99 us, 104 teams 150 us.
+#ifndef LOOM_DECODE_SPLIT_WAVES_PER_4CU_FP8
+#define LOOM_DECODE_SPLIT_WAVES_PER_4CU_FP8 32
+#endif
+constexpr int kSplitDepth = LOOM_DECODE_SPLIT_DEPTH;
 // Normalizer written into a state whose pages failed the guard.
 constexpr float kPoisonNormalizer = -1.0f;
 
@@ -145,11 +173,9 @@ struct Smem {
   int32_t req_tl[kLdsPrefix];
   int64_t blk_excl[kMaxScanBlocks];   // exclusive page prefix of each scan block
   int64_t wave_tot[kWaves];
-  float p[kWaves][GT][16];
-  float alpha[kWaves][GT];
   // Per-wave K tile: 16 token rows of 256 bytes padded to kKRowBytes so the
   // MFMA fragment reads (16 rows, same column) hit 16 distinct bank groups.
-  uint8_t ktile[kWaves][16 * kKRowBytes];
+  uint8_t ktile[kWaves][kKTileBytes];
   u32x4 qfrag[kWaves][4][64];  // per wave: MFMA B fragments of its query tile
 };
 
@@ -174,7 +200,13 @@ __device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int6
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int off = (quad * 4 + j) * a.row_elems * 2 + col * 16;
+#if LOOM_DECODE_K_DIRECT
+    // K straight into the MFMA A-fragment layout: lane (col, quad) holds
+    // dims 32 j + 8 quad + [0, 8) of token row col.
+    r.k[j] = load16_rows<LOOM_DECODE_NT_K>(rk, col * a.row_elems * 2 + (32 * j + 8 * quad) * 2);
+#else
     r.k[j] = load16_rows<LOOM_DECODE_NT_K>(rk, off);
+#endif
     r.v[j] = load16_rows<LOOM_DECODE_NT_V>(rv, off);
   }
 }
@@ -219,7 +251,11 @@ __device__ __forceinline__ void load_rows(PageRegs8 &r, const DecodeArgs &a, int
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int off = (quad * 4 + j) * a.row_elems + col * 8;
+#if LOOM_DECODE_K_DIRECT
+    r.k[j] = load8_rows<LOOM_DECODE_NT_K>(rk, col * a.row_elems + 32 * j + 8 * quad);
+#else
     r.k[j] = load8_rows<LOOM_DECODE_NT_K>(rk, off);
+#endif
     r.v[j] = load8_rows<LOOM_DECODE_NT_V>(rv, off);
   }
 }
@@ -229,34 +265,16 @@ __device__ __forceinline__ void load_page(PageRegs8 &r, const DecodeArgs &a, int
   load_rows(r, a, block_elem(a, page, sub), valid_rows, lane, kvh);
 }
 
-// K row words (BF16 pairs) and V row values (FP32) of a page in either form;
-// FP8 V bytes widen straight to FP32 (v_cvt_pk_f32_fp8), skipping BF16.
+// K and V row words (BF16 pairs) of a page in either form; FP8 E4M3 bytes
+// widen to BF16 exactly.
 __device__ __forceinline__ u32x4 k_words(const PageRegs &r, int j) { return r.k[j]; }
 __device__ __forceinline__ u32x4 k_words(const PageRegs8 &r, int j) {
   return fp8x8_to_bf16x8(r.k[j]);
 }
-__device__ __forceinline__ void v_values(const PageRegs &r, int j, float (&vf)[8]) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t wv = r.v[j][e];
-    vf[2 * e] = bf16_lo(wv);
-    vf[2 * e + 1] = bf16_hi(wv);
-  }
+__device__ __forceinline__ u32x4 v_words(const PageRegs &r, int j) { return r.v[j]; }
+__device__ __forceinline__ u32x4 v_words(const PageRegs8 &r, int j) {
+  return fp8x8_to_bf16x8(r.v[j]);
 }
-__device__ __forceinline__ void v_values(const PageRegs8 &r, int j, float (&vf)[8]) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)r.v[j][h], false);
-    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)r.v[j][h], true);
-    vf[4 * h] = lo[0];
-    vf[4 * h + 1] = lo[1];
-    vf[4 * h + 2] = hi[0];
-    vf[4 * h + 3] = hi[1];
-  }
-}
-
-
 
 // 16-row blocks request r contributes to the virtual block list (0 if the
 // request fails the per-request guard of decode.rs:430-478, last_page_len in
@@ -292,24 +310,23 @@ __device__ __forceinline__ int64_t team_of(int64_t total, int64_t v, int teams) 
 
 // Per-wave decode of one (request, kv-head, tile of GT query heads): the
 // online-softmax state over the pages the wave streams, and the page step.
+// Both products run on MFMA; the accumulator acc[e][i] holds O[query column
+// col][dim 32 quad + 8 i + e] (unnormalized), so every lane owns 32 output
+// dims of one query column and its softmax state is the column's.
 template <int GT>
 struct WaveDecoder {
   const DecodeArgs &a;
   uint8_t *kt;          // this wave's K tile (16 rows of kKRowBytes)
   u32x4 (*qfrag)[64];   // [4][64] MFMA B fragments of the query tile
-  float (*pbuf)[16];    // [GT][16] probabilities of the current page
-  float *alpha;         // [GT] rescale factors of the current page
   int lane, col, quad, kvh;
   float m_run, l_run;
-  float acc[GT][8];
+  f32x4 acc[8];
 
   __device__ void reset() {
     m_run = -INFINITY;
     l_run = 0.0f;
 #pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+    for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   // Q fragment: column `col` is query head qh0 + col (zero beyond gcount);
@@ -326,32 +343,36 @@ struct WaveDecoder {
     wave_lds_fence();
   }
 
-  // One page: S = K·Qᵀ on MFMA, online softmax, P·V on the VALU.  `rows` is
-  // the number of valid token rows (16, the request's tail on its last page,
-  // 0 for a page index that failed the guard).
+  // One page: S = K·Qᵀ and Oᵀ += Vᵀ·Pᵀ on MFMA, online softmax in between.
+  // `rows` is the number of valid token rows (16, the request's tail on its
+  // last page, 0 for a page index that failed the guard).
   template <class Page>
   __device__ void process(const Page &pr, int rows) {
+    u32x4 kf[4];
+#if LOOM_DECODE_K_DIRECT
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kf[c] = k_words(pr, c);
+#else
     // K rows -> LDS tile -> MFMA A fragments (lane: token row `col`, dims
     // 32c + 8*quad + [0, 8)).
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       *reinterpret_cast<u32x4 *>(kt + (quad * 4 + j) * kKRowBytes + col * 16) = k_words(pr, j);
     wave_lds_fence();
-    u32x4 kf[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       kf[c] = *reinterpret_cast<const u32x4 *>(kt + col * kKRowBytes + (c * 4 + quad) * 16);
+#endif
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[c]), as_bf16x8(qfrag[c][lane]), s,
                                                   0, 0, 0);
+    // s[i] = S[token 4 quad + i][query column col]
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = (quad * 4 + i < rows) ? s[i] * a.scale_log2 : -INFINITY;
-    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mx = quad_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
     const float m_new = fmaxf(m_run, mx);
     const float al = fast_exp2(m_run - m_new);
     float p[4];
@@ -359,32 +380,38 @@ struct WaveDecoder {
     for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_new);
     l_run = l_run * al + ((p[0] + p[1]) + (p[2] + p[3]));
     m_run = m_new;
-    if (col < GT) {
-      *reinterpret_cast<f32x4 *>(&pbuf[col][quad * 4]) = f32x4{p[0], p[1], p[2], p[3]};
-      if (quad == 0) alpha[col] = al;
+    // Rescale only when some column's max moved (after a stream's first pages
+    // it rarely does); the branch is wave-uniform.
+    if (__builtin_amdgcn_ballot_w64(al != 1.0f))
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= al;
+    // Pᵀ as the B fragment of v_mfma_f32_16x16x32_bf16 (lane: query column
+    // col, k = 8 quad + [0, 8)): k = 8 quad + i is token 4 quad + i with its
+    // BF16 high part, k = 8 quad + 4 + i the same token's BF16 residual, so
+    // each weight keeps 16 significant bits.
+    uint32_t pb[4], rb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pb[i] = __float_as_uint(p[i]);
+      rb[i] = __float_as_uint(p[i] - __uint_as_float(pb[i] & 0xffff0000u));
     }
-    wave_lds_fence();
-    // P·V on lane (col = 8-column slice, quad = rows 4*quad..4*quad+3).  Columns
-    // of the tile beyond the group carry finite junk and are never stored.
-    f32x4 pp[GT];
+    const bf16x8 pt = as_bf16x8(pack_hi16(pb[0], pb[1]), pack_hi16(pb[2], pb[3]),
+                                pack_hi16(rb[0], rb[1]), pack_hi16(rb[2], rb[3]));
+    // Vᵀ block e as the A fragment: row col is dim 8 col + e, k = 8 quad +
+    // [0, 4) and 8 quad + 4 + [0, 4) both token 4 quad + [0, 4), straight from
+    // the V rows this lane loaded.  Rows past the valid ones were loaded as
+    // zeros and have zero weight.
+    u32x4 vw[4];
 #pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      const float ag = alpha[g];
-      pp[g] = *reinterpret_cast<const f32x4 *>(&pbuf[g][quad * 4]);
+    for (int j = 0; j < 4; ++j) vw[j] = v_words(pr, j);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
+    for (int e = 0; e < 8; ++e) {
+      const int w = e >> 1;
+      const uint32_t x01 = (e & 1) ? pack_hi16(vw[0][w], vw[1][w]) : pack_lo16(vw[0][w], vw[1][w]);
+      const uint32_t x23 = (e & 1) ? pack_hi16(vw[2][w], vw[3][w]) : pack_lo16(vw[2][w], vw[3][w]);
+      acc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(x01, x23, x01, x23), pt, acc[e],
+                                                       0, 0, 0);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // rows past the valid ones were loaded as zeros and have zero weight
-      float vf[8];
-      v_values(pr, j, vf);
-#pragma unroll
-      for (int g = 0; g < GT; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pp[g][j], vf[e], acc[g][e]);
-    }
-    wave_lds_fence();
   }
 
   // Streams 16-row blocks 0..n-1 (n >= 1) through a kDepth-deep pipeline:
@@ -411,24 +438,42 @@ struct WaveDecoder {
     }
   }
 
-  // Sums the 4 row quads: afterwards every lane of column c holds the
-  // accumulators of its 8-column slice, and lane g (quad 0) the max and the
-  // returned normalizer of query column g.
-  __device__ float reduce() {
-    float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
-#pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float x = acc[g][e];
-        x += __shfl_xor(x, 16, 64);
-        x += __shfl_xor(x, 32, 64);
-        acc[g][e] = x;
-      }
-    return l_tot;
-  }
+  // The column's normalizer (sum over the four row quads); acc and m_run
+  // need no reduction.
+  __device__ float reduce() const { return quad_sum(l_run); }
 };
+
+// Normalized output of one query column: the 32 dims acc[e][i] (dim
+// 32 quad + 8 i + e) divided by the normalizer, times V's scale on FP8 pages,
+// as BF16 at o[0..32).
+template <bool FP8>
+__device__ __forceinline__ void store_out_row(uint16_t *o, const f32x4 (&acc)[8], float l,
+                                              float v_scale) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x0 = acc[2 * e][i] / l, x1 = acc[2 * e + 1][i] / l;
+      if constexpr (FP8) {
+        x0 *= v_scale;
+        x1 *= v_scale;
+      }
+      w[e] = (uint32_t)f32_to_bf16(x0) | ((uint32_t)f32_to_bf16(x1) << 16);
+    }
+    *reinterpret_cast<u32x4 *>(o + i * 8) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// Copies a wave's column state to LDS row `dst` (dims 32 quad + [0, 32)).
+__device__ __forceinline__ void stash_acc(float *dst, const f32x4 (&acc)[8], int quad) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float *o = dst + quad * 32 + i * 8;
+    *reinterpret_cast<f32x4 *>(o) = f32x4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+    *reinterpret_cast<f32x4 *>(o + 4) = f32x4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+  }
+}
 
 // Teams in use for `total` virtual pages: at most the planned count, and at
 // least kMinTeamPages pages each (short batches are latency-bound: fewer, longer
@@ -442,7 +487,7 @@ __device__ __forceinline__ int active_teams(int64_t total, int teams) {
 }
 
 template <int GT, bool FP8 = false>
-__global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_split_kv_kernel(
+__global__ __launch_bounds__(kThreads, LOOM_DECODE_SPLIT_WAVES) void paged_decode_split_kv_kernel(
     DecodeArgs a) {
   __shared__ Smem<GT> sm;
   // FP8 pages: K's scale folds into the score scale, V's into the output.
@@ -591,11 +636,11 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     tl_out = uni(tl_out);
     return uni(c);
   };
-  WaveDecoder<GT> w{a, kt, sm.qfrag[wave], sm.p[wave], sm.alpha[wave], lane, col, quad, kvh};
+  WaveDecoder<GT> w{a, kt, sm.qfrag[wave], lane, col, quad, kvh};
   const int64_t qh_base = (int64_t)kvh * a.group + g_base;
 
   // ---- one continuous page stream over [v_begin, v_end) --------------------
-  // Two cursors walk the virtual list: the load cursor kDepth-1 pages ahead of
+  // Two cursors walk the virtual list: the load cursor kSplitDepth-1 pages ahead of
   // the process cursor.  Page indices come in blocks of 64 (one per lane, read
   // back with v_readlane), the next block fetched while the current one is
   // used, so the K/V pipeline does not drain at request or block boundaries;
@@ -688,65 +733,49 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
     const float l_tot = w.reduce();
     const float m_run = w.m_run;
     const auto &acc = w.acc;
+    // Lane (col, quad) holds dims 32 quad + [0, 32) of query head qh_base + col.
+    const bool mine = col < gcount;
     if (whole) {
       // The request lies inside this wave's range: final output in place.  An
       // invalid page index leaves the request's sentinels untouched.
-      if (!bad) {
-#pragma unroll
-        for (int g = 0; g < GT; ++g) {
-          if (g >= gcount) break;
-          const float Lg = __shfl(l_tot, g, 64);
-          if (quad == 0) {
-            uint32_t o[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float x0 = acc[g][2 * e] / Lg, x1 = acc[g][2 * e + 1] / Lg;
-              if constexpr (FP8) {
-                x0 *= v_scale;
-                x1 *= v_scale;
-              }
-              o[e] = (uint32_t)f32_to_bf16(x0) | ((uint32_t)f32_to_bf16(x1) << 16);
-            }
-            *reinterpret_cast<u32x4 *>(a.out + ((int64_t)rr * a.hq + qh_base + g) * 128 +
-                                       col * 8) = u32x4{o[0], o[1], o[2], o[3]};
-          }
-        }
-        if (lane < gcount) a.lse[(int64_t)rr * a.hq + qh_base + lane] = m_run + __log2f(l_tot);
+      if (!bad && mine) {
+        uint16_t *o = a.out + ((int64_t)rr * a.hq + qh_base + col) * 128 + quad * 32;
+        store_out_row<FP8>(o, acc, l_tot, v_scale);
+        if (quad == 0) a.lse[(int64_t)rr * a.hq + qh_base + col] = m_run + __log2f(l_tot);
       }
     } else {
       // Split request: one state per (team, request), slot team + r (unique:
       // along the virtual list either the team or the request advances).
-      float *st_base = a.states + ((int64_t)(team + rr) * a.hq + qh_base) * kStateStride;
-      if (bad) {
-        if (lane < gcount) {
-          st_base[lane * kStateStride] = 0.0f;
-          st_base[lane * kStateStride + 1] = kPoisonNormalizer;
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < GT; ++g) {
-          if (g >= gcount) break;
+      float *st = a.states + (((int64_t)(team + rr) * a.hq + qh_base + col) * kStateStride);
+      if (mine) {
+        if (bad) {
           if (quad == 0) {
-            float *o = st_base + g * kStateStride + 4 + col * 8;
-            *reinterpret_cast<f32x4 *>(o) = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-            *reinterpret_cast<f32x4 *>(o + 4) = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+            st[0] = 0.0f;
+            st[1] = kPoisonNormalizer;
           }
-        }
-        if (lane < gcount) {
-          st_base[lane * kStateStride] = m_run;
-          st_base[lane * kStateStride + 1] = l_tot;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float *o = st + 4 + quad * 32 + i * 8;
+            *reinterpret_cast<f32x4 *>(o) = f32x4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+            *reinterpret_cast<f32x4 *>(o + 4) = f32x4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+          }
+          if (quad == 0) {
+            st[0] = m_run;
+            st[1] = l_tot;
+          }
         }
       }
     }
   };
 
-  // Pipeline: page v+kDepth-1 is issued before page v is consumed; the
+  // Pipeline: page v+kSplitDepth-1 is issued before page v is consumed; the
   // unrolled buffer rotation lets the compiler wait for exactly the oldest
   // page's loads.
-  PageBuf<FP8> buf[kDepth];
-  int brows[kDepth];
+  PageBuf<FP8> buf[kSplitDepth];
+  int brows[kSplitDepth];
 #pragma unroll
-  for (int j = 0; j < kDepth - 1; ++j) {
+  for (int j = 0; j < kSplitDepth - 1; ++j) {
     int pg, blk;
     describe(lc, v_begin + j, pg, blk, brows[j]);
     load_page(buf[j], a, pg, blk, brows[j], lane, kvh);
@@ -758,11 +787,11 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void paged_decode_spl
   int i = 0;
   while (true) {
 #pragma unroll
-    for (int s = 0; s < kDepth; ++s) {
+    for (int s = 0; s < kSplitDepth; ++s) {
       {
-        const int nb = (s + kDepth - 1) % kDepth;
+        const int nb = (s + kSplitDepth - 1) % kSplitDepth;
         int pg, blk;
-        describe(lc, v + kDepth - 1, pg, blk, brows[nb]);
+        describe(lc, v + kSplitDepth - 1, pg, blk, brows[nb]);
         load_page(buf[nb], a, pg, blk, brows[nb], lane, kvh);
       }
       if (v >= pc.pre + pc.cnt) {
@@ -798,9 +827,7 @@ stream_done:
 // is launch- and latency-bound.
 template <int GT, int W = kWaves>
 struct DirectSmem {
-  float p[W][GT][16];
-  float alpha[W][GT];
-  uint8_t ktile[W][16 * kKRowBytes];
+  uint8_t ktile[W][kKTileBytes];
   u32x4 qfrag[W][4][64];
   float wm[W][GT];
   float wl[W][GT];
@@ -809,8 +836,16 @@ struct DirectSmem {
 
 // W waves per workgroup (4 for the tiniest tables; 8 when a request may hold
 // more pages, so each wave streams fewer of them).
+// Waves per SIMD the direct kernel's LDS allows (160 KiB per CU), at most the
+// register target.
+template <int GT, int W>
+constexpr int direct_waves_per_eu() {
+  const int per_cu = (int)((160 * 1024) / sizeof(DirectSmem<GT, W>)) * W / 4;
+  return per_cu < 1 ? 1 : per_cu < waves_per_eu<GT>() ? per_cu : waves_per_eu<GT>();
+}
+
 template <int GT, int W, bool FP8 = false>
-__global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direct_kernel(
+__global__ __launch_bounds__(W * 64, direct_waves_per_eu<GT, W>()) void paged_decode_direct_kernel(
     DecodeArgs a) {
   __shared__ DirectSmem<GT, W> sm;
   float v_scale = 1.0f;
@@ -835,8 +870,7 @@ __global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direc
 
   const int g_base = gt * GT;
   const int gcount = min(GT, a.group - g_base);
-  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
-                    lane, col, quad, kvh};
+  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], lane, col, quad, kvh};
   // this wave's 16-row blocks: request-local positions wave + W*i (block b
   // is block b % (page_rows / 16) of the request's page b / (page_rows / 16))
   const int mine = cnt > wave ? (cnt - wave + W - 1) / W : 0;
@@ -869,15 +903,12 @@ __global__ __launch_bounds__(W * 64, waves_per_eu<GT>()) void paged_decode_direc
     }
   }
   const float l_tot = w.reduce();
-  if (quad == 0) {
-    if (col < GT) {
+  if (col < GT) {
+    if (quad == 0) {
       sm.wm[wave][col] = w.m_run;
       sm.wl[wave][col] = l_tot;
     }
-#pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.wacc[wave][g][col * 8 + e] = w.acc[g][e];
+    stash_acc(sm.wacc[wave][col], w.acc, quad);
   }
   // An invalid page index anywhere in the request keeps its sentinels.
   if (__syncthreads_or(bad)) return;
@@ -982,8 +1013,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_ke
   const int gt = (int)(blockIdx.x / a.hkv);
   const int g_base = gt * GT;
   const int gcount = min(GT, a.group - g_base);
-  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
-                    lane, col, quad, kvh};
+  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], lane, col, quad, kvh};
   const int64_t nblk = (kv_len + 15) / 16;
   const int mine = nblk > wave ? (int)((nblk - wave + kWaves - 1) / kWaves) : 0;
   {
@@ -1003,15 +1033,12 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_ke
     w.stream(mine, tok_of, rows_of);
   }
   const float l_tot = w.reduce();
-  if (quad == 0) {
-    if (col < GT) {
+  if (col < GT) {
+    if (quad == 0) {
       sm.wm[wave][col] = w.m_run;
       sm.wl[wave][col] = l_tot;
     }
-#pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.wacc[wave][g][col * 8 + e] = w.acc[g][e];
+    stash_acc(sm.wacc[wave][col], w.acc, quad);
   }
   __syncthreads();
   const int64_t qh_base = (int64_t)kvh * a.group + g_base;
@@ -1053,8 +1080,7 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_sp
   const int64_t base = kv_len / partitions, rem = kv_len % partitions;
   const int64_t start = part * base + min<int64_t>(part, rem);
   const int64_t end = start + base + (part < rem ? 1 : 0);
-  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], sm.p[wave], sm.alpha[wave],
-                    lane, col, quad, kvh};
+  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], lane, col, quad, kvh};
   {
     u32x4 qr[4];
     w.load_q(0, kvh * a.group + g_base, gcount, qr);
@@ -1069,18 +1095,19 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_sp
   w.stream(nb, tok_of, rows_of);
   const float l_tot = w.reduce();
   const int64_t qh_base = (int64_t)kvh * a.group + g_base;
-  for (int g = 0; g < gcount; ++g) {
-    float *st = ws + ((qh_base + g) * partitions + part) * (int64_t)loom::kStateWidth;
-    if (quad == 0) {
+  if (col < gcount) {
+    // [Hq, P, 130] rows are 8-byte aligned: dims as float2 pairs
+    float *st = ws + ((qh_base + col) * partitions + part) * (int64_t)loom::kStateWidth;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int e = 0; e < 8; e += 2)
-        *reinterpret_cast<float2 *>(st + 2 + col * 8 + e) = float2{w.acc[g][e], w.acc[g][e + 1]};
+        *reinterpret_cast<float2 *>(st + 2 + quad * 32 + i * 8 + e) =
+            float2{w.acc[e][i], w.acc[e + 1][i]};
+    if (quad == 0) {
+      st[0] = w.m_run;
+      st[1] = l_tot;
     }
-  }
-  if (lane < gcount) {
-    float *st = ws + ((qh_base + lane) * partitions + part) * (int64_t)loom::kStateWidth;
-    st[0] = w.m_run;
-    st[1] = l_tot;
   }
 }
 
@@ -1251,7 +1278,7 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   const uint64_t B = spec->batch_size, hq = spec->num_query_heads, hkv = spec->num_kv_heads;
   const uint64_t group = hq / hkv;
   // Query heads per workgroup column block: the group rounded up to a power
-  // of two, at most 8 (P·V accumulators are GT x 8 floats per lane).
+  // of two, at most 8.
   const uint32_t gtile = group <= 1 ? 1u : group <= 2 ? 2u : group <= 4 ? 4u : 8u;
   const uint64_t gtiles = (group + gtile - 1) / gtile;
   if (opt.flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
@@ -1298,11 +1325,15 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
     return loom::ok(err);
   }
 
-  // Teams: one wave per SIMD slot the kernel's register budget allows, so
-  // the whole grid is resident at once and every wave streams the same number
-  // of pages.
+  // Teams: about 13 waves per 4 CUs (a fraction of the register budget's
+  // slots, so the whole grid is resident at once, each CU holds at most one
+  // workgroup of each XCD's share and every wave streams the same number of
+  // pages; see LOOM_DECODE_SPLIT_WAVES_PER_4CU).
   const uint64_t members = hkv * gtiles;
-  const uint64_t slots = (uint64_t)provider->dev.cus * 4 * waves_per_eu_for((int)gtile);
+  const uint64_t slots =
+      (uint64_t)provider->dev.cus *
+      (spec->kv_dtype == LOOM_KV_DTYPE_FP8_E4M3 ? LOOM_DECODE_SPLIT_WAVES_PER_4CU_FP8
+                                                : LOOM_DECODE_SPLIT_WAVES_PER_4CU) / 4;
   uint64_t teams = opt.teams ? opt.teams : std::max<uint64_t>(1, slots / members);
   // Each XCD (every 8th workgroup) holds ceil(teams / 8) whole teams.
   const uint64_t xcd_waves = (teams + 7) / 8 * members;

@@ -47,7 +47,6 @@ using namespace loom_dev;
 
 namespace {
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
   const uint16_t *__restrict__ q;
@@ -173,37 +172,6 @@ __device__ __forceinline__ PrefillPage expand(const PrefillPage8 &p) {
 
 template <bool FP8>
 using PrefillBuf = typename std::conditional<FP8, PrefillPage8, PrefillPage>::type;
-
-// Upper 16 bits of two floats packed into one register (lo <- a, hi <- b).
-__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
-__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ s16x4 as_s16x4(uint32_t lo, uint32_t hi) {
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(s16x4, u32x2{lo, hi});
-}
-
-// Max / sum over the four 16-lane rows of a wave (the lanes l, l^16, l^32,
-// l^48 share a query column): v_permlane16_swap / v_permlane32_swap, no LDS.
-__device__ __forceinline__ float quad_max(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float quad_sum(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 
 struct PrefillWave {
   const PrefillArgs &a;
