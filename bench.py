@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode launch on config 3 from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (partial + merge kernels), each scaled by the factor the same
 # counter reads for a plain copy of known size; profiles/ holds the runs.
-TRAFFIC_C3 = 1.1628e9
+TRAFFIC_C3 = 1.1494e9
 
 
 def log(*a):
