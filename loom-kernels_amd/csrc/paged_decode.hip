@@ -845,7 +845,7 @@ constexpr int direct_waves_per_eu() {
 }
 
 template <int GT, int W, bool FP8 = false>
-__global__ __launch_bounds__(W * 64, direct_waves_per_eu<GT, W>()) void paged_decode_direct_kernel(
+__global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_decode_direct_kernel(
     DecodeArgs a) {
   __shared__ DirectSmem<GT, W> sm;
   float v_scale = 1.0f;
