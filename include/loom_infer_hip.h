@@ -829,7 +829,9 @@ typedef struct loom_rope_append_plan_info {
   uint64_t num_query_heads;
   uint64_t num_kv_heads;
   int32_t explicit_tokens;  /* 0: one token per request at kv_len-1 */
-  uint64_t workspace_bytes; /* 64 validation words + T slot keys + T positions */
+  uint64_t workspace_bytes; /* 64 reserved words, T slot keys, T positions, T hash-set
+                               entry indices, the duplicate-slot hash set (a power of
+                               two >= 2T words) and the validation verdicts */
   uint32_t validate_blocks;
 } loom_rope_append_plan_info_t;
 
@@ -856,7 +858,8 @@ void loom_rope_append_plan_get_info(const loom_rope_append_plan_t *plan,
 
 /* Bf16RopePagedKvAppendArgs / ...TokensArgs, rope/mod.rs:963-1047, plus the
  * caller-owned validation workspace (u8, plan.workspace_bytes, zero-filled
- * once; every command leaves its counter words at zero for the next).  batch_indices/positions are unused
+ * once; every command leaves its duplicate-slot hash set empty, i.e. zero,
+ * for the next).  batch_indices/positions are unused
  * (pass {0,0}) for the one-token form. */
 typedef struct loom_rope_append_args {
   loom_handle_t query;         /* Read<bf16> [T, Hq, 128] */

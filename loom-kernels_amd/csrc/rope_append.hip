@@ -8,13 +8,14 @@
 //
 // MI355X design:
 //   * validation runs once per command, not once per workgroup: a small grid
-//     checks the whole page-index array and every token's (request, position,
-//     slot) in parallel, one token per thread, and records the slot keys; the
-//     last workgroup to arrive checks the request table, finds duplicate
-//     physical slots with an LDS hash set in O(T), and publishes one validity
-//     word;
-//   * the apply kernel runs one workgroup per token: it reads the recorded
-//     slot instead of walking the page table again, 64 lanes compute the
+//     checks the whole page-index array, the request table and every token's
+//     (request, position, slot) in parallel, one token per thread, records
+//     the slot keys, finds duplicate physical slots by inserting every key
+//     into a workspace hash set with agent-scope compare-and-swap (O(T) in
+//     all, no last-arriver pass), and writes one verdict per workgroup;
+//   * the apply kernel runs one workgroup per token: it reads the verdicts
+//     and the recorded slot instead of walking the page table again, clears
+//     the token's hash-set entry for the next command, 64 lanes compute the
 //     token's 64 (sin, cos) pairs once into LDS, then 16 lanes per 256-byte
 //     head row rotate Q/K and scatter K/V rows into the page slot with 16-byte
 //     loads and stores;
@@ -37,21 +38,54 @@ namespace {
 
 constexpr int kValidateThreads = 256;
 constexpr int kApplyThreads = 256;
-constexpr int kIndicesPerValidateBlock = 2048;  // 8 per thread
+// Page indices per validation workgroup: at least 2048 (8 per thread), and
+// enough that at most kMaxIndexBlocks workgroups check them.
+constexpr int kIndicesPerValidateBlock = 2048;
+constexpr int kMaxIndexBlocks = 64;
+// Batches whose request table the validation kernel keeps in LDS.
+constexpr int kValidateLdsBatch = 2048;
 constexpr int kMaxTokens = LOOM_APPEND_MAX_TOKENS_EXTENDED;
-// Workspace: 64 header words ([0] validity, [1] bad accumulator, [2] arrival
-// counter), then the T slot keys (u32) and the T positions (i32).
-constexpr int kWsHeaderWords = 64;
 // Commands this small run as one fused launch (every workgroup validates).
 constexpr int kFusedMaxTokens = 64;
 constexpr int64_t kFusedMaxIndices = 4096;
 constexpr uint32_t kEmptyKey = 0xffffffffu;
-// LDS hash set for duplicate slots: a power of two >= 2T.
-constexpr int kHashSlots = 2 * kMaxTokens;
+// Hash set for duplicate slots: a power of two >= 2T.
 __host__ __device__ constexpr int hash_slots(int tokens) {
   int n = 64;
   while (n < 2 * tokens) n <<= 1;
   return n;
+}
+// Validation workgroups a plan's workspace holds verdicts for.
+__host__ __device__ constexpr int64_t max_validate_blocks(int64_t tokens, int64_t batch) {
+  const int64_t t = (tokens + 255) / 256, b = (batch + 255) / 256;
+  const int64_t m = t > b ? t : b;
+  return m > kMaxIndexBlocks ? m : kMaxIndexBlocks;
+}
+// Workspace (u32 words) of the two-kernel path:
+//   [0, 64)                 reserved
+//   keys       [T]          physical slot (page * page_rows + row) per token
+//   positions  [T]
+//   hash_at    [T]          the hash-set entry each token's key occupies, or
+//                           kEmptyKey (the apply kernel clears that entry)
+//   table      [hash_slots(T)]  key + 1, 0 = empty: zero before the first
+//                           command and again after every command
+//   verdicts   [max_validate_blocks]  1 = that validation workgroup found the
+//                           command valid, 0 = not (rewritten by every command)
+constexpr int kWsHeaderWords = 64;
+struct WsLayout {
+  uint32_t *keys, *positions, *hash_at, *table, *verdicts;
+};
+__host__ __device__ inline int64_t ws_words(int64_t tokens, int64_t batch) {
+  return kWsHeaderWords + 3 * tokens + hash_slots((int)tokens) + max_validate_blocks(tokens, batch);
+}
+__device__ inline WsLayout ws_layout(uint32_t *ws, int tokens) {
+  WsLayout w;
+  w.keys = ws + kWsHeaderWords;
+  w.positions = w.keys + tokens;
+  w.hash_at = w.positions + tokens;
+  w.table = w.hash_at + tokens;
+  w.verdicts = w.table + hash_slots(tokens);
+  return w;
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -68,7 +102,9 @@ struct AppendArgs {
   uint16_t *q_out;
   uint16_t *k_pages;
   uint16_t *v_pages;
-  uint32_t *ws;  // header words, then slot keys and positions
+  uint32_t *ws;  // see WsLayout
+  int32_t index_chunk;      // page indices per validation workgroup
+  int32_t validate_blocks;  // validation workgroups of this command
   int32_t tokens;
   int32_t batch;
   int32_t hq;
@@ -111,14 +147,19 @@ __device__ __forceinline__ bool table_bounds_bad(const AppendArgs &a, int32_t ip
          (a.indices_capacity ? (int64_t)ipB > a.n_indices : (int64_t)ipB != a.n_indices);
 }
 
+// `ip` / `ln`: the request table (page_indptr, last_page_len), in global
+// memory or an LDS copy.
 __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t pages, int *req,
-                                           int *pos, int64_t *page, int *off) {
+                                           int *pos, int64_t *page, int *off,
+                                           const int32_t *ip, const int32_t *ln) {
+  // both words in one round trip
   const int r = a.batch_indices ? a.batch_indices[t] : t;
+  const int p_given = a.batch_indices ? a.positions[t] : 0;
   if (r < 0 || r >= a.batch) return false;
-  const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
+  const int32_t st = ip[r], en = ip[r + 1], tl = ln[r];
   if (st < 0 || en <= st || (int64_t)en > pages || tl < 1 || tl > a.page_rows) return false;
   const int kv_len = (en - st - 1) * a.page_rows + tl;
-  const int p = a.batch_indices ? a.positions[t] : kv_len - 1;
+  const int p = a.batch_indices ? p_given : kv_len - 1;
   if (p < 0 || p >= kv_len) return false;
   const int32_t pg = a.indices[st + p / a.page_rows];
   if (pg < 0 || (int64_t)pg >= a.pool) return false;
@@ -130,116 +171,119 @@ __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t p
 }
 
 // Validation, all-or-nothing.  Workgroup b checks page indices
-// [b*8192, (b+1)*8192) (rope/mod.rs:143-150) and tokens [b*256, (b+1)*256)
-// (paged_append/mod.rs:262-309), one token per thread, and records each
-// token's physical slot key and position in the workspace for the apply
-// kernel.  The last workgroup to arrive checks the request table
-// (paged_decode/mod.rs:164-205), finds duplicate physical slots with an LDS
-// hash set over all T keys, and publishes one validity word.
+// [b*chunk, (b+1)*chunk) (rope/mod.rs:143-150), requests [b*256, (b+1)*256)
+// (paged_decode/mod.rs:164-205) and tokens [b*256, (b+1)*256)
+// (paged_append/mod.rs:262-309), one token per thread; records each token's
+// physical slot key and position for the apply kernel; inserts every valid
+// key into a workspace hash set (agent-scope compare-and-swap, so two tokens
+// with one slot meet whichever XCDs they run on; the second finds the first);
+// and writes its verdict.  The apply kernel reads every verdict.
 __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(AppendArgs a) {
-  __shared__ uint32_t table[kHashSlots];
-  __shared__ int s_last;
+  __shared__ int32_t s_ip[kValidateLdsBatch + 1], s_last[kValidateLdsBatch];
   const int tid = threadIdx.x;
-  uint32_t *flag = a.ws, *bad_acc = a.ws + 1, *arrivals = a.ws + 2;
-  uint32_t *keys = a.ws + kWsHeaderWords;
-  int32_t *positions = reinterpret_cast<int32_t *>(keys + a.tokens);
+  const WsLayout w = ws_layout(a.ws, a.tokens);
+  // The request table in LDS (batches up to kValidateLdsBatch), loaded with
+  // the page indices below, so a token's slot is one more round trip.
+  const bool lds_table = a.batch <= kValidateLdsBatch;
+  if (lds_table) {
+    for (int r = tid; r <= a.batch; r += kValidateThreads) {
+      s_ip[r] = a.indptr[r];
+      if (r < a.batch) s_last[r] = a.last[r];
+    }
+  }
+  const int32_t *ip = lds_table ? s_ip : a.indptr;
+  const int32_t *ln = lds_table ? s_last : a.last;
 
   int bad = 0;
   // this workgroup's page indices: all loads issued before any is tested
-  const int32_t ipB = a.indptr[a.batch];
-  const int64_t lo = (int64_t)blockIdx.x * kIndicesPerValidateBlock;
+  const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
+  const int64_t lo = (int64_t)blockIdx.x * a.index_chunk;
+  const int64_t hi = min<int64_t>(lo + a.index_chunk, a.n_indices);
   int32_t pgs[kIndicesPerValidateBlock / kValidateThreads];
-#pragma unroll
-  for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j) {
-    const int64_t i = lo + j * kValidateThreads + tid;
-    pgs[j] = i < a.n_indices ? a.indices[i] : 0;
-  }
   const int64_t pages = table_pages(a, ipB);
+  for (int64_t base = lo; base < hi; base += kIndicesPerValidateBlock) {
 #pragma unroll
-  for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j)
-    bad |= (lo + j * kValidateThreads + tid < pages &&
-            (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool)) ? 1 : 0;
-  const int t = blockIdx.x * kValidateThreads + tid;
-  if (t < a.tokens) {
-    int r, p, off;
-    int64_t pg;
-    uint32_t key = kEmptyKey;
-    if (token_slot(a, t, pages, &r, &p, &pg, &off))
-      key = (uint32_t)(pg * a.page_rows + off);
-    else
-      bad = 1;
-    keys[t] = key;
-    positions[t] = p;
+    for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j) {
+      const int64_t i = base + j * kValidateThreads + tid;
+      pgs[j] = i < hi ? a.indices[i] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j)
+      bad |= (base + j * kValidateThreads + tid < min<int64_t>(hi, pages) &&
+              (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool)) ? 1 : 0;
   }
-  bad = __syncthreads_or(bad);
-  if (tid == 0) {
-    if (bad) atomicOr(bad_acc, 1u);
-    __threadfence();  // keys and positions visible before the arrival
-    const uint32_t old = atomicAdd(arrivals, 1u);
-    s_last = (old + 1 == gridDim.x) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // Last workgroup: the request table, then duplicate slots.
-  bad = 0;
-  if (tid == 0) bad |= table_bounds_bad(a, a.indptr[0], a.indptr[a.batch]) ? 1 : 0;
-  for (int r = tid; r < a.batch; r += kValidateThreads) {
+  const int r = blockIdx.x * kValidateThreads + tid;
+  if (r < a.batch) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
     bad |= (en <= st || tl < 1 || tl > a.page_rows) ? 1 : 0;
   }
-  const int slots = hash_slots(a.tokens);
-  for (int i = tid; i < slots; i += kValidateThreads) table[i] = kEmptyKey;
-  bad = __syncthreads_or(bad);
-  if (!bad && atomicAdd(bad_acc, 0u) == 0u) {
-    // Open addressing at load <= 1/2: every probe sequence ends at an empty
-    // slot or at the same key (a duplicate).
-    int dup = 0;
-    const uint32_t mask = (uint32_t)slots - 1u;
-    for (int i = tid; i < a.tokens; i += kValidateThreads) {
-      const uint32_t key = __atomic_load_n(&keys[i], __ATOMIC_RELAXED);
+  if (blockIdx.x == 0 && tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
+  const int t = blockIdx.x * kValidateThreads + tid;
+  __syncthreads();  // the LDS request table
+  if (t < a.tokens) {
+    int rr = 0, p = 0, off = 0;
+    int64_t pg = 0;
+    uint32_t key = kEmptyKey, at = kEmptyKey;
+    if (token_slot(a, t, pages, &rr, &p, &pg, &off, ip, ln)) {
+      key = (uint32_t)(pg * a.page_rows + off);
+      // Open addressing at load <= 1/2: every probe sequence ends at an
+      // empty entry or at the same key (a duplicate slot).
+      const uint32_t mask = (uint32_t)hash_slots(a.tokens) - 1u;
       uint32_t h = (key * 0x9E3779B1u) >> 16 & mask;
       while (true) {
-        const uint32_t prev = atomicCAS(&table[h], kEmptyKey, key);
-        if (prev == kEmptyKey) break;
-        if (prev == key) {
-          dup = 1;
+        uint32_t expected = 0u;
+        if (__hip_atomic_compare_exchange_strong(&w.table[h], &expected, key + 1u,
+                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) {
+          at = h;
+          break;
+        }
+        if (expected == key + 1u) {
+          bad = 1;  // another token already holds this slot
           break;
         }
         h = (h + 1u) & mask;
       }
+    } else {
+      bad = 1;
     }
-    bad = __syncthreads_or(dup);
-  } else {
-    bad = 1;
+    w.keys[t] = key;
+    w.positions[t] = (uint32_t)p;
+    w.hash_at[t] = at;
   }
-  if (tid == 0) {
-    *flag = bad ? 0u : 1u;
-    atomicExch(bad_acc, 0u);
-    atomicExch(arrivals, 0u);
-  }
+  bad = __syncthreads_or(bad);
+  if (tid == 0) w.verdicts[blockIdx.x] = bad ? 0u : 1u;
 }
 
-// The first row slice of thread `tid` for token t (Q rows, then K rows with
-// their V row), loaded before the command's validity is known so the loads
-// overlap the metadata round trips.
+// The row slices of thread `tid` for token t (Q rows, then K rows with their
+// V row; rows tid / 16 + 16 i), loaded before the command's validity is known
+// so the loads overlap the metadata round trips and one another.
+constexpr int kPreloadRows = 4;  // row iterations preloaded: Hq + Hkv <= 64
 struct RowSlice {
-  u32x4 x, xp, v;
+  u32x4 x, v;
+};
+struct RowSlices {
+  RowSlice r[kPreloadRows];
 };
 
-__device__ __forceinline__ RowSlice load_first_slice(const AppendArgs &a, int t, int tid) {
-  RowSlice f = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-  const int c = tid & 15, row = tid >> 4;
+__device__ __forceinline__ RowSlice load_slice(const AppendArgs &a, int t, int row, int c) {
+  RowSlice f = {{0, 0, 0, 0}, {0, 0, 0, 0}};
   if (row < a.hq + a.hkv) {
     const bool is_kv = row >= a.hq;
     const uint16_t *src = is_kv ? a.k + ((int64_t)t * a.hkv + row - a.hq) * 128
                                 : a.q + ((int64_t)t * a.hq + row) * 128;
     f.x = *reinterpret_cast<const u32x4 *>(src + c * 8);
-    f.xp = *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
     if (is_kv)
       f.v = *reinterpret_cast<const u32x4 *>(a.v + ((int64_t)t * a.hkv + row - a.hq) * 128 + c * 8);
   }
+  return f;
+}
+
+__device__ __forceinline__ RowSlices load_first_slices(const AppendArgs &a, int t, int tid) {
+  RowSlices f;
+#pragma unroll
+  for (int i = 0; i < kPreloadRows; ++i)
+    f.r[i] = load_slice(a, t, (tid >> 4) + i * (kApplyThreads / 16), tid & 15);
   return f;
 }
 
@@ -260,25 +304,26 @@ __device__ __forceinline__ void token_sincos(const AppendArgs &a, int pos, int t
   }
 }
 
-// Rotates Q/K rows of token t (NeoX split-half) and scatters K/V into slot
-// (page, off): 16 lanes per 256-byte head row, 16-byte loads and stores.
-__device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t page, int off,
-                                            int tid, const float *s_sin, const float *s_cos,
-                                            const RowSlice &first_slice) {
-  const int c = tid & 15;
-  const int rows = a.hq + a.hkv;
-  int row = tid >> 4;
-  for (bool first = true; row < rows; row += kApplyThreads / 16, first = false) {
+// Rotates one Q/K row slice of token t (NeoX split-half) and, for K rows,
+// scatters K and V into slot (page, off): 16 lanes per 256-byte head row,
+// 16-byte loads and stores.
+template <bool FP8>
+__device__ __forceinline__ void apply_row(const AppendArgs &a, int t, int64_t page, int off,
+                                          int row, int c, const float *s_sin, const float *s_cos,
+                                          const RowSlice &sl) {
+  {
     const bool is_kv = row >= a.hq;
     const int kh = row - a.hq;
-    const uint16_t *src = is_kv ? a.k + ((int64_t)t * a.hkv + kh) * 128
-                                : a.q + ((int64_t)t * a.hq + row) * 128;
     const int64_t kv_dst =
         page * a.page_rows * a.hkv * 128 + (int64_t)kh * a.head_elems + (int64_t)off * a.row_elems;
     uint16_t *dst = is_kv ? a.k_pages + kv_dst : a.q_out + ((int64_t)t * a.hq + row) * 128;
-    const u32x4 x = first ? first_slice.x : *reinterpret_cast<const u32x4 *>(src + c * 8);
-    const u32x4 xp = first ? first_slice.xp : *reinterpret_cast<const u32x4 *>(src + (c ^ 8) * 8);
-    const bool fp8 = is_kv && a.kv_scales != nullptr;
+    // the other half of the NeoX pair: lane c ^ 8 of the same 16-lane row
+    const u32x4 x = sl.x;
+    u32x4 xp;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xp[e] = (uint32_t)__shfl_xor((int)x[e], 8, 16);
+
+    const bool fp8 = FP8 && is_kv;
     float y[8];
     {
 #pragma clang fp contract(off)
@@ -296,10 +341,7 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
         }
       }
     }
-    const u32x4 vv = !is_kv ? u32x4{0, 0, 0, 0}
-                     : first ? first_slice.v
-                             : *reinterpret_cast<const u32x4 *>(
-                                   a.v + ((int64_t)t * a.hkv + kh) * 128 + c * 8);
+    const u32x4 vv = sl.v;
     if (fp8) {
       // FP8 pages: the FP32 rotated K and the V row, divided by their scales
       // (correctly rounded) and encoded; 8 bytes per lane.
@@ -315,7 +357,7 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
       uint8_t *vp = reinterpret_cast<uint8_t *>(a.v_pages) + kv_dst + c * 8;
       *reinterpret_cast<loom_dev::u32x2 *>(kp) = k8;
       *reinterpret_cast<loom_dev::u32x2 *>(vp) = v8;
-      continue;
+      return;
     }
     u32x4 o;
 #pragma unroll
@@ -326,40 +368,68 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
   }
 }
 
-// Apply: one workgroup per token.  The validity word, the token's slot and
-// position and the first rows of Q/K/V are fetched in one round trip; 64
-// lanes compute the token's (sin, cos) pairs into LDS; then the rows.
+// Rotates the Q/K rows of token t and scatters its K/V rows into slot
+// (page, off).
+template <bool FP8>
+__device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t page, int off,
+                                            int tid, const float *s_sin, const float *s_cos,
+                                            const RowSlices &pre) {
+  const int c = tid & 15;
+  const int rows = a.hq + a.hkv;
+  int row = tid >> 4;
+#pragma unroll
+  for (int it = 0; it < kPreloadRows + 1; ++it) {
+    // rows beyond the preloaded iterations (Hq + Hkv > 64) load in a loop
+    if (it == kPreloadRows) {
+      for (; row < rows; row += kApplyThreads / 16) {
+        const RowSlice one = load_slice(a, t, row, c);
+        apply_row<FP8>(a, t, page, off, row, c, s_sin, s_cos, one);
+      }
+      break;
+    }
+    if (row >= rows) break;
+    apply_row<FP8>(a, t, page, off, row, c, s_sin, s_cos, pre.r[it]);
+    row += kApplyThreads / 16;
+  }
+}
+
+// Apply: one workgroup per token.  Every validation verdict, the token's
+// slot, position and hash-set entry, and the thread's Q/K/V row slices are
+// fetched in one round trip; 64 lanes compute the token's (sin, cos) pairs
+// into LDS; then, if every verdict is valid, the rows.  The token's hash-set
+// entry is cleared either way, so the set is empty for the next command.
+template <bool FP8>
 __global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs a) {
   __shared__ float s_cos[64], s_sin[64];
-  __shared__ int s_ok;
   const int tid = threadIdx.x;
   const int t = blockIdx.x;
-  const uint32_t *keys = a.ws + kWsHeaderWords;
-  const int32_t *positions = reinterpret_cast<const int32_t *>(keys + a.tokens);
-  const uint32_t ok = __atomic_load_n(a.ws, __ATOMIC_RELAXED);
-  const uint32_t key = keys[t];
-  const int pos = positions[t];
-  const RowSlice first = load_first_slice(a, t, tid);
-  if (tid == 0) s_ok = ok == 1u;
+  const WsLayout w = ws_layout(a.ws, a.tokens);
+  int bad = 0;
+  for (int b = tid; b < a.validate_blocks; b += kApplyThreads) bad |= w.verdicts[b] != 1u;
+  const uint32_t key = w.keys[t];
+  const int pos = (int)w.positions[t];
+  const uint32_t at = w.hash_at[t];
+  const RowSlices first = load_first_slices(a, t, tid);
   token_sincos(a, pos, tid, s_sin, s_cos);
-  __syncthreads();
-  if (!s_ok) return;
+  if (tid == 0 && at != kEmptyKey) w.table[at] = 0u;
+  if (__syncthreads_or(bad)) return;
   // key = page * page_rows + row
-  apply_token(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid, s_sin,
-              s_cos, first);
+  apply_token<FP8>(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid,
+                   s_sin, s_cos, first);
 }
 
 // Small commands (T <= 64 tokens, <= 4096 page indices): one launch.  Every
 // workgroup (one per token) validates the whole command itself, as the
 // reference's kernels do, and applies its own token only if all of it is
 // valid, so the all-or-nothing guard needs no second kernel.
+template <bool FP8>
 __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(AppendArgs a) {
   __shared__ float s_cos[64], s_sin[64];
   __shared__ uint32_t s_keys[kFusedMaxTokens];
   __shared__ int s_pos[kFusedMaxTokens];
   const int tid = threadIdx.x;
   const int t = blockIdx.x;
-  const RowSlice first = load_first_slice(a, t, tid);
+  const RowSlices first = load_first_slices(a, t, tid);
 
   int bad = 0;
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
@@ -381,7 +451,7 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
     int r, p, off;
     int64_t pg;
     uint32_t key = 0xffffffffu;
-    if (token_slot(a, tid, pages, &r, &p, &pg, &off))
+    if (token_slot(a, tid, pages, &r, &p, &pg, &off, a.indptr, a.last))
       key = (uint32_t)(pg * a.page_rows + off);
     else
       bad = 1;
@@ -401,7 +471,7 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
   if (__syncthreads_or(dup)) return;
   const uint32_t key = s_keys[t];
   // key = page * page_rows + row
-  apply_token(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid, s_sin,
+  apply_token<FP8>(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid, s_sin,
               s_cos, first);
 }
 
@@ -464,7 +534,7 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
   p->info.num_query_heads = s.num_query_heads;
   p->info.num_kv_heads = s.num_kv_heads;
   p->info.explicit_tokens = explicit_tokens ? 1 : 0;
-  p->info.workspace_bytes = (kWsHeaderWords + 2 * tokens) * 4;
+  p->info.workspace_bytes = ws_words((int64_t)tokens, (int64_t)s.batch_size) * 4;
   p->info.validate_blocks = 0;  // depends on the bound page_indices length
   p->max_num_pages = s.max_num_pages;
   p->flags = flags;
@@ -626,12 +696,22 @@ loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
   a.row_elems = plan->kv_layout == LOOM_KV_LAYOUT_HND ? 128 : (int32_t)hkv * 128;
   for (int i = 0; i < 64; ++i) a.inv_freq[i] = plan->inv_freq[i];
 
+  // page-index chunks: 2048 per workgroup, or more so that at most
+  // kMaxIndexBlocks workgroups check them (a multiple of 2048)
+  const uint64_t n_idx = L(6)->numel;
+  const uint64_t per_block = (n_idx + kMaxIndexBlocks - 1) / kMaxIndexBlocks;
+  const uint64_t chunk = std::max<uint64_t>(
+      kIndicesPerValidateBlock,
+      (per_block + kIndicesPerValidateBlock - 1) / kIndicesPerValidateBlock * kIndicesPerValidateBlock);
   const uint64_t vblocks = std::max<uint64_t>(
-      std::max<uint64_t>(1, (L(6)->numel + kIndicesPerValidateBlock - 1) / kIndicesPerValidateBlock),
-      (T + kValidateThreads - 1) / kValidateThreads);
+      {1, (n_idx + chunk - 1) / chunk, (T + kValidateThreads - 1) / kValidateThreads,
+       (B + kValidateThreads - 1) / kValidateThreads});
+  a.index_chunk = (int32_t)chunk;
+  a.validate_blocks = (int32_t)vblocks;
   hipStream_t stream = scope->queue->stream;
   if (T <= (uint64_t)kFusedMaxTokens && (int64_t)L(6)->numel <= kFusedMaxIndices) {
-    hipLaunchKernelGGL(append_fused_small_kernel, dim3((unsigned)T), dim3(kApplyThreads), 0,
+    hipLaunchKernelGGL(fp8 ? append_fused_small_kernel<true> : append_fused_small_kernel<false>,
+                       dim3((unsigned)T), dim3(kApplyThreads), 0,
                        stream, a);
     return loom::record_launch(scope, hipGetLastError(), err);
   }
@@ -640,7 +720,8 @@ loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
                      stream, a);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
-    hipLaunchKernelGGL(append_apply_kernel, dim3((unsigned)T), dim3(kApplyThreads), 0, stream, a);
+    hipLaunchKernelGGL(fp8 ? append_apply_kernel<true> : append_apply_kernel<false>,
+                       dim3((unsigned)T), dim3(kApplyThreads), 0, stream, a);
     e = hipGetLastError();
   }
   return loom::record_launch(scope, e, err);

@@ -73,10 +73,16 @@ class AppendRunner:
         out = [bf16_host(b.take_read_write(h[n])) for n in ("query_output", "key_pages",
                                                            "value_pages")]
         b.take_read_write(h["workspace"])
-        # word 0 is the published validity flag; the accumulator and arrival
-        # counter words must be back at zero for the next command
+        # the duplicate-slot hash set (after the 64 reserved words and the T
+        # keys, positions and entry indices) must be empty again for the next
+        # command
         ws = self.ws.cpu().numpy().view(np.uint32)
-        assert ws[1] == 0 and ws[2] == 0, f"validation words left at {ws[:3]}"
+        T = self.plan.info.tokens
+        slots = 64
+        while slots < 2 * T:
+            slots *= 2
+        table = ws[64 + 3 * T: 64 + 3 * T + slots]
+        assert not table.any(), f"hash set left with {np.count_nonzero(table)} entries"
         return out
 
 
@@ -218,41 +224,80 @@ def test_explicit_guards_preserve_all_sentinels(L, oracle, name, bi, pos, ix):
     assert np.array_equal(kp, ks) and np.array_equal(vp, vs)
 
 
-@pytest.mark.parametrize("dup", [False, True], ids=["valid", "duplicate_slot"])
-def test_small_command_on_the_two_kernel_path(L, oracle, dup):
-    """A few tokens over a page table longer than the fused single-launch path
-    takes (4096 indices): the parallel validation + apply kernels, valid and
-    with a duplicate physical slot (every output keeps its sentinels)."""
-    rng = np.random.default_rng(12)
-    B, hq, hkv = 2, 4, 2
-    lens = np.array([40, 4200 * 16 - 3])
+# The two device paths of the explicit-token command: one launch in which
+# every workgroup validates the whole command (T <= 64, <= 4096 page indices),
+# and the parallel validation kernel + apply kernel (anything larger).
+PATHS = [
+    # (name, tokens, page indices of the long request)
+    ("fused_small", 3, 100),
+    ("two_kernel", 300, 4200),
+    ("two_kernel_long_table", 300, 9000),
+    ("two_kernel_few_tokens", 3, 4200),
+]
+BREAKS = ["valid", "duplicate_slot", "batch_index", "position", "page_index", "last_page_len"]
+
+
+@pytest.mark.parametrize("brk", BREAKS)
+@pytest.mark.parametrize("path,T,long_pages", PATHS, ids=[p[0] for p in PATHS])
+def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, brk):
+    """Each path on valid metadata (against the oracle) and with one guard
+    broken (rope/mod.rs:407-466: every output keeps its sentinels)."""
+    log(f"append path {path} T={T} break={brk}")
+    rng = np.random.default_rng(hash((path, brk)) % 2**32)
+    B, hq, hkv = 3, 4, 2
+    lens = np.array([40, long_pages * 16 - 3, 500])
     pages = (lens + 15) // 16
     pool = int(pages.sum()) + 5
     indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
     indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
     last = (lens - (pages - 1) * 16).astype(np.int32)
-    bi = np.array([1, 0, 1], np.int32)
-    pos = np.array([lens[1] - 1, 39, lens[1] - 2 if not dup else lens[1] - 1], np.int32)
-    T = 3
+    # distinct (request, position) pairs
+    pairs = set()
+    while len(pairs) < T:
+        r = int(rng.integers(0, B))
+        pairs.add((r, int(rng.integers(0, lens[r]))))
+    pairs = sorted(pairs)
+    rng.shuffle(pairs)
+    bi = np.array([p[0] for p in pairs], np.int32)
+    pos = np.array([p[1] for p in pairs], np.int32)
+    j = int(rng.integers(0, T))
+    if brk == "duplicate_slot":
+        k2 = (j + 1) % T
+        bi[k2], pos[k2] = bi[j], pos[j]
+    elif brk == "batch_index":
+        bi[j] = B
+    elif brk == "position":
+        pos[j] = lens[bi[j]]
+    elif brk == "page_index":
+        indices[int(rng.integers(0, len(indices)))] = pool
+    elif brk == "last_page_len":
+        last[1] = 17
     q = oracle.bf16_from_f32(rng.standard_normal(T * hq * 128, dtype=np.float32))
     k = oracle.bf16_from_f32(rng.standard_normal(T * hkv * 128, dtype=np.float32))
     v = oracle.bf16_from_f32(rng.standard_normal(T * hkv * 128, dtype=np.float32))
     kp = np.full(pool * 16 * hkv * 128, 0x3F80, np.uint16)
     vp = np.full(pool * 16 * hkv * 128, 0x4000, np.uint16)
-    spec = L.Bf16RopePagedKvAppendTokensSpec(T, B, pool, hq, hkv)
+    spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv)
     r = AppendRunner(L, spec, True)
-    qo, okp, ovp = r.run(q, k, v, bi, pos, indptr, indices, last, kp, vp)
-    if dup:
-        assert np.all(np.isnan(oracle.bf16_to_f32(qo)))
-        assert np.array_equal(okp, kp) and np.array_equal(ovp, vp)
-        return
-    s = oracle.paged_spec(B, pool, hq, hkv)
-    ekp, evp = kp.copy(), vp.copy()
-    eq = oracle.append_tokens(s, T, q, k, v, bi, pos, indptr, indices, last, ekp, evp)
-    for got, want in ((qo, eq), (okp, ekp)):
-        ok, _ = within_one_ulp(oracle, got, want)
-        assert ok
-    assert np.array_equal(ovp, evp)
+    for call in range(2):  # the second command runs over the first one's workspace
+        qo, okp, ovp = r.run(q, k, v, bi, pos, indptr, indices, last, kp, vp)
+        if brk != "valid":
+            assert np.all(np.isnan(oracle.bf16_to_f32(qo))), call
+            assert np.array_equal(okp, kp) and np.array_equal(ovp, vp), call
+            continue
+        s = oracle.paged_spec(B, pool, hq, hkv)
+        ekp, evp = kp.copy(), vp.copy()
+        eq = oracle.append_tokens(s, T, q, k, v, bi, pos, indptr, indices, last, ekp, evp,
+                                  max_tokens=8192)
+        check_rope(oracle, qo, eq, q, np.repeat(pos, hq), "query")
+        slots = [(indices[indptr[b] + p // 16], p % 16) for b, p in zip(bi, pos)]
+        rows = np.array([(pg * 16 + off) * hkv + h for pg, off in slots for h in range(hkv)])
+        okr, ekr = okp.reshape(-1, 128), ekp.reshape(-1, 128)
+        check_rope(oracle, okr[rows], ekr[rows], k, np.repeat(pos, hkv), "key rows")
+        rest = np.ones(len(okr), bool)
+        rest[rows] = False
+        assert np.array_equal(okr[rest], ekr[rest]), call
+        assert np.array_equal(ovp, evp), call
 
 
 def test_bulk_append_config2_shape(L, oracle):
