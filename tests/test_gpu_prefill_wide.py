@@ -120,8 +120,10 @@ def test_ragged_shapes_wide(L, oracle, shape):
 
 def test_long_prompt_picks_wide_and_matches_row_tiles(L, oracle):
     """A 2048-row GQA4 prompt (Hq 32 / Hkv 8) over a longer cached prefix: the
-    default plan is the wide one, equal bit for bit to the 16-column plan;
-    sampled columns are checked against the oracle on a one-request slice."""
+    default plan is the wide one; it equals the 16-column plan within the
+    oracle tolerance with the same sentinels (the two sum a column's blocks in
+    different orders, so not bit for bit), and sampled columns are checked
+    against the oracle on a one-request slice."""
     import torch
     log("wide prefill long prompt")
     rng = np.random.default_rng(2048)
@@ -233,3 +235,37 @@ def test_wide_guards_equal_narrow(L, oracle, guard):
     nan_rows = int(np.isnan(oracle.bf16_to_f32(res[0][0])).reshape(nnz * hq, 128).all(1).sum())
     assert nan_rows > 0, "the guard case keeps some sentinels"
     log(f"  sentinel rows {nan_rows}")
+
+
+@pytest.mark.parametrize("kind", ["paged", "ragged"])
+def test_tile_flag_combinations_rejected(L, kind):
+    """Planner rejections of prefill_tile_cols (paged_prefill.hip): both tile
+    flags at once, and 64-column tiles with 8- or 16-wave workgroups (the wide
+    algorithm runs four waves) are LOOM_PLAN_INVALID_OPTION naming the field."""
+    import ctypes as C
+    prov = L.PrefillProvider.load(0)
+    if kind == "paged":
+        spec = L.Bf16PagedPrefillSpec(1, 64, 8, 32, 8)
+        fn = L.lib().loom_prefill_provider_plan_bf16_paged_options
+    else:
+        spec = L.Bf16RaggedPrefillSpec(1, 64, 64, 32, 8)
+        fn = L.lib().loom_prefill_provider_plan_bf16_ragged
+    both = L.PLAN_PREFILL_TILE_16 | L.PLAN_PREFILL_TILE_64
+    for waves, flags, field in ((0, both, "flags"), (4, both, "flags"),
+                                (8, L.PLAN_PREFILL_TILE_64, "waves"),
+                                (16, L.PLAN_PREFILL_TILE_64, "waves")):
+        opt = L._ffi.PagedPrefillPlanOptions(waves, flags)
+        out = C.c_void_p()
+        with pytest.raises(L.PlanError) as e:
+            L._call(fn, prov._p, C.byref(spec._c), C.byref(opt), C.byref(out))
+        assert e.value.code == 75 and e.value.operand == field, (waves, flags, e.value)
+        assert not out.value
+    # the valid single flags still plan
+    for waves, flags in ((4, L.PLAN_PREFILL_TILE_64), (8, L.PLAN_PREFILL_TILE_16),
+                         (16, L.PLAN_PREFILL_TILE_16)):
+        opt = L._ffi.PagedPrefillPlanOptions(waves, flags)
+        out = C.c_void_p()
+        L._call(fn, prov._p, C.byref(spec._c), C.byref(opt), C.byref(out))
+        assert out.value
+        (L.lib().loom_paged_prefill_plan_free if kind == "paged"
+         else L.lib().loom_ragged_prefill_plan_free)(out.value)
