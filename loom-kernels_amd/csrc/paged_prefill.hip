@@ -19,12 +19,12 @@
 //   * per page, S = K·Qᵀ is four v_mfma_f32_16x16x32_bf16 (16 tokens x 16
 //     columns x 128 dims) with K loaded straight into the A-fragment layout,
 //     the online softmax runs in the log2 domain with a per-column causal
-//     mask, and O += P·V is eight column blocks of v_mfma_f32_16x16x16_bf16:
-//     the S accumulator already has the A-fragment layout of Pᵀ, and the V
+//     mask, and O += P·V is eight column blocks of v_mfma_f32_16x16x32_bf16:
+//     the S accumulator already has the B-fragment layout of Pᵀ, and the V
 //     rows as loaded give each lane the four tokens of one head dimension.
-//     P is split into a BF16 high part and a BF16 residual, two MFMAs per
-//     block, so the weights carry 16 significant bits (relative error below
-//     2^-15 against FP32 weights);
+//     P enters as a BF16 high part and a BF16 residual in the two halves of
+//     the k = 32 operand (one MFMA per block), so the weights carry 16
+//     significant bits (relative error below 2^-15 against FP32 weights);
 //   * the W wave states merge in LDS (max, rescale, deterministic tree sum)
 //     and wave 0 writes O and the log2 LSE.
 // Wide tiles (long prompts; LOOM_PAGED_PREFILL_WIDE_TILE): a workgroup of
@@ -215,26 +215,27 @@ struct PrefillWave {
     if (__builtin_amdgcn_ballot_w64(al != 1.0f))
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] *= al;
-    // Pᵀ as the B fragment (lane: column col, tokens 4 quad + [0, 4)): BF16
-    // high part and BF16 residual.
+    // Pᵀ as the B fragment of v_mfma_f32_16x16x32_bf16 (lane: column col,
+    // k = 8 quad + [0, 8)): k = 8 quad + i is token 4 quad + i with its BF16
+    // high part, k = 8 quad + 4 + i the same token's BF16 residual.
     uint32_t pb[4], rb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       pb[i] = __float_as_uint(p[i]);
       rb[i] = __float_as_uint(p[i] - __uint_as_float(pb[i] & 0xffff0000u));
     }
-    const s16x4 p_hi = as_s16x4(pack_hi16(pb[0], pb[1]), pack_hi16(pb[2], pb[3]));
-    const s16x4 p_lo = as_s16x4(pack_hi16(rb[0], rb[1]), pack_hi16(rb[2], rb[3]));
+    const bf16x8 pt = as_bf16x8(pack_hi16(pb[0], pb[1]), pack_hi16(pb[2], pb[3]),
+                                pack_hi16(rb[0], rb[1]), pack_hi16(rb[2], rb[3]));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      // Vᵀ block e as the A fragment: row col is dim 8 col + e, tokens
-      // 4 quad + [0, 4) straight from the V rows this lane loaded
+      // Vᵀ block e as the A fragment: row col is dim 8 col + e, k = 8 quad +
+      // [0, 4) and 8 quad + 4 + [0, 4) both tokens 4 quad + [0, 4), straight
+      // from the V rows this lane loaded
       const int w = e >> 1;
-      const s16x4 vt =
-          (e & 1) ? as_s16x4(pack_hi16(pg.v[0][w], pg.v[1][w]), pack_hi16(pg.v[2][w], pg.v[3][w]))
-                  : as_s16x4(pack_lo16(pg.v[0][w], pg.v[1][w]), pack_lo16(pg.v[2][w], pg.v[3][w]));
-      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, p_hi, acc[e], 0, 0, 0);
-      acc[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, p_lo, acc[e], 0, 0, 0);
+      const uint32_t x01 = (e & 1) ? pack_hi16(pg.v[0][w], pg.v[1][w]) : pack_lo16(pg.v[0][w], pg.v[1][w]);
+      const uint32_t x23 = (e & 1) ? pack_hi16(pg.v[2][w], pg.v[3][w]) : pack_lo16(pg.v[2][w], pg.v[3][w]);
+      acc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(x01, x23, x01, x23), pt, acc[e],
+                                                       0, 0, 0);
     }
   }
 
