@@ -443,6 +443,32 @@ def reference_shapes(L, stream, samples=30):
                 ts.append(ev0.elapsed_time(ev1) * 1000.0)
         out[key] = med(ts)
     del tg
+    # Per-node cost of a replay: torch-captured graphs of 1..16 tiny kernels,
+    # one replay + completion event per sample; the slope over the node count
+    # is what each further node of a captured command adds.
+    by_nodes = {}
+    for nodes in (1, 2, 4, 8, 16):
+        gk = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gk, stream=stream):
+                for _ in range(nodes):
+                    x.add_(1)
+        torch.cuda.synchronize()
+        ts = []
+        for i in range(samples + 3):
+            with torch.cuda.stream(stream):
+                ev0.record(stream)
+                gk.replay()
+                ev1.record(stream)
+            ev1.synchronize()
+            if i >= 3:
+                ts.append(ev0.elapsed_time(ev1) * 1000.0)
+        by_nodes[nodes] = med(ts)
+        del gk
+    out["platform_graph_replay_us_by_nodes"] = by_nodes
+    out["platform_graph_replay_us_per_extra_node"] = round(
+        (by_nodes[16] - by_nodes[1]) / 15.0, 3)
 
     for c in g["paged_decode"]["cases"]:
         B, pool, hq, hkv = c["batch"], c["pool"], c["hq"], c["hkv"]
