@@ -1162,7 +1162,7 @@ struct loom_decode_provider {
 };
 
 struct loom_paged_decode_plan {
-  loom_paged_decode_plan_info_t info;
+  loom_paged_decode_plan_info_t info{};
   int device = 0;
 };
 

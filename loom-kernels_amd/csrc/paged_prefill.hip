@@ -648,11 +648,11 @@ struct loom_prefill_provider {
 };
 
 struct loom_paged_prefill_plan {
-  loom_paged_prefill_plan_info_t info;
+  loom_paged_prefill_plan_info_t info{};
 };
 
 struct loom_ragged_prefill_plan {
-  loom_ragged_prefill_plan_info_t info;
+  loom_ragged_prefill_plan_info_t info{};
 };
 
 namespace {

@@ -482,7 +482,7 @@ struct loom_rope_provider {
 };
 
 struct loom_rope_append_plan {
-  loom_rope_append_plan_info_t info;
+  loom_rope_append_plan_info_t info{};
   uint64_t max_num_pages = 0;
   uint32_t flags = 0;
   uint32_t kv_layout = LOOM_KV_LAYOUT_NHD;
