@@ -397,6 +397,37 @@ def cpu_baseline(case, min_s=10.0, max_s=30.0):
                       f"(host has {os.cpu_count()} logical CPUs)"}
 
 
+def cpu_baseline_parallel(case, threads=16, min_s=3.0):
+    """The same oracle over the whole config-3 batch with its requests split
+    over `threads` host threads (oracle.paged_decode_parallel: each request is
+    the single-threaded reference loop, so the bits are those of the serial
+    oracle).  The batch's pages are gathered to the host once (untimed) and
+    renumbered; the whole batch is decoded until at least `min_s` of wall
+    time.  Reported beside the single-thread figure with its thread count."""
+    import numpy as np
+    import torch
+    import oracle as O
+    threads = min(threads, os.cpu_count() or 1)
+    n = int(case.indptr_h[-1])
+    idx = torch.from_numpy(case.indices_h.astype(np.int64)).cuda()
+    kh = case.k.view(case.pool, -1)[idx].reshape(-1).view(torch.int16).cpu().numpy().view(np.uint16)
+    vh = case.v.view(case.pool, -1)[idx].reshape(-1).view(torch.int16).cpu().numpy().view(np.uint16)
+    qh = case.q.view(torch.int16).cpu().numpy().view(np.uint16)
+    s = O.paged_spec(case.B, n, case.hq, case.hkv)
+    ix = np.arange(n, dtype=np.int32)
+    t_total, calls = 0.0, 0
+    while t_total < min_s:
+        t0 = time.perf_counter()
+        O.paged_decode_parallel(s, qh, kh, vh, case.indptr_h, ix, case.last_h, threads=threads)
+        t_total += time.perf_counter() - t0
+        calls += 1
+    return {"value": round(case.bytes * calls / t_total / 1e9, 4), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{calls} whole config-3 batches ({case.bytes * calls / 1e9:.2f} GB "
+                      f"algorithmic), C oracle in the reference loop order with the requests "
+                      f"split over {threads} host threads, {t_total:.1f} s wall time"}
+
+
 def reference_shapes(L, stream, samples=30):
     """The reference's own published shapes (its H20 records):
     tiny decode and append fixtures, whose time is launch latency.  Eager = the
@@ -894,6 +925,8 @@ def main():
         return
     c3 = detail["c3_gqa4_b64_ragged"]
     cpu = None if a.no_cpu else cpu_baseline(head)
+    if cpu is not None:
+        detail["c3_gqa4_b64_ragged"]["cpu_baseline_parallel"] = cpu_baseline_parallel(head)
     line = {
         "metric": "paged-decode achieved HBM GB/s (% of peak) + µs/call; RoPE+append µs/call",
         "value": c3["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
