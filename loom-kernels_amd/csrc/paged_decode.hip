@@ -58,12 +58,7 @@ constexpr int kStateStride = 132;
 #define LOOM_DECODE_DIRECT_MAX_PAGES 128
 #endif
 constexpr int kKRowBytes = 256 + 16;
-// K loaded straight into MFMA fragments (64 bytes of each of 16 rows per
-// load) instead of whole rows transposed through LDS.
-#ifndef LOOM_DECODE_K_DIRECT
-#define LOOM_DECODE_K_DIRECT 0
-#endif
-constexpr int kKTileBytes = LOOM_DECODE_K_DIRECT ? 16 : 16 * kKRowBytes;
+constexpr int kKTileBytes = 16 * kKRowBytes;
 #ifndef LOOM_DECODE_DEPTH
 #define LOOM_DECODE_DEPTH 2
 #endif
@@ -200,13 +195,7 @@ __device__ __forceinline__ void load_rows(PageRegs &r, const DecodeArgs &a, int6
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int off = (quad * 4 + j) * a.row_elems * 2 + col * 16;
-#if LOOM_DECODE_K_DIRECT
-    // K straight into the MFMA A-fragment layout: lane (col, quad) holds
-    // dims 32 j + 8 quad + [0, 8) of token row col.
-    r.k[j] = load16_rows<LOOM_DECODE_NT_K>(rk, col * a.row_elems * 2 + (32 * j + 8 * quad) * 2);
-#else
     r.k[j] = load16_rows<LOOM_DECODE_NT_K>(rk, off);
-#endif
     r.v[j] = load16_rows<LOOM_DECODE_NT_V>(rv, off);
   }
 }
@@ -251,11 +240,7 @@ __device__ __forceinline__ void load_rows(PageRegs8 &r, const DecodeArgs &a, int
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int off = (quad * 4 + j) * a.row_elems + col * 8;
-#if LOOM_DECODE_K_DIRECT
-    r.k[j] = load8_rows<LOOM_DECODE_NT_K>(rk, col * a.row_elems + 32 * j + 8 * quad);
-#else
     r.k[j] = load8_rows<LOOM_DECODE_NT_K>(rk, off);
-#endif
     r.v[j] = load8_rows<LOOM_DECODE_NT_V>(rv, off);
   }
 }
@@ -349,10 +334,6 @@ struct WaveDecoder {
   template <class Page>
   __device__ void process(const Page &pr, int rows) {
     u32x4 kf[4];
-#if LOOM_DECODE_K_DIRECT
-#pragma unroll
-    for (int c = 0; c < 4; ++c) kf[c] = k_words(pr, c);
-#else
     // K rows -> LDS tile -> MFMA A fragments (lane: token row `col`, dims
     // 32c + 8*quad + [0, 8)).
 #pragma unroll
@@ -362,7 +343,6 @@ struct WaveDecoder {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       kf[c] = *reinterpret_cast<const u32x4 *>(kt + col * kKRowBytes + (c * 4 + quad) * 16);
-#endif
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c)
