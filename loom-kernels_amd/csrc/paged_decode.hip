@@ -98,7 +98,15 @@ constexpr int kDepth = LOOM_DECODE_DEPTH;
 #ifndef LOOM_DECODE_SPLIT_WAVES_PER_4CU_FP8
 #define LOOM_DECODE_SPLIT_WAVES_PER_4CU_FP8 32
 #endif
-constexpr int kSplitDepth = LOOM_DECODE_SPLIT_DEPTH;
+#ifndef LOOM_DECODE_SPLIT_DEPTH_FP8
+#define LOOM_DECODE_SPLIT_DEPTH_FP8 3
+#endif
+// Pages in flight per wave of the split kernel (FP8 pages take half the
+// registers per page).
+template <bool FP8>
+constexpr int split_depth() {
+  return FP8 ? LOOM_DECODE_SPLIT_DEPTH_FP8 : LOOM_DECODE_SPLIT_DEPTH;
+}
 // Normalizer written into a state whose pages failed the guard.
 constexpr float kPoisonNormalizer = -1.0f;
 
@@ -470,6 +478,7 @@ template <int GT, bool FP8 = false>
 __global__ __launch_bounds__(kThreads, LOOM_DECODE_SPLIT_WAVES) void paged_decode_split_kv_kernel(
     DecodeArgs a) {
   __shared__ Smem<GT> sm;
+  constexpr int kSD = split_depth<FP8>();
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   float v_scale = 1.0f;
   if constexpr (FP8) {
@@ -620,7 +629,7 @@ __global__ __launch_bounds__(kThreads, LOOM_DECODE_SPLIT_WAVES) void paged_decod
   const int64_t qh_base = (int64_t)kvh * a.group + g_base;
 
   // ---- one continuous page stream over [v_begin, v_end) --------------------
-  // Two cursors walk the virtual list: the load cursor kSplitDepth-1 pages ahead of
+  // Two cursors walk the virtual list: the load cursor kSD-1 pages ahead of
   // the process cursor.  Page indices come in blocks of 64 (one per lane, read
   // back with v_readlane), the next block fetched while the current one is
   // used, so the K/V pipeline does not drain at request or block boundaries;
@@ -749,13 +758,13 @@ __global__ __launch_bounds__(kThreads, LOOM_DECODE_SPLIT_WAVES) void paged_decod
     }
   };
 
-  // Pipeline: page v+kSplitDepth-1 is issued before page v is consumed; the
+  // Pipeline: page v+kSD-1 is issued before page v is consumed; the
   // unrolled buffer rotation lets the compiler wait for exactly the oldest
   // page's loads.
-  PageBuf<FP8> buf[kSplitDepth];
-  int brows[kSplitDepth];
+  PageBuf<FP8> buf[kSD];
+  int brows[kSD];
 #pragma unroll
-  for (int j = 0; j < kSplitDepth - 1; ++j) {
+  for (int j = 0; j < kSD - 1; ++j) {
     int pg, blk;
     describe(lc, v_begin + j, pg, blk, brows[j]);
     load_page(buf[j], a, pg, blk, brows[j], lane, kvh);
@@ -767,11 +776,11 @@ __global__ __launch_bounds__(kThreads, LOOM_DECODE_SPLIT_WAVES) void paged_decod
   int i = 0;
   while (true) {
 #pragma unroll
-    for (int s = 0; s < kSplitDepth; ++s) {
+    for (int s = 0; s < kSD; ++s) {
       {
-        const int nb = (s + kSplitDepth - 1) % kSplitDepth;
+        const int nb = (s + kSD - 1) % kSD;
         int pg, blk;
-        describe(lc, v + kSplitDepth - 1, pg, blk, brows[nb]);
+        describe(lc, v + kSD - 1, pg, blk, brows[nb]);
         load_page(buf[nb], a, pg, blk, brows[nb], lane, kvh);
       }
       if (v >= pc.pre + pc.cnt) {
