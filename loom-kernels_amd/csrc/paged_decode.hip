@@ -850,16 +850,27 @@ __global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_
   const int gt = rest % a.members;  // members = group tiles for this kernel
   const int r = rest / a.members;
 
-  // Guards (decode.rs:233-246 global, :430-478 per request), one round trip.
+  const int g_base = gt * GT;
+  const int gcount = min(GT, a.group - g_base);
+  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], lane, col, quad, kvh};
+  // One round trip for the guard words (decode.rs:233-246 global, :430-478
+  // per request), the query tile and, when the page-index array has at most
+  // 128 entries (as direct plans' tables do), the whole array (two words per
+  // lane): the request's page indices are then read from registers.
+  u32x4 qr[4];
+  w.load_q(r, kvh * a.group + g_base, gcount, qr);
+  const bool small_table = a.n_indices <= 128;
+  int tbl0 = 0, tbl1 = 0;
+  if (small_table) {
+    if (lane < a.n_indices) tbl0 = a.indices[lane];
+    if (lane + 64 < a.n_indices) tbl1 = a.indices[lane + 64];
+  }
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
   const int32_t st = uni(a.indptr[r]), en = uni(a.indptr[r + 1]), tl = uni(a.last[r]);
   if (ip0 != 0 || !batch_pages_ok(a, ipB)) return;
   const int cnt = request_pages(a, st, en, tl, ipB);
   if (cnt == 0) return;
 
-  const int g_base = gt * GT;
-  const int gcount = min(GT, a.group - g_base);
-  WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], lane, col, quad, kvh};
   // this wave's 16-row blocks: request-local positions wave + W*i (block b
   // is block b % (page_rows / 16) of the request's page b / (page_rows / 16))
   const int mine = cnt > wave ? (cnt - wave + W - 1) / W : 0;
@@ -867,10 +878,14 @@ __global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_
   const int bmask = (1 << a.blocks_lg) - 1;
   bool bad = false;
   {
-    u32x4 qr[4];
     int idx = 0;
-    if (lane < min(mine, 64)) idx = a.indices[st + ((wave + W * lane) >> a.blocks_lg)];
-    w.load_q(r, kvh * a.group + g_base, gcount, qr);
+    if (small_table) {
+      const int j = st + ((wave + W * lane) >> a.blocks_lg);  // < 128 for this wave's blocks
+      const int lo = __shfl(tbl0, j & 63, 64), hi = __shfl(tbl1, j & 63, 64);
+      if (lane < min(mine, 64)) idx = j < 64 ? lo : hi;
+    } else if (lane < min(mine, 64)) {
+      idx = a.indices[st + ((wave + W * lane) >> a.blocks_lg)];
+    }
     w.store_q(qr);
     w.reset();
     for (int s0 = 0; s0 < mine; s0 += 64) {
