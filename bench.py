@@ -428,6 +428,27 @@ def cpu_baseline_parallel(case, threads=16, min_s=3.0):
                       f"split over {threads} host threads, {t_total:.1f} s wall time"}
 
 
+CAPI_BENCH = os.path.join(ROOT, "loom-kernels_amd", "lib", "capi_bench")
+
+
+def capi_eager(B, pool, hq, hkv, indptr, indices, last, samples=30):
+    """The same eager protocol through the C ABI alone (capi_bench, a child
+    process: C++ calls of loom_paged_decode_enqueue_bf16, no Python on the
+    per-call path): {"capi_eager_us", "capi_host_enqueue_us"}, or {} when the
+    program is missing."""
+    import subprocess
+    if not os.path.exists(CAPI_BENCH):
+        return {}
+    lst = lambda xs: ",".join(str(int(x)) for x in xs)
+    r = subprocess.run([CAPI_BENCH, str(B), str(pool), str(hq), str(hkv), lst(indptr),
+                        lst(indices), lst(last), str(samples)],
+                       capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"capi_bench failed: {r.stderr.strip()}")
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"capi_eager_us": d["eager_us"], "capi_host_enqueue_us": d["host_enqueue_us"]}
+
+
 def reference_shapes(L, stream, samples=30):
     """The reference's own published shapes (its H20 records):
     tiny decode and append fixtures, whose time is launch latency.  Eager = the
@@ -498,6 +519,27 @@ def reference_shapes(L, stream, samples=30):
         by_nodes[nodes] = med(ts)
         del gk
     out["platform_graph_replay_us_by_nodes"] = by_nodes
+    # Back-to-back floor: 100 tiny torch kernels between one event pair, per
+    # kernel (the eager protocol of the shapes below, with no work).
+    ts = []
+    for i in range(samples + 3):
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            for _ in range(100):
+                x.add_(1)
+            ev1.record(stream)
+        ev1.synchronize()
+        if i >= 3:
+            ts.append(ev0.elapsed_time(ev1) * 1000.0 / 100)
+    out["platform_one_kernel_back_to_back_us"] = med(ts)
+    if os.path.exists(CAPI_BENCH):
+        import subprocess
+        r = subprocess.run([CAPI_BENCH, "--empty-kernel", str(samples)], capture_output=True,
+                           text=True, timeout=120)
+        if r.returncode == 0:
+            d = json.loads(r.stdout.strip().splitlines()[-1])
+            out["platform_empty_kernel_back_to_back_us"] = d["eager_us"]
+            out["platform_empty_kernel_host_launch_us"] = d["host_enqueue_us"]
     out["platform_graph_replay_us_per_extra_node"] = round(
         (by_nodes[16] - by_nodes[1]) / 15.0, 3)
 
@@ -522,6 +564,9 @@ def reference_shapes(L, stream, samples=30):
         e, gr = eager_and_graph(9, bind, plan.enqueue_into)
         out["decode_" + c["name"]] = {"eager_us": e, "graph_replay_us": gr,
                                       "teams": plan.info.teams}
+        cap = capi_eager(B, pool, hq, hkv, c["indptr"], c["indices"], c["last"])
+        if cap:
+            out["decode_" + c["name"]].update(cap)
     for name in ("append_one_token", "append_tokens_t6"):
         c = g[name]
         explicit = "tokens" in c
@@ -843,6 +888,8 @@ def main():
                                  "page64_GBps": round(case.bytes / (p_us * 1e-6) / 1e9, 1)})
             del pplan
         if name.startswith("c1"):
+            detail[name].update(capi_eager(B, pool, hq, hkv, case.indptr_h, case.indices_h,
+                                           case.last_h))
             # cold: 16 copies of the workload (537 MB) used round-robin
             copies = [case] + [DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name) + i)
                                for i in range(1, 16)]

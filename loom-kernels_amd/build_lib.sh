@@ -1,6 +1,7 @@
 #!/usr/bin/env bash
 # Builds libloom_infer_hip.so (gfx950 only) in-tree:
 #   loom-kernels_amd/lib/libloom_infer_hip.so
+#   loom-kernels_amd/lib/capi_bench  (C-ABI eager benchmark, links the library)
 # Every HIP translation unit is compiled with packed FP32 ops disabled.
 set -euo pipefail
 here="$(cd "$(dirname "$0")" && pwd)"
@@ -22,3 +23,7 @@ done
 for p in "${pids[@]}"; do wait "$p"; done
 "$HIPCC" --offload-arch=gfx950 -shared -fPIC "$obj"/*.o -o "$out/libloom_infer_hip.so.tmp"
 mv "$out/libloom_infer_hip.so.tmp" "$out/libloom_infer_hip.so"
+# the C-ABI eager benchmark (bench.py runs it as a child process)
+"$HIPCC" --offload-arch=gfx950 -O2 -std=c++17 -Wall -I"$root/include" "$here/csrc/capi_bench.cpp" \
+    -L"$out" -lloom_infer_hip -Wl,-rpath,'$ORIGIN' -o "$out/capi_bench.tmp"
+mv "$out/capi_bench.tmp" "$out/capi_bench"
