@@ -878,10 +878,12 @@ typedef struct loom_rope_append_args {
                                   Write<u8>); {0, 0} for BF16 pages */
 } loom_rope_append_args_t;
 
-/* enqueue_into, rope/mod.rs:758-830 / :846-934: a metadata-validation kernel
- * (whole page table, batch indices, positions, duplicate physical slots) and
- * the rotate+scatter kernel, stream ordered; commands with T <= 64 and at most
- * 4096 page indices run as one kernel that validates in every workgroup.  Invalid device metadata leaves
+/* enqueue_into, rope/mod.rs:758-830 / :846-934: one kernel per command.  Its
+ * first workgroups validate the metadata in chunks (whole page table, batch
+ * indices, positions, duplicate physical slots) while one workgroup per token
+ * loads and rotates; the token workgroups write only after every chunk has
+ * passed.  Commands with T <= 64 and at most 4096 page indices run as one
+ * kernel that validates in every workgroup.  Invalid device metadata leaves
  * every output untouched (the reference's sentinel guard). */
 loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
                                        loom_command_scope_t *scope,

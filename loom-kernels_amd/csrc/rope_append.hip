@@ -7,18 +7,17 @@
 // (invalid metadata anywhere leaves every output untouched).
 //
 // MI355X design:
-//   * validation runs once per command, not once per workgroup: a small grid
-//     checks the whole page-index array, the request table and every token's
-//     (request, position, slot) in parallel, one token per thread, records
-//     the slot keys, finds duplicate physical slots by inserting every key
-//     into a workspace hash set with agent-scope compare-and-swap (O(T) in
-//     all, no last-arriver pass), and writes one verdict per workgroup;
-//   * the apply kernel runs one workgroup per token: it reads the verdicts
-//     and the recorded slot instead of walking the page table again, clears
-//     the token's hash-set entry for the next command, 64 lanes compute the
-//     token's 64 (sin, cos) pairs once into LDS, then 16 lanes per 256-byte
-//     head row rotate Q/K and scatter K/V rows into the page slot with 16-byte
-//     loads and stores;
+//   * one launch per command, validation once per command, not once per
+//     workgroup: the grid's first workgroups each check one chunk of the
+//     page-index array, the request table and the tokens' (request,
+//     position, slot), one token per thread, find duplicate physical slots by
+//     inserting every key into a workspace hash set with agent-scope
+//     compare-and-swap (O(T) in all), and publish an epoch-tagged verdict;
+//   * one workgroup per token overlaps that validation with its own work: it
+//     loads its Q/K/V rows, walks the page table for its slot, computes the
+//     token's 64 (sin, cos) pairs into LDS, then waits for the verdicts and,
+//     if all pass, 16 lanes per 256-byte head row rotate Q/K and scatter K/V
+//     rows into the page slot with 16-byte loads and stores;
 //   * small commands (T <= 64, <= 4096 page indices) run as one launch in
 //     which every workgroup validates the whole command itself (the
 //     reference's approach), so there is no second kernel;
@@ -48,7 +47,6 @@ constexpr int kMaxTokens = LOOM_APPEND_MAX_TOKENS_EXTENDED;
 // Commands this small run as one fused launch (every workgroup validates).
 constexpr int kFusedMaxTokens = 64;
 constexpr int64_t kFusedMaxIndices = 4096;
-constexpr uint32_t kEmptyKey = 0xffffffffu;
 // Hash set for duplicate slots: a power of two >= 2T.
 __host__ __device__ constexpr int hash_slots(int tokens) {
   int n = 64;
@@ -61,30 +59,55 @@ __host__ __device__ constexpr int64_t max_validate_blocks(int64_t tokens, int64_
   const int64_t m = t > b ? t : b;
   return m > kMaxIndexBlocks ? m : kMaxIndexBlocks;
 }
-// Workspace (u32 words) of the two-kernel path:
-//   [0, 64)                 reserved
-//   keys       [T]          physical slot (page * page_rows + row) per token
-//   positions  [T]
-//   hash_at    [T]          the hash-set entry each token's key occupies, or
-//                           kEmptyKey (the apply kernel clears that entry)
-//   table      [hash_slots(T)]  key + 1, 0 = empty: zero before the first
-//                           command and again after every command
-//   verdicts   [max_validate_blocks]  1 = that validation workgroup found the
-//                           command valid, 0 = not (rewritten by every command)
+// Largest batch of the append contracts (the request table is indexed in 32
+// bits; validation chunks cover 256 requests each).
+constexpr int64_t kMaxBatch = 65536;
+constexpr int kMaxValidateBlocks = (int)max_validate_blocks(kMaxTokens, kMaxBatch);
+constexpr int kMaxGrid = kMaxTokens + kMaxValidateBlocks;
+constexpr int kTableSlots = hash_slots(kMaxTokens);
+// Workspace of the chunk-validated one-launch path, in u32 words, one layout
+// for every plan (a command queue's workspace serves all of its plans).  It
+// must be zero before its first command; after that it needs no clearing:
+// commands are told apart by the epoch's tags, and each command empties the
+// hash table the next command will use.
+//   [0, 2)   epoch (u64): chunk-validated commands run on this workspace.
+//            Every workgroup reads it at start and tags its start word with
+//            epoch + 1; workgroup 0 advances it once every start word carries
+//            that tag, i.e. once every workgroup of the command has read it.
+//   [2]      sticky diagnostic: 1 once a workgroup gave up waiting (only
+//            possible if the validation workgroups were never scheduled)
+//   [3, 64)  reserved
+//   started  [kMaxGrid] (u64): each workgroup's start tag, epoch + 1 (the
+//            validation workgroups first, then one per token)
+//   signals  [kSignalCopies][kMaxValidateBlocks] (u64): chunk b's verdict
+//            (epoch + 1) * 2 + valid, written to every copy; the workgroups
+//            of copy r = blockIdx % kSignalCopies poll copy r, so no word is
+//            polled by more than ~T / kSignalCopies workgroups (same-address
+//            accesses of many workgroups serialize)
+//   tables   [2][kTableSlots]: duplicate-slot hash sets, key + 1, 0 = empty;
+//            the command with epoch e inserts into table e & 1 and empties
+//            table (e + 1) & 1 for the next command
 constexpr int kWsHeaderWords = 64;
+constexpr int kWsEpoch = 0, kWsTimedOut = 2;
+constexpr int kSignalCopies = 64;
+constexpr int64_t kWsStarted = kWsHeaderWords;
+constexpr int64_t kWsSignals = kWsStarted + 2 * (int64_t)kMaxGrid;
+constexpr int64_t kWsTables = kWsSignals + 2 * (int64_t)kSignalCopies * kMaxValidateBlocks;
+constexpr int64_t kWsWords = kWsTables + 2 * (int64_t)kTableSlots;
+// Polls before a workgroup gives up waiting (about 0.3 s; only reachable if
+// the validation workgroups were never scheduled).
+constexpr int kPollLimit = 1 << 18;
 struct WsLayout {
-  uint32_t *keys, *positions, *hash_at, *table, *verdicts;
+  uint64_t *started;  // workgroup g's start tag
+  uint64_t *signals;  // copy r, chunk b at signals[r * kMaxValidateBlocks + b]
+  uint32_t *tables;   // table p at tables + p * kTableSlots
 };
-__host__ __device__ inline int64_t ws_words(int64_t tokens, int64_t batch) {
-  return kWsHeaderWords + 3 * tokens + hash_slots((int)tokens) + max_validate_blocks(tokens, batch);
-}
-__device__ inline WsLayout ws_layout(uint32_t *ws, int tokens) {
+__host__ __device__ constexpr int64_t ws_words(int64_t, int64_t) { return kWsWords; }
+__device__ inline WsLayout ws_layout(uint32_t *ws) {
   WsLayout w;
-  w.keys = ws + kWsHeaderWords;
-  w.positions = w.keys + tokens;
-  w.hash_at = w.positions + tokens;
-  w.table = w.hash_at + tokens;
-  w.verdicts = w.table + hash_slots(tokens);
+  w.started = reinterpret_cast<uint64_t *>(ws + kWsStarted);
+  w.signals = reinterpret_cast<uint64_t *>(ws + kWsSignals);
+  w.tables = ws + kWsTables;
   return w;
 }
 
@@ -149,12 +172,10 @@ __device__ __forceinline__ bool table_bounds_bad(const AppendArgs &a, int32_t ip
 
 // `ip` / `ln`: the request table (page_indptr, last_page_len), in global
 // memory or an LDS copy.
-__device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t pages, int *req,
-                                           int *pos, int64_t *page, int *off,
-                                           const int32_t *ip, const int32_t *ln) {
-  // both words in one round trip
-  const int r = a.batch_indices ? a.batch_indices[t] : t;
-  const int p_given = a.batch_indices ? a.positions[t] : 0;
+// `r` / `p_given`: the token's request and (explicit form) position.
+__device__ __forceinline__ bool slot_of(const AppendArgs &a, int r, int p_given, int64_t pages,
+                                        int *req, int *pos, int64_t *page, int *off,
+                                        const int32_t *ip, const int32_t *ln) {
   if (r < 0 || r >= a.batch) return false;
   const int32_t st = ip[r], en = ip[r + 1], tl = ln[r];
   if (st < 0 || en <= st || (int64_t)en > pages || tl < 1 || tl > a.page_rows) return false;
@@ -169,21 +190,34 @@ __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t p
   *off = p % a.page_rows;
   return true;
 }
+__device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t pages, int *req,
+                                           int *pos, int64_t *page, int *off,
+                                           const int32_t *ip, const int32_t *ln) {
+  // both words in one round trip
+  const int r = a.batch_indices ? a.batch_indices[t] : t;
+  const int p_given = a.batch_indices ? a.positions[t] : 0;
+  return slot_of(a, r, p_given, pages, req, pos, page, off, ip, ln);
+}
 
-// Validation, all-or-nothing.  Workgroup b checks page indices
-// [b*chunk, (b+1)*chunk) (rope/mod.rs:143-150), requests [b*256, (b+1)*256)
-// (paged_decode/mod.rs:164-205) and tokens [b*256, (b+1)*256)
-// (paged_append/mod.rs:262-309), one token per thread; records each token's
-// physical slot key and position for the apply kernel; inserts every valid
-// key into a workspace hash set (agent-scope compare-and-swap, so two tokens
-// with one slot meet whichever XCDs they run on; the second finds the first);
-// and writes its verdict.  The apply kernel reads every verdict.
-__global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(AppendArgs a) {
-  __shared__ int32_t s_ip[kValidateLdsBatch + 1], s_last[kValidateLdsBatch];
-  const int tid = threadIdx.x;
-  const WsLayout w = ws_layout(a.ws, a.tokens);
-  // The request table in LDS (batches up to kValidateLdsBatch), loaded with
-  // the page indices below, so a token's slot is one more round trip.
+// Validation of chunk b, all-or-nothing: page indices [b*chunk, (b+1)*chunk)
+// (rope/mod.rs:143-150), requests [b*256, (b+1)*256) (paged_decode/mod.rs:
+// 164-205) and tokens [b*256, (b+1)*256) (paged_append/mod.rs:262-309), one
+// token per thread.  Inserts every valid slot key into the hash set `table`
+// (agent-scope compare-and-swap, so two tokens with one slot meet whichever
+// XCDs they run on; the second finds the first).  Returns nonzero if the
+// chunk is invalid.  `s_ip` / `s_last` hold kValidateLdsBatch + 1 /
+// kValidateLdsBatch words of LDS.
+__device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int tid, int32_t *s_ip,
+                                              int32_t *s_last, uint32_t *table) {
+  // This chunk's tokens' requests and positions, the request table into LDS
+  // (batches up to kValidateLdsBatch) and the page indices below are all
+  // loaded in one round trip, so a token's slot is one more.
+  const int t = b * kValidateThreads + tid;
+  int r_given = 0, p_given = 0;
+  if (t < a.tokens) {
+    r_given = a.batch_indices ? a.batch_indices[t] : t;
+    p_given = a.batch_indices ? a.positions[t] : 0;
+  }
   const bool lds_table = a.batch <= kValidateLdsBatch;
   if (lds_table) {
     for (int r = tid; r <= a.batch; r += kValidateThreads) {
@@ -197,7 +231,7 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
   int bad = 0;
   // this workgroup's page indices: all loads issued before any is tested
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
-  const int64_t lo = (int64_t)blockIdx.x * a.index_chunk;
+  const int64_t lo = (int64_t)b * a.index_chunk;
   const int64_t hi = min<int64_t>(lo + a.index_chunk, a.n_indices);
   int32_t pgs[kIndicesPerValidateBlock / kValidateThreads];
   const int64_t pages = table_pages(a, ipB);
@@ -212,32 +246,28 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
       bad |= (base + j * kValidateThreads + tid < min<int64_t>(hi, pages) &&
               (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool)) ? 1 : 0;
   }
-  const int r = blockIdx.x * kValidateThreads + tid;
+  const int r = b * kValidateThreads + tid;
   if (r < a.batch) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
     bad |= (en <= st || tl < 1 || tl > a.page_rows) ? 1 : 0;
   }
-  if (blockIdx.x == 0 && tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
-  const int t = blockIdx.x * kValidateThreads + tid;
+  if (b == 0 && tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
   __syncthreads();  // the LDS request table
   if (t < a.tokens) {
     int rr = 0, p = 0, off = 0;
     int64_t pg = 0;
-    uint32_t key = kEmptyKey, at = kEmptyKey;
-    if (token_slot(a, t, pages, &rr, &p, &pg, &off, ip, ln)) {
-      key = (uint32_t)(pg * a.page_rows + off);
+    if (slot_of(a, r_given, p_given, pages, &rr, &p, &pg, &off, ip, ln)) {
+      const uint32_t key = (uint32_t)(pg * a.page_rows + off);
       // Open addressing at load <= 1/2: every probe sequence ends at an
       // empty entry or at the same key (a duplicate slot).
       const uint32_t mask = (uint32_t)hash_slots(a.tokens) - 1u;
       uint32_t h = (key * 0x9E3779B1u) >> 16 & mask;
       while (true) {
         uint32_t expected = 0u;
-        if (__hip_atomic_compare_exchange_strong(&w.table[h], &expected, key + 1u,
+        if (__hip_atomic_compare_exchange_strong(&table[h], &expected, key + 1u,
                                                  __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT)) {
-          at = h;
+                                                 __HIP_MEMORY_SCOPE_AGENT))
           break;
-        }
         if (expected == key + 1u) {
           bad = 1;  // another token already holds this slot
           break;
@@ -247,12 +277,8 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
     } else {
       bad = 1;
     }
-    w.keys[t] = key;
-    w.positions[t] = (uint32_t)p;
-    w.hash_at[t] = at;
   }
-  bad = __syncthreads_or(bad);
-  if (tid == 0) w.verdicts[blockIdx.x] = bad ? 0u : 1u;
+  return __syncthreads_or(bad);
 }
 
 // The row slices of thread `tid` for token t (Q rows, then K rows with their
@@ -393,29 +419,120 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
   }
 }
 
-// Apply: one workgroup per token.  Every validation verdict, the token's
-// slot, position and hash-set entry, and the thread's Q/K/V row slices are
-// fetched in one round trip; 64 lanes compute the token's (sin, cos) pairs
-// into LDS; then, if every verdict is valid, the rows.  The token's hash-set
-// entry is cleared either way, so the set is empty for the next command.
+// One launch per command.  Workgroups 0..V-1 each validate one chunk of the
+// command (validate_chunk) and publish the chunk's verdict, tagged with the
+// command's epoch, to every signal copy, then empty their share of the hash
+// table the next command will use; every token workgroup meanwhile loads its
+// token's Q/K/V row slices, walks the page table for its own slot and
+// computes the token's (sin, cos) pairs (validation workgroups do their own
+// token's walk after publishing), then polls one signal copy until all V
+// verdicts carry this command's tag and applies the token only if every
+// chunk is valid.  The decision rests on the polled words alone, so no
+// acquire or release fence is needed.  Last, workgroup 0 waits until every
+// workgroup has tagged its start word and advances the epoch for the next
+// command (stream order, graph replays).
+//
+// No wait can deadlock: workgroups are dispatched in index order on each XCD,
+// so the V <= 256 validation workgroups (the first of the grid) are resident
+// before any waiting workgroup can hold their place, and they wait for
+// nothing before publishing; workgroup 0 waits for start tags only after
+// publishing, so every other workgroup can finish and free its place.  The
+// waits are still bounded (kPollLimit polls); a workgroup that gives up writes
+// nothing and sets the sticky diagnostic word, and workgroup 0 advances the
+// epoch regardless, so a later command never sees this one's verdicts as its
+// own.  Same-address atomics of many workgroups serialize (about 0.1 us each
+// here), so there is no shared counter: every polled word has a few readers
+// and one writer.
 template <bool FP8>
-__global__ __launch_bounds__(kApplyThreads) void append_apply_kernel(AppendArgs a) {
+__global__ __launch_bounds__(kApplyThreads) __attribute__((amdgpu_waves_per_eu(FP8 ? 5 : 6)))
+void append_validated_kernel(AppendArgs a) {
+  __shared__ int32_t s_ip[kValidateLdsBatch + 1], s_last[kValidateLdsBatch];
   __shared__ float s_cos[64], s_sin[64];
+  __shared__ int s_bad;
   const int tid = threadIdx.x;
-  const int t = blockIdx.x;
-  const WsLayout w = ws_layout(a.ws, a.tokens);
-  int bad = 0;
-  for (int b = tid; b < a.validate_blocks; b += kApplyThreads) bad |= w.verdicts[b] != 1u;
-  const uint32_t key = w.keys[t];
-  const int pos = (int)w.positions[t];
-  const uint32_t at = w.hash_at[t];
+  const WsLayout w = ws_layout(a.ws);
+  uint64_t *epoch_word = reinterpret_cast<uint64_t *>(a.ws + kWsEpoch);
+  const uint64_t epoch = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t tag = epoch + 1u;
+  if (tid == 0)
+    __hip_atomic_store(&w.started[blockIdx.x], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  if ((int)blockIdx.x < a.validate_blocks) {
+    // validation workgroup b
+    const int b = blockIdx.x;
+    const int bad = validate_chunk(a, b, tid, s_ip, s_last, w.tables + (epoch & 1u) * kTableSlots);
+    if (tid < kSignalCopies)
+      __hip_atomic_store(&w.signals[tid * kMaxValidateBlocks + b], tag * 2u + (bad ? 0u : 1u),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // empty this chunk's share of the next command's table (the previous
+    // command's, complete in stream order)
+    uint32_t *next = w.tables + ((epoch + 1u) & 1u) * kTableSlots;
+    for (int i = b * kValidateThreads + tid; i < kTableSlots; i += a.validate_blocks * kValidateThreads)
+      next[i] = 0u;
+    if (b != 0) return;
+    // Workgroup 0 advances the epoch once every workgroup has read it.
+    const int grid = (int)gridDim.x;
+    int polls = 0;
+    while (true) {
+      int mine = 1;
+      for (int base = 0; base < grid; base += 4 * kValidateThreads) {
+        uint64_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int g = base + k * kValidateThreads + tid;
+          v[k] = g < grid ? __hip_atomic_load(&w.started[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : tag;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) mine &= v[k] == tag;
+      }
+      if (__syncthreads_and(mine)) break;
+      if (++polls >= kPollLimit) {
+        if (tid == 0)
+          __hip_atomic_store(a.ws + kWsTimedOut, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (tid == 0) __hip_atomic_store(epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // token workgroup t
+  const int t = blockIdx.x - a.validate_blocks;
+  // The token's own slot and position (the validation chunks check the same
+  // walk; nothing is written unless they all pass).
+  int r = 0, pos = 0, off = 0;
+  int64_t page = 0;
+  const int64_t pages = table_pages(a, a.indptr[a.batch]);
+  if (!token_slot(a, t, pages, &r, &pos, &page, &off, a.indptr, a.last)) pos = 0, page = 0;
+  // Row loads after the walk: the validation's dependent loads run while the
+  // memory system is not yet flooded with the command's row traffic, and the
+  // rows still arrive before the verdicts.
   const RowSlices first = load_first_slices(a, t, tid);
   token_sincos(a, pos, tid, s_sin, s_cos);
-  if (tid == 0 && at != kEmptyKey) w.table[at] = 0u;
-  if (__syncthreads_or(bad)) return;
-  // key = page * page_rows + row
-  apply_token<FP8>(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid,
-                   s_sin, s_cos, first);
+  if (tid < 64) {  // wave 0 polls copy t % kSignalCopies
+    const uint64_t *copy = w.signals + (t % kSignalCopies) * kMaxValidateBlocks;
+    int polls = 0, ready = 0, valid = 0;
+    while (true) {
+      int mine_ready = 1, mine_valid = 1;
+      for (int b = tid; b < a.validate_blocks; b += 64) {
+        const uint64_t v = __hip_atomic_load(&copy[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mine_ready &= (v >> 1) == tag;
+        mine_valid &= (int)(v & 1u);
+      }
+      ready = __all(mine_ready);
+      valid = __all(mine_valid);
+      if (ready || ++polls >= kPollLimit) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (tid == 0) {
+      s_bad = !(ready && valid);
+      if (!ready) __hip_atomic_store(a.ws + kWsTimedOut, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (!s_bad) apply_token<FP8>(a, t, page, off, tid, s_sin, s_cos, first);
 }
 
 // Small commands (T <= 64 tokens, <= 4096 page indices): one launch.  Every
@@ -715,15 +832,11 @@ loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
                        stream, a);
     return loom::record_launch(scope, hipGetLastError(), err);
   }
-  // One command (one completion slot) of two stream-ordered kernels.
-  hipLaunchKernelGGL(append_validate_kernel, dim3((unsigned)vblocks), dim3(kValidateThreads), 0,
-                     stream, a);
+  // One launch: the validation workgroups first, then one per token.
+  const uint64_t grid = vblocks + T;
+  hipLaunchKernelGGL(fp8 ? append_validated_kernel<true> : append_validated_kernel<false>,
+                     dim3((unsigned)grid), dim3(kApplyThreads), 0, stream, a);
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess) {
-    hipLaunchKernelGGL(fp8 ? append_apply_kernel<true> : append_apply_kernel<false>,
-                       dim3((unsigned)T), dim3(kApplyThreads), 0, stream, a);
-    e = hipGetLastError();
-  }
   return loom::record_launch(scope, e, err);
 }
 

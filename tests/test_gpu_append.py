@@ -29,6 +29,23 @@ def log(msg):
     sys.stdout.flush()
 
 
+def check_workspace_ready(ws, chunked_before, chunked):
+    """The append workspace after a command: the chunk-validated path (T > 64
+    or more than 4096 page indices) advanced the epoch once, gave up no wait
+    and left the hash table of the next command empty; the small one-launch
+    path leaves it alone.  Layout in u32 words (one for every plan): 64 header
+    words (epoch u64, diagnostic), 8192 u64 start tags, 64 x 256 u64 verdict
+    copies, two 16384-entry hash tables."""
+    w = ws.cpu().numpy().view(np.uint32)
+    epoch = int(w[0]) | int(w[1]) << 32
+    assert w[2] == 0, "a workgroup gave up waiting"
+    assert epoch == chunked_before + chunked, (epoch, chunked_before, chunked)
+    tables = 64 + 2 * (8192 + 256) + 2 * 64 * 256
+    assert len(w) == tables + 2 * 16384
+    nxt = w[tables + (epoch & 1) * 16384: tables + ((epoch & 1) + 1) * 16384]
+    assert not nxt.any(), f"next command's hash table holds {np.count_nonzero(nxt)} entries"
+
+
 class AppendRunner:
     def __init__(self, L, spec, explicit):
         import torch
@@ -38,6 +55,7 @@ class AppendRunner:
                      else prov.plan_bf16_paged_append(spec))
         self.ws = torch.zeros(self.plan.workspace_bytes, dtype=torch.uint8, device="cuda")
         self.queue = L.CommandQueue(torch.cuda.current_stream(), 2)
+        self.epochs = 0  # chunk-validated commands run on self.ws
 
     def bind(self, b, q, k, v, bi, pos, ip, ix, ln, qo, kp, vp):
         L = self.L
@@ -73,16 +91,10 @@ class AppendRunner:
         out = [bf16_host(b.take_read_write(h[n])) for n in ("query_output", "key_pages",
                                                            "value_pages")]
         b.take_read_write(h["workspace"])
-        # the duplicate-slot hash set (after the 64 reserved words and the T
-        # keys, positions and entry indices) must be empty again for the next
-        # command
-        ws = self.ws.cpu().numpy().view(np.uint32)
         T = self.plan.info.tokens
-        slots = 64
-        while slots < 2 * T:
-            slots *= 2
-        table = ws[64 + 3 * T: 64 + 3 * T + slots]
-        assert not table.any(), f"hash set left with {np.count_nonzero(table)} entries"
+        chunked = int(not (T <= 64 and len(ix) <= 4096))
+        check_workspace_ready(self.ws, self.epochs, chunked)
+        self.epochs += chunked
         return out
 
 
@@ -226,24 +238,26 @@ def test_explicit_guards_preserve_all_sentinels(L, oracle, name, bi, pos, ix):
 
 # The two device paths of the explicit-token command: one launch in which
 # every workgroup validates the whole command (T <= 64, <= 4096 page indices),
-# and the parallel validation kernel + apply kernel (anything larger).
+# and one launch in which the first workgroups validate one chunk each and the
+# token workgroups wait for their verdicts (anything larger).
 PATHS = [
     # (name, tokens, page indices of the long request)
     ("fused_small", 3, 100),
-    ("two_kernel", 300, 4200),
-    ("two_kernel_long_table", 300, 9000),
-    ("two_kernel_few_tokens", 3, 4200),
+    ("chunked", 300, 4200),
+    ("chunked_long_table", 300, 9000),
+    ("chunked_few_tokens", 3, 4200),
+    ("chunked_many_tokens", 1500, 4200),
 ]
-BREAKS = ["valid", "duplicate_slot", "batch_index", "position", "page_index", "last_page_len"]
+BREAKS = ["valid", "duplicate_slot", "duplicate_far", "batch_index", "position", "page_index",
+          "last_page_len"]
 
 
-@pytest.mark.parametrize("brk", BREAKS)
-@pytest.mark.parametrize("path,T,long_pages", PATHS, ids=[p[0] for p in PATHS])
-def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, brk):
-    """Each path on valid metadata (against the oracle) and with one guard
-    broken (rope/mod.rs:407-466: every output keeps its sentinels)."""
-    log(f"append path {path} T={T} break={brk}")
-    rng = np.random.default_rng(hash((path, brk)) % 2**32)
+def explicit_case(oracle, seed, T, long_pages, brk):
+    """Explicit-token command inputs over 3 requests (lens 40, long, 500), with
+    one guard broken as `brk` names; the metadata of every break except
+    page_index / last_page_len differs from the valid case only in the
+    batch-index / position arrays."""
+    rng = np.random.default_rng(seed)
     B, hq, hkv = 3, 4, 2
     lens = np.array([40, long_pages * 16 - 3, 500])
     pages = (lens + 15) // 16
@@ -264,6 +278,10 @@ def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, brk):
     if brk == "duplicate_slot":
         k2 = (j + 1) % T
         bi[k2], pos[k2] = bi[j], pos[j]
+    elif brk == "duplicate_far":
+        # first and last token: different validation chunks (256 tokens
+        # each) once T > 256, so the two keys meet only in the shared table
+        bi[T - 1], pos[T - 1] = bi[0], pos[0]
     elif brk == "batch_index":
         bi[j] = B
     elif brk == "position":
@@ -277,6 +295,20 @@ def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, brk):
     v = oracle.bf16_from_f32(rng.standard_normal(T * hkv * 128, dtype=np.float32))
     kp = np.full(pool * 16 * hkv * 128, 0x3F80, np.uint16)
     vp = np.full(pool * 16 * hkv * 128, 0x4000, np.uint16)
+    return dict(B=B, hq=hq, hkv=hkv, pool=pool, indptr=indptr, indices=indices, last=last,
+                bi=bi, pos=pos, q=q, k=k, v=v, kp=kp, vp=vp)
+
+
+@pytest.mark.parametrize("brk", BREAKS)
+@pytest.mark.parametrize("path,T,long_pages", PATHS, ids=[p[0] for p in PATHS])
+def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, brk):
+    """Each path on valid metadata (against the oracle) and with one guard
+    broken (rope/mod.rs:407-466: every output keeps its sentinels)."""
+    log(f"append path {path} T={T} break={brk}")
+    c = explicit_case(oracle, hash((path, brk)) % 2**32, T, long_pages, brk)
+    B, hq, hkv, pool = c["B"], c["hq"], c["hkv"], c["pool"]
+    indptr, indices, last, bi, pos = c["indptr"], c["indices"], c["last"], c["bi"], c["pos"]
+    q, k, v, kp, vp = c["q"], c["k"], c["v"], c["kp"], c["vp"]
     spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv)
     r = AppendRunner(L, spec, True)
     for call in range(2):  # the second command runs over the first one's workspace
@@ -298,6 +330,40 @@ def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, brk):
         rest[rows] = False
         assert np.array_equal(okr[rest], ekr[rest]), call
         assert np.array_equal(ovp, evp), call
+
+
+def test_chunked_path_alternating_valid_and_broken_commands(L, oracle):
+    """One plan and one workspace, commands alternating valid and broken
+    metadata (chunk-validated path, T = 300): a broken command must not be
+    let through by an earlier command's verdicts, and a valid one must not be
+    held back by an earlier broken one (the workspace's epoch tags them)."""
+    T, long_pages = 300, 4200
+    cases = {brk: explicit_case(oracle, 7, T, long_pages, brk)
+             for brk in ("valid", "duplicate_slot", "page_index", "position")}
+    c = cases["valid"]
+    spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, c["B"], c["pool"], c["hq"], c["hkv"])
+    r = AppendRunner(L, spec, True)
+    want = None
+    for i, brk in enumerate(["valid", "duplicate_slot", "valid", "page_index", "position",
+                             "valid", "valid", "duplicate_slot"]):
+        log(f"append alternating command {i}: {brk}")
+        x = cases[brk]
+        qo, okp, ovp = r.run(x["q"], x["k"], x["v"], x["bi"], x["pos"], x["indptr"],
+                             x["indices"], x["last"], x["kp"], x["vp"])
+        if brk != "valid":
+            assert np.all(np.isnan(oracle.bf16_to_f32(qo))), i
+            assert np.array_equal(okp, x["kp"]) and np.array_equal(ovp, x["vp"]), i
+        elif want is None:
+            s = oracle.paged_spec(c["B"], c["pool"], c["hq"], c["hkv"])
+            ekp, evp = c["kp"].copy(), c["vp"].copy()
+            eq = oracle.append_tokens(s, T, c["q"], c["k"], c["v"], c["bi"], c["pos"],
+                                      c["indptr"], c["indices"], c["last"], ekp, evp,
+                                      max_tokens=8192)
+            check_rope(oracle, qo, eq, c["q"], np.repeat(c["pos"], c["hq"]), "query")
+            assert np.array_equal(ovp, evp)
+            want = (qo, okp, ovp)
+        else:
+            assert all(np.array_equal(a, b) for a, b in zip((qo, okp, ovp), want)), i
 
 
 def test_bulk_append_config2_shape(L, oracle):

@@ -143,7 +143,7 @@ def test_full_decode_step_graph(L, oracle):
     exec_.into_bindings()
 
 
-@pytest.mark.parametrize("cap", [200, 5000], ids=["fused_append", "two_kernel_append"])
+@pytest.mark.parametrize("cap", [200, 5000], ids=["fused_append", "chunked_append"])
 def test_serving_loop_replays_one_graph_over_changing_page_tables(L, oracle, cap):
     """A decode step graph (one-token RoPE append + paged decode) captured once
     and replayed over 8 steps while the page table is rewritten in place:
@@ -151,7 +151,8 @@ def test_serving_loop_replays_one_graph_over_changing_page_tables(L, oracle, cap
     last one fills.  The plans are made with LOOM_PLAN_PAGE_INDICES_CAPACITY,
     so the fixed page_indices buffer is a capacity and the entries past
     indptr[B] (left as garbage) are ignored.  Each replay is checked against
-    the oracle's append + decode on host copies of the pools."""
+    the oracle's append + decode on host copies of the pools.  Steps 2 and 5
+    first replay the graph over broken metadata, which must change nothing."""
     import torch
     log("graph serving loop with page-table updates")
     rng = np.random.default_rng(808)
@@ -221,6 +222,17 @@ def test_serving_loop_replays_one_graph_over_changing_page_tables(L, oracle, cap
         t_q.copy_(to_dev_bf16(qn))
         t_k.copy_(to_dev_bf16(kn))
         t_v.copy_(to_dev_bf16(vn))
+        if step in (2, 5):
+            # a replay over broken metadata (last_page_len 17) between valid
+            # ones must leave the pools and the rotated queries untouched
+            qrot_before = bf16_host(qrot)
+            t_ln[0] = 17
+            torch.cuda.synchronize()
+            exec_.launch().wait()
+            assert np.array_equal(bf16_host(t_kp), kp_h) and np.array_equal(bf16_host(t_vp), vp_h)
+            assert np.array_equal(bf16_host(qrot), qrot_before)
+            t_ln.copy_(torch.from_numpy(last))
+            log(f"  step {step}: broken replay left every output untouched")
         torch.cuda.synchronize()
         exec_.launch().wait()
         eq = oracle.append(s, qn, kn, vn, indptr, indices, last, kp_h, vp_h)  # updates pools

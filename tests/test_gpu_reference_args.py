@@ -180,15 +180,15 @@ def run_append(L, queue, plan, spec, tokens, inputs, bi=None, pos=None, workspac
     return [bf16_host(b.take_read_write(h)) for h in (hqo, hkp, hvp)]
 
 
-@pytest.mark.parametrize("form", ["one_token_fused", "one_token_two_kernel", "tokens_fused",
-                                  "tokens_two_kernel"])
+@pytest.mark.parametrize("form", ["one_token_fused", "one_token_chunked", "tokens_fused",
+                                  "tokens_chunked"])
 def test_append_reference_args_equal_workspace_form(L, oracle, form):
     import torch
     log(f"reference-shaped append {form}")
     rng = np.random.default_rng(len(form))
     hq, hkv = 16, 4
-    two = form.endswith("two_kernel")
-    B = 80 if two else 4  # more than 64 tokens: validation kernel + apply kernel
+    chunked = form.endswith("chunked")
+    B = 80 if chunked else 4  # more than 64 tokens: chunked validation
     lens = list(rng.integers(1, 200, size=B))
     prov = L.RopeProvider.load(0)
     queue = L.CommandQueue(torch.cuda.current_stream(), 2)
@@ -198,7 +198,7 @@ def test_append_reference_args_equal_workspace_form(L, oracle, form):
         plan = prov.plan_bf16_paged_append(spec)
         T, bi, pos = B, None, None
     else:
-        T = 70 if two else 6
+        T = 70 if chunked else 6
         bi = rng.integers(0, B, size=T).astype(np.int32)
         lens = [x + 2 for x in lens]
         pos = np.array([rng.integers(0, lens[b]) for b in bi], np.int32)
