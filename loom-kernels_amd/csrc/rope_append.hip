@@ -36,6 +36,9 @@ using loom::fail;
 namespace {
 
 constexpr int kValidateThreads = 256;
+// Tokens per token-validation workgroup (one per thread; 64 and 128 measured
+// no faster).
+constexpr int kTokensPerChunk = 256;
 constexpr int kApplyThreads = 256;
 // Page indices per validation workgroup: at least 2048 (8 per thread), and
 // enough that at most kMaxIndexBlocks workgroups check them.
@@ -53,11 +56,11 @@ __host__ __device__ constexpr int hash_slots(int tokens) {
   while (n < 2 * tokens) n <<= 1;
   return n;
 }
-// Validation workgroups a plan's workspace holds verdicts for.
+// Validation workgroups of a command: at most kMaxIndexBlocks for the page
+// indices, then one per 256 tokens or 256 requests, whichever is more.
 __host__ __device__ constexpr int64_t max_validate_blocks(int64_t tokens, int64_t batch) {
-  const int64_t t = (tokens + 255) / 256, b = (batch + 255) / 256;
-  const int64_t m = t > b ? t : b;
-  return m > kMaxIndexBlocks ? m : kMaxIndexBlocks;
+  const int64_t t = (tokens + kTokensPerChunk - 1) / kTokensPerChunk, b = (batch + 255) / 256;
+  return kMaxIndexBlocks + (t > b ? t : b);
 }
 // Largest batch of the append contracts (the request table is indexed in 32
 // bits; validation chunks cover 256 requests each).
@@ -126,7 +129,8 @@ struct AppendArgs {
   uint16_t *k_pages;
   uint16_t *v_pages;
   uint32_t *ws;  // see WsLayout
-  int32_t index_chunk;      // page indices per validation workgroup
+  int32_t index_chunk;      // page indices per index-validation workgroup
+  int32_t index_blocks;     // index-validation workgroups (the first ones)
   int32_t validate_blocks;  // validation workgroups of this command
   int32_t tokens;
   int32_t batch;
@@ -199,22 +203,50 @@ __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t p
   return slot_of(a, r, p_given, pages, req, pos, page, off, ip, ln);
 }
 
-// Validation of chunk b, all-or-nothing: page indices [b*chunk, (b+1)*chunk)
-// (rope/mod.rs:143-150), requests [b*256, (b+1)*256) (paged_decode/mod.rs:
-// 164-205) and tokens [b*256, (b+1)*256) (paged_append/mod.rs:262-309), one
-// token per thread.  Inserts every valid slot key into the hash set `table`
-// (agent-scope compare-and-swap, so two tokens with one slot meet whichever
-// XCDs they run on; the second finds the first).  Returns nonzero if the
-// chunk is invalid.  `s_ip` / `s_last` hold kValidateLdsBatch + 1 /
-// kValidateLdsBatch words of LDS.
+// Validation of chunk b, all-or-nothing.  Chunks [0, index_blocks) check the
+// page indices [b*chunk, (b+1)*chunk) (rope/mod.rs:143-150), chunk 0 also
+// the table bounds; chunk index_blocks + j checks requests [j*256, (j+1)*256)
+// (paged_decode/mod.rs:164-205) and tokens [j*256, (j+1)*256)
+// (paged_append/mod.rs:262-309), one token per thread, and inserts every
+// valid slot key into the hash set `table` (agent-scope compare-and-swap, so
+// two tokens with one slot meet whichever XCDs they run on; the second finds
+// the first).  The two kinds run in different workgroups so that neither
+// waits for the other's loads.  Returns nonzero if the chunk is invalid.
+// `s_ip` / `s_last` hold kValidateLdsBatch + 1 / kValidateLdsBatch words of
+// LDS.
 __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int tid, int32_t *s_ip,
                                               int32_t *s_last, uint32_t *table) {
-  // This chunk's tokens' requests and positions, the request table into LDS
-  // (batches up to kValidateLdsBatch) and the page indices below are all
-  // loaded in one round trip, so a token's slot is one more.
-  const int t = b * kValidateThreads + tid;
+  int bad = 0;
+  const int32_t ipB = a.indptr[a.batch];
+  const int64_t pages = table_pages(a, ipB);
+  if (b < a.index_blocks) {
+    // page indices: all loads issued before any is tested
+    const int32_t ip0 = a.indptr[0];
+    const int64_t lo = (int64_t)b * a.index_chunk;
+    const int64_t hi = min<int64_t>(lo + a.index_chunk, a.n_indices);
+    int32_t pgs[kIndicesPerValidateBlock / kValidateThreads];
+    for (int64_t base = lo; base < hi; base += kIndicesPerValidateBlock) {
+#pragma unroll
+      for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j) {
+        const int64_t i = base + j * kValidateThreads + tid;
+        pgs[j] = i < hi ? a.indices[i] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j)
+        bad |= (base + j * kValidateThreads + tid < min<int64_t>(hi, pages) &&
+                (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool)) ? 1 : 0;
+    }
+    if (b == 0 && tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
+    return __syncthreads_or(bad);
+  }
+  const int j = b - a.index_blocks;
+  // This chunk's tokens' requests and positions, its requests and the request
+  // table into LDS (batches up to kValidateLdsBatch) in one round trip, so a
+  // token's slot is one more.
+  const int t = j * kTokensPerChunk + tid;
+  const bool has_token = tid < kTokensPerChunk && t < a.tokens;
   int r_given = 0, p_given = 0;
-  if (t < a.tokens) {
+  if (has_token) {
     r_given = a.batch_indices ? a.batch_indices[t] : t;
     p_given = a.batch_indices ? a.positions[t] : 0;
   }
@@ -227,33 +259,13 @@ __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int ti
   }
   const int32_t *ip = lds_table ? s_ip : a.indptr;
   const int32_t *ln = lds_table ? s_last : a.last;
-
-  int bad = 0;
-  // this workgroup's page indices: all loads issued before any is tested
-  const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
-  const int64_t lo = (int64_t)b * a.index_chunk;
-  const int64_t hi = min<int64_t>(lo + a.index_chunk, a.n_indices);
-  int32_t pgs[kIndicesPerValidateBlock / kValidateThreads];
-  const int64_t pages = table_pages(a, ipB);
-  for (int64_t base = lo; base < hi; base += kIndicesPerValidateBlock) {
-#pragma unroll
-    for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j) {
-      const int64_t i = base + j * kValidateThreads + tid;
-      pgs[j] = i < hi ? a.indices[i] : 0;
-    }
-#pragma unroll
-    for (int j = 0; j < kIndicesPerValidateBlock / kValidateThreads; ++j)
-      bad |= (base + j * kValidateThreads + tid < min<int64_t>(hi, pages) &&
-              (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool)) ? 1 : 0;
-  }
-  const int r = b * kValidateThreads + tid;
+  const int r = j * kValidateThreads + tid;
   if (r < a.batch) {
     const int32_t st = a.indptr[r], en = a.indptr[r + 1], tl = a.last[r];
     bad |= (en <= st || tl < 1 || tl > a.page_rows) ? 1 : 0;
   }
-  if (b == 0 && tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
   __syncthreads();  // the LDS request table
-  if (t < a.tokens) {
+  if (has_token) {
     int rr = 0, p = 0, off = 0;
     int64_t pg = 0;
     if (slot_of(a, r_given, p_given, pages, &rr, &p, &pg, &off, ip, ln)) {
@@ -284,7 +296,7 @@ __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int ti
 // The row slices of thread `tid` for token t (Q rows, then K rows with their
 // V row; rows tid / 16 + 16 i), loaded before the command's validity is known
 // so the loads overlap the metadata round trips and one another.
-constexpr int kPreloadRows = 4;  // row iterations preloaded: Hq + Hkv <= 64
+constexpr int kPreloadRows = 3;  // row iterations preloaded: Hq + Hkv <= 48
 struct RowSlice {
   u32x4 x, v;
 };
@@ -381,16 +393,18 @@ __device__ __forceinline__ void apply_row(const AppendArgs &a, int t, int64_t pa
       }
       uint8_t *kp = reinterpret_cast<uint8_t *>(a.k_pages) + kv_dst + c * 8;
       uint8_t *vp = reinterpret_cast<uint8_t *>(a.v_pages) + kv_dst + c * 8;
-      *reinterpret_cast<loom_dev::u32x2 *>(kp) = k8;
-      *reinterpret_cast<loom_dev::u32x2 *>(vp) = v8;
+      __builtin_nontemporal_store(k8, reinterpret_cast<loom_dev::u32x2 *>(kp));
+      __builtin_nontemporal_store(v8, reinterpret_cast<loom_dev::u32x2 *>(vp));
       return;
     }
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       o[e] = (uint32_t)f32_to_bf16(y[2 * e]) | ((uint32_t)f32_to_bf16(y[2 * e + 1]) << 16);
-    *reinterpret_cast<u32x4 *>(dst + c * 8) = o;
-    if (is_kv) *reinterpret_cast<u32x4 *>(a.v_pages + kv_dst + c * 8) = vv;
+    // Streaming stores: nothing in this command reads them back, and dirty
+    // L2 lines would only be written back at the end of the kernel.
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4 *>(dst + c * 8));
+    if (is_kv) __builtin_nontemporal_store(vv, reinterpret_cast<u32x4 *>(a.v_pages + kv_dst + c * 8));
   }
 }
 
@@ -405,7 +419,7 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
   int row = tid >> 4;
 #pragma unroll
   for (int it = 0; it < kPreloadRows + 1; ++it) {
-    // rows beyond the preloaded iterations (Hq + Hkv > 64) load in a loop
+    // rows beyond the preloaded iterations (Hq + Hkv > 48) load in a loop
     if (it == kPreloadRows) {
       for (; row < rows; row += kApplyThreads / 16) {
         const RowSlice one = load_slice(a, t, row, c);
@@ -433,7 +447,7 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
 // command (stream order, graph replays).
 //
 // No wait can deadlock: workgroups are dispatched in index order on each XCD,
-// so the V <= 256 validation workgroups (the first of the grid) are resident
+// so the V <= 320 validation workgroups (the first of the grid) are resident
 // before any waiting workgroup can hold their place, and they wait for
 // nothing before publishing; workgroup 0 waits for start tags only after
 // publishing, so every other workgroup can finish and free its place.  The
@@ -444,7 +458,7 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
 // here), so there is no shared counter: every polled word has a few readers
 // and one writer.
 template <bool FP8>
-__global__ __launch_bounds__(kApplyThreads) __attribute__((amdgpu_waves_per_eu(FP8 ? 5 : 6)))
+__global__ __launch_bounds__(kApplyThreads) __attribute__((amdgpu_waves_per_eu(6)))
 void append_validated_kernel(AppendArgs a) {
   __shared__ int32_t s_ip[kValidateLdsBatch + 1], s_last[kValidateLdsBatch];
   __shared__ float s_cos[64], s_sin[64];
@@ -820,10 +834,11 @@ loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
   const uint64_t chunk = std::max<uint64_t>(
       kIndicesPerValidateBlock,
       (per_block + kIndicesPerValidateBlock - 1) / kIndicesPerValidateBlock * kIndicesPerValidateBlock);
-  const uint64_t vblocks = std::max<uint64_t>(
-      {1, (n_idx + chunk - 1) / chunk, (T + kValidateThreads - 1) / kValidateThreads,
-       (B + kValidateThreads - 1) / kValidateThreads});
+  const uint64_t iblocks = std::max<uint64_t>(1, (n_idx + chunk - 1) / chunk);
+  const uint64_t vblocks = iblocks + std::max<uint64_t>({1, (T + kTokensPerChunk - 1) / kTokensPerChunk,
+                                                         (B + kValidateThreads - 1) / kValidateThreads});
   a.index_chunk = (int32_t)chunk;
+  a.index_blocks = (int32_t)iblocks;
   a.validate_blocks = (int32_t)vblocks;
   hipStream_t stream = scope->queue->stream;
   if (T <= (uint64_t)kFusedMaxTokens && (int64_t)L(6)->numel <= kFusedMaxIndices) {

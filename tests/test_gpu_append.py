@@ -40,7 +40,7 @@ def check_workspace_ready(ws, chunked_before, chunked):
     epoch = int(w[0]) | int(w[1]) << 32
     assert w[2] == 0, "a workgroup gave up waiting"
     assert epoch == chunked_before + chunked, (epoch, chunked_before, chunked)
-    tables = 64 + 2 * (8192 + 256) + 2 * 64 * 256
+    tables = 64 + 2 * (8192 + 320) + 2 * 64 * 320
     assert len(w) == tables + 2 * 16384
     nxt = w[tables + (epoch & 1) * 16384: tables + ((epoch & 1) + 1) * 16384]
     assert not nxt.any(), f"next command's hash table holds {np.count_nonzero(nxt)} entries"
