@@ -857,9 +857,10 @@ void loom_rope_append_plan_get_info(const loom_rope_append_plan_t *plan,
                                     loom_rope_append_plan_info_t *info);
 
 /* Bf16RopePagedKvAppendArgs / ...TokensArgs, rope/mod.rs:963-1047, plus the
- * caller-owned validation workspace (u8, plan.workspace_bytes, zero-filled
- * once; every command leaves its duplicate-slot hash set empty, i.e. zero,
- * for the next).  batch_indices/positions are unused
+ * caller-owned validation workspace (u8, plan.workspace_bytes, zero before its
+ * first command and not written by the caller afterwards; every command
+ * leaves it ready for the next; one workspace may serve several append plans
+ * in stream order).  batch_indices/positions are unused
  * (pass {0,0}) for the one-token form. */
 typedef struct loom_rope_append_args {
   loom_handle_t query;         /* Read<bf16> [T, Hq, 128] */
