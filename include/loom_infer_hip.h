@@ -390,8 +390,11 @@ typedef enum loom_paged_decode_algorithm {
    * boundary merge through log2-LSE states in a second kernel. */
   LOOM_PAGED_DECODE_BALANCED_SPLIT_KV = 1,
   /* Small page capacity (max_total_pages <= 128, teams option 0): one
-   * workgroup of 4-16 waves per (request, kv-head, tile), one launch, no
-   * split. */
+   * workgroup of 4-16 waves per (request, kv-head, tile), one launch.  When
+   * few such workgroups would stream long requests (max_total_pages / B >=
+   * 16 and at most 2 * CUs workgroups after splitting), each request's pages
+   * split over 2-8 workgroups of 4 waves (plan info `teams`), whose states a
+   * second kernel merges. */
   LOOM_PAGED_DECODE_DIRECT = 2
 } loom_paged_decode_algorithm_t;
 
@@ -414,11 +417,12 @@ typedef struct loom_paged_decode_plan_options {
 typedef struct loom_paged_decode_plan_info {
   loom_paged_decode_spec_t spec;
   int32_t algorithm;
-  uint32_t teams;
+  uint32_t teams;            /* balanced: page ranges; direct: workgroups per
+                                (request, kv-head, tile) when split, else 0 */
   uint32_t group_tile;       /* query heads per wave column block */
   uint32_t group_tiles;      /* ceil(group / group_tile) */
   uint64_t max_total_pages;
-  uint64_t state_slots;      /* teams + batch */
+  uint64_t state_slots;      /* balanced: teams + batch; split direct: teams * batch */
   uint64_t workspace_bytes;  /* header_bytes + state_slots * Hq * 132 FP32 */
   uint64_t header_bytes;     /* (batch + 2) int64 page prefixes, 256-byte rounded */
   uint32_t block_threads;

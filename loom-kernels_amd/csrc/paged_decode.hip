@@ -156,6 +156,11 @@ struct DecodeArgs {
   // FP8 E4M3 pages: device [k_scale, v_scale] (K = fp8 * k_scale, V = fp8 *
   // v_scale); null for BF16 pages.
   const float *__restrict__ kv_scales;
+  // Direct kernel: workgroups per (request, kv-head, tile).  1: the workgroup
+  // writes O and LSE; more: each writes the state of its share of the
+  // request's blocks to states[((split * B + r) * Hq + qh) * kStateStride]
+  // and paged_decode_direct_merge_kernel combines them.
+  int32_t splits;
 };
 
 // decode.rs:233-246: indptr[B] is the page_indices length (or, for plans made
@@ -810,10 +815,12 @@ stream_done:
 }
 
 // Direct decode for small page tables: one workgroup per (request, kv-head,
-// tile), its 4 waves taking pages w, w+4, ... of the request and merging in
+// tile), its W waves taking pages w, w+W, ... of the request and merging in
 // LDS, so the request finishes in one launch (no scan, no split states, no
 // merge kernel).  Used when the plan's page capacity is small, where the call
-// is launch- and latency-bound.
+// is launch- and latency-bound.  With a.splits > 1 each request's blocks are
+// cut into a.splits equal ranges, one workgroup each, which write states for
+// paged_decode_direct_merge_kernel instead of O and LSE.
 template <int GT, int W = kWaves>
 struct DirectSmem {
   uint8_t ktile[W][kKTileBytes];
@@ -845,13 +852,24 @@ __global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, quad = lane >> 4;
-  const int kvh = (int)(blockIdx.x % a.hkv);
-  const int rest = (int)(blockIdx.x / a.hkv);
+  const int split = (int)(blockIdx.x % a.splits);
+  const int head = (int)(blockIdx.x / a.splits);
+  const int kvh = head % a.hkv;
+  const int rest = head / a.hkv;
   const int gt = rest % a.members;  // members = group tiles for this kernel
   const int r = rest / a.members;
 
   const int g_base = gt * GT;
   const int gcount = min(GT, a.group - g_base);
+  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
+  // Split workgroups always write their state (a poisoned normalizer for
+  // a request that fails a guard), so the merge never reads a stale one.
+  auto state_of = [&](int g) {
+    return a.states + (((int64_t)split * a.batch + r) * a.hq + qh_base + g) * kStateStride;
+  };
+  auto poison = [&]() {
+    if (a.splits > 1 && tid < gcount) state_of(tid)[1] = kPoisonNormalizer;
+  };
   WaveDecoder<GT> w{a, sm.ktile[wave], sm.qfrag[wave], lane, col, quad, kvh};
   // One round trip for the guard words (decode.rs:233-246 global, :430-478
   // per request), the query tile and, when the page-index array has at most
@@ -867,41 +885,45 @@ __global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_
   }
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
   const int32_t st = uni(a.indptr[r]), en = uni(a.indptr[r + 1]), tl = uni(a.last[r]);
-  if (ip0 != 0 || !batch_pages_ok(a, ipB)) return;
+  if (ip0 != 0 || !batch_pages_ok(a, ipB)) return poison();
   const int cnt = request_pages(a, st, en, tl, ipB);
-  if (cnt == 0) return;
+  if (cnt == 0) return poison();
 
-  // this wave's 16-row blocks: request-local positions wave + W*i (block b
-  // is block b % (page_rows / 16) of the request's page b / (page_rows / 16))
-  const int mine = cnt > wave ? (cnt - wave + W - 1) / W : 0;
+  // this split's blocks [lo, hi) of the request; this wave's: request-local
+  // positions lo + wave + W*i (block b is block b % (page_rows / 16) of the
+  // request's page b / (page_rows / 16))
+  const int lo = (int)((int64_t)cnt * split / a.splits);
+  const int hi = (int)((int64_t)cnt * (split + 1) / a.splits);
+  const int mine = hi - lo > wave ? (hi - lo - wave + W - 1) / W : 0;
   const int tl_rows = last_block_rows(tl);
   const int bmask = (1 << a.blocks_lg) - 1;
   bool bad = false;
   {
     int idx = 0;
     if (small_table) {
-      const int j = st + ((wave + W * lane) >> a.blocks_lg);  // < 128 for this wave's blocks
+      const int j = st + ((lo + wave + W * lane) >> a.blocks_lg);  // < 128 for this wave's blocks
       const int lo = __shfl(tbl0, j & 63, 64), hi = __shfl(tbl1, j & 63, 64);
       if (lane < min(mine, 64)) idx = j < 64 ? lo : hi;
     } else if (lane < min(mine, 64)) {
-      idx = a.indices[st + ((wave + W * lane) >> a.blocks_lg)];
+      idx = a.indices[st + ((lo + wave + W * lane) >> a.blocks_lg)];
     }
     w.store_q(qr);
     w.reset();
     for (int s0 = 0; s0 < mine; s0 += 64) {
       if (s0 > 0)
-        idx = lane < min(mine - s0, 64) ? a.indices[st + ((wave + W * (s0 + lane)) >> a.blocks_lg)]
-                                        : 0;
+        idx = lane < min(mine - s0, 64)
+                  ? a.indices[st + ((lo + wave + W * (s0 + lane)) >> a.blocks_lg)]
+                  : 0;
       const int n = min(mine - s0, 64);
       const int ok = (idx >= 0 && (int64_t)idx < a.pool) ? 1 : 0;
       bad |= __ballot(lane < n && !ok) != 0;
       auto tok_of = [&](int i) {
         const int j = min(i, n - 1);
-        return block_elem(a, __builtin_amdgcn_readlane(idx, j), (wave + W * (s0 + j)) & bmask);
+        return block_elem(a, __builtin_amdgcn_readlane(idx, j), (lo + wave + W * (s0 + j)) & bmask);
       };
       auto rows_of = [&](int i) {
         if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
-        return wave + W * (s0 + i) == cnt - 1 ? tl_rows : 16;
+        return lo + wave + W * (s0 + i) == cnt - 1 ? tl_rows : 16;
       };
       w.template stream<FP8>(n, tok_of, rows_of);
     }
@@ -915,11 +937,10 @@ __global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_
     stash_acc(sm.wacc[wave][col], w.acc, quad);
   }
   // An invalid page index anywhere in the request keeps its sentinels.
-  if (__syncthreads_or(bad)) return;
+  if (__syncthreads_or(bad)) return poison();
 
   // Workgroup merge of the W wave states (a wave without pages has max -inf
   // and weight 0).
-  const int64_t qh_base = (int64_t)kvh * a.group + g_base;
   for (int idx = tid; idx < GT * 128; idx += W * 64) {
     const int g = idx >> 7, d = idx & 127;
     if (g >= gcount) continue;
@@ -933,11 +954,65 @@ __global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_
       L = fmaf(sm.wl[wv][g], f, L);
       O = fmaf(sm.wacc[wv][g][d], f, O);
     }
+    if (a.splits > 1) {  // this split's state: max, normalizer, unnormalized O
+      // (a split without blocks has max -inf: weight and O zero)
+      const bool empty = M == -INFINITY;
+      float *ss = state_of(g);
+      ss[4 + d] = empty ? 0.f : O;
+      if (d == 0) {
+        ss[0] = M;
+        ss[1] = empty ? 0.f : L;
+      }
+      continue;
+    }
     float o = O / L;
     if constexpr (FP8) o *= v_scale;
     a.out[((int64_t)r * a.hq + qh_base + g) * 128 + d] = f32_to_bf16(o);
     if (d == 0) a.lse[(int64_t)r * a.hq + qh_base + g] = M + __log2f(L);
   }
+}
+
+// Combines the a.splits states of one (request, query head) written by the
+// direct kernel into O and log2-LSE (128 lanes, one per output column, in
+// split order); a poisoned state leaves the request's sentinels.
+constexpr int kMaxDirectSplits = 8;
+constexpr uint64_t kMaxDirectSplitsPlanned = kMaxDirectSplits;
+__global__ __launch_bounds__(128) void paged_decode_direct_merge_kernel(DecodeArgs a) {
+  const int tid = threadIdx.x;
+  const int r = blockIdx.x / a.hq;
+  const int qh = blockIdx.x % a.hq;
+  float ms[kMaxDirectSplits], ls[kMaxDirectSplits], xs[kMaxDirectSplits];
+#pragma unroll
+  for (int u = 0; u < kMaxDirectSplits; ++u) {
+    ms[u] = -INFINITY;
+    ls[u] = 0.f;
+    xs[u] = 0.f;
+    if (u < a.splits) {
+      const float *ss = a.states + (((int64_t)u * a.batch + r) * a.hq + qh) * kStateStride;
+      ms[u] = ss[0];
+      ls[u] = ss[1];
+      xs[u] = ss[4 + tid];
+    }
+  }
+  float M = -INFINITY;
+  bool poisoned = false;
+#pragma unroll
+  for (int u = 0; u < kMaxDirectSplits; ++u) {
+    M = fmaxf(M, ms[u]);
+    poisoned |= ls[u] < 0.0f;
+  }
+  if (poisoned) return;
+  float l = 0.f, o = 0.f;
+#pragma unroll
+  for (int u = 0; u < kMaxDirectSplits; ++u) {
+    const float f = fast_exp2(ms[u] - M);
+    l = fmaf(ls[u], f, l);
+    o = fmaf(xs[u], f, o);
+  }
+  float ov = o / l;
+  if (a.kv_scales) ov *= a.kv_scales[1];  // FP8 pages: V's scale
+  a.out[((int64_t)r * a.hq + qh) * 128 + tid] = f32_to_bf16(ov);
+  if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(l);
 }
 
 // Merges the states of one (request, query head) whose pages span several
@@ -1206,6 +1281,7 @@ DecodeArgs single_args(const loom_single_decode_spec_t &s, uint32_t gtiles, uint
   a.blocks_lg = 0;
   a.page_elems = (int64_t)16 * a.hkv * 128;
   a.block_elems = 16 * a.row_elems;
+  a.splits = 1;
   return a;
 }
 }  // namespace
@@ -1305,8 +1381,21 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
   if (opt.teams == 0 && max_pages <= LOOM_DECODE_DIRECT_MAX_PAGES) {
     // More waves per request when a request may hold more pages; 16-wave
     // workgroups only where the page step fits 128 VGPRs (tiles of <= 2 heads).
-    const uint32_t waves = max_pages <= 32 ? 4 : gtile <= 2 ? 16 : 8;
-    const uint64_t grid = B * gtiles * hkv;
+    uint32_t waves = max_pages <= 32 ? 4 : gtile <= 2 ? 16 : 8;
+    const uint64_t heads = B * gtiles * hkv;
+    // Few (request, kv-head, tile) workgroups with long requests leave most
+    // CUs idle and stream each request through one CU: split each request's
+    // blocks over 2-8 workgroups of 4 waves (at least 8 pages each on
+    // average, at most two workgroups per CU), combined by a merge kernel.
+    // Config 1 (32 workgroups, 64 pages each): 10.3 -> 8.1 us per call.
+    uint64_t splits = 1;
+    for (uint64_t s = kMaxDirectSplitsPlanned; s >= 2; s /= 2)
+      if (max_pages / B >= s * 8 && heads * s <= 2 * (uint64_t)provider->dev.cus) {
+        splits = s;
+        waves = 4;
+        break;
+      }
+    const uint64_t grid = heads * splits;
     if (grid > (uint64_t)INT32_MAX || B * hq > (uint64_t)INT32_MAX)
       return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "paged batch-decode", grid);
     auto *p = new loom_paged_decode_plan;
@@ -1314,12 +1403,13 @@ loom_status_t loom_decode_provider_plan_bf16_paged_batch(
     loom_paged_decode_plan_info_t &i = p->info;
     i.spec = *spec;
     i.algorithm = LOOM_PAGED_DECODE_DIRECT;
-    i.teams = 0;
     i.group_tile = gtile;
     i.group_tiles = (uint32_t)gtiles;
     i.max_total_pages = max_pages;
-    i.state_slots = 0;
-    i.workspace_bytes = 256;  // unused by this algorithm; kept for a uniform operand list
+    i.teams = (uint32_t)(splits > 1 ? splits : 0);
+    i.state_slots = splits > 1 ? splits * B : 0;
+    // (unused without splits; kept for a uniform operand list)
+    i.workspace_bytes = splits > 1 ? splits * B * hq * kStateStride * 4 : 256;
     i.header_bytes = 0;
     i.block_threads = waves * 64;
     i.grid_blocks = (uint32_t)grid;
@@ -1525,6 +1615,7 @@ loom_status_t paged_decode_enqueue_impl(const loom_paged_decode_plan_t *plan,
   // the direct kernel indexes (request, tile, kv-head) and takes the tile count here
   a.members = (int32_t)(direct ? pi.group_tiles : s.num_kv_heads * pi.group_tiles);
   a.teams = (int32_t)pi.teams;
+  a.splits = direct && pi.teams > 1 ? (int32_t)pi.teams : 1;
   a.pool = (int64_t)s.max_num_pages;
   a.n_indices = (int64_t)l(4)->numel;
   a.indices_capacity = (pi.flags & LOOM_PLAN_PAGE_INDICES_CAPACITY) ? 1 : 0;
@@ -1546,7 +1637,13 @@ loom_status_t paged_decode_enqueue_impl(const loom_paged_decode_plan_t *plan,
       launch_direct<true>(pi, g3, bd, stream, a);
     else
       launch_direct<false>(pi, g3, bd, stream, a);
-    return loom::record_launch(scope, hipGetLastError(), err);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && a.splits > 1) {
+      hipLaunchKernelGGL(paged_decode_direct_merge_kernel,
+                         dim3((unsigned)(s.batch_size * s.num_query_heads)), dim3(128), 0, stream, a);
+      e = hipGetLastError();
+    }
+    return loom::record_launch(scope, e, err);
   }
   if (fp8)
     launch_split<true>(pi, g3, b3, stream, a);

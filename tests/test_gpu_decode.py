@@ -298,11 +298,21 @@ def test_plan_selection_and_rejections(L):
     p = prov.plan_bf16_paged_batch(small)
     assert p.algorithm == "direct" and p.info.grid_blocks == 4 * 4
     assert p.info.block_threads == 256
-    mid = L.Bf16PagedBatchDecodeSpec(2, 100, 8, 8, 128, 16)
+    mid = L.Bf16PagedBatchDecodeSpec(4, 60, 8, 8, 128, 16)
     p = prov.plan_bf16_paged_batch(mid)
     assert p.algorithm == "direct" and p.info.block_threads == 1024  # 16 waves, 1-head tiles
-    p = prov.plan_bf16_paged_batch(L.Bf16PagedBatchDecodeSpec(2, 100, 32, 8, 128, 16))
+    assert p.info.teams == 0 and p.info.grid_blocks == 4 * 8
+    p = prov.plan_bf16_paged_batch(L.Bf16PagedBatchDecodeSpec(4, 60, 32, 8, 128, 16))
     assert p.algorithm == "direct" and p.info.block_threads == 512
+    # long requests over few workgroups: each request's blocks split over
+    # 2-8 workgroups of 4 waves (teams = the split count), states merged by a
+    # second kernel
+    p = prov.plan_bf16_paged_batch(L.Bf16PagedBatchDecodeSpec(2, 100, 8, 8, 128, 16))
+    assert p.algorithm == "direct" and p.info.teams == 4 and p.info.block_threads == 256
+    assert p.info.grid_blocks == 2 * 8 * 4 and p.info.state_slots == 4 * 2
+    assert p.info.workspace_bytes == 4 * 2 * 8 * 132 * 4
+    c1 = prov.plan_bf16_paged_batch(L.Bf16PagedBatchDecodeSpec(1, 128, 32, 32, 128, 16))
+    assert c1.algorithm == "direct" and c1.info.teams == 8 and c1.info.grid_blocks == 32 * 8
     p = prov.plan_bf16_paged_batch(L.Bf16PagedBatchDecodeSpec(2, 129, 32, 8, 128, 16))
     assert p.algorithm == "balanced_split_kv"
     p = prov.plan_bf16_paged_batch(small, teams=3)
