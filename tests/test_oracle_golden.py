@@ -262,9 +262,9 @@ def test_split_k_state_layout_known_answer(oracle):
     # crates/loom-infer/src/attention/single_decode/tests.rs:276-301
     s = oracle.single_spec(2, 1, 1)
     q = np.zeros(128, np.uint16)
-    q[0] = oracle.bf16_from_f32(np.float32(math.sqrt(128.0)))
+    q[0] = oracle.bf16_from_f32(np.float32(math.sqrt(128.0)))[0]
     k = np.zeros(256, np.uint16)
-    k[128] = oracle.bf16_from_f32(np.float32(1.0))
+    k[128] = oracle.bf16_from_f32(np.float32(1.0))[0]
     v = np.concatenate([np.full(128, oracle.bf16_from_f32(np.float32(1.5))),
                         np.full(128, oracle.bf16_from_f32(np.float32(-2.0)))]).astype(np.uint16)
     _, _, ws = oracle.split_k(s, 2, q, k, v)
@@ -308,7 +308,7 @@ def test_rope_closed_form_d6_rot4(oracle):
     c1, s1 = math.cos(a1), math.sin(a1)
     exp = [f32(1) * f32(c0) - f32(3) * f32(s0), f32(2) * f32(c1) - f32(4) * f32(s1),
            f32(3) * f32(c0) + f32(1) * f32(s0), f32(4) * f32(c1) + f32(2) * f32(s1)]
-    assert list(qo[:4]) == [int(oracle.bf16_from_f32(f32(x))) for x in exp]
+    assert list(qo[:4]) == [int(oracle.bf16_from_f32(np.array([x], f32))[0]) for x in exp]
     assert list(qo[4:]) == list(vals[4:]) and np.array_equal(qo, ko)
 
 
