@@ -557,10 +557,24 @@ template <bool FP8>
 __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(AppendArgs a) {
   __shared__ float s_cos[64], s_sin[64];
   __shared__ uint32_t s_keys[kFusedMaxTokens];
-  __shared__ int s_pos[kFusedMaxTokens];
   const int tid = threadIdx.x;
   const int t = blockIdx.x;
   const RowSlices first = load_first_slices(a, t, tid);
+  // Wave 1 takes this workgroup's token position straight from the metadata
+  // and computes its (sin, cos) pairs while wave 0 walks the validation's
+  // dependent loads.  Nothing is written unless the validation passes, and
+  // then this position is the validated one (explicit tokens: positions[t];
+  // one-token form: kv_len - 1 of request t).
+  if (tid >= 64 && tid < 128) {
+    int pos_t;
+    if (a.batch_indices) {
+      pos_t = a.positions[t];
+    } else {
+      const int32_t st = a.indptr[t], en = a.indptr[t + 1], tl = a.last[t];
+      pos_t = (en - st - 1) * a.page_rows + tl - 1;
+    }
+    token_sincos(a, pos_t, tid - 64, s_sin, s_cos);
+  }
 
   int bad = 0;
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
@@ -587,7 +601,6 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
     else
       bad = 1;
     s_keys[tid] = key;
-    s_pos[tid] = p;
   }
   bad = __syncthreads_or(bad);
   if (bad) return;
@@ -597,8 +610,6 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
     const uint32_t k = s_keys[tid];
     for (int j = 0; j < tid; ++j) dup |= s_keys[j] == k;
   }
-  const int pos = s_pos[t];
-  token_sincos(a, pos, tid, s_sin, s_cos);
   if (__syncthreads_or(dup)) return;
   const uint32_t key = s_keys[t];
   // key = page * page_rows + row
