@@ -556,7 +556,7 @@ void append_validated_kernel(AppendArgs a) {
 template <bool FP8>
 __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(AppendArgs a) {
   __shared__ float s_cos[64], s_sin[64];
-  __shared__ uint32_t s_keys[kFusedMaxTokens];
+  __shared__ __align__(16) uint32_t s_keys[kFusedMaxTokens];
   const int tid = threadIdx.x;
   const int t = blockIdx.x;
   const RowSlices first = load_first_slices(a, t, tid);
@@ -604,11 +604,16 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
   }
   bad = __syncthreads_or(bad);
   if (bad) return;
-  // duplicate physical slots: token i against every earlier token
+  // duplicate physical slots: token i against every earlier token, four
+  // keys per LDS read
   int dup = 0;
   if (tid < a.tokens) {
     const uint32_t k = s_keys[tid];
-    for (int j = 0; j < tid; ++j) dup |= s_keys[j] == k;
+    for (int j = 0; j < tid; j += 4) {
+      const u32x4 kk = *reinterpret_cast<const u32x4 *>(&s_keys[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dup |= (j + e < tid && kk[e] == k) ? 1 : 0;
+    }
   }
   if (__syncthreads_or(dup)) return;
   const uint32_t key = s_keys[t];
