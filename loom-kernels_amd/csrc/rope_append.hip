@@ -44,7 +44,7 @@ constexpr int kApplyThreads = 256;
 // enough that at most kMaxIndexBlocks workgroups check them.
 constexpr int kIndicesPerValidateBlock = 2048;
 constexpr int kMaxIndexBlocks = 64;
-// Batches whose request table the validation kernel keeps in LDS.
+// Batches whose request table the validation workgroups keep in LDS.
 constexpr int kValidateLdsBatch = 2048;
 constexpr int kMaxTokens = LOOM_APPEND_MAX_TOKENS_EXTENDED;
 // Commands this small run as one fused launch (every workgroup validates).
