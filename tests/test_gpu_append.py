@@ -439,3 +439,63 @@ def test_large_position_stays_finite_and_matches(L, oracle):
     want_k = ekp.reshape(-1, 128)[row:row + hkv].reshape(-1)
     check_rope(oracle, got_k, want_k, k, np.full(hkv, kv_len - 1), "key")
     assert np.array_equal(ovp, evp)
+
+
+def _many_requests_case(oracle, rng, B, T, hq, hkv):
+    """B requests of 1-40 existing tokens (more when T needs them), T distinct
+    (request, position) tokens among them, seeded shuffled page table."""
+    lens = rng.integers(1, max(41, 4 * T // B), size=B)
+    pages = (lens + 15) // 16
+    pool = int(pages.sum()) + 7
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
+    last = (lens - (pages - 1) * 16).astype(np.int32)
+    flat = rng.choice(int(lens.sum()), size=T, replace=False)
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    bi = (np.searchsorted(starts, flat, side="right") - 1).astype(np.int32)
+    pos = (flat - starts[bi]).astype(np.int32)
+    q = oracle.bf16_from_f32(rng.standard_normal(T * hq * 128, dtype=np.float32))
+    k = oracle.bf16_from_f32(rng.standard_normal(T * hkv * 128, dtype=np.float32))
+    v = oracle.bf16_from_f32(rng.standard_normal(T * hkv * 128, dtype=np.float32))
+    return pool, indptr, indices, last, bi, pos, q, k, v
+
+
+@pytest.mark.parametrize("B,T", [(3000, 300), (64, 8192)], ids=["batch3000_table_in_memory",
+                                                               "tokens8192_grid_over_residency"])
+@pytest.mark.parametrize("brk", ["valid", "duplicate_far"])
+def test_chunked_path_large_batch_and_max_tokens(L, oracle, B, T, brk):
+    """The chunk-validated path where the validation workgroups read the
+    request table from memory (B > 2048 requests), and at the contract's
+    largest command (T = 8192 tokens: 8192 + V workgroups, more than the
+    device holds at once, so later token workgroups start only after earlier
+    ones finish); valid commands against the oracle, a duplicate pair in the
+    first and last chunk leaving every output untouched."""
+    log(f"append chunked B={B} T={T} break={brk}")
+    rng = np.random.default_rng(B * 7 + T)
+    hq, hkv = 4, 2
+    pool, indptr, indices, last, bi, pos, q, k, v = _many_requests_case(oracle, rng, B, T, hq, hkv)
+    if brk == "duplicate_far":
+        bi[T - 1], pos[T - 1] = bi[0], pos[0]
+    kp = np.full(pool * 16 * hkv * 128, 0x3F80, np.uint16)
+    vp = np.full(pool * 16 * hkv * 128, 0x4000, np.uint16)
+    spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv)
+    r = AppendRunner(L, spec, True)
+    for call in range(2):
+        qo, okp, ovp = r.run(q, k, v, bi, pos, indptr, indices, last, kp, vp)
+        if brk != "valid":
+            assert np.all(np.isnan(oracle.bf16_to_f32(qo))), call
+            assert np.array_equal(okp, kp) and np.array_equal(ovp, vp), call
+            continue
+        s = oracle.paged_spec(B, pool, hq, hkv)
+        ekp, evp = kp.copy(), vp.copy()
+        eq = oracle.append_tokens(s, T, q, k, v, bi, pos, indptr, indices, last, ekp, evp,
+                                  max_tokens=8192)
+        check_rope(oracle, qo, eq, q, np.repeat(pos, hq), "query")
+        assert np.array_equal(ovp, evp), call
+        slots = [(indices[indptr[b] + p // 16], p % 16) for b, p in zip(bi, pos)]
+        rows = np.array([(pg * 16 + off) * hkv + h for pg, off in slots for h in range(hkv)])
+        okr, ekr = okp.reshape(-1, 128), ekp.reshape(-1, 128)
+        check_rope(oracle, okr[rows], ekr[rows], k, np.repeat(pos, hkv), "key rows")
+        rest = np.ones(len(okr), bool)
+        rest[rows] = False
+        assert np.array_equal(okr[rest], ekr[rest]), call
