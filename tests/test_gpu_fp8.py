@@ -18,7 +18,7 @@ import pytest
 
 from gpu_util import (bf16_host, compare_decode, nan_bf16, ragged_table, seeded_normal_bf16,
                       to_dev_bf16, to_dev_i32)
-from test_gpu_append import within_one_ulp
+from test_gpu_append import check_rope, within_one_ulp
 from test_gpu_layout import to_hnd
 
 pytestmark = pytest.mark.gpu
@@ -211,3 +211,39 @@ def test_fp8_append_matches_oracle_then_decodes(L, oracle, explicit):
     dspec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, kv_dtype="fp8_e4m3")
     out, lse, _ = run_decode(L, dspec, {"teams": 5}, qd, gk, gv, ip, ix, last, [ks, vs])
     log(f"  decode after append {compare_decode(oracle, out, lse, *ref)}")
+
+
+def test_fp8_append_chunked_path_matches_oracle(L, oracle):
+    """The chunk-validated append (T > 64 tokens) on FP8 E4M3 pages against
+    the FP8 oracle (same bar as the small path: V bytes exact, K bytes within
+    one code where the encode's input differs by the RoPE rounding)."""
+    log("fp8 append chunked path")
+    rng = np.random.default_rng(97)
+    B, hq, hkv = 4, 8, 2
+    lens = [40, 300, 17, 129]
+    pool = sum((n + 15) // 16 for n in lens) + 4
+    ip, ix, last = ragged_table(rng, lens, pool)
+    T = 120
+    flat = rng.choice(int(sum(lens)), size=T, replace=False)
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    bi = (np.searchsorted(starts, flat, side="right") - 1).astype(np.int32)
+    pos = (flat - starts[bi]).astype(np.int32)
+    spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv, kv_dtype="fp8_e4m3")
+    q = seeded_normal_bf16(oracle, rng, T * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, T * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, T * hkv * 128)
+    n = pool * 16 * hkv * 128
+    kp8, vp8 = random_fp8(rng, n, 0x5F), random_fp8(rng, n, 0x5F)
+    ks, vs = 0.02, 0.015
+    ek, ev = kp8.copy(), vp8.copy()
+    eq = oracle.append_tokens_fp8(oracle.paged_spec(B, pool, hq, hkv), T, q, k, v, bi, pos, ip,
+                                  ix, last, ek, ev, ks, vs, max_tokens=8192)
+    qo, gk, gv = run_append(L, spec, True, q, k, v, bi, pos, ip, ix, last, kp8, vp8, [ks, vs])
+    check_rope(oracle, qo, eq, q, np.repeat(pos, hq), "query")
+    assert np.array_equal(gv, ev), "V bytes"
+    diff = gk != ek
+    if diff.any():
+        step = np.abs(gk[diff].astype(np.int32) - ek[diff].astype(np.int32))
+        same_sign = (gk[diff] & 0x80) == (ek[diff] & 0x80)
+        log(f"  K bytes differing: {int(diff.sum())} of {T * hkv * 128} written")
+        assert np.all(same_sign & (step == 1)) and diff.sum() <= max(4, T * hkv * 128 // 2000)

@@ -142,3 +142,35 @@ def test_unknown_layout_is_rejected(L):
     with pytest.raises(L.PlanError) as e:
         L.DecodeProvider.load(0).plan_bf16_paged_batch(spec)
     assert e.value.variant == "InvalidOption" and e.value.operand == "kv_layout"
+
+
+def test_append_hnd_chunked_path_writes_the_same_slots(L, oracle):
+    """The chunk-validated append (T > 64 tokens) on HND pages writes the
+    same bytes as on NHD pages."""
+    log("append HND chunked path")
+    rng = np.random.default_rng(29)
+    B, hq, hkv = 5, 8, 2
+    lens = np.array([40, 300, 17, 129, 64])
+    pages = (lens + 15) // 16
+    pool = int(pages.sum()) + 4
+    ip = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    ix = rng.permutation(pool)[: ip[-1]].astype(np.int32)
+    last = (lens - (pages - 1) * 16).astype(np.int32)
+    T = 100
+    flat = rng.choice(int(lens.sum()), size=T, replace=False)
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    bi = (np.searchsorted(starts, flat, side="right") - 1).astype(np.int32)
+    pos = (flat - starts[bi]).astype(np.int32)
+    nhd_spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv)
+    hnd_spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv, kv_layout="HND")
+    q = seeded_normal_bf16(oracle, rng, T * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, T * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, T * hkv * 128)
+    kp = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    vp = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    q1, k1, v1 = AppendRunner(L, nhd_spec, True).run(q, k, v, bi, pos, ip, ix, last, kp, vp)
+    q2, k2, v2 = AppendRunner(L, hnd_spec, True).run(q, k, v, bi, pos, ip, ix, last,
+                                                     to_hnd(kp, pool, hkv), to_hnd(vp, pool, hkv))
+    assert not np.array_equal(k1, kp)
+    assert np.array_equal(q1, q2)
+    assert np.array_equal(to_nhd(k2, pool, hkv), k1) and np.array_equal(to_nhd(v2, pool, hkv), v1)

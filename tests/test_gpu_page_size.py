@@ -283,3 +283,33 @@ def test_fp8_prefill_equals_bf16_on_widened_pages(L, oracle, P):
         ref = oracle.prefill(oracle.prefill_spec(B, nnz, pool, hq, hkv), q,
                              oracle.bf16_from_f32(kd), oracle.bf16_from_f32(vd), qo, ip, ix, last)
         compare_decode(oracle, o3, l3, *ref)
+
+
+@pytest.mark.parametrize("P", [32, 64])
+def test_append_page_size_chunked_path_writes_the_same_slots(L, oracle, P):
+    """The chunk-validated append (T > 64 tokens) on P-row pages equals the
+    16-row command on the table naming the same bytes."""
+    log(f"append page size {P} chunked path")
+    rng = np.random.default_rng(300 + P)
+    B, hq, hkv = 4, 8, 2
+    lens = [40, 3 * P + 5, 2 * P, 70]
+    pool = sum((n + P - 1) // P for n in lens) + 3
+    ip, ix, last = table(rng, lens, pool, P)
+    ip16, ix16, last16 = to_rows16(ip, ix, last, P)
+    m = P // 16
+    T = 100
+    flat = rng.choice(int(sum(lens)), size=T, replace=False)
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    bi = (np.searchsorted(starts, flat, side="right") - 1).astype(np.int32)
+    pos = (flat - starts[bi]).astype(np.int32)
+    spec_p = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv, kv_page_size=P)
+    spec_16 = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool * m, hq, hkv)
+    q = seeded_normal_bf16(oracle, rng, T * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, T * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, T * hkv * 128)
+    kp = seeded_normal_bf16(oracle, rng, pool * P * hkv * 128)
+    vp = seeded_normal_bf16(oracle, rng, pool * P * hkv * 128)
+    q1, k1, v1 = AppendRunner(L, spec_16, True).run(q, k, v, bi, pos, ip16, ix16, last16, kp, vp)
+    assert not np.array_equal(k1, kp)
+    q2, k2, v2 = AppendRunner(L, spec_p, True).run(q, k, v, bi, pos, ip, ix, last, kp, vp)
+    assert np.array_equal(q1, q2) and np.array_equal(k1, k2) and np.array_equal(v1, v2)
