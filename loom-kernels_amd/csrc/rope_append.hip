@@ -669,6 +669,10 @@ static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t token
     return fail(err, LOOM_PLAN_STATE_COUNT_OVERFLOW, "RoPE");
   if (states > (uint64_t)INT32_MAX || tokens > (uint64_t)kMaxTokens)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE", states);
+  // The validation chunks and the workspace layout cover batches up to
+  // kMaxBatch requests.
+  if (s.batch_size > (uint64_t)kMaxBatch)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE batch", s.batch_size);
   // Slot keys are page*page_rows+offset in 32 bits.
   const uint64_t page_rows = s.page_size ? s.page_size : loom::kPageSize;
   if (page_rows != 16 && page_rows != 32 && page_rows != 64)
@@ -863,8 +867,11 @@ loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
                        stream, a);
     return loom::record_launch(scope, hipGetLastError(), err);
   }
-  // One launch: the validation workgroups first, then one per token.
+  // One launch: the validation workgroups first, then one per token (the
+  // plan's bounds keep both within the workspace layout).
   const uint64_t grid = vblocks + T;
+  if (vblocks > (uint64_t)kMaxValidateBlocks || grid > (uint64_t)kMaxGrid)
+    return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE validation grid", grid);
   hipLaunchKernelGGL(fp8 ? append_validated_kernel<true> : append_validated_kernel<false>,
                      dim3((unsigned)grid), dim3(kApplyThreads), 0, stream, a);
   hipError_t e = hipGetLastError();

@@ -499,3 +499,16 @@ def test_chunked_path_large_batch_and_max_tokens(L, oracle, B, T, brk):
         rest = np.ones(len(okr), bool)
         rest[rows] = False
         assert np.array_equal(okr[rest], ekr[rest]), call
+
+
+def test_append_plan_rejects_batches_beyond_the_validation_layout(L):
+    """Append plans take batches of at most 65536 requests (the validation
+    chunks and the fixed workspace layout cover that many); more is a plan
+    error, before any enqueue."""
+    prov = L.RopeProvider.load(0)
+    prov.plan_bf16_paged_append_tokens(
+        L.Bf16RopePagedKvAppendTokensSpec.extended(100, 65536, 70000, 4, 2))
+    with pytest.raises(L.PlanError) as e:
+        prov.plan_bf16_paged_append_tokens(
+            L.Bf16RopePagedKvAppendTokensSpec.extended(100, 65537, 70000, 4, 2))
+    assert e.value.variant == "StateCountOutOfRange"
