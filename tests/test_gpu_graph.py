@@ -23,15 +23,17 @@ def log(msg):
     print(msg, flush=True)
 
 
-def test_decode_graph_replays_match_eager_and_oracle(L, oracle):
+@pytest.mark.parametrize("B,hq,hkv,lens,teams", [
+    (5, 32, 8, [40, 1000, 17, 3000, 256], 7),  # balanced split-KV + merge kernel
+    (1, 32, 32, [1024], 0),                    # direct plan split over 8 workgroups + merge
+], ids=["balanced", "split_direct"])
+def test_decode_graph_replays_match_eager_and_oracle(L, oracle, B, hq, hkv, lens, teams):
     """Replays with eager work and host synchronization between them; every
     replay is compared with the eager result (no memset nodes are captured; the
     split-KV workspace is scratch and needs no clearing between replays)."""
     import torch
-    log("graph decode replay")
+    log(f"graph decode replay B={B} teams={teams}")
     rng = np.random.default_rng(21)
-    B, hq, hkv = 5, 32, 8
-    lens = [40, 1000, 17, 3000, 256]
     pool = sum((x + 15) // 16 for x in lens) + 8
     indptr, indices, last = ragged_table(rng, lens, pool)
     q = seeded_normal_bf16(oracle, rng, B * hq * 128)
@@ -39,7 +41,9 @@ def test_decode_graph_replays_match_eager_and_oracle(L, oracle):
     v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
     ref_o, ref_l = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v, indptr,
                                        indices, last)
-    r = DecodeRunner(L, B, pool, hq, hkv, teams=7)
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
+    if teams == 0:
+        assert r.plan.algorithm == "direct" and r.plan.info.teams == 8
     eager_o, eager_l = r.run(q, k, v, indptr, indices, last)
     compare_decode(oracle, eager_o, eager_l, ref_o, ref_l)
 
