@@ -158,8 +158,9 @@ def test_invalid_page_in_split_request(L, oracle, teams):
 
 
 @pytest.mark.parametrize("lens,teams", [([100, 50, 300, 20, 64], 0), ([100, 50, 300, 20, 64], 1),
-                                        ([100, 50, 300, 20, 64], 5), ([20, 5, 40, 3, 30], 0)],
-                         ids=["balanced", "one_team", "five_teams", "direct"])
+                                        ([100, 50, 300, 20, 64], 5), ([20, 5, 40, 3, 30], 0),
+                                        ([500, 400, 300, 200], 0)],
+                         ids=["balanced", "one_team", "five_teams", "direct", "split_direct"])
 def test_invalid_request_leaves_sentinels(L, oracle, lens, teams):
     """Requests failing the per-request guard (decode.rs:430-478: last page
     length outside 1..16) contribute no pages; the others are computed as
@@ -178,12 +179,14 @@ def test_invalid_request_leaves_sentinels(L, oracle, lens, teams):
     bad_last[1] = 0
     bad_last[3] = 17
     r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
+    if len(lens) == 4:  # each request over two 4-wave workgroups, states merged
+        assert r.plan.algorithm == "direct" and r.plan.info.teams == 2
     out, lse = r.run(q, k, v, indptr, indices, bad_last)
     o = oracle.bf16_to_f32(out).reshape(B, hq * 128)
     l = lse.reshape(B, hq)
     for rq in (1, 3):
         assert np.all(np.isnan(o[rq])) and np.all(np.isnan(l[rq]))
-    for rq in (0, 2, 4):
+    for rq in range(0, B, 2):
         compare_decode(oracle, out.reshape(B, -1)[rq], l[rq], ref_out.reshape(B, -1)[rq],
                        ref_lse.reshape(B, hq)[rq])
 
