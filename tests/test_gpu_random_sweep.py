@@ -97,3 +97,35 @@ def test_append_random_shapes(L, oracle, seed):
     rest = np.ones(len(okr), bool)
     rest[rows] = False
     assert np.array_equal(okr[rest], ekr[rest])
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_paged_prefill_random_shapes(L, oracle, seed):
+    """Paged causal prefill: random group sizes, query rows up to the KV
+    length of each request, 16- or 64-column tiles (the wide tiles forced on
+    shapes the planner would give row tiles)."""
+    from gpu_util import PrefillRunner
+    rng = np.random.default_rng(3000 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 3, 4, 8]))
+    B = int(rng.integers(1, 6))
+    kv_lens = rng.integers(1, 700, size=B)
+    qo_lens = np.array([int(rng.integers(1, min(k, 160) + 1)) for k in kv_lens])
+    tile_cols = int(rng.choice([0, 16, 64]))
+    pages = (kv_lens + 15) // 16
+    pool = int(pages.sum()) + int(rng.integers(0, 6))
+    log(f"prefill sweep {seed}: B={B} hq={hq} hkv={hkv} qo={qo_lens.tolist()} "
+        f"kv={kv_lens.tolist()} tile_cols={tile_cols}")
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
+    last = (kv_lens - (pages - 1) * 16).astype(np.int32)
+    qo = np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32)
+    nnz = int(qo[-1])
+    q = seeded_normal_bf16(oracle, rng, nnz * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    ref = oracle.prefill(oracle.prefill_spec(B, nnz, pool, hq, hkv), q, k, v, qo, indptr,
+                         indices, last)
+    r = PrefillRunner(L, B, nnz, pool, hq, hkv, tile_cols=tile_cols)
+    out, lse = r.run(q, k, v, qo, indptr, indices, last)
+    log(f"  plan {r.plan.algorithm} {compare_decode(oracle, out, lse, *ref)}")
