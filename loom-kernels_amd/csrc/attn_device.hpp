@@ -17,12 +17,20 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// half::bf16::from_f32 (round to nearest even, quiet NaN).
+// half::bf16::from_f32: round to nearest even; a NaN keeps its sign and top
+// payload bits with the quiet bit set ((bits >> 16) | 0x40).  gfx950's
+// v_cvt_pk_bf16_f32 gives exactly these bits for every one of the 2^32 FP32
+// inputs (checked exhaustively on MI355X against the integer form
+// ((bits + 0x7fff + ((bits >> 16) & 1)) >> 16, NaN as above)); the integer
+// form compiles to a branch per element, which costs more than the stores
+// it feeds in the latency-bound kernels.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_pack(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return (uint16_t)(x >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ u32x4 load16(const uint16_t *p) {

@@ -452,7 +452,7 @@ __device__ __forceinline__ void store_out_row(uint16_t *o, const f32x4 (&acc)[8]
         x0 *= v_scale;
         x1 *= v_scale;
       }
-      w[e] = (uint32_t)f32_to_bf16(x0) | ((uint32_t)f32_to_bf16(x1) << 16);
+      w[e] = bf16x2_pack(x0, x1);
     }
     *reinterpret_cast<u32x4 *>(o + i * 8) = u32x4{w[0], w[1], w[2], w[3]};
   }

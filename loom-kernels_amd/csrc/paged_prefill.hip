@@ -561,8 +561,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
       u32x4 o;
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2)
-        o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv * v_scale) |
-                ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv * v_scale) << 16);
+        o[e2] = bf16x2_pack(w.acc[2 * e2][r4] * inv * v_scale, w.acc[2 * e2 + 1][r4] * inv * v_scale);
       *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
     }
     if (quad == 0) a.lse[row_head] = w.m_run + __log2f(L);
@@ -615,8 +614,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     u32x4 o;
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2)
-      o[e2] = (uint32_t)f32_to_bf16(w.acc[2 * e2][r4] * inv * v_scale) |
-              ((uint32_t)f32_to_bf16(w.acc[2 * e2 + 1][r4] * inv * v_scale) << 16);
+      o[e2] = bf16x2_pack(w.acc[2 * e2][r4] * inv * v_scale, w.acc[2 * e2 + 1][r4] * inv * v_scale);
     *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
   }
   if (quad == 0) a.lse[row_head] = M + __log2f(L);

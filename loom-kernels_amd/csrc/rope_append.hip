@@ -153,13 +153,6 @@ struct AppendArgs {
   float inv_freq[64];
 };
 
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return (uint16_t)(x >> 16);
-}
-
 // Request and token geometry shared by both kernels.  Returns false for any
 // invalid mapping; on success fills the physical slot.
 // Entries of page_indices that belong to the page table: all of them, or the
@@ -400,7 +393,7 @@ __device__ __forceinline__ void apply_row(const AppendArgs &a, int t, int64_t pa
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      o[e] = (uint32_t)f32_to_bf16(y[2 * e]) | ((uint32_t)f32_to_bf16(y[2 * e + 1]) << 16);
+      o[e] = loom_dev::bf16x2_pack(y[2 * e], y[2 * e + 1]);
     // Streaming stores: nothing in this command reads them back, and dirty
     // L2 lines would only be written back at the end of the kernel.
     __builtin_nontemporal_store(o, reinterpret_cast<u32x4 *>(dst + c * 8));

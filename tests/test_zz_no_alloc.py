@@ -51,6 +51,7 @@ def test_no_alloc_matches_workspace_entry_point(L, oracle):
     cases = [  # (lens, teams): the second call is smaller than the first
         ([3000, 40, 8000, 17, 1000, 2049, 5, 600], 0),
         ([700, 33, 1500], 0),
+        ([1024], 0),  # the direct algorithm split over 8 workgroups (split states)
         ([90, 15], 0),  # the direct algorithm (no split states)
     ]
     for i, (lens, teams) in enumerate(cases):
@@ -62,11 +63,13 @@ def test_no_alloc_matches_workspace_entry_point(L, oracle):
         v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
         log(f"no-alloc call {i}: batch {B}, {int(ip[-1])} pages")
         r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
+        if lens == [1024]:
+            assert r.plan.algorithm == "direct" and r.plan.info.teams == 8
         want_o, want_l = r.run(q, k, v, ip, ix, ln)
         got_o, got_l = no_alloc_call(L, r, q, k, v, ip, ix, ln)
         assert np.array_equal(got_o, want_o), f"call {i}: output"
         assert np.array_equal(got_l, want_l), f"call {i}: lse"
-        log(f"  {r.plan.algorithm}, workspace {r.plan.workspace_bytes} B: bit-equal")
+        log(f"  {r.plan.algorithm} (teams {r.plan.info.teams}), workspace {r.plan.workspace_bytes} B: bit-equal")
     torch.cuda.synchronize()
 
 
