@@ -244,11 +244,17 @@ struct PrefillWave {
   // have no valid rows and move no bytes).  page_tok(i): element offset of
   // block i's first row (kv-head 0); rows_of(i): valid rows (0 past the end);
   // lt_of(i): logical token of its first row.  All wave-uniform.
-  template <int D, bool FP8, class PageTok, class RowsOf, class LtOf>
-  __device__ void stream(int n, PageTok page_tok, RowsOf rows_of, LtOf lt_of) {
-    PrefillBuf<FP8> buf[D];
+  template <int D, bool FP8, class PageTok, class RowsOf>
+  __device__ void prime(PrefillBuf<FP8> (&buf)[D], PageTok page_tok, RowsOf rows_of) {
 #pragma unroll
     for (int j = 0; j < D - 1; ++j) load_prefill_page(buf[j], a, page_tok(j), rows_of(j), lane, kvh);
+  }
+
+  // `primed`: the loads of pages 0..D-2 are already in flight in `buf`.
+  template <int D, bool FP8, class PageTok, class RowsOf, class LtOf>
+  __device__ void stream(PrefillBuf<FP8> (&buf)[D], bool primed, int n, PageTok page_tok,
+                         RowsOf rows_of, LtOf lt_of) {
+    if (!primed) prime<D, FP8>(buf, page_tok, rows_of);
     int i = 0;
     while (true) {
 #pragma unroll
@@ -361,6 +367,16 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   // together; the guards are applied after the scan that locates this tile.
   const int32_t qo0 = a.qo[0], qoB = a.qo[a.batch];
   const int32_t ip0 = a.indptr[0], ipB = a.indptr[a.batch];
+  // A page-index array of at most 128 entries (the reference's shapes) is
+  // loaded whole in the same round trip, two words per lane: the request's
+  // page indices and their check then come from registers, so the query tile
+  // and the first K/V blocks share the second round trip.
+  const bool small_table = !RAGGED && !SH && a.n_indices <= 128;
+  int tbl0 = 0, tbl1 = 0;
+  if (small_table) {
+    if (lane < a.n_indices) tbl0 = a.indices[lane];
+    if (lane + 64 < a.n_indices) tbl1 = a.indices[lane + 64];
+  }
 
   // Locate the request owning this tile: prefix of the requests' tile counts.
   // Paged (prefill.rs:303-313): rows belong to the requests before the first
@@ -492,50 +508,82 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   const int mine = SH ? npages : uni(npages > wave ? (npages - wave + W - 1) / W : 0);
   auto blk = [&](int i) { return SH ? i : wave + W * i; };
 
-  // One round trip for: every page index of the request (the reference
-  // rejects the whole request; strided over the workgroup, the verdict is
-  // read after the stream), the query tile (wave 0, into LDS) and each wave's
-  // first block of page indices.
+  // Every page index of the request is checked (the reference rejects the
+  // whole request; the verdict is read after the stream) and each wave takes
+  // its first block of page indices: from the registers of a small table, else
+  // in one round trip with the query tile (wave 0).
   bool bad = false;
   int idx = 0;
   if constexpr (!RAGGED) {
-    for (int i = tid; i < pe - ps; i += W * 64) {
-      const int32_t x = a.indices[ps + i];
-      bad |= x < 0 || (int64_t)x >= a.pool;
+    if (small_table) {
+      // entries ps..pe-1 of the table (pe <= n_indices <= 128)
+      const int j0 = lane, j1 = lane + 64;
+      bad = (j0 >= ps && j0 < pe && (tbl0 < 0 || (int64_t)tbl0 >= a.pool)) ||
+            (j1 >= ps && j1 < pe && (tbl1 < 0 || (int64_t)tbl1 >= a.pool));
+      const int j = ps + (blk(lane) >> a.blocks_lg);  // < pe for this wave's blocks
+      const int x0 = __shfl(tbl0, j & 63, 64), x1 = __shfl(tbl1, j & 63, 64);
+      if (lane < min(mine, 64)) idx = j < 64 ? x0 : x1;
+    } else {
+      for (int i = tid; i < pe - ps; i += W * 64) {
+        const int32_t x = a.indices[ps + i];
+        bad |= x < 0 || (int64_t)x >= a.pool;
+      }
+      idx = lane < min(mine, 64) ? a.indices[ps + (blk(lane) >> a.blocks_lg)] : 0;
     }
-    idx = lane < min(mine, 64) ? a.indices[ps + (blk(lane) >> a.blocks_lg)] : 0;
   }
-  if (SH || wave == 0) {
-    const uint16_t *qp = a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 +
-                         quad * 8;
-    u32x4 qr[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qr[c] = colv ? load16(qp + c * 32) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) sm.qfrag[SH ? wave : 0][c][lane] = qr[c];
-  }
-  __syncthreads();
 
   PrefillWave w{a, sm.qfrag[SH ? wave : 0], lane, col, quad, kvh};
   w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
   w.reset();
-  for (int s0 = 0; s0 < mine; s0 += 64) {
-    const int n = uni(min(mine - s0, 64));
-    if (!RAGGED && s0 > 0)
-      idx = lane < n ? a.indices[ps + (blk(s0 + lane) >> a.blocks_lg)] : 0;
-    const int ok = (RAGGED || (idx >= 0 && (int64_t)idx < a.pool)) ? 1 : 0;
-    auto page_tok = [&](int i) {
-      if constexpr (RAGGED) return ((int64_t)ps + (int64_t)blk(s0 + i) * 16) * a.hkv * 128;
-      const int j = uni(min(i, n - 1));
-      const int b = blk(s0 + j);
-      return (int64_t)__builtin_amdgcn_readlane(idx, j) * a.page_rows * a.hkv * 128 +
-             (int64_t)((b & ((1 << a.blocks_lg) - 1)) * 16) * a.row_elems;
-    };
-    auto rows_of = [&](int i) {
-      if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
-      return uni(blk(s0 + i) == req_pages - 1 ? (int)tl : 16);
-    };
-    auto lt_of = [&](int i) { return (int64_t)blk(s0 + i) * 16; };
+  // The current block of up to 64 page indices (one per lane) of this wave.
+  int s0 = 0;
+  int n = uni(min(mine, 64));
+  int ok = (RAGGED || (idx >= 0 && (int64_t)idx < a.pool)) ? 1 : 0;
+  auto page_tok = [&](int i) {
+    if constexpr (RAGGED) return ((int64_t)ps + (int64_t)blk(s0 + i) * 16) * a.hkv * 128;
+    const int j = uni(min(i, n - 1));
+    const int b = blk(s0 + j);
+    return (int64_t)__builtin_amdgcn_readlane(idx, j) * a.page_rows * a.hkv * 128 +
+           (int64_t)((b & ((1 << a.blocks_lg) - 1)) * 16) * a.row_elems;
+  };
+  auto rows_of = [&](int i) {
+    if (i >= n || !__builtin_amdgcn_readlane(ok, i)) return 0;
+    return uni(blk(s0 + i) == req_pages - 1 ? (int)tl : 16);
+  };
+  auto lt_of = [&](int i) { return (int64_t)blk(s0 + i) * 16; };
+  // The query tile's loads and the first blocks' loads go out together,
+  // before the barrier that publishes the tile.  They follow the first index
+  // block, so no wait for it holds back the page loads.  Lanes past the tile's
+  // last column load row 0 of Q (it exists, since a tile was found) and store
+  // zeros: with no branch around the loads, no wait at a join stalls them.
+  // (the empty asm pins the index check here, ahead of the query loads: sunk
+  // below them, its wait for a loaded index block would also wait for Q)
+  asm volatile("" ::"v"(ok) : "memory");
+  u32x4 qr[4];
+  if (SH || wave == 0) {
+    const uint16_t *qp =
+        colv ? a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 + quad * 8
+             : a.q + quad * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qr[c] = load16(qp + c * 32);
+  }
+  constexpr int D = SH ? 1 : prefill_depth(W);
+  PrefillBuf<FP8> buf[D];
+  if constexpr (!SH) {
+    if (mine > 0) w.template prime<D, FP8>(buf, page_tok, rows_of);
+  }
+  if (SH || wave == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sm.qfrag[SH ? wave : 0][c][lane] = colv ? qr[c] : u32x4{0, 0, 0, 0};
+  }
+  __syncthreads();
+
+  for (; s0 < mine; s0 += 64) {
+    if (s0 > 0) {
+      n = uni(min(mine - s0, 64));
+      if constexpr (!RAGGED) idx = lane < n ? a.indices[ps + (blk(s0 + lane) >> a.blocks_lg)] : 0;
+      ok = (RAGGED || (idx >= 0 && (int64_t)idx < a.pool)) ? 1 : 0;
+    }
     if constexpr (SH) {
       __shared__ u32x4 ring[2][2][16][17];
       // causal end of this wave's last column (0: the wave's tile is empty)
@@ -545,7 +593,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
               : 0;
       w.template stream_shared<FP8>(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
     } else {
-      w.template stream<prefill_depth(W), FP8>(n, page_tok, rows_of, lt_of);
+      w.template stream<D, FP8>(buf, s0 == 0, n, page_tok, rows_of, lt_of);
     }
   }
 
