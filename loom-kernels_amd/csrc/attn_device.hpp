@@ -112,6 +112,22 @@ __device__ __forceinline__ uint32_t fp8_e4m3_from_f32(float x) {
   return s | code;
 }
 
+// OR of `p` over a workgroup of W waves with one barrier (HIP's
+// __syncthreads_or takes three and an LDS atomic): each wave publishes its
+// ballot in slots[wave].  `slots` belongs to one call site, and that site must
+// not run twice without a barrier in between (a fast wave would overwrite a
+// word that a slow one has yet to read).
+template <int W>
+__device__ __forceinline__ bool block_or(bool p, uint32_t (&slots)[W]) {
+  const uint32_t any_lane = __builtin_amdgcn_ballot_w64(p) != 0 ? 1u : 0u;
+  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = any_lane;
+  __syncthreads();
+  uint32_t any = 0;
+#pragma unroll
+  for (int i = 0; i < W; ++i) any |= slots[i];
+  return any != 0;
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

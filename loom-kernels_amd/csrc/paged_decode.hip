@@ -828,6 +828,7 @@ struct DirectSmem {
   float wm[W][GT];
   float wl[W][GT];
   float wacc[W][GT][128];
+  uint32_t bad[W];  // per-wave invalid-page-index flags
 };
 
 // W waves per workgroup (4 for the tiniest tables; 8 when a request may hold
@@ -937,7 +938,7 @@ __global__ __launch_bounds__(W * 64, (direct_waves_per_eu<GT, W>())) void paged_
     stash_acc(sm.wacc[wave][col], w.acc, quad);
   }
   // An invalid page index anywhere in the request keeps its sentinels.
-  if (__syncthreads_or(bad)) return poison();
+  if (block_or(bad, sm.bad)) return poison();
 
   // Workgroup merge of the W wave states (a wave without pages has max -inf
   // and weight 0).

@@ -110,6 +110,7 @@ struct PrefillSmem {
   u32x4 qfrag[SH ? W : 1][4][64];  // MFMA B fragments of 16 query columns (per wave: SH)
   float m[W][16];      // per-wave running max (log2 domain) per column
   float l[W][16];      // per-wave normalizer per column
+  uint32_t bad[W];     // per-wave invalid-page-index flags
   f32x4 red[SH ? 1 : (W / 2 > 0 ? W / 2 : 1)][4][64];  // tree-sum staging (row tiles only)
 };
 
@@ -600,7 +601,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   if constexpr (SH) {
     // No cross-wave merge: each wave finishes its own tile.
     const float L = quad_sum(w.l_run);
-    if (__syncthreads_or(bad) || !colv) return;
+    if (block_or(bad, sm.bad) || !colv) return;
     const float inv = 1.0f / L;
     const int64_t row_head = (int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh;
     uint16_t *orow = a.out + row_head * 128 + quad * 32;
@@ -623,7 +624,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     sm.m[wave][col] = w.m_run;
     sm.l[wave][col] = l_tot;
   }
-  if (__syncthreads_or(bad)) return;
+  if (block_or(bad, sm.bad)) return;
   float M = -INFINITY;
 #pragma unroll
   for (int wv = 0; wv < W; ++wv) M = fmaxf(M, sm.m[wv][col]);

@@ -550,6 +550,7 @@ template <bool FP8>
 __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(AppendArgs a) {
   __shared__ float s_cos[64], s_sin[64];
   __shared__ __align__(16) uint32_t s_keys[kFusedMaxTokens];
+  __shared__ uint32_t s_bad[kApplyThreads / 64], s_dup[kApplyThreads / 64];
   const int tid = threadIdx.x;
   const int t = blockIdx.x;
   const RowSlices first = load_first_slices(a, t, tid);
@@ -595,8 +596,7 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
       bad = 1;
     s_keys[tid] = key;
   }
-  bad = __syncthreads_or(bad);
-  if (bad) return;
+  if (loom_dev::block_or(bad != 0, s_bad)) return;
   // duplicate physical slots: token i against every earlier token, four
   // keys per LDS read
   int dup = 0;
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
       for (int e = 0; e < 4; ++e) dup |= (j + e < tid && kk[e] == k) ? 1 : 0;
     }
   }
-  if (__syncthreads_or(dup)) return;
+  if (loom_dev::block_or(dup != 0, s_dup)) return;
   const uint32_t key = s_keys[t];
   // key = page * page_rows + row
   apply_token<FP8>(a, t, key / (uint32_t)a.page_rows, (int)(key % (uint32_t)a.page_rows), tid, s_sin,
