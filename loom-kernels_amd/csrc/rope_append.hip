@@ -206,9 +206,10 @@ __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t p
 // the first).  The two kinds run in different workgroups so that neither
 // waits for the other's loads.  Returns nonzero if the chunk is invalid.
 // `s_ip` / `s_last` hold kValidateLdsBatch + 1 / kValidateLdsBatch words of
-// LDS.
+// LDS; `s_or` one word per wave for the verdict.
 __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int tid, int32_t *s_ip,
-                                              int32_t *s_last, uint32_t *table) {
+                                              int32_t *s_last, uint32_t *table,
+                                              uint32_t (&s_or)[kValidateThreads / 64]) {
   int bad = 0;
   const int32_t ipB = a.indptr[a.batch];
   const int64_t pages = table_pages(a, ipB);
@@ -230,7 +231,7 @@ __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int ti
                 (pgs[j] < 0 || (int64_t)pgs[j] >= a.pool)) ? 1 : 0;
     }
     if (b == 0 && tid == 0) bad |= table_bounds_bad(a, ip0, ipB) ? 1 : 0;
-    return __syncthreads_or(bad);
+    return loom_dev::block_or(bad != 0, s_or) ? 1 : 0;
   }
   const int j = b - a.index_blocks;
   // This chunk's tokens' requests and positions, its requests and the request
@@ -283,7 +284,7 @@ __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int ti
       bad = 1;
     }
   }
-  return __syncthreads_or(bad);
+  return loom_dev::block_or(bad != 0, s_or) ? 1 : 0;
 }
 
 // The row slices of thread `tid` for token t (Q rows, then K rows with their
@@ -454,6 +455,7 @@ template <bool FP8>
 __global__ __launch_bounds__(kApplyThreads) __attribute__((amdgpu_waves_per_eu(6)))
 void append_validated_kernel(AppendArgs a) {
   __shared__ int32_t s_ip[kValidateLdsBatch + 1], s_last[kValidateLdsBatch];
+  __shared__ uint32_t s_or[kValidateThreads / 64];
   __shared__ float s_cos[64], s_sin[64];
   __shared__ int s_bad;
   const int tid = threadIdx.x;
@@ -467,7 +469,7 @@ void append_validated_kernel(AppendArgs a) {
   if ((int)blockIdx.x < a.validate_blocks) {
     // validation workgroup b
     const int b = blockIdx.x;
-    const int bad = validate_chunk(a, b, tid, s_ip, s_last, w.tables + (epoch & 1u) * kTableSlots);
+    const int bad = validate_chunk(a, b, tid, s_ip, s_last, w.tables + (epoch & 1u) * kTableSlots, s_or);
     if (tid < kSignalCopies)
       __hip_atomic_store(&w.signals[tid * kMaxValidateBlocks + b], tag * 2u + (bad ? 0u : 1u),
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
