@@ -733,7 +733,7 @@ typedef struct loom_paged_prefill_args {
  * every output untouched; a request with an invalid page range, last-page
  * length, page index or qo_len > kv_len keeps its sentinels, and so does every
  * request after the first malformed qo_indptr range.  Q, K, V and O must be
- * 16-byte aligned (the reference asks 4: this kernel moves 16-byte rows). */
+ * 4-byte aligned, as in the reference (prefill.rs:2496-2503, 3015-3029). */
 loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
                                          loom_command_scope_t *scope,
                                          const loom_paged_prefill_args_t *args,
