@@ -26,10 +26,11 @@
  *     Binding a buffer read-write transfers it to the binding set until the
  *     command completion that used it is settled and the caller takes it back.
  *   - No function here allocates device memory except *_new/_load, graph
- *     instantiation, loom_command_queue_reserve_workspace and the first
- *     enqueue of a reference-shaped argument struct on a queue whose
- *     workspace is too small (the *_enqueue_bf16 forms); enqueues that take
- *     a caller-owned workspace never allocate.
+ *     instantiation, loom_command_queue_reserve_workspace and a
+ *     loom_paged_decode_enqueue_bf16 whose split-KV states need more than
+ *     the queue's workspace holds, outside stream capture (under capture it
+ *     fails with LOOM_ENQ_WORKSPACE_NOT_RESERVED instead); every other
+ *     enqueue never allocates.
  */
 #ifndef LOOM_INFER_HIP_H
 #define LOOM_INFER_HIP_H
@@ -108,6 +109,16 @@ enum {
   LOOM_CMD_BINDINGS_IN_USE = 58,      /* bindings were moved into a live scope */
   LOOM_NULL_ARGUMENT = 59,
   LOOM_CMD_SCOPE_ACTIVE = 60,         /* the queue already has a live scope or unsettled completion */
+  /* No reference counterpart: a kernel of a settled command (or graph replay)
+   * reported through the queue's device status words that it could not finish
+   * the command as specified (fields[0]: bit 0 = an append token workgroup
+   * gave up waiting for the validation verdicts, so a valid command may be
+   * applied only in part; bit 1 = the append's epoch handover gave up, the
+   * validation workspace is marked broken; bit 2 = an append found its
+   * workspace marked broken and wrote nothing).  The queue (or graph
+   * execution) is poisoned.  An append command is idempotent: re-running it
+   * on a healthy queue writes the same bytes. */
+  LOOM_CMD_DEVICE_STATUS = 61,
 
   /* Plan errors (decode.rs:1498-1513, rope/mod.rs:1049-1061). */
   LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE = 70,
@@ -123,6 +134,8 @@ enum {
   LOOM_ENQ_MISALIGNED_BUFFER = 92,
   LOOM_ENQ_PAGE_INDICES_TOO_LONG = 93, /* more pages than the plan's workspace covers */
   LOOM_ENQ_STATIC_SCRATCH_TOO_SMALL = 94, /* plan workspace beyond the static scratch */
+  LOOM_ENQ_WORKSPACE_NOT_RESERVED = 95, /* the queue's workspace would have to grow while
+                                           its stream is being captured */
 
   /* GraphError, crates/loom-infer-cuda/src/graph/mod.rs:688-721. */
   LOOM_GRAPH_DEFAULT_STREAM_UNSUPPORTED = 110,
@@ -311,17 +324,24 @@ typedef struct loom_handle {
 } loom_handle_t;
 
 /* CommandQueue::new(stream, max_commands), submission.rs:31-46.  `stream` is
- * a hipStream_t owned by the caller (it must outlive the queue). */
+ * a hipStream_t owned by the caller (it must outlive the queue).  Beyond the
+ * reference, the queue allocates its append validation workspace here (device
+ * memory, zero-filled by a kernel on `stream`; fails with
+ * LOOM_ENQ_WORKSPACE_NOT_RESERVED if `stream` is being captured) and four
+ * device status words in pinned host memory, which kernels write when they
+ * cannot finish a command as specified (see LOOM_CMD_DEVICE_STATUS). */
 loom_status_t loom_command_queue_new(void *hip_stream, uint64_t max_commands,
                                      loom_command_queue_t **out, loom_error_t *err);
 /* Drop: synchronizes the stream if commands are still retained. */
 void loom_command_queue_free(loom_command_queue_t *queue);
 /* No reference counterpart: the reference's plans need no workspace.  The
- * enqueue forms that take the reference's argument structs keep their scratch
- * in device buffers owned by the queue; this allocates them ahead of the
- * first command (split-KV `scratch_bytes` = a decode plan's workspace_bytes,
- * append `zeroed_bytes` = an append plan's workspace_bytes) so that those
- * enqueues allocate nothing.  Buffers only grow; they are freed with the
+ * paged-decode enqueue that takes the reference's argument struct keeps its
+ * split-KV states in a device buffer owned by the queue; this allocates it
+ * ahead of the first command (`scratch_bytes` = a decode plan's
+ * workspace_bytes) so that those enqueues allocate nothing, which is required
+ * when they are captured.  `zeroed_bytes` (an append plan's workspace_bytes)
+ * is already held from queue creation; asking for more than that fails with
+ * LOOM_ENQ_WORKSPACE_NOT_RESERVED.  Buffers only grow; they are freed with the
  * queue (or with the graph that captured its commands). */
 loom_status_t loom_command_queue_reserve_workspace(loom_command_queue_t *queue,
                                                    uint64_t scratch_bytes, uint64_t zeroed_bytes,
@@ -484,8 +504,10 @@ typedef struct loom_bf16_paged_batch_decode_args {
  * states live in a workspace owned by the scope's command queue: it is
  * allocated (hipMalloc) the first time a command needs more than the queue
  * holds, then reused by every later command on that queue (stream-ordered, so
- * without races), and freed with the queue.  Callers that must not allocate
- * here reserve it first (loom_command_queue_reserve_workspace with
+ * without races), and freed with the queue.  While the queue's stream is
+ * being captured it never grows: a command that would need more fails with
+ * LOOM_ENQ_WORKSPACE_NOT_RESERVED.  Callers that must not allocate here
+ * reserve it first (loom_command_queue_reserve_workspace with
  * plan.workspace_bytes) or pass their own (loom_paged_decode_enqueue).  BF16
  * pages only (the reference's args carry no FP8 scales). */
 loom_status_t loom_paged_decode_enqueue_bf16(const loom_paged_decode_plan_t *plan,
@@ -833,9 +855,12 @@ typedef struct loom_rope_append_plan_info {
   uint64_t num_query_heads;
   uint64_t num_kv_heads;
   int32_t explicit_tokens;  /* 0: one token per request at kv_len-1 */
-  uint64_t workspace_bytes; /* 64 reserved words, T slot keys, T positions, T hash-set
-                               entry indices, the duplicate-slot hash set (a power of
-                               two >= 2T words) and the validation verdicts */
+  uint64_t workspace_bytes; /* the validation workspace, one fixed layout for every
+                               plan: a header (epoch, broken flag), one start tag per
+                               workgroup of the largest grid, 64 copies of the chunk
+                               verdicts, two duplicate-slot hash tables and the
+                               two-launch verdicts.  It carries the epoch from one
+                               command to the next (all zeros is a valid start) */
   uint32_t validate_blocks;
 } loom_rope_append_plan_info_t;
 
@@ -848,8 +873,22 @@ loom_status_t loom_rope_provider_plan_bf16_paged_append(const loom_rope_provider
 loom_status_t loom_rope_provider_plan_bf16_paged_append_tokens(
     const loom_rope_provider_t *provider, const loom_rope_append_tokens_spec_t *spec,
     loom_rope_append_plan_t **out, loom_error_t *err);
-/* The same two plans with plan flags (0 or LOOM_PLAN_PAGE_INDICES_CAPACITY;
- * no reference counterpart). */
+/* Append plan flags (no reference counterpart).
+ * LOOM_PLAN_APPEND_TWO_LAUNCH: commands that take the chunk-validated path
+ *   (T > 64 or more than 4096 page indices) run as two kernels, validation
+ *   then apply, ordered on the stream, instead of one kernel whose token
+ *   workgroups wait (bounded) for the validation workgroups' verdicts.  For
+ *   callers that cannot rule out other streams or processes holding CUs
+ *   while the append runs; slower at small T (one more launch).
+ * LOOM_PLAN_APPEND_TEST_NO_WAIT: for tests of the failure path only: every
+ *   bounded wait of the one-launch form gives up at once, so the command
+ *   writes nothing and its completion fails with LOOM_CMD_DEVICE_STATUS
+ *   (and the validation workspace is marked broken: zero it again before
+ *   reusing it). */
+#define LOOM_PLAN_APPEND_TWO_LAUNCH 8u
+#define LOOM_PLAN_APPEND_TEST_NO_WAIT 16u
+/* The same two plans with plan flags (LOOM_PLAN_PAGE_INDICES_CAPACITY and the
+ * append flags above; no reference counterpart). */
 loom_status_t loom_rope_provider_plan_bf16_paged_append_flags(
     const loom_rope_provider_t *provider, const loom_rope_append_spec_t *spec, uint32_t flags,
     loom_rope_append_plan_t **out, loom_error_t *err);
@@ -862,9 +901,11 @@ void loom_rope_append_plan_get_info(const loom_rope_append_plan_t *plan,
 
 /* Bf16RopePagedKvAppendArgs / ...TokensArgs, rope/mod.rs:963-1047, plus the
  * caller-owned validation workspace (u8, plan.workspace_bytes, zero before its
- * first command and not written by the caller afterwards; every command
- * leaves it ready for the next; one workspace may serve several append plans
- * in stream order).  batch_indices/positions are unused
+ * first command and not written by the caller afterwards; it carries the
+ * commands' epoch from one command to the next, and all zeros is a valid
+ * starting state; one workspace may serve several append plans in stream
+ * order; after a command fails with LOOM_CMD_DEVICE_STATUS bit 1 it is marked
+ * broken and must be zeroed again).  batch_indices/positions are unused
  * (pass {0,0}) for the one-token form. */
 typedef struct loom_rope_append_args {
   loom_handle_t query;         /* Read<bf16> [T, Hq, 128] */
@@ -889,7 +930,13 @@ typedef struct loom_rope_append_args {
  * loads and rotates; the token workgroups write only after every chunk has
  * passed.  Commands with T <= 64 and at most 4096 page indices run as one
  * kernel that validates in every workgroup.  Invalid device metadata leaves
- * every output untouched (the reference's sentinel guard). */
+ * every output untouched (the reference's sentinel guard).  The token
+ * workgroups' wait for the verdicts is bounded (about 0.3 s); a wait that
+ * gives up is reported when the completion settles (LOOM_CMD_DEVICE_STATUS,
+ * the queue is poisoned): a workgroup that gave up wrote nothing, so an
+ * invalid command still writes nothing, while a valid one may be applied in
+ * part and should be re-run (appends are idempotent).  Plans with
+ * LOOM_PLAN_APPEND_TWO_LAUNCH never wait. */
 loom_status_t loom_rope_append_enqueue(const loom_rope_append_plan_t *plan,
                                        loom_command_scope_t *scope,
                                        const loom_rope_append_args_t *args,
@@ -927,9 +974,9 @@ typedef struct loom_bf16_rope_paged_kv_append_tokens_args {
 /* Bf16RopePagedKvAppendPlan::enqueue_into (rope/mod.rs:758-830) and
  * Bf16RopePagedKvAppendTokensPlan::enqueue_into (:846-934) with the
  * reference's argument structs.  The validation words live in a
- * zero-initialised workspace owned by the scope's command queue (allocated on
- * the first command that needs more than the queue holds, or ahead of time by
- * loom_command_queue_reserve_workspace; see loom_paged_decode_enqueue_bf16).
+ * zero-initialised workspace owned by the scope's command queue, allocated
+ * when the queue is created (one size serves every append plan), so these
+ * enqueues never allocate.
  * A one-token plan takes the first form, an explicit-token plan the second
  * (LOOM_NULL_ARGUMENT "args" otherwise). */
 loom_status_t loom_rope_append_enqueue_bf16(const loom_rope_append_plan_t *plan,
@@ -953,6 +1000,14 @@ loom_status_t loom_graph_queue_new(int device, uint64_t max_commands,
 void loom_graph_queue_free(loom_graph_queue_t *queue);
 loom_status_t loom_graph_queue_bindings(loom_graph_queue_t *queue, uint64_t capacity,
                                         loom_bindings_t **out, loom_error_t *err);
+/* No reference counterpart: loom_command_queue_reserve_workspace and
+ * loom_command_queue_workspace_bytes for the graph queue's private command
+ * queue.  A reference-shaped paged-decode command captured on a graph queue
+ * needs its split-KV workspace reserved here first (the capture does not
+ * allocate: LOOM_ENQ_WORKSPACE_NOT_RESERVED). */
+loom_status_t loom_graph_queue_reserve_workspace(loom_graph_queue_t *queue, uint64_t scratch_bytes,
+                                                 uint64_t zeroed_bytes, loom_error_t *err);
+uint64_t loom_graph_queue_workspace_bytes(const loom_graph_queue_t *queue);
 /* GraphQueue::capture split in two C calls (graph/mod.rs:54-131): begin
  * synchronizes the device, begins thread-local capture on the private stream
  * and returns an ordinary scope to enqueue into; end_capture finishes the

@@ -201,6 +201,13 @@ void format_message(loom_error_t *e) {
     case LOOM_CMD_SCOPE_ACTIVE:
       snprintf(m, n, "the command queue already has a live scope or an unsettled completion");
       break;
+    case LOOM_CMD_DEVICE_STATUS:
+      snprintf(m, n,
+               "a kernel reported device status %#llx: the command did not complete as "
+               "specified (1: append verdict wait gave up, 2: append epoch handover gave up, "
+               "4: append workspace marked broken)",
+               (unsigned long long)f[0]);
+      break;
     case LOOM_NULL_ARGUMENT:
       snprintf(m, n, "required argument %s is null", op);
       break;
@@ -242,6 +249,12 @@ void format_message(loom_error_t *e) {
                "the plan's %s needs %lld bytes but the static scratch of the allocation-free "
                "enqueue holds %lld",
                op, (long long)f[1], (long long)f[0]);
+      break;
+    case LOOM_ENQ_WORKSPACE_NOT_RESERVED:
+      snprintf(m, n,
+               "the command queue's %s holds %lld bytes, the command needs %lld, and the queue's "
+               "stream is being captured (reserve the workspace before capture)",
+               op, (long long)f[0], (long long)f[1]);
       break;
     case LOOM_GRAPH_DEFAULT_STREAM_UNSUPPORTED:
       snprintf(m, n, "HIP graph capture requires a non-default stream");

@@ -64,16 +64,26 @@ struct loom_command_queue {
   bool active = false;  // a scope or completion borrows the queue (Rust's &mut)
   // Device workspaces owned by the queue for the enqueue forms that take the
   // reference's argument structs (no workspace operand).  `scratch` holds
-  // split-KV states (no initialisation needed); `zeroed` holds append
-  // validation words (zero-filled when allocated; every command leaves them
-  // at zero).  Commands on one queue are ordered on its one stream, so they
-  // reuse the buffers without races.  A buffer that grows is retired, not
-  // freed, until the queue is dropped: commands already submitted may use it.
+  // split-KV states (no initialisation needed; grown on demand outside
+  // stream capture, or reserved ahead).  `zeroed` holds the append
+  // validation state: allocated and zero-filled when the queue is created
+  // (its size is the same for every append plan), it carries the append
+  // kernels' epoch from one command to the next; all zeros is a valid
+  // starting state.  Commands on one queue are ordered on its one stream, so
+  // they reuse the buffers without races.  A buffer that grows is retired,
+  // not freed, until the queue is dropped: commands already submitted may
+  // use it.
   uint8_t *scratch = nullptr;
   uint64_t scratch_bytes = 0;
   uint8_t *zeroed = nullptr;
   uint64_t zeroed_bytes = 0;
   std::vector<void *> retired;
+  // Device-written status words in pinned, mapped host memory (kStatusWords).
+  // A kernel that could not finish a command as specified (see DeviceStatus)
+  // stores 1 into one of them; settling the completion (or the graph replay)
+  // reads them and reports LOOM_CMD_DEVICE_STATUS, poisoning the queue.
+  uint32_t *status_host = nullptr;
+  uint32_t *status_dev = nullptr;
 };
 
 struct loom_command_scope {
@@ -115,6 +125,25 @@ hipError_t synchronize_stream_or_abort(hipStream_t stream);
 // buffer.
 loom_status_t queue_workspace(loom_command_queue *queue, uint64_t bytes, bool zeroed,
                               uint8_t **out, loom_error_t *err);
+
+// Device status words of a command queue (loom_command_queue::status_*).
+enum DeviceStatus : int {
+  // An append token workgroup gave up waiting for the validation verdicts and
+  // wrote nothing: a valid command may be applied only in part.
+  kStatusAppendVerdictWait = 0,
+  // The append's epoch handover gave up waiting for every workgroup to start:
+  // the validation workspace is marked broken (it must be zeroed again).
+  kStatusAppendHandover = 1,
+  // An append command found its validation workspace marked broken and wrote
+  // nothing.
+  kStatusAppendRefused = 2,
+  kStatusWords = 4
+};
+// Bytes of the append validation workspace (one size for every plan).
+uint64_t append_workspace_bytes();
+// Reads and reports the queue's device status words (0 when all are clear);
+// the returned value has bit i set for word i.
+uint32_t read_device_status(const loom_command_queue *queue);
 
 // Device facts used by providers.
 struct DeviceInfo {

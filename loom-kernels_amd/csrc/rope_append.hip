@@ -68,17 +68,22 @@ constexpr int64_t kMaxBatch = 65536;
 constexpr int kMaxValidateBlocks = (int)max_validate_blocks(kMaxTokens, kMaxBatch);
 constexpr int kMaxGrid = kMaxTokens + kMaxValidateBlocks;
 constexpr int kTableSlots = hash_slots(kMaxTokens);
-// Workspace of the chunk-validated one-launch path, in u32 words, one layout
-// for every plan (a command queue's workspace serves all of its plans).  It
-// must be zero before its first command; after that it needs no clearing:
+// Workspace of the chunk-validated paths, in u32 words, one layout for every
+// plan (a command queue's workspace serves all of its plans).  It must be zero
+// before its first command; after that it needs no clearing: one-launch
 // commands are told apart by the epoch's tags, and each command empties the
-// hash table the next command will use.
-//   [0, 2)   epoch (u64): chunk-validated commands run on this workspace.
-//            Every workgroup reads it at start and tags its start word with
-//            epoch + 1; workgroup 0 advances it once every start word carries
-//            that tag, i.e. once every workgroup of the command has read it.
-//   [2]      sticky diagnostic: 1 once a workgroup gave up waiting (only
-//            possible if the validation workgroups were never scheduled)
+// hash table the next command will use.  The workspace therefore carries
+// state (the epoch) from one command to the next; all zeros is a valid
+// starting state.
+//   [0, 2)   epoch (u64).  Every one-launch workgroup reads it at start and
+//            tags its start word with epoch + 1; workgroup 0 advances it once
+//            every start word carries that tag, i.e. once every workgroup of
+//            the command has read it.
+//   [2]      broken: 1 once an epoch handover gave up waiting (workgroup 0
+//            then leaves the epoch as it is, so a workgroup that starts late
+//            still belongs to its own command).  Every later command on this
+//            workspace writes nothing and reports it, until the workspace is
+//            zeroed again.
 //   [3, 64)  reserved
 //   started  [kMaxGrid] (u64): each workgroup's start tag, epoch + 1 (the
 //            validation workgroups first, then one per token)
@@ -88,17 +93,25 @@ constexpr int kTableSlots = hash_slots(kMaxTokens);
 //            polled by more than ~T / kSignalCopies workgroups (same-address
 //            accesses of many workgroups serialize)
 //   tables   [2][kTableSlots]: duplicate-slot hash sets, key + 1, 0 = empty;
-//            the command with epoch e inserts into table e & 1 and empties
-//            table (e + 1) & 1 for the next command
+//            the one-launch command with epoch e inserts into table e & 1 and
+//            empties table (e + 1) & 1 for the next command; a two-launch
+//            command (which leaves the epoch alone) inserts into table e & 1
+//            and its apply kernel empties it again
+//   verdicts [kMaxValidateBlocks]: the two-launch form's chunk verdicts
+//            (1 = valid), written by its validation kernel and read by its
+//            apply kernel in stream order
 constexpr int kWsHeaderWords = 64;
-constexpr int kWsEpoch = 0, kWsTimedOut = 2;
+constexpr int kWsEpoch = 0, kWsBroken = 2;
 constexpr int kSignalCopies = 64;
 constexpr int64_t kWsStarted = kWsHeaderWords;
 constexpr int64_t kWsSignals = kWsStarted + 2 * (int64_t)kMaxGrid;
 constexpr int64_t kWsTables = kWsSignals + 2 * (int64_t)kSignalCopies * kMaxValidateBlocks;
-constexpr int64_t kWsWords = kWsTables + 2 * (int64_t)kTableSlots;
-// Polls before a workgroup gives up waiting (about 0.3 s; only reachable if
-// the validation workgroups were never scheduled).
+constexpr int64_t kWsVerdicts = kWsTables + 2 * (int64_t)kTableSlots;
+constexpr int64_t kWsWords = kWsVerdicts + kMaxValidateBlocks;
+// Polls before a workgroup gives up waiting (about 0.3 s).  Reaching it means
+// the validation workgroups were not scheduled in that time (for example, the
+// CUs of one XCD held by long kernels of other streams or processes); the
+// command then fails loudly through the queue's device status words.
 constexpr int kPollLimit = 1 << 18;
 struct WsLayout {
   uint64_t *started;  // workgroup g's start tag
@@ -129,6 +142,13 @@ struct AppendArgs {
   uint16_t *k_pages;
   uint16_t *v_pages;
   uint32_t *ws;  // see WsLayout
+  // The command queue's device status words (pinned host memory;
+  // loom::DeviceStatus): a workgroup that cannot finish the command as
+  // specified stores 1 into one of them.
+  uint32_t *status;
+  // Polls of a bounded wait before giving up (kPollLimit; 0 makes every wait
+  // give up at once, a plan option for testing the failure path).
+  int32_t poll_limit;
   int32_t index_chunk;      // page indices per index-validation workgroup
   int32_t index_blocks;     // index-validation workgroups (the first ones)
   int32_t validate_blocks;  // validation workgroups of this command
@@ -427,30 +447,60 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
   }
 }
 
+// Stores 1 into the queue's device status word `word` (system scope: the
+// words live in host memory and are read when the command is settled).
+__device__ __forceinline__ void report_status(const AppendArgs &a, int word) {
+  __hip_atomic_store(&a.status[word], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The workspace's epoch and broken word, read together at the start of a
+// command.
+struct WsEpoch {
+  uint64_t epoch;
+  uint32_t broken;
+};
+__device__ __forceinline__ WsEpoch read_epoch(const AppendArgs &a) {
+  WsEpoch e;
+  e.epoch = __hip_atomic_load(reinterpret_cast<uint64_t *>(a.ws + kWsEpoch), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+  e.broken = __hip_atomic_load(a.ws + kWsBroken, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return e;
+}
+
 // One launch per command.  Workgroups 0..V-1 each validate one chunk of the
 // command (validate_chunk) and publish the chunk's verdict, tagged with the
 // command's epoch, to every signal copy, then empty their share of the hash
 // table the next command will use; every token workgroup meanwhile loads its
 // token's Q/K/V row slices, walks the page table for its own slot and
-// computes the token's (sin, cos) pairs (validation workgroups do their own
-// token's walk after publishing), then polls one signal copy until all V
-// verdicts carry this command's tag and applies the token only if every
+// computes the token's (sin, cos) pairs, then polls one signal copy until all
+// V verdicts carry this command's tag and applies the token only if every
 // chunk is valid.  The decision rests on the polled words alone, so no
 // acquire or release fence is needed.  Last, workgroup 0 waits until every
 // workgroup has tagged its start word and advances the epoch for the next
 // command (stream order, graph replays).
 //
-// No wait can deadlock: workgroups are dispatched in index order on each XCD,
-// so the V <= 320 validation workgroups (the first of the grid) are resident
-// before any waiting workgroup can hold their place, and they wait for
-// nothing before publishing; workgroup 0 waits for start tags only after
-// publishing, so every other workgroup can finish and free its place.  The
-// waits are still bounded (kPollLimit polls); a workgroup that gives up writes
-// nothing and sets the sticky diagnostic word, and workgroup 0 advances the
-// epoch regardless, so a later command never sees this one's verdicts as its
-// own.  Same-address atomics of many workgroups serialize (about 0.1 us each
-// here), so there is no shared counter: every polled word has a few readers
-// and one writer.
+// Progress: the validation workgroups wait for nothing before publishing, and
+// workgroup 0 waits for start tags only after publishing, so every other
+// workgroup can finish and free its place.  Whether the validation
+// workgroups get a CU before the token workgroups' waits run out depends on
+// the dispatcher: the hardware dispatches a launch's workgroups in index
+// order on each XCD (the V <= 320 validation workgroups come first), but HIP
+// does not promise it, and other streams or processes may hold the CUs of an
+// XCD for longer than a wait lasts.  Every wait is therefore bounded
+// (poll_limit), and a give-up is never silent:
+//   * a token workgroup that gives up writes nothing and reports
+//     kStatusAppendVerdictWait.  The verdicts it did not see cannot make an
+//     invalid command write anything (every writer saw all verdicts valid),
+//     so the only possible harm is a valid command applied in part, and the
+//     command's completion fails (LOOM_CMD_DEVICE_STATUS);
+//   * if workgroup 0's handover gives up, it leaves the epoch as it is (a
+//     workgroup that starts late still reads this command's epoch and
+//     belongs to this command), marks the workspace broken and reports
+//     kStatusAppendHandover; every later command on the workspace then writes
+//     nothing and reports kStatusAppendRefused until it is zeroed.
+// Same-address atomics of many workgroups serialize (about 0.1 us each here),
+// so there is no shared counter: every polled word has a few readers and one
+// writer.
 template <bool FP8>
 __global__ __launch_bounds__(kApplyThreads) __attribute__((amdgpu_waves_per_eu(6)))
 void append_validated_kernel(AppendArgs a) {
@@ -460,9 +510,13 @@ void append_validated_kernel(AppendArgs a) {
   __shared__ int s_bad;
   const int tid = threadIdx.x;
   const WsLayout w = ws_layout(a.ws);
-  uint64_t *epoch_word = reinterpret_cast<uint64_t *>(a.ws + kWsEpoch);
-  const uint64_t epoch = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const WsEpoch ep = read_epoch(a);
+  const uint64_t epoch = ep.epoch;
   const uint64_t tag = epoch + 1u;
+  if (ep.broken) {
+    if (tid == 0) report_status(a, loom::kStatusAppendRefused);
+    return;
+  }
   if (tid == 0)
     __hip_atomic_store(&w.started[blockIdx.x], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
@@ -482,7 +536,8 @@ void append_validated_kernel(AppendArgs a) {
     // Workgroup 0 advances the epoch once every workgroup has read it.
     const int grid = (int)gridDim.x;
     int polls = 0;
-    while (true) {
+    bool all_started = false;
+    while (polls < a.poll_limit) {
       int mine = 1;
       for (int base = 0; base < grid; base += 4 * kValidateThreads) {
         uint64_t v[4];
@@ -495,15 +550,22 @@ void append_validated_kernel(AppendArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) mine &= v[k] == tag;
       }
-      if (__syncthreads_and(mine)) break;
-      if (++polls >= kPollLimit) {
-        if (tid == 0)
-          __hip_atomic_store(a.ws + kWsTimedOut, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__syncthreads_and(mine)) {
+        all_started = true;
         break;
       }
+      ++polls;
       __builtin_amdgcn_s_sleep(2);
     }
-    if (tid == 0) __hip_atomic_store(epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      if (all_started) {
+        __hip_atomic_store(reinterpret_cast<uint64_t *>(a.ws + kWsEpoch), tag, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        __hip_atomic_store(a.ws + kWsBroken, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        report_status(a, loom::kStatusAppendHandover);
+      }
+    }
     return;
   }
 
@@ -523,7 +585,7 @@ void append_validated_kernel(AppendArgs a) {
   if (tid < 64) {  // wave 0 polls copy t % kSignalCopies
     const uint64_t *copy = w.signals + (t % kSignalCopies) * kMaxValidateBlocks;
     int polls = 0, ready = 0, valid = 0;
-    while (true) {
+    while (polls < a.poll_limit) {
       int mine_ready = 1, mine_valid = 1;
       for (int b = tid; b < a.validate_blocks; b += 64) {
         const uint64_t v = __hip_atomic_load(&copy[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -532,16 +594,68 @@ void append_validated_kernel(AppendArgs a) {
       }
       ready = __all(mine_ready);
       valid = __all(mine_valid);
-      if (ready || ++polls >= kPollLimit) break;
+      if (ready) break;
+      ++polls;
       __builtin_amdgcn_s_sleep(2);
     }
     if (tid == 0) {
       s_bad = !(ready && valid);
-      if (!ready) __hip_atomic_store(a.ws + kWsTimedOut, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!ready) report_status(a, loom::kStatusAppendVerdictWait);
     }
   }
   __syncthreads();
   if (!s_bad) apply_token<FP8>(a, t, page, off, tid, s_sin, s_cos, first);
+}
+
+// Two-launch form (plan flag LOOM_PLAN_APPEND_TWO_LAUNCH), for callers that
+// cannot rule out other work holding CUs while the append runs: the
+// validation kernel publishes one verdict per chunk, and the apply kernel,
+// ordered after it on the stream, reads them.  Nothing waits on another
+// workgroup.  The epoch is read, not advanced: this form inserts slot keys
+// into table e & 1 and its apply kernel empties that table again, so the
+// one-launch form's invariants hold for whatever command comes next.
+__global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(AppendArgs a) {
+  __shared__ int32_t s_ip[kValidateLdsBatch + 1], s_last[kValidateLdsBatch];
+  __shared__ uint32_t s_or[kValidateThreads / 64];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const WsEpoch ep = read_epoch(a);
+  int bad = 1;
+  if (ep.broken) {
+    if (b == 0 && tid == 0) report_status(a, loom::kStatusAppendRefused);
+  } else {
+    bad = validate_chunk(a, b, tid, s_ip, s_last, ws_layout(a.ws).tables + (ep.epoch & 1u) * kTableSlots,
+                         s_or);
+  }
+  if (tid == 0)
+    __hip_atomic_store(a.ws + kWsVerdicts + b, bad ? 0u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(kApplyThreads) __attribute__((amdgpu_waves_per_eu(6)))
+void append_apply_kernel(AppendArgs a) {
+  __shared__ float s_cos[64], s_sin[64];
+  __shared__ uint32_t s_ok[kApplyThreads / 64];
+  const int tid = threadIdx.x;
+  const int t = blockIdx.x;
+  const WsEpoch ep = read_epoch(a);
+  // every chunk's verdict (written by the validation kernel before this one)
+  int ok = 1;
+  for (int b = tid; b < a.validate_blocks; b += kApplyThreads)
+    ok &= (int)__hip_atomic_load(a.ws + kWsVerdicts + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int r = 0, pos = 0, off = 0;
+  int64_t page = 0;
+  const int64_t pages = table_pages(a, a.indptr[a.batch]);
+  if (!token_slot(a, t, pages, &r, &pos, &page, &off, a.indptr, a.last)) pos = 0, page = 0;
+  const RowSlices first = load_first_slices(a, t, tid);
+  token_sincos(a, pos, tid, s_sin, s_cos);
+  // empty this workgroup's share of the table the validation kernel filled
+  if (!ep.broken) {
+    uint32_t *table = ws_layout(a.ws).tables + (ep.epoch & 1u) * kTableSlots;
+    for (int i = t * kApplyThreads + tid; i < kTableSlots; i += a.tokens * kApplyThreads) table[i] = 0u;
+  }
+  if (loom_dev::block_or(!ok, s_ok)) return;
+  apply_token<FP8>(a, t, page, off, tid, s_sin, s_cos, first);
 }
 
 // Small commands (T <= 64 tokens, <= 4096 page indices): one launch.  Every
@@ -619,6 +733,10 @@ __global__ __launch_bounds__(kApplyThreads) void append_fused_small_kernel(Appen
 
 }  // namespace
 
+namespace loom {
+uint64_t append_workspace_bytes() { return (uint64_t)kWsWords * 4; }
+}  // namespace loom
+
 struct loom_rope_provider {
   loom::DeviceInfo dev;
 };
@@ -652,7 +770,8 @@ void loom_rope_provider_free(loom_rope_provider_t *p) { delete p; }
 static loom_status_t make_plan(const loom_paged_decode_spec_t &s, uint64_t tokens,
                                bool explicit_tokens, uint32_t flags,
                                loom_rope_append_plan_t **out, loom_error_t *err) {
-  if (flags & ~LOOM_PLAN_PAGE_INDICES_CAPACITY)
+  if (flags & ~(LOOM_PLAN_PAGE_INDICES_CAPACITY | LOOM_PLAN_APPEND_TWO_LAUNCH |
+                LOOM_PLAN_APPEND_TEST_NO_WAIT))
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
   if (s.kv_layout != LOOM_KV_LAYOUT_NHD && s.kv_layout != LOOM_KV_LAYOUT_HND)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", s.kv_layout);
@@ -855,6 +974,8 @@ loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
   a.index_chunk = (int32_t)chunk;
   a.index_blocks = (int32_t)iblocks;
   a.validate_blocks = (int32_t)vblocks;
+  a.status = scope->queue->status_dev;
+  a.poll_limit = (plan->flags & LOOM_PLAN_APPEND_TEST_NO_WAIT) ? 0 : kPollLimit;
   hipStream_t stream = scope->queue->stream;
   if (T <= (uint64_t)kFusedMaxTokens && (int64_t)L(6)->numel <= kFusedMaxIndices) {
     hipLaunchKernelGGL(fp8 ? append_fused_small_kernel<true> : append_fused_small_kernel<false>,
@@ -867,6 +988,17 @@ loom_status_t rope_append_enqueue_impl(const loom_rope_append_plan_t *plan,
   const uint64_t grid = vblocks + T;
   if (vblocks > (uint64_t)kMaxValidateBlocks || grid > (uint64_t)kMaxGrid)
     return fail(err, LOOM_PLAN_STATE_COUNT_OUT_OF_RANGE, "RoPE validation grid", grid);
+  if (plan->flags & LOOM_PLAN_APPEND_TWO_LAUNCH) {
+    hipLaunchKernelGGL(append_validate_kernel, dim3((unsigned)vblocks), dim3(kValidateThreads), 0,
+                       stream, a);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(fp8 ? append_apply_kernel<true> : append_apply_kernel<false>,
+                         dim3((unsigned)T), dim3(kApplyThreads), 0, stream, a);
+      e = hipGetLastError();
+    }
+    return loom::record_launch(scope, e, err);
+  }
   hipLaunchKernelGGL(fp8 ? append_validated_kernel<true> : append_validated_kernel<false>,
                      dim3((unsigned)grid), dim3(kApplyThreads), 0, stream, a);
   hipError_t e = hipGetLastError();

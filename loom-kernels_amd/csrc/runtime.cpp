@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 
 #include "loom_internal.hpp"
 
@@ -113,34 +114,43 @@ loom_status_t queue_workspace(loom_command_queue *q, uint64_t bytes, bool zeroed
     *out = buf;
     return LOOM_OK;
   }
-  // Grow to the next 1 MiB multiple.  hipMalloc is not a stream operation; a
-  // capturing thread switches to relaxed capture mode around it so the
-  // allocation is legal while a graph queue records its commands.
+  // The zero-initialised append workspace is sized for every append plan when
+  // the queue is created; it never grows.
+  if (zeroed)
+    return fail(err, LOOM_ENQ_WORKSPACE_NOT_RESERVED, "append validation workspace",
+                (int64_t)have, (int64_t)bytes);
+  // The split-KV scratch grows to the next 1 MiB multiple, but never while the
+  // stream is being captured: an allocation is not a stream operation and
+  // would not replay.  Such callers reserve it before capture.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(q->stream, &cap);
+  if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "queue workspace", 0, 0, 0, 0, 0.0, e);
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(err, LOOM_ENQ_WORKSPACE_NOT_RESERVED, "split-KV workspace", (int64_t)have,
+                (int64_t)bytes);
   const uint64_t want = std::max<uint64_t>(((bytes + (1u << 20) - 1) >> 20) << 20, 1u << 20);
   int prev = 0;
   hipGetDevice(&prev);
   hipSetDevice(q->device);
-  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
-  hipThreadExchangeStreamCaptureMode(&mode);
   void *p = nullptr;
-  hipError_t e = hipMalloc(&p, want);
-  hipThreadExchangeStreamCaptureMode(&mode);
+  e = hipMalloc(&p, want);
   hipSetDevice(prev);
   if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "queue workspace", 0, 0, 0, 0, 0.0, e);
   if (buf) q->retired.push_back(buf);
   buf = (uint8_t *)p;
   have = want;
-  if (zeroed) {
-    // Stream-ordered fill kernel (a captured graph replays it harmlessly: the
-    // words it clears are zero again after every command).
-    const uint64_t words = want / 4;
-    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)std::min<uint64_t>((words + 255) / 256, 1024)),
-                       dim3(256), 0, q->stream, (uint32_t *)p, words);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "queue workspace", 0, 0, 0, 0, 0.0, e);
-  }
   *out = buf;
   return LOOM_OK;
+}
+
+uint32_t read_device_status(const loom_command_queue *q) {
+  uint32_t bits = 0;
+  if (!q || !q->status_host) return 0;
+  for (int i = 0; i < kStatusWords; ++i) {
+    const uint32_t w = __atomic_load_n(&q->status_host[i], __ATOMIC_ACQUIRE);
+    if (w) bits |= 1u << i;
+  }
+  return bits;
 }
 
 }  // namespace loom
@@ -176,6 +186,44 @@ int32_t settle(loom_command_completion *c, int32_t *sync_error) {
   return e;
 }
 
+
+// The queue's device status words (pinned, mapped host memory, zeroed) and its
+// append validation workspace (device memory, zero-filled by a kernel on the
+// queue's stream, so every later command on the queue sees it zero).
+loom_status_t init_queue_memory(loom_command_queue *q, loom_error_t *err) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(q->stream, &cap);
+  if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "stream", 0, 0, 0, 0, 0.0, e);
+  const uint64_t ws_bytes = loom::append_workspace_bytes();
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(err, LOOM_ENQ_WORKSPACE_NOT_RESERVED, "append validation workspace", 0,
+                (int64_t)ws_bytes);
+  int prev = 0;
+  hipGetDevice(&prev);
+  hipSetDevice(q->device);
+  void *h = nullptr, *d = nullptr, *w = nullptr;
+  e = hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocPortable);
+  if (e == hipSuccess) {
+    memset(h, 0, 64);
+    e = hipHostGetDevicePointer(&d, h, 0);
+  }
+  if (e == hipSuccess) e = hipMalloc(&w, ws_bytes);
+  if (e == hipSuccess) {
+    const uint64_t words = ws_bytes / 4;
+    hipLaunchKernelGGL(loom::zero_words_kernel,
+                       dim3((unsigned)std::min<uint64_t>((words + 255) / 256, 1024)), dim3(256), 0,
+                       q->stream, (uint32_t *)w, words);
+    e = hipGetLastError();
+  }
+  hipSetDevice(prev);
+  q->status_host = (uint32_t *)h;
+  q->status_dev = (uint32_t *)d;
+  q->zeroed = (uint8_t *)w;
+  q->zeroed_bytes = w ? ws_bytes : 0;
+  if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "queue memory", 0, 0, 0, 0, 0.0, e);
+  return LOOM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -202,6 +250,11 @@ loom_status_t loom_command_queue_new(void *hip_stream, uint64_t max_commands,
   q->device = device;
   q->completion_event = ev;
   q->max_commands = max_commands;
+  loom_status_t rc = init_queue_memory(q, err);
+  if (rc) {
+    loom_command_queue_free(q);
+    return rc;
+  }
   *out = q;
   return loom::ok(err);
 }
@@ -230,6 +283,7 @@ void loom_command_queue_free(loom_command_queue_t *q) {
     for (void *p : q->retired) hipFree(p);
     hipSetDevice(prev);
   }
+  if (q->status_host) hipHostFree(q->status_host);
   hipEventDestroy(q->completion_event);
   if (q->owns_stream) hipStreamDestroy(q->stream);
   delete q;
@@ -464,8 +518,12 @@ loom_status_t loom_command_completion_wait(loom_command_completion_t *c, loom_bi
   q->retained = 0;
   q->active = false;
   loom_bindings *b = c->bindings;
+  const bool ran = c->submitted > 0;
   delete c;
-  if (!failure) {
+  // A settled command whose kernels reported a device status did not complete
+  // as specified: the completion fails and poisons the queue.
+  const uint32_t status = !failure && ran ? loom::read_device_status(q) : 0;
+  if (!failure && !status) {
     b->moved = false;
     if (out) *out = b;
     return loom::ok(err);
@@ -473,6 +531,7 @@ loom_status_t loom_command_completion_wait(loom_command_completion_t *c, loom_bi
   q->poisoned = true;
   delete b;
   if (out) *out = nullptr;
+  if (status) return fail(err, LOOM_CMD_DEVICE_STATUS, "completion", status);
   return fail(err, LOOM_CMD_DRIVER, "completion", 0, 0, 0, 0, 0.0, failure);
 }
 
@@ -483,7 +542,8 @@ void loom_command_completion_free(loom_command_completion_t *c) {
   int32_t failure = settle(c, &sync_error);
   c->queue->retained = 0;
   c->queue->active = false;
-  if (failure) c->queue->poisoned = true;
+  if (failure || (c->submitted > 0 && loom::read_device_status(c->queue)))
+    c->queue->poisoned = true;
   delete c->bindings;
   delete c;
 }
@@ -514,6 +574,7 @@ struct loom_graph_exec {
   bool in_flight = false;
   int32_t record_error = 0;
   int32_t poll_error = 0;
+  uint32_t device_status = 0;  // status words read at the last settlement
   bool poisoned = false;
 };
 
@@ -524,6 +585,10 @@ struct loom_graph_completion {
 };
 
 namespace {
+
+// settle_exec's failure value when the replay completed but its kernels
+// reported a device status (not a hipError_t).
+constexpr int32_t kDeviceStatusFailure = -1;
 
 // graph/mod.rs:418-446 settle_in_flight.
 int32_t settle_exec(loom_graph_exec *x, int32_t *sync_error) {
@@ -541,6 +606,9 @@ int32_t settle_exec(loom_graph_exec *x, int32_t *sync_error) {
     if (e != hipSuccess) {
       failure = e;
       *sync_error = loom::synchronize_stream_or_abort(x->queue->stream);
+    } else {
+      x->device_status = loom::read_device_status(x->queue);
+      if (x->device_status) failure = kDeviceStatusFailure;
     }
   }
   x->in_flight = false;
@@ -550,7 +618,9 @@ int32_t settle_exec(loom_graph_exec *x, int32_t *sync_error) {
 }
 
 loom_status_t settlement_error(loom_error_t *err, const char *op, int32_t failure,
-                               int32_t sync_error) {
+                               int32_t sync_error, uint32_t device_status = 0) {
+  if (failure == kDeviceStatusFailure)
+    return fail(err, LOOM_CMD_DEVICE_STATUS, op, device_status);
   if (sync_error)
     return fail(err, LOOM_GRAPH_SETTLEMENT, op, sync_error, 0, 0, 0, 0.0, failure);
   return fail(err, LOOM_GRAPH_DRIVER, op, 0, 0, 0, 0, 0.0, failure);
@@ -610,6 +680,16 @@ loom_status_t loom_graph_queue_bindings(loom_graph_queue_t *g, uint64_t capacity
                                         loom_bindings_t **out, loom_error_t *err) {
   if (!g || g->consumed) return fail(err, LOOM_NULL_ARGUMENT, "graph_queue");
   return loom_command_queue_bindings(g->queue, capacity, out, err);
+}
+
+loom_status_t loom_graph_queue_reserve_workspace(loom_graph_queue_t *g, uint64_t scratch_bytes,
+                                                 uint64_t zeroed_bytes, loom_error_t *err) {
+  if (!g || g->consumed) return fail(err, LOOM_NULL_ARGUMENT, "graph_queue");
+  return loom_command_queue_reserve_workspace(g->queue, scratch_bytes, zeroed_bytes, err);
+}
+
+uint64_t loom_graph_queue_workspace_bytes(const loom_graph_queue_t *g) {
+  return g && g->queue ? loom_command_queue_workspace_bytes(g->queue) : 0;
 }
 
 loom_status_t loom_graph_queue_begin_capture(loom_graph_queue_t *g, loom_bindings_t *b,
@@ -789,7 +869,7 @@ loom_status_t loom_graph_exec_into_bindings(loom_graph_exec_t *x, loom_bindings_
   int32_t failure = settle_exec(x, &sync);
   if (failure) {
     x->poisoned = true;
-    return settlement_error(err, "completion", failure, sync);
+    return settlement_error(err, "completion", failure, sync, x->device_status);
   }
   loom_bindings *b = x->bindings;
   x->bindings = nullptr;
@@ -841,7 +921,7 @@ loom_status_t loom_graph_completion_wait(loom_graph_completion_t *c, loom_error_
   int32_t failure = settle_exec(x, &sync);
   if (!failure) return loom::ok(err);
   x->poisoned = true;
-  return settlement_error(err, "completion", failure, sync);
+  return settlement_error(err, "completion", failure, sync, x->device_status);
 }
 
 void loom_graph_completion_free(loom_graph_completion_t *c) {

@@ -36,6 +36,8 @@ PARTIAL_STATE_WIDTH = 130
 PLAN_PAGE_INDICES_CAPACITY = 1
 PLAN_PREFILL_TILE_16 = 2
 PLAN_PREFILL_TILE_64 = 4
+PLAN_APPEND_TWO_LAUNCH = 8
+PLAN_APPEND_TEST_NO_WAIT = 16
 
 
 def _prefill_tile_flag(tile_cols: int) -> int:
@@ -104,13 +106,14 @@ COMMAND_VARIANTS = {
     49: "BindingSlotOutOfRange", 50: "BindingIsReadOnly", 51: "BindingSlotVacant",
     52: "BindingTypeMismatch", 53: "DuplicateBindingSlot", 54: "CommandCapacityExceeded",
     55: "External", 56: "Driver", 57: "AliasedBinding", 58: "BindingsInUse", 59: "NullArgument",
-    60: "ScopeActive",
+    60: "ScopeActive", 61: "DeviceStatus",
 }
 PLAN_VARIANTS = {70: "StateCountOutOfRange", 71: "StateCountOverflow",
                  72: "UnsupportedHeadDimension", 73: "UnsupportedRotaryDimension",
                  74: "UnsupportedDevice", 75: "InvalidOption"}
 ENQUEUE_VARIANTS = {90: "LengthMismatch", 91: "PageIndicesTooShort", 92: "MisalignedBuffer",
-                    93: "PageIndicesTooLong", 94: "StaticScratchTooSmall"}
+                    93: "PageIndicesTooLong", 94: "StaticScratchTooSmall",
+                    95: "WorkspaceNotReserved"}
 GRAPH_VARIANTS = {110: "DefaultStreamUnsupported", 111: "EmptyCapture",
                   112: "CaptureInvalidated", 113: "NullExecutableHandle",
                   114: "ExecutionPoisoned", 115: "ReplayInFlight", 116: "LaunchCountExhausted",
@@ -1239,17 +1242,20 @@ class RopeProvider:
         return cls(out.value, device)
 
     def plan_bf16_paged_append(self, spec: Bf16RopePagedKvAppendSpec,
-                               indices_capacity: bool = False):
+                               indices_capacity: bool = False, flags: int = 0):
+        """rope/mod.rs:628-654.  `flags`: PLAN_APPEND_TWO_LAUNCH and
+        PLAN_APPEND_TEST_NO_WAIT (no reference counterpart)."""
         out = C.c_void_p()
         _call(lib().loom_rope_provider_plan_bf16_paged_append_flags, self._p, C.byref(spec._c),
-              PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0, C.byref(out))
+              (PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0) | flags, C.byref(out))
         return Bf16RopePagedKvAppendPlan(out.value, spec)
 
     def plan_bf16_paged_append_tokens(self, spec: Bf16RopePagedKvAppendTokensSpec,
-                                      indices_capacity: bool = False):
+                                      indices_capacity: bool = False, flags: int = 0):
+        """rope/mod.rs:656-682, with the same `flags` as plan_bf16_paged_append."""
         out = C.c_void_p()
         _call(lib().loom_rope_provider_plan_bf16_paged_append_tokens_flags, self._p,
-              C.byref(spec._c), PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0,
+              C.byref(spec._c), (PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0) | flags,
               C.byref(out))
         return Bf16RopePagedKvAppendPlan(out.value, spec)
 
@@ -1370,6 +1376,15 @@ class GraphQueue:
         out = C.c_void_p()
         _call(lib().loom_graph_queue_bindings, self._p, capacity, C.byref(out))
         return CheckedBindings(out.value)
+
+    def reserve_workspace(self, scratch_bytes: int = 0, zeroed_bytes: int = 0):
+        """CommandQueue.reserve_workspace for the private queue (no reference
+        counterpart): reference-shaped decode commands need it before capture."""
+        _call(lib().loom_graph_queue_reserve_workspace, self._p, scratch_bytes, zeroed_bytes)
+
+    @property
+    def workspace_bytes(self) -> int:
+        return lib().loom_graph_queue_workspace_bytes(self._p)
 
     def capture(self, bindings: CheckedBindings,
                 record: Callable[[CommandScope], Any]) -> CapturedGraph:

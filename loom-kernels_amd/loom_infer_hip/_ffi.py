@@ -255,6 +255,8 @@ SIGNATURES = {
     "loom_graph_queue_new": (i32, [C.c_int, u64, P(vp), E]),
     "loom_graph_queue_free": (None, [vp]),
     "loom_graph_queue_bindings": (i32, [vp, u64, P(vp), E]),
+    "loom_graph_queue_reserve_workspace": (i32, [vp, u64, u64, E]),
+    "loom_graph_queue_workspace_bytes": (u64, [vp]),
     "loom_graph_queue_begin_capture": (i32, [vp, vp, P(vp), E]),
     "loom_graph_queue_end_capture": (i32, [vp, vp, P(vp), E]),
     "loom_captured_graph_commands": (u64, [vp]),

@@ -30,29 +30,32 @@ def log(msg):
 
 
 def check_workspace_ready(ws, chunked_before, chunked):
-    """The append workspace after a command: the chunk-validated path (T > 64
-    or more than 4096 page indices) advanced the epoch once, gave up no wait
-    and left the hash table of the next command empty; the small one-launch
-    path leaves it alone.  Layout in u32 words (one for every plan): 64 header
-    words (epoch u64, diagnostic), 8192 u64 start tags, 64 x 256 u64 verdict
-    copies, two 16384-entry hash tables."""
+    """The append workspace after a command: the one-launch chunk-validated
+    path (T > 64 or more than 4096 page indices) advanced the epoch once; no
+    epoch handover gave up (the broken word is clear); the hash table the
+    next command inserts into is empty.  The two-launch form and the small
+    one-launch path leave the epoch alone.  Layout in u32 words (one for every
+    plan): 64 header words (epoch u64, broken), 8512 u64 start tags, 64 x 320
+    u64 verdict copies, two 16384-entry hash tables, 320 two-launch
+    verdicts."""
     w = ws.cpu().numpy().view(np.uint32)
     epoch = int(w[0]) | int(w[1]) << 32
-    assert w[2] == 0, "a workgroup gave up waiting"
+    assert w[2] == 0, "the workspace is marked broken"
     assert epoch == chunked_before + chunked, (epoch, chunked_before, chunked)
     tables = 64 + 2 * (8192 + 320) + 2 * 64 * 320
-    assert len(w) == tables + 2 * 16384
+    assert len(w) == tables + 2 * 16384 + 320
     nxt = w[tables + (epoch & 1) * 16384: tables + ((epoch & 1) + 1) * 16384]
     assert not nxt.any(), f"next command's hash table holds {np.count_nonzero(nxt)} entries"
 
 
 class AppendRunner:
-    def __init__(self, L, spec, explicit):
+    def __init__(self, L, spec, explicit, flags=0):
         import torch
         self.L, self.spec, self.explicit = L, spec, explicit
+        self.two_launch = bool(flags & L.PLAN_APPEND_TWO_LAUNCH)
         prov = L.RopeProvider.load(0)
-        self.plan = (prov.plan_bf16_paged_append_tokens(spec) if explicit
-                     else prov.plan_bf16_paged_append(spec))
+        self.plan = (prov.plan_bf16_paged_append_tokens(spec, flags=flags) if explicit
+                     else prov.plan_bf16_paged_append(spec, flags=flags))
         self.ws = torch.zeros(self.plan.workspace_bytes, dtype=torch.uint8, device="cuda")
         self.queue = L.CommandQueue(torch.cuda.current_stream(), 2)
         self.epochs = 0  # chunk-validated commands run on self.ws
@@ -92,7 +95,7 @@ class AppendRunner:
                                                            "value_pages")]
         b.take_read_write(h["workspace"])
         T = self.plan.info.tokens
-        chunked = int(not (T <= 64 and len(ix) <= 4096))
+        chunked = int(not (T <= 64 and len(ix) <= 4096) and not self.two_launch)
         check_workspace_ready(self.ws, self.epochs, chunked)
         self.epochs += chunked
         return out
@@ -299,18 +302,25 @@ def explicit_case(oracle, seed, T, long_pages, brk):
                 bi=bi, pos=pos, q=q, k=k, v=v, kp=kp, vp=vp)
 
 
+# The two-launch plan option (validation kernel, then apply kernel) on the
+# chunk-validated shapes.
+PATHS_TWO_LAUNCH = [p + (True,) for p in PATHS if p[0].startswith("chunked")]
+
+
 @pytest.mark.parametrize("brk", BREAKS)
-@pytest.mark.parametrize("path,T,long_pages", PATHS, ids=[p[0] for p in PATHS])
-def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, brk):
+@pytest.mark.parametrize("path,T,long_pages,two_launch",
+                         [p + (False,) for p in PATHS] + PATHS_TWO_LAUNCH,
+                         ids=[p[0] for p in PATHS] + [p[0] + "_two_launch" for p in PATHS_TWO_LAUNCH])
+def test_explicit_paths_valid_and_guarded(L, oracle, path, T, long_pages, two_launch, brk):
     """Each path on valid metadata (against the oracle) and with one guard
     broken (rope/mod.rs:407-466: every output keeps its sentinels)."""
-    log(f"append path {path} T={T} break={brk}")
+    log(f"append path {path} T={T} two_launch={two_launch} break={brk}")
     c = explicit_case(oracle, hash((path, brk)) % 2**32, T, long_pages, brk)
     B, hq, hkv, pool = c["B"], c["hq"], c["hkv"], c["pool"]
     indptr, indices, last, bi, pos = c["indptr"], c["indices"], c["last"], c["bi"], c["pos"]
     q, k, v, kp, vp = c["q"], c["k"], c["v"], c["kp"], c["vp"]
     spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv)
-    r = AppendRunner(L, spec, True)
+    r = AppendRunner(L, spec, True, L.PLAN_APPEND_TWO_LAUNCH if two_launch else 0)
     for call in range(2):  # the second command runs over the first one's workspace
         qo, okp, ovp = r.run(q, k, v, bi, pos, indptr, indices, last, kp, vp)
         if brk != "valid":

@@ -83,15 +83,22 @@ def test_decode_reference_args_use_the_queue_workspace(L, oracle, name, B, hq, h
     r = DecodeRunner(L, B, pool, hq, hkv, teams=teams)
     want_o, want_l = r.run(q, k, v, ip, ix, ln)
     queue = L.CommandQueue(torch.cuda.current_stream(), 2)
-    assert queue.workspace_bytes == 0
+    # the queue holds its append validation workspace from creation, no scratch
+    base = queue.workspace_bytes
+    assert base == append_workspace_bytes(L)
     dev = [to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), to_dev_i32(ip), to_dev_i32(ix),
            to_dev_i32(ln)]
     for i in range(2):  # the second command reuses the workspace the first allocated
         o, l_ = run_decode_reference_args(L, queue, r.plan, r.spec, *dev)
         assert np.array_equal(o, want_o) and np.array_equal(l_, want_l), f"call {i}"
-        assert queue.workspace_bytes >= r.plan.workspace_bytes
+        assert queue.workspace_bytes >= base + r.plan.workspace_bytes
     log(f"  {r.plan.algorithm} queue workspace {queue.workspace_bytes} B "
         f"{compare_decode(oracle, o, l_, ref_o, ref_l)}")
+
+
+def append_workspace_bytes(L):
+    spec = L.Bf16RopePagedKvAppendSpec(1, 1, 1, 1)
+    return L.RopeProvider.load(0).plan_bf16_paged_append(spec).workspace_bytes
 
 
 def test_reserved_workspace_is_not_regrown(L, oracle):
@@ -251,6 +258,10 @@ def test_decode_step_graph_with_reference_args(L, oracle):
     out = torch.empty(B * hq * 128, dtype=torch.bfloat16, device="cuda")
     lse = torch.empty(B * hq, dtype=torch.float32, device="cuda")
     gq = L.GraphQueue(0, 2)
+    # the capture allocates nothing: the decode's split-KV workspace is
+    # reserved first (the append's is held from queue creation)
+    gq.reserve_workspace(scratch_bytes=dplan.workspace_bytes)
+    reserved = gq.workspace_bytes
     b = gq.bindings(14)
     hq_, hk, hv = b.bind_read(t["q"]), b.bind_read(t["k"]), b.bind_read(t["v"])
     hip_, hix, hln = b.bind_read(t["ip"]), b.bind_read(t["ix"]), b.bind_read(t["ln"])
@@ -265,7 +276,9 @@ def test_decode_step_graph_with_reference_args(L, oracle):
         aplan.enqueue_into(scope, a_args)
         dplan.enqueue_into(scope, d_args)
 
-    exec_ = gq.capture(b, record).instantiate()
+    captured = gq.capture(b, record)
+    assert reserved >= dplan.workspace_bytes + aplan.workspace_bytes
+    exec_ = captured.instantiate()
     first = None
     for i in range(4):
         out.fill_(float("nan"))
@@ -327,3 +340,50 @@ def test_four_byte_aligned_operands_decode_and_prefill(L, oracle):
                        out=out)
     assert np.array_equal(bf16_host(o), want[0]) and np.array_equal(l_.cpu().numpy(), want[1])
     torch.cuda.synchronize()
+
+
+def test_unreserved_decode_capture_fails_typed_and_reserved_one_never_grows(L, oracle):
+    """A reference-shaped split-KV decode captured on a graph queue whose
+    workspace was not reserved fails with WorkspaceNotReserved (no hipMalloc
+    during capture); after reserve_workspace the same capture succeeds and the
+    queue's workspace does not grow; eagerly (no capture) the queue still
+    grows its own."""
+    import torch
+    log("decode capture without a reserved workspace")
+    rng = np.random.default_rng(31)
+    B, hq, hkv = 3, 32, 8
+    pool, (q, k, v, ip, ix, ln) = decode_case(oracle, rng, B, hq, hkv, [300, 2000, 45])
+    r = DecodeRunner(L, B, pool, hq, hkv, teams=5)
+    want_o, want_l = r.run(q, k, v, ip, ix, ln)
+    assert r.plan.workspace_bytes > 0
+    dev = [to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), to_dev_i32(ip), to_dev_i32(ix),
+           to_dev_i32(ln)]
+    out = torch.empty(r.spec.output_numel, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(r.spec.lse_numel, dtype=torch.float32, device="cuda")
+
+    def capture(gq):
+        b = gq.bindings(8)
+        h = [b.bind_read(x) for x in dev]
+        ho, hl = b.bind_read_write(out), b.bind_read_write(lse)
+        args = L.Bf16PagedBatchDecodeArgs(*h, ho.write(), hl.write())
+        return gq.capture(b, lambda scope: r.plan.enqueue_into(scope, args))
+
+    gq = L.GraphQueue(0, 1)
+    before = gq.workspace_bytes
+    with pytest.raises(L.EnqueueError) as e:
+        capture(gq)
+    assert e.value.variant == "WorkspaceNotReserved", e.value
+    log(f"  unreserved: {e.value}")
+
+    gq = L.GraphQueue(0, 1)
+    gq.reserve_workspace(scratch_bytes=r.plan.workspace_bytes)
+    reserved = gq.workspace_bytes
+    assert reserved >= before + r.plan.workspace_bytes
+    exec_ = capture(gq).instantiate()
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        exec_.launch().wait()
+        assert np.array_equal(bf16_host(out), want_o), f"replay {i}"
+        assert np.array_equal(lse.cpu().numpy(), want_l), f"replay {i}"
+    exec_.into_bindings()
