@@ -202,6 +202,32 @@ def test_global_indptr_guard(L):
     assert torch.isnan(out.float()).all() and torch.isnan(lse).all()
 
 
+def test_global_indptr_guard_split_direct_then_valid(L, oracle):
+    """The global guard on a split direct plan (every split workgroup poisons
+    its state and still counts itself in, so the queue's arrival counters
+    return to zero): all sentinels kept, then a valid call on the same queue
+    matches the oracle, twice."""
+    rng = np.random.default_rng(21)
+    lens = [1000, 700]
+    B, hq, hkv = 2, 8, 2
+    pool = sum((x + 15) // 16 for x in lens) + 4
+    indptr, indices, last = ragged_table(rng, lens, pool)
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    r = DecodeRunner(L, B, pool, hq, hkv)
+    assert r.plan.algorithm == "direct" and r.plan.info.teams > 1
+    bad_ptr = indptr.copy()
+    bad_ptr[0] = 1
+    out, lse = r.run(q, k, v, bad_ptr, indices, last)
+    assert np.all(np.isnan(oracle.bf16_to_f32(out))) and np.all(np.isnan(lse))
+    ref_out, ref_lse = oracle.paged_decode(oracle.paged_spec(B, pool, hq, hkv), q, k, v,
+                                           indptr, indices, last)
+    for _ in range(2):
+        out, lse = r.run(q, k, v, indptr, indices, last)
+        compare_decode(oracle, out, lse, ref_out, ref_lse)
+
+
 def test_short_indptr_rejected_before_submission(L):
     # crates/loom-infer-validation/src/gates/paged_batch_decode.rs:150-222
     torch = pytest.importorskip("torch")
