@@ -11,6 +11,12 @@ decode kernel measured with HIP events on its own stream, and the CPU oracle
 timed on this host over a bounded sample of the same workload.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--quick]
+                    [--records gpurun_out/bench_records.jsonl]
+
+Besides the one JSON line on stdout, every decode and append config writes
+evidence records (JSON Lines, the reference's BenchmarkRecord schema) to
+--records: raw per-sample µs, fixture digests, kernels per call and the build's
+source commit.
 """
 import argparse
 import json
@@ -34,6 +40,93 @@ TRAFFIC_C3 = 1.1494e9
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+# ---- evidence records ---------------------------------------------------------
+# One JSON line per (config, measurement) in the reference's BenchmarkRecord
+# schema (crates/loom-infer-validation/src/support/benchmark.rs:5-24): raw
+# per-sample µs, fixture digests of the seeded inputs, kernels per call and the
+# source commit of the build (loom-kernels_amd/lib/BUILD_INFO.json, written by
+# build_lib.sh; the GPU box has no git metadata).
+BUILD_INFO = os.path.join(ROOT, "loom-kernels_amd", "lib", "BUILD_INFO.json")
+RECORDS = []
+
+
+def fnv1a64(data: bytes) -> str:
+    h = 0xCBF29CE484222325
+    for b in data:
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return f"{h:016x}"
+
+
+def host_digest(a) -> str:
+    """FNV-1a 64 of a host array's bytes (metadata: page tables, positions)."""
+    import numpy as np
+    return fnv1a64(np.ascontiguousarray(a).tobytes())
+
+
+def device_digest(t) -> str:
+    """A position-weighted 64-bit checksum of a device tensor's 16-bit words,
+    Σ u16[i]·(i mod 65521 + 1) mod 2^64, computed on the GPU in chunks (the
+    K/V pools are GBs; hashing them on the host would take minutes)."""
+    import torch
+    w16 = t.reshape(-1).view(torch.int16)
+    n = w16.numel()
+    total = 0
+    step = 1 << 26
+    for s0 in range(0, n, step):
+        e0 = min(n, s0 + step)
+        v = w16[s0:e0].to(torch.int64) & 0xFFFF
+        wt = torch.arange(s0, e0, dtype=torch.int64, device=t.device) % 65521 + 1
+        total = (total + int((v * wt).sum().item())) & 0xFFFFFFFFFFFFFFFF
+    return f"{total:016x}"
+
+
+def execution_info():
+    import torch
+    p = torch.cuda.get_device_properties(0)
+    return {"device": p.name, "arch": getattr(p, "gcnArchName", ""), "cus": p.multi_processor_count,
+            "hip": torch.version.hip, "torch": torch.__version__, "host": platform.node(),
+            "stream": "one non-default stream, default priority"}
+
+
+def record(operator, case, kernels_per_call, shape, fixture_id, digests, warmup, per_sample,
+           samples_us, measurement, layout="NHD, page 16", dtype="bf16"):
+    """Appends one BenchmarkRecord (benchmark.rs:5-24) to RECORDS."""
+    info = {}
+    if os.path.exists(BUILD_INFO):
+        info = json.load(open(BUILD_INFO))
+    RECORDS.append({
+        "schema_version": 1, "provider": "loom-infer-hip",
+        "provider_version": info.get("abi_version", "1"),
+        "provider_commit": info.get("commit", "unknown"),
+        "provider_worktree_dirty": info.get("dirty"),
+        "provider_library_sha256": info.get("library_sha256"),
+        "run_label": os.environ.get("LOOM_BENCH_RUN_LABEL", "bench.py"),
+        "measurement": measurement, "operator": operator, "case": case, "dtype": dtype,
+        "layout": layout, "execution": execution_info(), "kernels_per_call": kernels_per_call,
+        "shape": shape, "fixture_id": fixture_id, "fixture_digests": digests,
+        "warmup_launches": warmup, "launches_per_sample": per_sample,
+        "samples_us": [round(x, 4) for x in samples_us]})
+
+
+def write_records(path):
+    if not path:
+        return
+    d = os.path.dirname(path)
+    if d:
+        os.makedirs(d, exist_ok=True)
+    with open(path, "w") as f:
+        for r in RECORDS:
+            f.write(json.dumps(r) + "\n")
+    log(f"[bench] wrote {len(RECORDS)} evidence records to {path}")
+
+
+def decode_kernels_per_call(plan) -> int:
+    """Launches per decode command: the balanced split-KV plan and a split
+    direct plan add a merge kernel; an unsplit direct plan is one kernel."""
+    i = plan.info
+    return 1 if (plan.algorithm == "direct" and i.teams <= 1) else 2
 
 
 def algorithmic_decode_bytes(lens, B, hq, hkv):
@@ -75,6 +168,7 @@ class DecodeCase:
         self.last = torch.from_numpy(last).to(dev)
         self.out = torch.empty(B * hq * 128, dtype=torch.bfloat16, device=dev)
         self.lse = torch.empty(B * hq, dtype=torch.float32, device=dev)
+        self.seed = seed
         self.spec = L.Bf16PagedBatchDecodeSpec(B, pool, hq, hkv, 128, 16)
         self.plan = L.DecodeProvider.load(0).plan_bf16_paged_batch(
             self.spec, max_total_pages=int(indptr[-1]), teams=teams)
@@ -217,9 +311,10 @@ def _timed_rotating(L, stream, n_bind, binders, enqueue, steps, warmup):
     return start.elapsed_time(end) * 1000.0 / steps
 
 
-def _graph_replay(L, n_bind, n_cmds, bind, record, replays=20):
+def _graph_replay(L, n_bind, n_cmds, bind, record, replays=20, samples_out=None):
     """One fixed-address replay + its completion event per sample
-    (graph/mod.rs:301-323); returns the median µs."""
+    (graph/mod.rs:301-323); returns the median µs (and appends the raw
+    samples to `samples_out` when given)."""
     import torch
     gq = L.GraphQueue(0, n_cmds)
     b = gq.bindings(n_bind)
@@ -233,6 +328,8 @@ def _graph_replay(L, n_bind, n_cmds, bind, record, replays=20):
         if i >= 3:
             samples.append(ms * 1000.0)
     exec_.into_bindings()
+    if samples_out is not None:
+        samples_out.extend(samples)
     samples.sort()
     return samples[len(samples) // 2]
 
@@ -241,8 +338,26 @@ def time_eager(L, case, stream, steps, warmup):
     return _timed_enqueues(L, stream, 9, case.bind, case.plan.enqueue_into, steps, warmup)
 
 
-def time_graph(L, case, replays=20):
-    return _graph_replay(L, 9, 1, case.bind, case.plan.enqueue_into, replays)
+def time_graph(L, case, replays=20, samples_out=None):
+    return _graph_replay(L, 9, 1, case.bind, case.plan.enqueue_into, replays, samples_out)
+
+
+def decode_fixture(case):
+    """(fixture_id, digests, shape) of a DecodeCase for its evidence records."""
+    fid = (f"{case.name}: lengths and page table from numpy default_rng({case.seed}), "
+           f"q/K/V torch.randn(generator seed {case.seed}) cast to bf16")
+    dig = {"page_indptr": host_digest(case.indptr_h), "page_indices": host_digest(case.indices_h),
+           "last_page_len": host_digest(case.last_h), "query": device_digest(case.q),
+           "key_pages": device_digest(case.k), "value_pages": device_digest(case.v),
+           "digest_kinds": {"metadata": "fnv1a64 of int32 bytes",
+                            "tensors": "sum u16[i]*(i mod 65521 + 1) mod 2^64"}}
+    shape = {"batch": case.B, "num_query_heads": case.hq, "num_kv_heads": case.hkv,
+             "head_dim": 128, "page_size": 16, "max_num_pages": case.pool,
+             "total_pages": int(case.indptr_h[-1]), "kv_len_sum": int(case.lens.sum()),
+             "kv_len_min": int(case.lens.min()), "kv_len_max": int(case.lens.max()),
+             "algorithmic_bytes": case.bytes, "plan_algorithm": case.plan.algorithm,
+             "plan_teams": case.plan.info.teams}
+    return fid, dig, shape
 
 
 class AppendCase:
@@ -264,11 +379,13 @@ class AppendCase:
             indices = rng.permutation(pool)[: int(indptr[-1])].astype(np.int32)
             last = (lens - (pages - 1) * 16).astype(np.int32)
         self.explicit = n_new is not None
+        self.seed = seed
         if self.explicit:
             bi = np.concatenate([np.full(n, r) for r, n in enumerate(n_new)]).astype(np.int32)
             pos = np.concatenate([np.arange(l - n, l) for l, n in zip(lens, n_new)]).astype(np.int32)
             perm = rng.permutation(len(bi))
             bi, pos = bi[perm], pos[perm]
+            self.bi_h, self.pos_h = bi, pos
             T = len(bi)
             self.spec = L.Bf16RopePagedKvAppendTokensSpec(T, B, pool, hq, hkv,
                                                           extended=T > 64)
@@ -321,13 +438,36 @@ class AppendCase:
             b.bind_read(self.pos) if self.explicit else None)
 
 
-def time_append(L, case, stream, steps, warmup):
+def time_append(L, case, stream, steps, warmup, graph_samples=None):
     n = 12 if case.explicit else 10
     return (_timed_enqueues(L, stream, n, case.bind, case.plan.enqueue_into, steps, warmup),
-            _graph_replay(L, n, 1, case.bind, case.plan.enqueue_into))
+            _graph_replay(L, n, 1, case.bind, case.plan.enqueue_into, samples_out=graph_samples))
 
 
-def time_full_step(L, app, dec):
+def record_append(name, app, stream, warmup, graph_samples):
+    """Evidence records of an append config: raw eager samples (20 samples of
+    10 back-to-back commands) and the graph replays' samples."""
+    import torch
+    n = 12 if app.explicit else 10
+    xs = _sampled_enqueues(app.L, stream, n, app.bind, app.plan.enqueue_into, 20, 10, warmup)
+    ip, ix, ln = app.tables
+    dig = {"page_indptr": host_digest(ip), "page_indices": host_digest(ix),
+           "last_page_len": host_digest(ln), "query": device_digest(app.q),
+           "key": device_digest(app.k), "value": device_digest(app.v)}
+    if app.explicit:
+        dig.update(batch_indices=host_digest(app.bi_h), positions=host_digest(app.pos_h))
+    fid = (f"{name}: lengths, page table and token order from numpy default_rng({app.seed}), "
+           f"q/k/v torch.randn(generator seed {app.seed}) cast to bf16")
+    shape = {"tokens": app.T, "batch": app.B, "num_query_heads": app.hq,
+             "num_kv_heads": app.hkv, "head_dim": 128, "page_size": 16,
+             "explicit_tokens": app.explicit, "algorithmic_bytes": app.bytes}
+    op = "rope_paged_append_tokens" if app.explicit else "rope_paged_append"
+    record(op, name, 1, shape, fid, dig, warmup, 10, xs, "eager_stream_batch_hip_event")
+    record(op, name, 1, shape, fid, dig, 3, 1, graph_samples, "graph_replay_with_completion_event")
+    del torch
+
+
+def time_full_step(L, app, dec, samples_out=None):
     """Config 5: RoPE + one-token append writing the rotated query and the new
     K/V rows, then paged decode reading them, captured as one graph."""
     def bind(b):
@@ -345,7 +485,7 @@ def time_full_step(L, app, dec):
     def record(scope, args):
         app.plan.enqueue_into(scope, args[0])
         dec.plan.enqueue_into(scope, args[1])
-    return _graph_replay(L, 16, 2, bind, record)
+    return _graph_replay(L, 16, 2, bind, record, samples_out=samples_out)
 
 
 def cpu_baseline(case, min_s=10.0, max_s=30.0):
@@ -600,6 +740,114 @@ def reference_shapes(L, stream, samples=30):
     return out
 
 
+def replay_floor(L, stream, n=200):
+    """Where a graph replay's time goes (run under rocprofv3 --runtime-trace
+    --kernel-trace for the per-call breakdown): the reference's T=6
+    explicit-token append (its gate fixture's page table) as a captured graph,
+    replayed `n` times with one completion event each (graph/mod.rs:301-323),
+    the same command eagerly (enqueue, finish, wait) `n` times, and a
+    torch-captured graph of one tiny kernel `n` times.  Reports the HIP-event
+    µs and the host wall-clock µs of each form (median)."""
+    import torch
+    g = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_digests.json")))
+    c = g["append_tokens_t6"]
+    dev = "cuda"
+    B, pool, hq, hkv, T = c["batch"], c["pool"], c["hq"], c["hkv"], c["tokens"]
+    plan = L.RopeProvider.load(0).plan_bf16_paged_append_tokens(
+        L.Bf16RopePagedKvAppendTokensSpec(T, B, pool, hq, hkv))
+    q, k, v = (torch.randn(T * h * 128, device=dev).to(torch.bfloat16) for h in (hq, hkv, hkv))
+    kp = torch.zeros(pool * 16 * hkv * 128, dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros_like(kp)
+    qo = torch.empty_like(q)
+    ip, ix, ln = (torch.tensor(c[x], dtype=torch.int32, device=dev)
+                  for x in ("indptr", "indices", "last"))
+    bi = torch.tensor(c.get("batch_indices", [0] * T), dtype=torch.int32, device=dev)
+    ps = torch.tensor(c.get("positions", list(range(T))), dtype=torch.int32, device=dev)
+    ws = torch.zeros(plan.workspace_bytes, dtype=torch.uint8, device=dev)
+
+    def bind(b):
+        return L.Bf16RopePagedKvAppendTokensArgs(
+            b.bind_read(q), b.bind_read(k), b.bind_read(v), b.bind_read(bi), b.bind_read(ps),
+            b.bind_read(ip), b.bind_read(ix), b.bind_read(ln), b.bind_read_write(qo).write(),
+            b.bind_read_write(kp).write(), b.bind_read_write(vp).write(),
+            b.bind_read_write(ws).write())
+
+    def med(xs):
+        xs = sorted(xs)
+        return round(xs[len(xs) // 2], 3)
+
+    out = {}
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gq = L.GraphQueue(0, 1)
+    b = gq.bindings(12)
+    args = bind(b)
+    exec_ = gq.capture(b, lambda scope: plan.enqueue_into(scope, args)).instantiate()
+    out["append_t6_graph_default_replay_mode"] = exec_.replay_mode
+    for mode, key in (("kernel_nodes", "append_t6_graph_replay"),
+                      ("hip_graph_launch", "append_t6_graph_replay_hip_graph_launch")):
+        exec_.set_replay_mode(mode)
+        gpu, host = [], []
+        for i in range(n + 5):
+            t0 = time.perf_counter()
+            ms = exec_.measure_launch_ms(ev0, ev1)
+            t1 = time.perf_counter()
+            if i >= 5:
+                gpu.append(ms * 1000.0)
+                host.append((t1 - t0) * 1e6)
+        out[key + "_event_us"] = med(gpu)
+        out[key + "_host_us"] = med(host)
+    exec_.into_bindings()
+    q_ = L.CommandQueue(stream, 1)
+    b = q_.bindings(12)
+    args = bind(b)
+    gpu, host = [], []
+    with torch.cuda.stream(stream):
+        for i in range(n + 5):
+            t0 = time.perf_counter()
+            ev0.record(stream)
+            scope = q_.begin(b)
+            plan.enqueue_into(scope, args)
+            ev1.record(stream)
+            b = scope.finish().wait()
+            ev1.synchronize()
+            t1 = time.perf_counter()
+            if i >= 5:
+                gpu.append(ev0.elapsed_time(ev1) * 1000.0)
+                host.append((t1 - t0) * 1e6)
+    out["append_t6_eager_single_event_us"] = med(gpu)
+    out["append_t6_eager_single_host_us"] = med(host)
+    x = torch.zeros(16, device=dev)
+    tg = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        x.add_(1)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(tg, stream=stream):
+            x.add_(1)
+    torch.cuda.synchronize()
+    gpu, host = [], []
+    for i in range(n + 5):
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            tg.replay()
+            ev1.record(stream)
+        ev1.synchronize()
+        t1 = time.perf_counter()
+        if i >= 5:
+            gpu.append(ev0.elapsed_time(ev1) * 1000.0)
+            host.append((t1 - t0) * 1e6)
+    out["torch_one_kernel_graph_replay_event_us"] = med(gpu)
+    out["torch_one_kernel_graph_replay_host_us"] = med(host)
+    if os.path.exists(CAPI_BENCH):
+        # the same forms from C++ with an empty kernel (no Python on the path)
+        import subprocess
+        r = subprocess.run([CAPI_BENCH, "--graph-floor", str(n)], capture_output=True, text=True,
+                           timeout=120)
+        if r.returncode == 0:
+            out["capi_empty_kernel"] = json.loads(r.stdout.strip().splitlines()[-1])
+    return out
+
+
 def prefill_shapes(L, stream, samples=30):
     """Paged causal prefill at the five shapes the reference times on H20
     (benchmarks/matched.rs:1355-1425; its eager and long-eager records): eager
@@ -789,6 +1037,9 @@ def main():
                     help="skip the seeds 0..4 sample statistics of the decode configs")
     ap.add_argument("--only", default=None,
                     help="run one config (prefix match, e.g. c3) and print its detail")
+    ap.add_argument("--records", default=os.path.join("gpurun_out", "bench_records.jsonl"),
+                    help="JSON Lines evidence records (raw samples, fixture digests, source "
+                         "commit) per config; '' to skip")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 20 plain device copies of MIB MiB (counter calibration)")
     a = ap.parse_args()
@@ -817,7 +1068,17 @@ def main():
         log(f"[bench] setting up {name}")
         case = DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name))
         us = time_eager(L, case, stream, a.steps, a.warmup)
-        g_us = time_graph(L, case)
+        g_samples = []
+        g_us = time_graph(L, case, samples_out=g_samples)
+        if a.records:
+            fid, dig, shape = decode_fixture(case)
+            xs = _sampled_enqueues(L, stream, 9, case.bind, case.plan.enqueue_into, 20, 10,
+                                   a.warmup)
+            kpc = decode_kernels_per_call(case.plan)
+            record("paged_batch_decode", name, kpc, shape, fid, dig, a.warmup, 10, xs,
+                   "eager_stream_batch_hip_event")
+            record("paged_batch_decode", name, kpc, shape, fid, dig, 3, 1, g_samples,
+                   "graph_replay_with_completion_event")
         gbs = case.bytes / (us * 1e-6) / 1e9
         detail[name] = {"us_per_call": round(us, 3), "graph_replay_us": round(g_us, 3),
                         "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
@@ -901,8 +1162,19 @@ def main():
         if name.startswith("c5"):
             # the one-token append of the same step, then the whole step as one graph
             app = AppendCase(L, B, hq, hkv, pool, lens, seed=5, share=case)
-            ap_us, ap_g = time_append(L, app, stream, a.steps, a.warmup)
-            step_g = time_full_step(L, app, case)
+            ap_gs = []
+            ap_us, ap_g = time_append(L, app, stream, a.steps, a.warmup, ap_gs)
+            if a.records:
+                record_append(name + "_one_token_append", app, stream, a.warmup, ap_gs)
+            st_gs = []
+            step_g = time_full_step(L, app, case, st_gs)
+            if a.records:
+                fid, dig, shape = decode_fixture(case)
+                dig.update(new_query=device_digest(app.q), new_key=device_digest(app.k),
+                           new_value=device_digest(app.v))
+                record("rope_paged_append+paged_batch_decode", name + "_full_step", 1 +
+                       decode_kernels_per_call(case.plan), shape, fid + "; new tokens seed 5",
+                       dig, 3, 1, st_gs, "graph_replay_with_completion_event")
             detail[name].update({"append_us_per_call": round(ap_us, 3),
                                  "append_graph_replay_us": round(ap_g, 3),
                                  "full_step_graph_replay_us": round(step_g, 3)})
@@ -923,7 +1195,10 @@ def main():
         existing = rng.integers(0, 4096, size=32)
         n_new = rng.integers(1, 65, size=32)
         app = AppendCase(L, 32, 32, 8, 16384, existing + n_new, seed=2, n_new=n_new)
-        ap_us, ap_g = time_append(L, app, stream, a.steps, a.warmup)
+        ap_gs = []
+        ap_us, ap_g = time_append(L, app, stream, a.steps, a.warmup, ap_gs)
+        if a.records:
+            record_append("c2_rope_append_b32_tokens", app, stream, a.warmup, ap_gs)
         # cold: 24 sets of the token inputs and query outputs (each ~20 MB)
         # rotated over the same page pools
         extra = []
@@ -955,6 +1230,20 @@ def main():
             detail["c2_rope_append_b32_tokens"]["cpu_baseline"] = cpu_append_baseline(app)
         log(f"[bench] c2: {detail['c2_rope_append_b32_tokens']}")
         del app
+    if a.only == "replay":
+        detail["replay_floor"] = replay_floor(L, stream)
+    elif not a.quick and (not a.only or a.only == "ref"):
+        detail["replay_floor"] = replay_floor(L, stream)
+        # the same in a child process with the HIP runtime's graph packet
+        # capture off (read at HIP initialisation: DEBUG_CLR_GRAPH_PACKET_CAPTURE=0)
+        import subprocess
+        env = dict(os.environ, DEBUG_CLR_GRAPH_PACKET_CAPTURE="0")
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "replay",
+                            "--no-cpu", "--records", ""], capture_output=True, text=True,
+                           timeout=300, env=env)
+        if r.returncode == 0:
+            d = json.loads(r.stdout.strip().splitlines()[-1])["replay_floor"]
+            detail["replay_floor"]["packet_capture_off"] = d
     if not a.quick and (not a.only or a.only == "ref"):
         log("[bench] reference published shapes")
         detail["reference_shapes"] = reference_shapes(L, stream)
@@ -967,6 +1256,7 @@ def main():
         log(f"[bench] {detail['ragged_prefill']}")
         detail["long_prefill"] = long_prefill_shapes(L, stream)
         log(f"[bench] {detail['long_prefill']}")
+    write_records(a.records)
     if a.only:
         print(json.dumps(detail), flush=True)
         return

@@ -1024,6 +1024,24 @@ void loom_captured_graph_free(loom_captured_graph_t *graph);
 loom_status_t loom_captured_graph_instantiate(loom_captured_graph_t *graph,
                                               loom_graph_exec_t **out, loom_error_t *err);
 uint64_t loom_graph_exec_commands(const loom_graph_exec_t *exec);
+/* No reference counterpart: how loom_graph_exec_launch replays the captured
+ * graph.  LOOM_GRAPH_REPLAY_KERNEL_NODES (the default whenever the capture is
+ * a chain of kernel nodes, which every capture of this library's commands
+ * is): each captured kernel node is launched with hipLaunchKernel, with the
+ * node's captured function, launch shape and argument copy, in dependency
+ * order, on the replay stream — the same work at the same fixed addresses.
+ * On MI355X with ROCm 7 a hipGraphLaunch of a one-node graph costs 15-23 us
+ * of host time before the kernel can start, against about 2.3 us for one
+ * hipLaunchKernel.  LOOM_GRAPH_REPLAY_HIP_GRAPH_LAUNCH submits the
+ * instantiated hipGraphExec with hipGraphLaunch (the only mode for other
+ * graphs).  set_replay_mode fails with LOOM_PLAN_INVALID_OPTION for a mode
+ * the graph cannot use and LOOM_GRAPH_REPLAY_IN_FLIGHT while a replay is in
+ * flight. */
+#define LOOM_GRAPH_REPLAY_HIP_GRAPH_LAUNCH 1
+#define LOOM_GRAPH_REPLAY_KERNEL_NODES 2
+int32_t loom_graph_exec_replay_mode(const loom_graph_exec_t *exec);
+loom_status_t loom_graph_exec_set_replay_mode(loom_graph_exec_t *exec, int32_t mode,
+                                              loom_error_t *err);
 uint64_t loom_graph_exec_launches(const loom_graph_exec_t *exec);
 /* GraphExec::launch, graph/mod.rs:249-293. */
 loom_status_t loom_graph_exec_launch(loom_graph_exec_t *exec, loom_graph_completion_t **out,

@@ -23,6 +23,13 @@ done
 for p in "${pids[@]}"; do wait "$p"; done
 "$HIPCC" --offload-arch=gfx950 -shared -fPIC "$obj"/*.o -o "$out/libloom_infer_hip.so.tmp"
 mv "$out/libloom_infer_hip.so.tmp" "$out/libloom_infer_hip.so"
+# provenance of this build for the benchmark's evidence records (the GPU box
+# has no git metadata): source commit, worktree state, library hash
+commit=$(git -C "$root" rev-parse HEAD 2>/dev/null || echo unknown)
+dirty=$( [ -n "$(git -C "$root" status --porcelain -- loom-kernels_amd include 2>/dev/null)" ] && echo true || echo false)
+sha=$(sha256sum "$out/libloom_infer_hip.so" | cut -d' ' -f1)
+printf '{"commit": "%s", "dirty": %s, "library_sha256": "%s", "abi_version": "1", "built_utc": "%s"}\n' \
+    "$commit" "$dirty" "$sha" "$(date -u +%Y-%m-%dT%H:%M:%SZ)" > "$out/BUILD_INFO.json"
 # the C-ABI eager benchmark (bench.py runs it as a child process)
 "$HIPCC" --offload-arch=gfx950 -O2 -std=c++17 -Wall -I"$root/include" "$here/csrc/capi_bench.cpp" \
     -L"$out" -lloom_infer_hip -Wl,-rpath,'$ORIGIN' -o "$out/capi_bench.tmp"

@@ -5,6 +5,7 @@
 //
 //   capi_bench B POOL HQ HKV "indptr,..." "indices,..." "last,..." [SAMPLES]
 //   capi_bench --empty-kernel [SAMPLES]
+//   capi_bench --graph-floor [SAMPLES]
 //
 // The second form times an empty kernel launched with hipLaunchKernelGGL the
 // same way: the platform's floor for one launch per command.
@@ -97,11 +98,73 @@ int empty_kernel_floor(int samples) {
   return 0;
 }
 
+// Where one graph replay's time goes, with no profiler attached: an empty
+// kernel launched eagerly and as a captured one-node hipGraph, each followed
+// by an event and a wait for it.  Per form (medians over SAMPLES): the
+// GPU-side time between an event recorded before the launch call and one
+// after it, the host time inside the launch call, and the host time from
+// before the launch call until the wait returns.
+int graph_floor(int samples) {
+  hipStream_t stream;
+  hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "stream");
+  hipEvent_t ev0, ev1;
+  hip_check(hipEventCreate(&ev0), "event");
+  hip_check(hipEventCreate(&ev1), "event");
+  hipGraph_t graph = nullptr;
+  hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture");
+  hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, stream, nullptr);
+  hip_check(hipStreamEndCapture(stream, &graph), "capture end");
+  hipGraphExec_t exec = nullptr, exec_up = nullptr;
+  hip_check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
+  hip_check(hipGraphInstantiate(&exec_up, graph, nullptr, nullptr, 0), "instantiate");
+  hip_check(hipGraphUpload(exec_up, stream), "upload");
+  hip_check(hipStreamSynchronize(stream), "sync");
+  auto measure = [&](auto launch) {
+    std::vector<double> gpu, call, wall;
+    for (int s = 0; s < samples + 5; ++s) {
+      hip_check(hipEventRecord(ev0, stream), "record");
+      const auto h0 = std::chrono::steady_clock::now();
+      launch();
+      const auto h1 = std::chrono::steady_clock::now();
+      hip_check(hipEventRecord(ev1, stream), "record");
+      hip_check(hipEventSynchronize(ev1), "sync");
+      const auto h2 = std::chrono::steady_clock::now();
+      float ms = 0.f;
+      hip_check(hipEventElapsedTime(&ms, ev0, ev1), "elapsed");
+      if (s >= 5) {
+        gpu.push_back(ms * 1000.0);
+        call.push_back(std::chrono::duration<double, std::micro>(h1 - h0).count());
+        wall.push_back(std::chrono::duration<double, std::micro>(h2 - h0).count());
+      }
+    }
+    for (auto *v : {&gpu, &call, &wall}) std::sort(v->begin(), v->end());
+    char buf[256];
+    std::snprintf(buf, sizeof buf, "{\"event_us\": %.3f, \"launch_call_us\": %.3f, \"wall_us\": %.3f}",
+                  gpu[gpu.size() / 2], call[call.size() / 2], wall[wall.size() / 2]);
+    return std::string(buf);
+  };
+  const std::string eager = measure([&] {
+    hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, stream, nullptr);
+  });
+  const std::string replay = measure([&] { hip_check(hipGraphLaunch(exec, stream), "launch"); });
+  const std::string uploaded = measure([&] { hip_check(hipGraphLaunch(exec_up, stream), "launch"); });
+  const char *pc = std::getenv("DEBUG_CLR_GRAPH_PACKET_CAPTURE");
+  std::printf("{\"eager_one_kernel\": %s, \"graph_one_node\": %s, \"graph_one_node_uploaded\": %s, "
+              "\"DEBUG_CLR_GRAPH_PACKET_CAPTURE\": \"%s\", \"samples\": %d}\n",
+              eager.c_str(), replay.c_str(), uploaded.c_str(), pc ? pc : "unset", samples);
+  (void)hipGraphExecDestroy(exec);
+  (void)hipGraphExecDestroy(exec_up);
+  (void)hipGraphDestroy(graph);
+  return 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
   if (argc >= 2 && std::string(argv[1]) == "--empty-kernel")
     return empty_kernel_floor(argc > 2 ? std::atoi(argv[2]) : 30);
+  if (argc >= 2 && std::string(argv[1]) == "--graph-floor")
+    return graph_floor(argc > 2 ? std::atoi(argv[2]) : 200);
   if (argc < 8) {
     std::fprintf(stderr, "usage: capi_bench B POOL HQ HKV indptr indices last [samples]\n");
     return 2;

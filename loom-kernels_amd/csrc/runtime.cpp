@@ -563,9 +563,23 @@ struct loom_captured_graph {
   uint64_t commands = 0;
 };
 
+// One captured kernel node, replayed with hipLaunchKernel: the function, its
+// launch shape and the node's own copy of the kernel arguments (owned by the
+// hipGraph, which the executable keeps).
+struct ReplayLaunch {
+  const void *func = nullptr;
+  dim3 grid, block;
+  void **params = nullptr;
+  unsigned shared = 0;
+};
+
 struct loom_graph_exec {
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
+  // The captured graph as a chain of kernel nodes (empty if it is not one)
+  // and how launch() replays it (LOOM_GRAPH_REPLAY_*).
+  std::vector<ReplayLaunch> chain;
+  int32_t replay_mode = LOOM_GRAPH_REPLAY_HIP_GRAPH_LAUNCH;
   loom_command_queue *queue = nullptr;
   hipEvent_t completion_event = nullptr;
   loom_bindings *bindings = nullptr;
@@ -624,6 +638,99 @@ loom_status_t settlement_error(loom_error_t *err, const char *op, int32_t failur
   if (sync_error)
     return fail(err, LOOM_GRAPH_SETTLEMENT, op, sync_error, 0, 0, 0, 0.0, failure);
   return fail(err, LOOM_GRAPH_DRIVER, op, 0, 0, 0, 0, 0.0, failure);
+}
+
+__global__ void grid_probe_kernel(int *p, int v) {
+  if (p) p[blockIdx.x] = v;
+}
+
+// How this HIP runtime reports a captured kernel node: its grid in workgroups
+// (1) or in work-items (2), with kernelParams an array of pointers to the
+// argument values; 0 when the node does not read back as expected (the
+// executable then replays with hipGraphLaunch only).  Probed once per process
+// by capturing (never running) a launch of known shape and arguments.
+int node_grid_semantics() {
+  static int probed = -1;
+  if (probed >= 0) return probed;
+  probed = 0;
+  hipStream_t s = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return probed;
+  int *const marker = reinterpret_cast<int *>(uintptr_t{0x7a5e1000});  // never dereferenced
+  hipGraph_t g = nullptr;
+  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+    hipLaunchKernelGGL(grid_probe_kernel, dim3(3), dim3(64), 0, s, marker, 7);
+    (void)hipStreamEndCapture(s, &g);
+  }
+  if (g) {
+    hipGraphNode_t node = nullptr;
+    size_t n = 1;
+    hipKernelNodeParams p{};
+    if (hipGraphGetNodes(g, &node, &n) == hipSuccess && n == 1 &&
+        hipGraphKernelNodeGetParams(node, &p) == hipSuccess && p.blockDim.x == 64 &&
+        p.blockDim.y == 1 && p.blockDim.z == 1 && p.kernelParams && !p.extra &&
+        p.kernelParams[0] && p.kernelParams[1] &&
+        *static_cast<int **>(p.kernelParams[0]) == marker &&
+        *static_cast<int *>(p.kernelParams[1]) == 7) {
+      if (p.gridDim.x == 3 && p.gridDim.y == 1 && p.gridDim.z == 1) probed = 1;
+      else if (p.gridDim.x == 3 * 64 && p.gridDim.y == 1 && p.gridDim.z == 1) probed = 2;
+    }
+    hipGraphDestroy(g);
+  }
+  (void)hipGetLastError();
+  hipStreamDestroy(s);
+  return probed;
+}
+
+// The graph's nodes as a chain of kernel nodes in dependency order (each node
+// depends on exactly the one before it), or false.
+bool kernel_chain(hipGraph_t g, std::vector<ReplayLaunch> *out) {
+  const int sem = node_grid_semantics();
+  if (!sem) return false;
+  size_t n = 0;
+  if (hipGraphGetNodes(g, nullptr, &n) != hipSuccess || n == 0) return false;
+  std::vector<hipGraphNode_t> nodes(n), order;
+  if (hipGraphGetNodes(g, nodes.data(), &n) != hipSuccess) return false;
+  std::vector<hipGraphNode_t> dep(n, nullptr);
+  for (size_t i = 0; i < n; ++i) {
+    hipGraphNodeType t;
+    if (hipGraphNodeGetType(nodes[i], &t) != hipSuccess || t != hipGraphNodeTypeKernel) return false;
+    size_t nd = 0;
+    if (hipGraphNodeGetDependencies(nodes[i], nullptr, &nd) != hipSuccess || nd > 1) return false;
+    if (nd == 1 && hipGraphNodeGetDependencies(nodes[i], &dep[i], &nd) != hipSuccess) return false;
+  }
+  hipGraphNode_t prev = nullptr;
+  for (size_t k = 0; k < n; ++k) {  // follow the chain from its root
+    size_t found = n;
+    for (size_t i = 0; i < n; ++i)
+      if (dep[i] == prev && std::find(order.begin(), order.end(), nodes[i]) == order.end()) {
+        if (found != n) return false;  // two nodes after one: not a chain
+        found = i;
+      }
+    if (found == n) return false;
+    order.push_back(nodes[found]);
+    prev = nodes[found];
+  }
+  std::vector<ReplayLaunch> chain;
+  for (hipGraphNode_t node : order) {
+    hipKernelNodeParams p{};
+    if (hipGraphKernelNodeGetParams(node, &p) != hipSuccess || !p.func || !p.kernelParams || p.extra)
+      return false;
+    ReplayLaunch l;
+    l.func = p.func;
+    l.block = p.blockDim;
+    l.grid = p.gridDim;
+    if (sem == 2) {
+      if (!p.blockDim.x || !p.blockDim.y || !p.blockDim.z || p.gridDim.x % p.blockDim.x ||
+          p.gridDim.y % p.blockDim.y || p.gridDim.z % p.blockDim.z)
+        return false;
+      l.grid = dim3(p.gridDim.x / p.blockDim.x, p.gridDim.y / p.blockDim.y, p.gridDim.z / p.blockDim.z);
+    }
+    l.params = p.kernelParams;
+    l.shared = p.sharedMemBytes;
+    chain.push_back(l);
+  }
+  *out = std::move(chain);
+  return true;
 }
 
 void destroy_exec(loom_graph_exec *x) {
@@ -796,6 +903,7 @@ loom_status_t loom_captured_graph_instantiate(loom_captured_graph_t *c, loom_gra
   auto *x = new loom_graph_exec;
   x->exec = exec;
   x->graph = c->graph;
+  if (kernel_chain(c->graph, &x->chain)) x->replay_mode = LOOM_GRAPH_REPLAY_KERNEL_NODES;
   x->queue = c->queue;
   x->completion_event = ev;
   x->bindings = c->bindings;
@@ -806,6 +914,20 @@ loom_status_t loom_captured_graph_instantiate(loom_captured_graph_t *c, loom_gra
 }
 
 uint64_t loom_graph_exec_commands(const loom_graph_exec_t *x) { return x ? x->commands : 0; }
+
+int32_t loom_graph_exec_replay_mode(const loom_graph_exec_t *x) { return x ? x->replay_mode : 0; }
+
+loom_status_t loom_graph_exec_set_replay_mode(loom_graph_exec_t *x, int32_t mode,
+                                              loom_error_t *err) {
+  if (!x) return fail(err, LOOM_NULL_ARGUMENT, "exec");
+  if (x->in_flight) return fail(err, LOOM_GRAPH_REPLAY_IN_FLIGHT);
+  if (mode == LOOM_GRAPH_REPLAY_HIP_GRAPH_LAUNCH ||
+      (mode == LOOM_GRAPH_REPLAY_KERNEL_NODES && !x->chain.empty())) {
+    x->replay_mode = mode;
+    return loom::ok(err);
+  }
+  return fail(err, LOOM_PLAN_INVALID_OPTION, "replay_mode", mode);
+}
 uint64_t loom_graph_exec_launches(const loom_graph_exec_t *x) { return x ? x->launches : 0; }
 
 loom_status_t loom_graph_exec_launch(loom_graph_exec_t *x, loom_graph_completion_t **out,
@@ -818,7 +940,18 @@ loom_status_t loom_graph_exec_launch(loom_graph_exec_t *x, loom_graph_completion
   x->in_flight = true;
   x->record_error = 0;
   x->poll_error = 0;
-  hipError_t e = hipGraphLaunch(x->exec, x->queue->stream);
+  hipError_t e = hipSuccess;
+  if (x->replay_mode == LOOM_GRAPH_REPLAY_KERNEL_NODES) {
+    // The captured kernel nodes with their captured arguments, in order, on
+    // the replay stream: the same work as hipGraphLaunch of this chain, at
+    // the cost of one kernel launch per node.
+    for (const ReplayLaunch &l : x->chain) {
+      e = hipLaunchKernel(l.func, l.grid, l.block, l.params, l.shared, x->queue->stream);
+      if (e != hipSuccess) break;
+    }
+  } else {
+    e = hipGraphLaunch(x->exec, x->queue->stream);
+  }
   if (e != hipSuccess) {
     hipError_t sync = loom::synchronize_stream_or_abort(x->queue->stream);
     x->in_flight = false;

@@ -36,6 +36,7 @@ PARTIAL_STATE_WIDTH = 130
 PLAN_PAGE_INDICES_CAPACITY = 1
 PLAN_PREFILL_TILE_16 = 2
 PLAN_PREFILL_TILE_64 = 4
+GRAPH_REPLAY_MODES = {1: "hip_graph_launch", 2: "kernel_nodes"}
 PLAN_APPEND_TWO_LAUNCH = 8
 PLAN_APPEND_TEST_NO_WAIT = 16
 
@@ -1306,6 +1307,16 @@ class GraphExec:
 
     def launches(self) -> int:
         return lib().loom_graph_exec_launches(self._p)
+
+    @property
+    def replay_mode(self) -> str:
+        """'kernel_nodes' (the captured kernel nodes relaunched in order) or
+        'hip_graph_launch' (no reference counterpart)."""
+        return GRAPH_REPLAY_MODES.get(lib().loom_graph_exec_replay_mode(self._p), "unknown")
+
+    def set_replay_mode(self, mode: str):
+        code = {v: k for k, v in GRAPH_REPLAY_MODES.items()}[mode]
+        _call(lib().loom_graph_exec_set_replay_mode, self._p, code)
 
     def launch(self) -> GraphLaunchCompletion:
         out = C.c_void_p()

@@ -263,6 +263,8 @@ SIGNATURES = {
     "loom_captured_graph_free": (None, [vp]),
     "loom_captured_graph_instantiate": (i32, [vp, P(vp), E]),
     "loom_graph_exec_commands": (u64, [vp]),
+    "loom_graph_exec_replay_mode": (i32, [vp]),
+    "loom_graph_exec_set_replay_mode": (i32, [vp, i32, E]),
     "loom_graph_exec_launches": (u64, [vp]),
     "loom_graph_exec_launch": (i32, [vp, P(vp), E]),
     "loom_graph_exec_measure_launch_ms": (i32, [vp, vp, vp, P(f32), E]),

@@ -116,7 +116,30 @@ def within_one_ulp(oracle, got, want):
     return bool(not bad.any()), int(np.sum(~same))
 
 
-def check_rope(oracle, got, want, inputs, positions_per_row, what):
+ROPE_PINS_PATH = os.path.join(os.path.dirname(__file__), "golden", "rope_beyond_one_ulp.json")
+
+
+def pin_rope_counts(key, beyond, mism):
+    """The number of elements beyond one BF16 ulp (all explained by the host
+    sinf/cosf rounding) and of bit mismatches, pinned per case in
+    tests/golden/rope_beyond_one_ulp.json: a change in the device's sin/cos
+    or rotation arithmetic shifts them even when every element stays
+    explainable.  With LOOM_RECORD_ROPE_COUNTS=<file> the observed counts are
+    written there instead (to create the pins)."""
+    rec = os.environ.get("LOOM_RECORD_ROPE_COUNTS")
+    if rec:
+        d = json.load(open(rec)) if os.path.exists(rec) else {}
+        d[key] = {"beyond_one_ulp": beyond, "bit_mismatches": mism}
+        os.makedirs(os.path.dirname(os.path.abspath(rec)), exist_ok=True)
+        json.dump(d, open(rec, "w"), indent=1, sort_keys=True)
+        return
+    pins = json.load(open(ROPE_PINS_PATH))
+    assert key in pins, f"no pinned RoPE counts for {key}"
+    assert pins[key] == {"beyond_one_ulp": beyond, "bit_mismatches": mism}, (key, pins[key],
+                                                                            beyond, mism)
+
+
+def check_rope(oracle, got, want, inputs, positions_per_row, what, pin=None):
     """RoPE output against the oracle: within one BF16 ulp everywhere, except
     elements proven to differ only through the oracle's sin/cos rounding.
 
@@ -137,6 +160,8 @@ def check_rope(oracle, got, want, inputs, positions_per_row, what):
     assert not unexplained, (f"{what}: {len(unexplained)} of {beyond} elements beyond 1 BF16 "
                              f"ulp not explained by sin/cos rounding, first "
                              f"(row, col, pos, got, want, host, cr) {unexplained[:4]}")
+    if pin:
+        pin_rope_counts(pin, beyond, mism)
     return beyond
 
 
@@ -407,12 +432,13 @@ def test_bulk_append_config2_shape(L, oracle):
     spec = L.Bf16RopePagedKvAppendTokensSpec.extended(T, B, pool, hq, hkv)
     r = AppendRunner(L, spec, True)
     qo, okp, ovp = r.run(q, k, v, bi, pos, indptr, indices, last, kp, vp)
-    n_q = check_rope(oracle, qo, eq, q, np.repeat(pos, hq), "query")
+    n_q = check_rope(oracle, qo, eq, q, np.repeat(pos, hq), "query", pin="c2_bulk_query")
     # appended K rows: gather the slots, then require the rest of the pool untouched
     slots = [(indices[indptr[b] + p // 16], p % 16) for b, p in zip(bi, pos)]
     rows = np.array([(pg * 16 + off) * hkv + h for pg, off in slots for h in range(hkv)])
     okr, ekr = okp.reshape(-1, 128), ekp.reshape(-1, 128)
-    n_k = check_rope(oracle, okr[rows], ekr[rows], k, np.repeat(pos, hkv), "key rows")
+    n_k = check_rope(oracle, okr[rows], ekr[rows], k, np.repeat(pos, hkv), "key rows",
+                     pin="c2_bulk_key_rows")
     log(f"  config 2: {T} tokens, {n_q + n_k} elements beyond 1 BF16 ulp, every one explained")
     okr[rows] = 0
     ekr[rows] = 0

@@ -162,13 +162,15 @@ def test_config5_full_step_graph_b256_pool262144(L, oracle):
         if i == 0:
             # RoPE within one BF16 ulp, or proven sin/cos rounding differences
             pos = (lens - 1).astype(np.int64)
-            check_rope(oracle, bf16_host(qrot), eq, qn_h, np.repeat(pos, hq), "query")
+            check_rope(oracle, bf16_host(qrot), eq, qn_h, np.repeat(pos, hq), "query",
+                       pin="c5_one_token_query")
             # the appended K rows, then every other row of the used pages bit-exact
             got_k = gather_pages(kp, pool, indices).reshape(-1, 128)
             want_k = kp_h.reshape(-1, 128)
             slot = indptr[:-1] + (pos // 16)  # compact page of each request's new token
             rows = ((slot * 16 + pos % 16)[:, None] * hkv + np.arange(hkv)).reshape(-1)
-            check_rope(oracle, got_k[rows], want_k[rows], kn_h, np.repeat(pos, hkv), "key rows")
+            check_rope(oracle, got_k[rows], want_k[rows], kn_h, np.repeat(pos, hkv), "key rows",
+                       pin="c5_one_token_key_rows")
             got_k[rows] = 0
             want_k[rows] = 0
             assert np.array_equal(got_k, want_k), "key pages outside the appended rows"

@@ -63,7 +63,13 @@ def test_decode_graph_replays_match_eager_and_oracle(L, oracle, B, hq, hkv, lens
     # external owners dropped before replay: the graph's bindings keep them alive
     del tq, tk, tv, tip, tix, tln
     exec_ = graph.instantiate()
-    for i in range(1, 4):
+    # the captured kernel nodes relaunched in order (default), then the same
+    # executable through hipGraphLaunch: every replay equals the eager call
+    assert exec_.replay_mode == "kernel_nodes"
+    for i in range(1, 7):
+        if i == 4:
+            exec_.set_replay_mode("hip_graph_launch")
+            assert exec_.replay_mode == "hip_graph_launch"
         out.fill_(float("nan"))  # eager work between replays
         torch.cuda.synchronize()
         c = exec_.launch()
@@ -71,14 +77,18 @@ def test_decode_graph_replays_match_eager_and_oracle(L, oracle, B, hq, hkv, lens
         with pytest.raises(L.GraphError) as e:
             exec_.launch()
         assert e.value.variant == "ReplayInFlight"
+        with pytest.raises(L.GraphError) as e:
+            exec_.set_replay_mode("kernel_nodes")
+        assert e.value.variant == "ReplayInFlight"
         c.wait()
         assert np.array_equal(bf16_host(out), eager_o), f"replay {i}"
         assert np.array_equal(lse.cpu().numpy(), eager_l), f"replay {i}"
+    exec_.set_replay_mode("kernel_nodes")
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     ms = exec_.measure_launch_ms(start, end)
     assert ms > 0
-    assert exec_.launches() == 4 and exec_.commands() == 1
+    assert exec_.launches() == 7 and exec_.commands() == 1
     b = exec_.into_bindings()
     assert b.take_read_write(h[6]) is out
 
@@ -133,7 +143,10 @@ def test_full_decode_step_graph(L, oracle):
 
     exec_ = gq.capture(b, record).instantiate()
     assert exec_.commands() == 2
-    for i in range(3):
+    assert exec_.replay_mode == "kernel_nodes"
+    for i in range(6):
+        if i == 3:  # the same executable through hipGraphLaunch
+            exec_.set_replay_mode("hip_graph_launch")
         out.zero_()
         torch.cuda.synchronize()
         exec_.launch().wait()
