@@ -938,7 +938,7 @@ def ragged_shapes(L, stream, samples=30):
     return out
 
 
-def long_prefill_shapes(L, stream, samples=5):
+def long_prefill_shapes(L, stream, samples=5, shapes=None):
     """Paged causal prefill on long prompts (no reference counterpart: its
     timed shapes stop at 64 query rows): GQA4 Hq 32 / Hkv 8, qo_len = kv_len per
     request, a seeded permutation page table; eager µs (median of `samples`
@@ -946,7 +946,7 @@ def long_prefill_shapes(L, stream, samples=5):
     import torch
     dev = "cuda"
     out = {}
-    for B, n in ((1, 512), (1, 1024), (1, 4096), (1, 8192), (4, 2048), (8, 256)):
+    for B, n in shapes or ((1, 512), (1, 1024), (1, 4096), (1, 8192), (4, 2048), (8, 256)):
         hq, hkv = 32, 8
         nnz, pages = B * n, (n + 15) // 16
         pool = B * pages
@@ -970,9 +970,17 @@ def long_prefill_shapes(L, stream, samples=5):
         us = sorted(_timed_enqueues(L, stream, 9, bind, plan.enqueue_into, 5, 2)
                     for _ in range(samples))[samples // 2]
         flops = B * (n * (n + 1) // 2) * hq * 128 * 4
-        out[f"gqa4_b{B}_q{n}_kv{n}"] = {"eager_us": round(us, 2), "causal_gflop": round(flops / 1e9, 2),
-                                       "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1),
-                                       "grid_blocks": plan.info.grid_blocks}
+        rec = {"eager_us": round(us, 2), "causal_gflop": round(flops / 1e9, 2),
+               "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1), "algorithm": plan.algorithm,
+               "grid_blocks": plan.info.grid_blocks}
+        if plan.algorithm == "long_tile":
+            # the wide tiles on the same command, for comparison
+            wplan = L.PrefillProvider.load(0).plan_bf16_paged(spec, tile_cols=64)
+            wus = sorted(_timed_enqueues(L, stream, 9, bind, wplan.enqueue_into, 5, 2)
+                         for _ in range(samples))[samples // 2]
+            rec.update(wide_eager_us=round(wus, 2),
+                       wide_TFLOPs=round(flops / (wus * 1e-6) / 1e12, 1))
+        out[f"gqa4_b{B}_q{n}_kv{n}"] = rec
     return out
 
 
@@ -1230,6 +1238,8 @@ def main():
             detail["c2_rope_append_b32_tokens"]["cpu_baseline"] = cpu_append_baseline(app)
         log(f"[bench] c2: {detail['c2_rope_append_b32_tokens']}")
         del app
+    if a.only == "long_prefill":  # profiling: the 8192-row prompt alone
+        detail["long_prefill"] = long_prefill_shapes(L, stream, samples=3, shapes=((1, 8192),))
     if a.only == "replay":
         detail["replay_floor"] = replay_floor(L, stream)
     elif not a.quick and (not a.only or a.only == "ref"):

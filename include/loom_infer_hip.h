@@ -694,18 +694,26 @@ typedef enum loom_paged_prefill_algorithm {
    * staged through LDS and read by all four waves, so a workgroup reads a
    * quarter of the L2 bytes per column that ROW_TILE reads.  No cross-wave
    * merge.  No workspace. */
-  LOOM_PAGED_PREFILL_WIDE_TILE = 2
+  LOOM_PAGED_PREFILL_WIDE_TILE = 2,
+  /* Long prompts on BF16 pages (paged prefill only): WIDE_TILE's columns and
+   * page walk with 32-token blocks, the query fragments in registers, the
+   * softmax weights P rounded once to BF16 for the P·V product (the
+   * normalizer is summed in FP32; within the attention tolerance of the f32
+   * reference) and V staged transposed in LDS.  No workspace. */
+  LOOM_PAGED_PREFILL_LONG_TILE = 3
 } loom_paged_prefill_algorithm_t;
 
-/* Prefill plan flags (no reference counterpart): force ROW_TILE or WIDE_TILE;
- * with neither, the plan picks one from the spec. */
+/* Prefill plan flags (no reference counterpart): force ROW_TILE, WIDE_TILE
+ * or LONG_TILE; with none, the plan picks one from the spec. */
 #define LOOM_PLAN_PREFILL_TILE_16 2u
 #define LOOM_PLAN_PREFILL_TILE_64 4u
+#define LOOM_PLAN_PREFILL_TILE_LONG 8u
 
 typedef struct loom_paged_prefill_plan_options {
   uint32_t waves; /* waves per workgroup: 0 (the default, four), 4, 8 or 16 */
   uint32_t flags; /* LOOM_PLAN_PAGE_INDICES_CAPACITY (paged only) and at most one of
-                     LOOM_PLAN_PREFILL_TILE_16 / LOOM_PLAN_PREFILL_TILE_64 (four waves) */
+                     LOOM_PLAN_PREFILL_TILE_16 / _64 / _LONG (the last two: four waves;
+                     _LONG: paged prefill on BF16 pages only) */
 } loom_paged_prefill_plan_options_t;
 
 typedef struct loom_paged_prefill_plan_info {

@@ -98,7 +98,7 @@ constexpr int64_t kNoTiles = (int64_t)1 << 50;
 #endif
 constexpr int prefill_depth(int w) { return w >= 16 ? 1 : LOOM_PREFILL_DEPTH; }
 
-template <int W, bool SH>
+template <int W, bool SH, bool LT = false>
 struct PrefillSmem {
   int64_t wave_tot[W];
   int32_t wave_max[W];
@@ -107,11 +107,11 @@ struct PrefillSmem {
   // the located request's qo_indptr pair, page (or kv) indptr pair, tail, and
   // the first flattened column it owns
   int32_t meta[6];
-  u32x4 qfrag[SH ? W : 1][4][64];  // MFMA B fragments of 16 query columns (per wave: SH)
+  u32x4 qfrag[(SH && !LT) ? W : 1][4][64];  // MFMA B fragments of 16 query columns (per wave: SH)
   float m[W][16];      // per-wave running max (log2 domain) per column
   float l[W][16];      // per-wave normalizer per column
   uint32_t bad[W];     // per-wave invalid-page-index flags
-  f32x4 red[SH ? 1 : (W / 2 > 0 ? W / 2 : 1)][4][64];  // tree-sum staging (row tiles only)
+  f32x4 red[(SH || LT) ? 1 : (W / 2 > 0 ? W / 2 : 1)][4][64];  // tree-sum staging (row tiles only)
 };
 
 // One page of K (A-fragment layout) and V (row layout) for one wave.
@@ -341,13 +341,156 @@ struct PrefillWave {
       }
     }
   }
+
+  // ---- long tiles (LOOM_PAGED_PREFILL_LONG_TILE, BF16 pages) ----------------
+  // The workgroup's four waves own 16 columns each and walk 32-token blocks
+  // (two 16-row blocks).  Per block, in a two-slot LDS ring:
+  //   K as 32 rows of 272 bytes (the A-fragment reads of S = K·Qᵀ are conflict
+  //   free), staged by waves 0-1 (four 16-byte loads per lane);
+  //   Vᵀ as 8 token groups x 128 dims x 4 tokens (8 bytes: the four tokens of
+  //   one dimension), staged by waves 2-3, each lane transposing the 8 dims x
+  //   4 tokens it loaded with v_perm, so a lane's A fragment of Oᵀ += Vᵀ·Pᵀ
+  //   (one dimension, eight tokens) is two 8-byte reads.
+  // The query fragments stay in registers.  P enters the MFMA as BF16 (one
+  // rounding per weight, the normalizer summed in FP32), so each 32-token block
+  // is 8 S and 8 P·V MFMAs of 16x16x32 per wave, against 12 per 16 tokens with
+  // the wide tiles' high/residual split of P.  The accumulator holds
+  // acc[e][i] = O[column col][dim 16 e + 4 quad + i].
+  static constexpr int kLongKBytes = 32 * 272;
+  static constexpr int kLongSlotBytes = kLongKBytes + 8 * 128 * 8;
+
+  __device__ void process_long(const uint8_t *slot, int64_t lt0, const u32x4 (&qreg)[4]) {
+    const uint8_t *kt = slot;
+    const uint8_t *vt = slot + kLongKBytes;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kt + col * 272 + (4 * c + quad) * 16);
+      const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kt + (16 + col) * 272 + (4 * c + quad) * 16);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k0), as_bf16x8(qreg[c]), s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k1), as_bf16x8(qreg[c]), s1, 0, 0, 0);
+    }
+    // s0[i] = S[token 4 quad + i][column col], s1[i] = S[16 + 4 quad + i][col];
+    // tokens at or past the column's causal end are masked
+    const int vis = (int)max<int64_t>(-1, min<int64_t>(32, end_col - lt0));
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sv[i] = (quad * 4 + i < vis) ? s0[i] * a.scale_log2 : -INFINITY;
+      sv[4 + i] = (16 + quad * 4 + i < vis) ? s1[i] * a.scale_log2 : -INFINITY;
+    }
+    float mx = sv[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+    mx = quad_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet
+    const float al = fast_exp2(m_run - m_use);
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
+    l_run = l_run * al + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+    m_run = m_new;
+    if (__builtin_amdgcn_ballot_w64(al != 1.0f))
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= al;
+    // Pᵀ as the B fragment (lane: column col, k = 8 quad + [0, 8)): k = 8 quad
+    // + i is token 4 quad + i, k = 8 quad + 4 + i token 16 + 4 quad + i
+    const bf16x8 pt = as_bf16x8(bf16x2_pack(p[0], p[1]), bf16x2_pack(p[2], p[3]),
+                                bf16x2_pack(p[4], p[5]), bf16x2_pack(p[6], p[7]));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int dim = 16 * e + col;
+      const u32x2 lo = *reinterpret_cast<const u32x2 *>(vt + (quad * 128 + dim) * 8);
+      const u32x2 hi = *reinterpret_cast<const u32x2 *>(vt + ((4 + quad) * 128 + dim) * 8);
+      acc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(lo[0], lo[1], hi[0], hi[1]), pt,
+                                                       acc[e], 0, 0, 0);
+    }
+  }
+
+  // 16-row blocks 0..n16-1 of the current page-index window as 32-token
+  // blocks (the second half of the last one is empty when n16 is odd: no
+  // rows, no traffic).  Every wave stages its share of each block two blocks
+  // ahead; one barrier per block.  A slot is rewritten two blocks later, after
+  // every wave has passed the barrier that follows its reads; windows hold 64
+  // 16-row blocks (an even number of 32-token blocks), so a window's first
+  // block never reuses the slot its predecessor's last block is read from.
+  template <class PageTok, class RowsOf, class LtOf>
+  __device__ void stream_long(int n16, PageTok page_tok, RowsOf rows_of, LtOf lt_of,
+                              uint8_t *ring, int wave, int64_t own_end, const u32x4 (&qreg)[4]) {
+    const int t = threadIdx.x & 127;
+    const bool stage_v = wave >= 2;
+    const int row_bytes = a.row_elems * 2;
+    const int nb = (n16 + 1) >> 1;
+    // K stagers: chunk j of lane t is row 8 (j & 1) + (t >> 4) of 16-row block
+    // 2i + (j >> 1), bytes (t & 15) * 16 .. +16.  V stagers: token group g =
+    // t >> 4 (tokens 4g .. 4g + 3 of the 32), dims 8 (t & 15) .. +8.
+    auto fetch = [&](int i, u32x4 (&d)[4]) {
+      if (!stage_v) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int b16 = 2 * i + h;
+          const __amdgpu_buffer_rsrc_t r = page_rows_rsrc(
+              a.k + page_tok(b16) + (int64_t)kvh * a.head_elems, rows_of(b16), a.row_elems);
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+            d[2 * h + jj] = load16_rows<false>(r, (8 * jj + (t >> 4)) * row_bytes + (t & 15) * 16);
+        }
+      } else {
+        const int g = t >> 4;
+        const int b16 = 2 * i + (wave - 2);  // wave 2: tokens 0-15, wave 3: 16-31
+        const __amdgpu_buffer_rsrc_t r = page_rows_rsrc(
+            a.v + page_tok(b16) + (int64_t)kvh * a.head_elems, rows_of(b16), a.row_elems);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          d[j] = load16_rows<false>(r, (4 * (g & 3) + j) * row_bytes + (t & 15) * 16);
+      }
+    };
+    auto store = [&](int i, const u32x4 (&d)[4]) {
+      uint8_t *slot = ring + (i & 1) * kLongSlotBytes;
+      if (!stage_v) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<u32x4 *>(slot + (8 * j + (t >> 4)) * 272 + (t & 15) * 16) = d[j];
+      } else {
+        uint8_t *vt = slot + kLongKBytes;
+        const int g = t >> 4, d8 = t & 15;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          // dims 8 d8 + 2k (low halves) and + 2k + 1 (high halves) of tokens
+          // 4g .. 4g + 3: two 8-byte entries, adjacent
+          const u32x4 w = {pack_lo16(d[0][k], d[1][k]), pack_lo16(d[2][k], d[3][k]),
+                           pack_hi16(d[0][k], d[1][k]), pack_hi16(d[2][k], d[3][k])};
+          *reinterpret_cast<u32x4 *>(vt + (g * 128 + 8 * d8 + 2 * k) * 8) = w;
+        }
+      }
+    };
+    auto step = [&](int i, u32x4 (&d)[4]) {
+      store(i, d);
+      fetch(i + 2, d);  // past the end: no valid rows, no traffic
+      __syncthreads();
+      const int64_t lt0 = lt_of(2 * i);
+      if (lt0 < own_end) process_long(ring + (i & 1) * kLongSlotBytes, lt0, qreg);
+    };
+    u32x4 d0[4], d1[4];
+    fetch(0, d0);
+    fetch(1, d1);
+    for (int i = 0; i < nb; i += 2) {
+      step(i, d0);
+      if (i + 1 >= nb) break;
+      step(i + 1, d1);
+    }
+  }
 };
 
 // SH: the wide-tile algorithm (W = 4, BF16): 16 * W columns per workgroup,
 // one 16-column tile per wave, every wave over the whole page range.
-template <int W, bool RAGGED, bool FP8, bool SH>
+// LT: the long-tile algorithm (SH's columns and block walk; 32-token blocks,
+// query fragments in registers, BF16 P, Vᵀ staged transposed).
+template <int W, bool RAGGED, bool FP8, bool SH, bool LT = false>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   static_assert(!SH || W == 4, "wide tiles: four waves");
+  static_assert(!LT || (SH && !FP8), "long tiles: the wide tiles' columns, BF16 pages");
   constexpr int TC = SH ? 16 * W : 16;  // flattened columns per workgroup
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   PrefillArgs a = args;
@@ -356,7 +499,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     a.scale_log2 *= a.kv_scales[0];
     v_scale = a.kv_scales[1];
   }
-  __shared__ PrefillSmem<W, SH> sm;
+  __shared__ PrefillSmem<W, SH, LT> sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, quad = lane >> 4;
@@ -533,7 +676,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     }
   }
 
-  PrefillWave w{a, sm.qfrag[SH ? wave : 0], lane, col, quad, kvh};
+  PrefillWave w{a, sm.qfrag[(SH && !LT) ? wave : 0], lane, col, quad, kvh};
   w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
   w.reset();
   // The current block of up to 64 page indices (one per lane) of this wave.
@@ -573,9 +716,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   if constexpr (!SH) {
     if (mine > 0) w.template prime<D, FP8>(buf, page_tok, rows_of);
   }
-  if (SH || wave == 0) {
+  if (!LT && (SH || wave == 0)) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) sm.qfrag[SH ? wave : 0][c][lane] = colv ? qr[c] : u32x4{0, 0, 0, 0};
+  }
+  if constexpr (LT) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qr[c] = colv ? qr[c] : u32x4{0, 0, 0, 0};
   }
   __syncthreads();
 
@@ -586,13 +733,18 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
       ok = (RAGGED || (idx >= 0 && (int64_t)idx < a.pool)) ? 1 : 0;
     }
     if constexpr (SH) {
-      __shared__ u32x4 ring[2][2][16][17];
       // causal end of this wave's last column (0: the wave's tile is empty)
       const int64_t own_end =
           own0 < fcols
               ? kv_len - qo_len + (int)((uint32_t)min(own0 + 15, fcols - 1) / (uint32_t)a.group) + 1
               : 0;
-      w.template stream_shared<FP8>(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
+      if constexpr (LT) {
+        __shared__ __align__(16) uint8_t lring[2 * PrefillWave::kLongSlotBytes];
+        w.stream_long(n, page_tok, rows_of, lt_of, lring, wave, uni64(own_end), qr);
+      } else {
+        __shared__ u32x4 ring[2][2][16][17];
+        w.template stream_shared<FP8>(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
+      }
     } else {
       w.template stream<D, FP8>(buf, s0 == 0, n, page_tok, rows_of, lt_of);
     }
@@ -604,14 +756,24 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     if (block_or(bad, sm.bad) || !colv) return;
     const float inv = 1.0f / L;
     const int64_t row_head = (int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh;
-    uint16_t *orow = a.out + row_head * 128 + quad * 32;
+    if constexpr (LT) {
+      // acc[e][i] = O[col][16 e + 4 quad + i]: 8 bytes per dim block
+      uint16_t *orow = a.out + row_head * 128 + quad * 4;
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      u32x4 o;
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<u32x2 *>(orow + 16 * e) =
+            u32x2{bf16x2_pack(w.acc[e][0] * inv, w.acc[e][1] * inv),
+                  bf16x2_pack(w.acc[e][2] * inv, w.acc[e][3] * inv)};
+    } else {
+      uint16_t *orow = a.out + row_head * 128 + quad * 32;
 #pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2)
-        o[e2] = bf16x2_pack(w.acc[2 * e2][r4] * inv * v_scale, w.acc[2 * e2 + 1][r4] * inv * v_scale);
-      *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
+      for (int r4 = 0; r4 < 4; ++r4) {
+        u32x4 o;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2)
+          o[e2] = bf16x2_pack(w.acc[2 * e2][r4] * inv * v_scale, w.acc[2 * e2 + 1][r4] * inv * v_scale);
+        *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
+      }
     }
     if (quad == 0) a.lse[row_head] = w.m_run + __log2f(L);
     return;
@@ -674,9 +836,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
 // those gaps (the four-wave BF16 kernel would otherwise settle at two).
 constexpr int kPrefillWavesPerEu = 3;
 
-template <int W, bool FP8, bool SH = false>
+template <int W, bool FP8, bool SH = false, bool LT = false>
 __global__ __launch_bounds__(W * 64, kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
-  prefill_body<W, false, FP8, SH>(a);
+  prefill_body<W, false, FP8, SH, LT>(a);
 }
 
 // Ragged prefill: contiguous K/V rows [nnz_kv, Hkv, 128]; any 16 consecutive
@@ -741,16 +903,23 @@ loom_status_t prefill_grid(uint64_t batch, uint64_t nnz_qo, uint64_t hq, uint64_
 #ifndef LOOM_PREFILL_WIDE_MIN_GRID
 #define LOOM_PREFILL_WIDE_MIN_GRID 512
 #endif
+#ifndef LOOM_PREFILL_LONG_DEFAULT
+#define LOOM_PREFILL_LONG_DEFAULT 1
+#endif
 loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
-                                uint64_t nnz_qo, uint64_t hq, uint64_t hkv, uint32_t *tile_cols,
-                                loom_error_t *err) {
-  const uint32_t t = flags & (LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64);
-  if (t == (LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64))
-    return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
-  if (t == LOOM_PLAN_PREFILL_TILE_64 && waves != 4)
+                                uint64_t nnz_qo, uint64_t hq, uint64_t hkv, bool long_ok,
+                                uint32_t *tile_cols, bool *long_tile, loom_error_t *err) {
+  const uint32_t t = flags & (LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64 |
+                              LOOM_PLAN_PREFILL_TILE_LONG);
+  *long_tile = false;
+  if (t & (t - 1)) return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
+  if ((t == LOOM_PLAN_PREFILL_TILE_64 || t == LOOM_PLAN_PREFILL_TILE_LONG) && waves != 4)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", waves);
+  if (t == LOOM_PLAN_PREFILL_TILE_LONG && !long_ok)
+    return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
   if (t) {
-    *tile_cols = t == LOOM_PLAN_PREFILL_TILE_64 ? 64 : 16;
+    *tile_cols = t == LOOM_PLAN_PREFILL_TILE_16 ? 16 : 64;
+    *long_tile = t == LOOM_PLAN_PREFILL_TILE_LONG;
     return LOOM_OK;
   }
   const uint64_t cols = nnz_qo * (hq / hkv);
@@ -758,6 +927,9 @@ loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
                 (cols / 64) * hkv >= LOOM_PREFILL_WIDE_MIN_GRID)
                    ? 64
                    : 16;
+  // Long prompts on BF16 pages take the long tiles (see the algorithm's
+  // measurements in the plan's documentation).
+  *long_tile = *tile_cols == 64 && long_ok && LOOM_PREFILL_LONG_DEFAULT;
   return LOOM_OK;
 }
 
@@ -794,7 +966,7 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   const loom_paged_prefill_plan_options_t opt =
       options ? *options : loom_paged_prefill_plan_options_t{0, 0};
   if (opt.flags & ~(LOOM_PLAN_PAGE_INDICES_CAPACITY | LOOM_PLAN_PREFILL_TILE_16 |
-                    LOOM_PLAN_PREFILL_TILE_64))
+                    LOOM_PLAN_PREFILL_TILE_64 | LOOM_PLAN_PREFILL_TILE_LONG))
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", opt.flags);
   if (spec->kv_layout != LOOM_KV_LAYOUT_NHD && spec->kv_layout != LOOM_KV_LAYOUT_HND)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "kv_layout", spec->kv_layout);
@@ -807,9 +979,11 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
   const uint32_t waves = opt.waves ? opt.waves : waves_for();
   uint32_t tile_cols = 16;
+  bool long_tile = false;
   loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->batch_size, spec->nnz_qo,
-                                       spec->num_query_heads,
-                                       spec->num_kv_heads, &tile_cols, err);
+                                       spec->num_query_heads, spec->num_kv_heads,
+                                       spec->kv_dtype == LOOM_KV_DTYPE_BF16, &tile_cols,
+                                       &long_tile, err);
   if (rc) return rc;
   uint64_t tiles = 0, grid = 0;
   rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads, spec->num_kv_heads,
@@ -817,7 +991,9 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   if (rc) return rc;
   auto *p = new loom_paged_prefill_plan;
   p->info.spec = *spec;
-  p->info.algorithm = tile_cols == 64 ? LOOM_PAGED_PREFILL_WIDE_TILE : LOOM_PAGED_PREFILL_ROW_TILE;
+  p->info.algorithm = long_tile        ? LOOM_PAGED_PREFILL_LONG_TILE
+                      : tile_cols == 64 ? LOOM_PAGED_PREFILL_WIDE_TILE
+                                        : LOOM_PAGED_PREFILL_ROW_TILE;
   p->info.waves = waves;
   p->info.row_tiles = tiles;
   p->info.block_threads = p->info.waves * 64;
@@ -929,7 +1105,9 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   } else {
     switch (plan->info.waves) {
       case 4:
-        if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
+        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE)
+          hipLaunchKernelGGL((paged_prefill_kernel<4, false, true, true>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
           hipLaunchKernelGGL((paged_prefill_kernel<4, false, true>), grid, block, 0, stream, a);
         else
           hipLaunchKernelGGL((paged_prefill_kernel<4, false>), grid, block, 0, stream, a);
@@ -957,8 +1135,10 @@ loom_status_t loom_prefill_provider_plan_bf16_ragged(
     return fail(err, LOOM_PLAN_INVALID_OPTION, "waves", opt.waves);
   const uint32_t waves = opt.waves ? opt.waves : waves_for();
   uint32_t tile_cols = 16;
+  bool long_tile = false;
   loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->batch_size, spec->nnz_qo,
-                                       spec->num_query_heads, spec->num_kv_heads, &tile_cols, err);
+                                       spec->num_query_heads, spec->num_kv_heads, false,
+                                       &tile_cols, &long_tile, err);
   if (rc) return rc;
   uint64_t tiles = 0, grid = 0;
   rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads, spec->num_kv_heads,

@@ -36,15 +36,19 @@ PARTIAL_STATE_WIDTH = 130
 PLAN_PAGE_INDICES_CAPACITY = 1
 PLAN_PREFILL_TILE_16 = 2
 PLAN_PREFILL_TILE_64 = 4
+PLAN_PREFILL_TILE_LONG = 8
 GRAPH_REPLAY_MODES = {1: "hip_graph_launch", 2: "kernel_nodes"}
 PLAN_APPEND_TWO_LAUNCH = 8
 PLAN_APPEND_TEST_NO_WAIT = 16
 
 
-def _prefill_tile_flag(tile_cols: int) -> int:
-    if tile_cols not in (0, 16, 64):
-        raise ValueError(f"tile_cols must be 0, 16 or 64, got {tile_cols}")
-    return {0: 0, 16: PLAN_PREFILL_TILE_16, 64: PLAN_PREFILL_TILE_64}[tile_cols]
+def _prefill_tile_flag(tile_cols) -> int:
+    """0 (chosen from the spec), 16 (row tiles), 64 (wide tiles) or "long"
+    (long tiles, paged prefill on BF16 pages)."""
+    if tile_cols not in (0, 16, 64, "long"):
+        raise ValueError(f"tile_cols must be 0, 16, 64 or 'long', got {tile_cols}")
+    return {0: 0, 16: PLAN_PREFILL_TILE_16, 64: PLAN_PREFILL_TILE_64,
+            "long": PLAN_PREFILL_TILE_LONG}[tile_cols]
 # K/V page layouts (loom_kv_layout_t): NHD pages [16, Hkv, 128], HND pages
 # [Hkv, 16, 128].  The reference supports NHD only.
 KV_LAYOUTS = {"NHD": 0, "HND": 1}
@@ -969,7 +973,7 @@ class Bf16PagedPrefillPlan:
 
     @property
     def algorithm(self) -> str:
-        return {1: "row_tile", 2: "wide_tile"}[self.info.algorithm]
+        return {1: "row_tile", 2: "wide_tile", 3: "long_tile"}[self.info.algorithm]
 
     def enqueue_into(self, scope: CommandScope, args: Bf16PagedPrefillArgs):
         _enqueue(_ffi.load().loom_paged_prefill_enqueue, self._p, scope._p, args._ref)
@@ -1116,7 +1120,8 @@ class PrefillProvider:
         """`waves` per workgroup (0: chosen from the spec; 4, 8 or 16);
         `indices_capacity`: page_indices is a capacity (LOOM_PLAN_PAGE_INDICES_CAPACITY);
         `tile_cols`: query columns per workgroup (0: chosen from the spec; 16 for
-        the row-tile algorithm, 64 for the wide-tile one)."""
+        the row-tile algorithm, 64 for the wide-tile one, "long" for the long
+        tiles on BF16 pages)."""
         opt = _ffi.PagedPrefillPlanOptions(
             waves, (PLAN_PAGE_INDICES_CAPACITY if indices_capacity else 0)
             | _prefill_tile_flag(tile_cols))

@@ -43,7 +43,7 @@ def paged_pair(L, B, nnz, pool, hq, hkv, q, k, v, qo, ip, ix, last, spec_kw=None
         if spec_kw:
             r.spec = L.Bf16PagedPrefillSpec(B, nnz, pool, hq, hkv, **spec_kw)
         r.plan = r.provider.plan_bf16_paged(r.spec, tile_cols=tc)
-        assert r.plan.algorithm == ("wide_tile" if tc == 64 else "row_tile")
+        assert r.plan.algorithm == {64: "wide_tile", 16: "row_tile", "long": "long_tile"}[tc]
         dev = [x if isinstance(x, torch.Tensor) else to_dev_bf16(x) for x in (q, k, v)]
         out, lse = r.run_dev(*dev, *(to_dev_i32(x) for x in (qo, ip, ix, last)),
                              scales=None if scales is None else
@@ -118,12 +118,14 @@ def test_ragged_shapes_wide(L, oracle, shape):
     log(f"  {compare_decode(oracle, out, lse, ref_out, ref_lse)}")
 
 
-def test_long_prompt_picks_wide_and_matches_row_tiles(L, oracle):
+@pytest.mark.parametrize("tile", [64, "long"], ids=["wide", "long"])
+def test_long_prompt_matches_row_tiles(L, oracle, tile):
     """A 2048-row GQA4 prompt (Hq 32 / Hkv 8) over a longer cached prefix: the
-    default plan is the wide one; it equals the 16-column plan within the
-    oracle tolerance with the same sentinels (the two sum a column's blocks in
-    different orders, so not bit for bit), and sampled columns are checked
-    against the oracle on a one-request slice."""
+    default plan is the long-tile one (BF16 pages); the wide and long plans
+    equal the 16-column plan within the oracle tolerance with the same
+    sentinels (they sum a column's blocks in different orders, and the long
+    tiles round P to BF16, so not bit for bit), and the last query rows are
+    checked against the oracle on a one-request slice."""
     import torch
     log("wide prefill long prompt")
     rng = np.random.default_rng(2048)
@@ -131,13 +133,13 @@ def test_long_prompt_picks_wide_and_matches_row_tiles(L, oracle):
     pool = (kvl + 15) // 16
     qo, ip, ix, last = ragged_meta(rng, [n], [kvl], pool)
     spec = L.Bf16PagedPrefillSpec(B, n, pool, hq, hkv)
-    assert L.PrefillProvider.load(0).plan_bf16_paged(spec).algorithm == "wide_tile"
+    assert L.PrefillProvider.load(0).plan_bf16_paged(spec).algorithm == "long_tile"
     g = torch.Generator(device="cuda").manual_seed(7)
     q = torch.randn(n * hq * 128, device="cuda", generator=g).to(torch.bfloat16)
     k = torch.randn(pool * 16 * hkv * 128, device="cuda", generator=g).to(torch.bfloat16)
     v = torch.randn(pool * 16 * hkv * 128, device="cuda", generator=g).to(torch.bfloat16)
-    res = paged_pair(L, B, n, pool, hq, hkv, q, k, v, qo, ip, ix, last)
-    log(f"  vs 16-column: {assert_close(oracle, res)}")
+    res = paged_pair(L, B, n, pool, hq, hkv, q, k, v, qo, ip, ix, last, tile=tile)
+    log(f"  {tile} vs 16-column: {assert_close(oracle, res)}")
     # oracle on the last 24 query rows (their causal ends are the largest)
     tail = 24
     qt = bf16_host(q)[(n - tail) * hq * 128:]
