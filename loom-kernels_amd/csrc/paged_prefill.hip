@@ -358,6 +358,18 @@ struct PrefillWave {
   // acc[e][i] = O[column col][dim 16 e + 4 quad + i].
   static constexpr int kLongKBytes = 32 * 272;
   static constexpr int kLongSlotBytes = kLongKBytes + 8 * 128 * 8;
+  // Vᵀ entry (token group g, dims 2u, 2u + 1) is the 16-byte unit at
+  // v_unit(g, u) * 16 of the Vᵀ region (dim 2u in its first 8 bytes).  With
+  // u = 8a + b the unit index is swizzled as 8a + (b ^ h(a)) within the group,
+  // h(a) = (a ^ (a >> 2)) & 3, and bit 3 flipped for odd groups, so that the
+  // stagers' 16-byte stores (16 lanes: u = 4 d8 + k, d8 = 0..15) and the
+  // 8-byte fragment reads (32 lanes: two groups, u = 8e + 0..7) each touch
+  // distinct banks (with 32 or 64 LDS banks of 4 bytes).
+  __device__ static int v_unit(int g, int u) {
+    const int a = u >> 3;
+    const int h = (a ^ (a >> 2)) & 3;
+    return g * 64 + ((8 * a + ((u & 7) ^ h)) ^ ((g & 1) << 3));
+  }
 
   __device__ void process_long(const uint8_t *slot, int64_t lt0, const u32x4 (&qreg)[4]) {
     const uint8_t *kt = slot;
@@ -400,9 +412,11 @@ struct PrefillWave {
                                 bf16x2_pack(p[4], p[5]), bf16x2_pack(p[6], p[7]));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int dim = 16 * e + col;
-      const u32x2 lo = *reinterpret_cast<const u32x2 *>(vt + (quad * 128 + dim) * 8);
-      const u32x2 hi = *reinterpret_cast<const u32x2 *>(vt + ((4 + quad) * 128 + dim) * 8);
+      // dim 16 e + col: unit 8e + col / 2 of groups quad and 4 + quad, half col & 1
+      const int u = 8 * e + (col >> 1);
+      const u32x2 lo = *reinterpret_cast<const u32x2 *>(vt + v_unit(quad, u) * 16 + (col & 1) * 8);
+      const u32x2 hi =
+          *reinterpret_cast<const u32x2 *>(vt + v_unit(4 + quad, u) * 16 + (col & 1) * 8);
       acc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(lo[0], lo[1], hi[0], hi[1]), pt,
                                                        acc[e], 0, 0, 0);
     }
@@ -461,7 +475,7 @@ struct PrefillWave {
           // 4g .. 4g + 3: two 8-byte entries, adjacent
           const u32x4 w = {pack_lo16(d[0][k], d[1][k]), pack_lo16(d[2][k], d[3][k]),
                            pack_hi16(d[0][k], d[1][k]), pack_hi16(d[2][k], d[3][k])};
-          *reinterpret_cast<u32x4 *>(vt + (g * 128 + 8 * d8 + 2 * k) * 8) = w;
+          *reinterpret_cast<u32x4 *>(vt + v_unit(g, 4 * d8 + k) * 16) = w;
         }
       }
     };
