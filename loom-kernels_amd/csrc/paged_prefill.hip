@@ -342,22 +342,35 @@ struct PrefillWave {
     }
   }
 
-  // ---- long tiles (LOOM_PAGED_PREFILL_LONG_TILE, BF16 pages) ----------------
-  // The workgroup's four waves own 16 columns each and walk 32-token blocks
-  // (two 16-row blocks).  Per block, in a two-slot LDS ring:
-  //   K as 32 rows of 272 bytes (the A-fragment reads of S = K·Qᵀ are conflict
-  //   free), staged by waves 0-1 (four 16-byte loads per lane);
-  //   Vᵀ as 8 token groups x 128 dims x 4 tokens (8 bytes: the four tokens of
-  //   one dimension), staged by waves 2-3, each lane transposing the 8 dims x
-  //   4 tokens it loaded with v_perm, so a lane's A fragment of Oᵀ += Vᵀ·Pᵀ
-  //   (one dimension, eight tokens) is two 8-byte reads.
-  // The query fragments stay in registers.  P enters the MFMA as BF16 (one
-  // rounding per weight, the normalizer summed in FP32), so each 32-token block
-  // is 8 S and 8 P·V MFMAs of 16x16x32 per wave, against 12 per 16 tokens with
-  // the wide tiles' high/residual split of P.  The accumulator holds
-  // acc[e][i] = O[column col][dim 16 e + 4 quad + i].
-  static constexpr int kLongKBytes = 32 * 272;
-  static constexpr int kLongSlotBytes = kLongKBytes + 8 * 128 * 8;
+};
+
+// ---- long tiles (LOOM_PAGED_PREFILL_LONG_TILE, BF16 pages) --------------------
+// A workgroup of four waves owns 16 * CT * 4 flattened columns; each wave owns
+// CT tiles of 16 and walks the whole causal range in 32-token blocks (two
+// 16-row blocks).  Per block, in a two-slot LDS ring:
+//   K as 32 rows of 272 bytes (the A-fragment reads of S = K·Qᵀ are conflict
+//   free), staged by waves 0-1 (four 16-byte loads per lane);
+//   Vᵀ as 8 token groups x 128 dims x 4 tokens (8 bytes: the four tokens of
+//   one dimension), staged by waves 2-3, each lane transposing the 8 dims x 4
+//   tokens it loaded with v_perm, so a lane's A fragment of Oᵀ += Vᵀ·Pᵀ (one
+//   dimension, eight tokens) is two 8-byte reads.
+// The query fragments stay in registers and every K and V fragment read from
+// LDS feeds all CT tiles.  P enters the MFMA as BF16 (one rounding per
+// weight; the normalizer is summed in FP32), so each 32-token block is 8 S
+// and 8 P·V MFMAs of 16x16x32 per tile, against 12 per 16 tokens with the
+// wide tiles' high/residual split of P.  acc[t][e][i] = O[column col of tile
+// t][dim 16 e + 4 quad + i].
+template <int CT>
+struct LongWave {
+  const PrefillArgs &a;
+  int lane, col, quad, kvh;
+  int64_t end_col[CT];  // causal end (exclusive) of the lane's column of each tile
+  float m_run[CT], l_run[CT];
+  f32x4 acc[CT][8];
+  u32x4 qf[CT][4];      // B fragments of the query tiles
+
+  static constexpr int kKBytes = 32 * 272;
+  static constexpr int kSlotBytes = kKBytes + 8 * 128 * 8;
   // Vᵀ entry (token group g, dims 2u, 2u + 1) is the 16-byte unit at
   // v_unit(g, u) * 16 of the Vᵀ region (dim 2u in its first 8 bytes).  With
   // u = 8a + b the unit index is swizzled as 8a + (b ^ h(a)) within the group,
@@ -366,50 +379,71 @@ struct PrefillWave {
   // 8-byte fragment reads (32 lanes: two groups, u = 8e + 0..7) each touch
   // distinct banks (with 32 or 64 LDS banks of 4 bytes).
   __device__ static int v_unit(int g, int u) {
-    const int a = u >> 3;
-    const int h = (a ^ (a >> 2)) & 3;
-    return g * 64 + ((8 * a + ((u & 7) ^ h)) ^ ((g & 1) << 3));
+    const int ah = u >> 3;
+    const int h = (ah ^ (ah >> 2)) & 3;
+    return g * 64 + ((8 * ah + ((u & 7) ^ h)) ^ ((g & 1) << 3));
   }
 
-  __device__ void process_long(const uint8_t *slot, int64_t lt0, const u32x4 (&qreg)[4]) {
+  __device__ void reset() {
+#pragma unroll
+    for (int t = 0; t < CT; ++t) {
+      m_run[t] = -INFINITY;
+      l_run[t] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[t][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  __device__ void process(const uint8_t *slot, int64_t lt0) {
     const uint8_t *kt = slot;
-    const uint8_t *vt = slot + kLongKBytes;
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    const uint8_t *vt = slot + kKBytes;
+    f32x4 s0[CT], s1[CT];
+#pragma unroll
+    for (int t = 0; t < CT; ++t) s0[t] = s1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kt + col * 272 + (4 * c + quad) * 16);
       const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kt + (16 + col) * 272 + (4 * c + quad) * 16);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k0), as_bf16x8(qreg[c]), s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k1), as_bf16x8(qreg[c]), s1, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < CT; ++t) {
+        s0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k0), as_bf16x8(qf[t][c]), s0[t], 0,
+                                                        0, 0);
+        s1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k1), as_bf16x8(qf[t][c]), s1[t], 0,
+                                                        0, 0);
+      }
     }
-    // s0[i] = S[token 4 quad + i][column col], s1[i] = S[16 + 4 quad + i][col];
-    // tokens at or past the column's causal end are masked
-    const int vis = (int)max<int64_t>(-1, min<int64_t>(32, end_col - lt0));
-    float sv[8];
+    bf16x8 pt[CT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sv[i] = (quad * 4 + i < vis) ? s0[i] * a.scale_log2 : -INFINITY;
-      sv[4 + i] = (16 + quad * 4 + i < vis) ? s1[i] * a.scale_log2 : -INFINITY;
+    for (int t = 0; t < CT; ++t) {
+      // s0[i] = S[token 4 quad + i][column], s1[i] = S[16 + 4 quad + i][column];
+      // tokens at or past the column's causal end are masked
+      const int vis = (int)max<int64_t>(-1, min<int64_t>(32, end_col[t] - lt0));
+      float sv[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv[i] = (quad * 4 + i < vis) ? s0[t][i] * a.scale_log2 : -INFINITY;
+        sv[4 + i] = (16 + quad * 4 + i < vis) ? s1[t][i] * a.scale_log2 : -INFINITY;
+      }
+      float mx = sv[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+      mx = quad_max(mx);
+      const float m_new = fmaxf(m_run[t], mx);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet
+      const float al = fast_exp2(m_run[t] - m_use);
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
+      l_run[t] = l_run[t] * al + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+      m_run[t] = m_new;
+      if (__builtin_amdgcn_ballot_w64(al != 1.0f))
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[t][e] *= al;
+      // Pᵀ as the B fragment (lane: column, k = 8 quad + [0, 8)): k = 8 quad +
+      // i is token 4 quad + i, k = 8 quad + 4 + i token 16 + 4 quad + i
+      pt[t] = as_bf16x8(bf16x2_pack(p[0], p[1]), bf16x2_pack(p[2], p[3]), bf16x2_pack(p[4], p[5]),
+                        bf16x2_pack(p[6], p[7]));
     }
-    float mx = sv[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-    mx = quad_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet
-    const float al = fast_exp2(m_run - m_use);
-    float p[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
-    l_run = l_run * al + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
-    m_run = m_new;
-    if (__builtin_amdgcn_ballot_w64(al != 1.0f))
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] *= al;
-    // Pᵀ as the B fragment (lane: column col, k = 8 quad + [0, 8)): k = 8 quad
-    // + i is token 4 quad + i, k = 8 quad + 4 + i token 16 + 4 quad + i
-    const bf16x8 pt = as_bf16x8(bf16x2_pack(p[0], p[1]), bf16x2_pack(p[2], p[3]),
-                                bf16x2_pack(p[4], p[5]), bf16x2_pack(p[6], p[7]));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       // dim 16 e + col: unit 8e + col / 2 of groups quad and 4 + quad, half col & 1
@@ -417,8 +451,10 @@ struct PrefillWave {
       const u32x2 lo = *reinterpret_cast<const u32x2 *>(vt + v_unit(quad, u) * 16 + (col & 1) * 8);
       const u32x2 hi =
           *reinterpret_cast<const u32x2 *>(vt + v_unit(4 + quad, u) * 16 + (col & 1) * 8);
-      acc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(lo[0], lo[1], hi[0], hi[1]), pt,
-                                                       acc[e], 0, 0, 0);
+      const bf16x8 va = as_bf16x8(lo[0], lo[1], hi[0], hi[1]);
+#pragma unroll
+      for (int t = 0; t < CT; ++t)
+        acc[t][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pt[t], acc[t][e], 0, 0, 0);
     }
   }
 
@@ -429,9 +465,11 @@ struct PrefillWave {
   // every wave has passed the barrier that follows its reads; windows hold 64
   // 16-row blocks (an even number of 32-token blocks), so a window's first
   // block never reuses the slot its predecessor's last block is read from.
+  // `own_end`: causal end of the wave's last column; blocks at or past it are
+  // staged but not computed.
   template <class PageTok, class RowsOf, class LtOf>
-  __device__ void stream_long(int n16, PageTok page_tok, RowsOf rows_of, LtOf lt_of,
-                              uint8_t *ring, int wave, int64_t own_end, const u32x4 (&qreg)[4]) {
+  __device__ void stream(int n16, PageTok page_tok, RowsOf rows_of, LtOf lt_of, uint8_t *ring,
+                         int wave, int64_t own_end) {
     const int t = threadIdx.x & 127;
     const bool stage_v = wave >= 2;
     const int row_bytes = a.row_elems * 2;
@@ -461,18 +499,18 @@ struct PrefillWave {
       }
     };
     auto store = [&](int i, const u32x4 (&d)[4]) {
-      uint8_t *slot = ring + (i & 1) * kLongSlotBytes;
+      uint8_t *slot = ring + (i & 1) * kSlotBytes;
       if (!stage_v) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           *reinterpret_cast<u32x4 *>(slot + (8 * j + (t >> 4)) * 272 + (t & 15) * 16) = d[j];
       } else {
-        uint8_t *vt = slot + kLongKBytes;
+        uint8_t *vt = slot + kKBytes;
         const int g = t >> 4, d8 = t & 15;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           // dims 8 d8 + 2k (low halves) and + 2k + 1 (high halves) of tokens
-          // 4g .. 4g + 3: two 8-byte entries, adjacent
+          // 4g .. 4g + 3: one unit
           const u32x4 w = {pack_lo16(d[0][k], d[1][k]), pack_lo16(d[2][k], d[3][k]),
                            pack_hi16(d[0][k], d[1][k]), pack_hi16(d[2][k], d[3][k])};
           *reinterpret_cast<u32x4 *>(vt + v_unit(g, 4 * d8 + k) * 16) = w;
@@ -484,7 +522,7 @@ struct PrefillWave {
       fetch(i + 2, d);  // past the end: no valid rows, no traffic
       __syncthreads();
       const int64_t lt0 = lt_of(2 * i);
-      if (lt0 < own_end) process_long(ring + (i & 1) * kLongSlotBytes, lt0, qreg);
+      if (lt0 < own_end) process(ring + (i & 1) * kSlotBytes, lt0);
     };
     u32x4 d0[4], d1[4];
     fetch(0, d0);
@@ -497,6 +535,12 @@ struct PrefillWave {
   }
 };
 
+// Query tiles per wave of the long-tile algorithm.
+#ifndef LOOM_PREFILL_LONG_TILES
+#define LOOM_PREFILL_LONG_TILES 2
+#endif
+constexpr int kLongTiles = LOOM_PREFILL_LONG_TILES;
+
 // SH: the wide-tile algorithm (W = 4, BF16): 16 * W columns per workgroup,
 // one 16-column tile per wave, every wave over the whole page range.
 // LT: the long-tile algorithm (SH's columns and block walk; 32-token blocks,
@@ -505,7 +549,7 @@ template <int W, bool RAGGED, bool FP8, bool SH, bool LT = false>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   static_assert(!SH || W == 4, "wide tiles: four waves");
   static_assert(!LT || (SH && !FP8), "long tiles: the wide tiles' columns, BF16 pages");
-  constexpr int TC = SH ? 16 * W : 16;  // flattened columns per workgroup
+  constexpr int TC = LT ? 16 * W * kLongTiles : SH ? 16 * W : 16;  // flattened columns per workgroup
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   PrefillArgs a = args;
   float v_scale = 1.0f;
@@ -652,7 +696,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   // This lane's column and the tile's page range.
   // (fcols <= nnz_qo * Hq fits int32: the plan checks it)
   const int fcols = qo_len * a.group;
-  const int own0 = fbeg + tile0 * TC + (SH ? 16 * wave : 0);  // first column of this wave's tile
+  // first column of this wave's tile(s)
+  const int own0 = fbeg + tile0 * TC + (LT ? 16 * kLongTiles * wave : SH ? 16 * wave : 0);
   const int f = own0 + col;
   const bool colv = f < fcols;
   const int qi = colv ? (int)((uint32_t)f / (uint32_t)a.group) : 0;
@@ -693,6 +738,22 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   PrefillWave w{a, sm.qfrag[(SH && !LT) ? wave : 0], lane, col, quad, kvh};
   w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
   w.reset();
+  // Long tiles: this lane's column of each of the wave's tiles.
+  constexpr int LTT = LT ? kLongTiles : 1;
+  LongWave<LTT> lw{a, lane, col, quad, kvh};
+  bool colv_t[LTT];
+  int qi_t[LTT], gh_t[LTT];
+  if constexpr (LT) {
+#pragma unroll
+    for (int t = 0; t < LTT; ++t) {
+      const int ft = own0 + 16 * t + col;
+      colv_t[t] = ft < fcols;
+      qi_t[t] = colv_t[t] ? (int)((uint32_t)ft / (uint32_t)a.group) : 0;
+      gh_t[t] = colv_t[t] ? ft - qi_t[t] * a.group : 0;
+      lw.end_col[t] = colv_t[t] ? kv_len - qo_len + qi_t[t] + 1 : 0;
+    }
+    lw.reset();
+  }
   // The current block of up to 64 page indices (one per lane) of this wave.
   int s0 = 0;
   int n = uni(min(mine, 64));
@@ -718,7 +779,16 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   // below them, its wait for a loaded index block would also wait for Q)
   asm volatile("" ::"v"(ok) : "memory");
   u32x4 qr[4];
-  if (SH || wave == 0) {
+  if constexpr (LT) {
+#pragma unroll
+    for (int t = 0; t < LTT; ++t) {
+      const uint16_t *qp = colv_t[t] ? a.q + ((int64_t)(qs + qi_t[t]) * a.hq +
+                                              (int64_t)kvh * a.group + gh_t[t]) * 128 + quad * 8
+                                     : a.q + quad * 8;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) lw.qf[t][c] = load16(qp + c * 32);
+    }
+  } else if (SH || wave == 0) {
     const uint16_t *qp =
         colv ? a.q + ((int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh) * 128 + quad * 8
              : a.q + quad * 8;
@@ -736,7 +806,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   }
   if constexpr (LT) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qr[c] = colv ? qr[c] : u32x4{0, 0, 0, 0};
+    for (int t = 0; t < LTT; ++t)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) lw.qf[t][c] = colv_t[t] ? lw.qf[t][c] : u32x4{0, 0, 0, 0};
   }
   __syncthreads();
 
@@ -748,13 +820,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     }
     if constexpr (SH) {
       // causal end of this wave's last column (0: the wave's tile is empty)
+      const int last_own = own0 + (LT ? 16 * LTT : 16) - 1;
       const int64_t own_end =
           own0 < fcols
-              ? kv_len - qo_len + (int)((uint32_t)min(own0 + 15, fcols - 1) / (uint32_t)a.group) + 1
+              ? kv_len - qo_len + (int)((uint32_t)min(last_own, fcols - 1) / (uint32_t)a.group) + 1
               : 0;
       if constexpr (LT) {
-        __shared__ __align__(16) uint8_t lring[2 * PrefillWave::kLongSlotBytes];
-        w.stream_long(n, page_tok, rows_of, lt_of, lring, wave, uni64(own_end), qr);
+        __shared__ __align__(16) uint8_t lring[2 * LongWave<LTT>::kSlotBytes];
+        lw.stream(n, page_tok, rows_of, lt_of, lring, wave, uni64(own_end));
       } else {
         __shared__ u32x4 ring[2][2][16][17];
         w.template stream_shared<FP8>(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
@@ -764,30 +837,42 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     }
   }
 
-  if constexpr (SH) {
+  if constexpr (LT) {
+    // Each wave finishes its own tiles; an invalid page index anywhere in the
+    // request keeps its sentinels.
+    float Lt[LTT];
+#pragma unroll
+    for (int t = 0; t < LTT; ++t) Lt[t] = quad_sum(lw.l_run[t]);
+    if (block_or(bad, sm.bad)) return;
+#pragma unroll
+    for (int t = 0; t < LTT; ++t) {
+      if (!colv_t[t]) continue;
+      const float inv = 1.0f / Lt[t];
+      const int64_t row_head = (int64_t)(qs + qi_t[t]) * a.hq + (int64_t)kvh * a.group + gh_t[t];
+      // acc[t][e][i] = O[column][16 e + 4 quad + i]: 8 bytes per dim block
+      uint16_t *orow = a.out + row_head * 128 + quad * 4;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<u32x2 *>(orow + 16 * e) =
+            u32x2{bf16x2_pack(lw.acc[t][e][0] * inv, lw.acc[t][e][1] * inv),
+                  bf16x2_pack(lw.acc[t][e][2] * inv, lw.acc[t][e][3] * inv)};
+      if (quad == 0) a.lse[row_head] = lw.m_run[t] + __log2f(Lt[t]);
+    }
+    return;
+  } else if constexpr (SH) {
     // No cross-wave merge: each wave finishes its own tile.
     const float L = quad_sum(w.l_run);
     if (block_or(bad, sm.bad) || !colv) return;
     const float inv = 1.0f / L;
     const int64_t row_head = (int64_t)(qs + qi) * a.hq + (int64_t)kvh * a.group + gh;
-    if constexpr (LT) {
-      // acc[e][i] = O[col][16 e + 4 quad + i]: 8 bytes per dim block
-      uint16_t *orow = a.out + row_head * 128 + quad * 4;
+    uint16_t *orow = a.out + row_head * 128 + quad * 32;
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<u32x2 *>(orow + 16 * e) =
-            u32x2{bf16x2_pack(w.acc[e][0] * inv, w.acc[e][1] * inv),
-                  bf16x2_pack(w.acc[e][2] * inv, w.acc[e][3] * inv)};
-    } else {
-      uint16_t *orow = a.out + row_head * 128 + quad * 32;
+    for (int r4 = 0; r4 < 4; ++r4) {
+      u32x4 o;
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        u32x4 o;
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2)
-          o[e2] = bf16x2_pack(w.acc[2 * e2][r4] * inv * v_scale, w.acc[2 * e2 + 1][r4] * inv * v_scale);
-        *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
-      }
+      for (int e2 = 0; e2 < 4; ++e2)
+        o[e2] = bf16x2_pack(w.acc[2 * e2][r4] * inv * v_scale, w.acc[2 * e2 + 1][r4] * inv * v_scale);
+      *reinterpret_cast<u32x4 *>(orow + r4 * 8) = o;
     }
     if (quad == 0) a.lse[row_head] = w.m_run + __log2f(L);
     return;
@@ -850,8 +935,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
 // those gaps (the four-wave BF16 kernel would otherwise settle at two).
 constexpr int kPrefillWavesPerEu = 3;
 
+// The long tiles hold two query tiles per wave (about 200 registers): two
+// waves per SIMD.
 template <int W, bool FP8, bool SH = false, bool LT = false>
-__global__ __launch_bounds__(W * 64, kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(W * 64, LT ? (kLongTiles > 1 ? 2 : 3) : kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
   prefill_body<W, false, FP8, SH, LT>(a);
 }
 
@@ -932,7 +1019,7 @@ loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
   if (t == LOOM_PLAN_PREFILL_TILE_LONG && !long_ok)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
   if (t) {
-    *tile_cols = t == LOOM_PLAN_PREFILL_TILE_16 ? 16 : 64;
+    *tile_cols = t == LOOM_PLAN_PREFILL_TILE_16 ? 16 : t == LOOM_PLAN_PREFILL_TILE_64 ? 64 : 16 * 4 * kLongTiles;
     *long_tile = t == LOOM_PLAN_PREFILL_TILE_LONG;
     return LOOM_OK;
   }
@@ -944,6 +1031,7 @@ loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
   // Long prompts on BF16 pages take the long tiles (see the algorithm's
   // measurements in the plan's documentation).
   *long_tile = *tile_cols == 64 && long_ok && LOOM_PREFILL_LONG_DEFAULT;
+  if (*long_tile) *tile_cols = 16 * 4 * kLongTiles;
   return LOOM_OK;
 }
 
@@ -1008,6 +1096,7 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   p->info.algorithm = long_tile        ? LOOM_PAGED_PREFILL_LONG_TILE
                       : tile_cols == 64 ? LOOM_PAGED_PREFILL_WIDE_TILE
                                         : LOOM_PAGED_PREFILL_ROW_TILE;
+
   p->info.waves = waves;
   p->info.row_tiles = tiles;
   p->info.block_threads = p->info.waves * 64;
