@@ -562,7 +562,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, quad = lane >> 4;
   const int kvh = (int)(blockIdx.x % a.hkv);
-  const int64_t tile = blockIdx.x / a.hkv;
+  // Tiles in reverse order: a request's later rows see longer causal ranges,
+  // so the heaviest tiles are dispatched first and the launch does not end
+  // with a few long tiles running alone (the grid's excess workgroups, which
+  // find no tile, come first and exit at once).  Workgroup b runs on XCD
+  // b % 8; with the kv-head fastest, each XCD keeps to a fixed set of
+  // kv-heads, whose K/V its L2 shares across tiles.
+  const int64_t tile = (int64_t)(gridDim.x / a.hkv) - 1 - blockIdx.x / a.hkv;
 
   // Metadata in as few dependent round trips as possible: the global guard
   // words and every request's qo range, page (kv) range and tail are loaded
