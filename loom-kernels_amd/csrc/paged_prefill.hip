@@ -365,7 +365,9 @@ struct LongWave {
   const PrefillArgs &a;
   int lane, col, quad, kvh;
   int64_t end_col[CT];  // causal end (exclusive) of the lane's column of each tile
-  float m_run[CT], l_run[CT];
+  int64_t full_end;     // smallest causal end of the wave's valid columns
+  float m_run[CT];      // running max (log2 domain, scaled) of each column
+  f32x4 lsum[CT];       // running normalizer of each column (every element)
   f32x4 acc[CT][8];
   u32x4 qf[CT][4];      // B fragments of the query tiles
 
@@ -388,13 +390,15 @@ struct LongWave {
 #pragma unroll
     for (int t = 0; t < CT; ++t) {
       m_run[t] = -INFINITY;
-      l_run[t] = 0.0f;
+      lsum[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[t][e] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
 
-  __device__ void process(const uint8_t *slot, int64_t lt0) {
+  // `full`: every token of the block lies inside the causal range of every
+  // valid column of the wave (no masking needed).
+  __device__ void process(const uint8_t *slot, int64_t lt0, bool full) {
     const uint8_t *kt = slot;
     const uint8_t *vt = slot + kKBytes;
     f32x4 s0[CT], s1[CT];
@@ -415,34 +419,46 @@ struct LongWave {
     bf16x8 pt[CT];
 #pragma unroll
     for (int t = 0; t < CT; ++t) {
-      // s0[i] = S[token 4 quad + i][column], s1[i] = S[16 + 4 quad + i][column];
-      // tokens at or past the column's causal end are masked
-      const int vis = (int)max<int64_t>(-1, min<int64_t>(32, end_col[t] - lt0));
-      float sv[8];
+      // sr[i] = S[token 4 quad + i][column], sr[4 + i] = S[16 + 4 quad + i][column]
+      // (unscaled); tokens at or past the column's causal end are masked
+      float sr[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sv[i] = (quad * 4 + i < vis) ? s0[t][i] * a.scale_log2 : -INFINITY;
-        sv[4 + i] = (16 + quad * 4 + i < vis) ? s1[t][i] * a.scale_log2 : -INFINITY;
+        sr[i] = s0[t][i];
+        sr[4 + i] = s1[t][i];
       }
-      float mx = sv[0];
+      if (!full) {
+        const int vis = (int)max<int64_t>(-1, min<int64_t>(32, end_col[t] - lt0));
 #pragma unroll
-      for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-      mx = quad_max(mx);
+        for (int i = 0; i < 4; ++i) {
+          sr[i] = (quad * 4 + i < vis) ? sr[i] : -INFINITY;
+          sr[4 + i] = (16 + quad * 4 + i < vis) ? sr[4 + i] : -INFINITY;
+        }
+      }
+      // the scale is positive, so the max is taken before scaling
+      float mx = fmaxf(fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])),
+                       fmaxf(fmaxf(sr[4], sr[5]), fmaxf(sr[6], sr[7])));
+      mx = quad_max(mx) * a.scale_log2;
       const float m_new = fmaxf(m_run[t], mx);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet
       const float al = fast_exp2(m_run[t] - m_use);
       float p[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
-      l_run[t] = l_run[t] * al + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+      for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(sr[i], a.scale_log2, -m_use));
       m_run[t] = m_new;
-      if (__builtin_amdgcn_ballot_w64(al != 1.0f))
+      if (__builtin_amdgcn_ballot_w64(al != 1.0f)) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[t][e] *= al;
+        lsum[t] *= al;
+      }
       // Pᵀ as the B fragment (lane: column, k = 8 quad + [0, 8)): k = 8 quad +
       // i is token 4 quad + i, k = 8 quad + 4 + i token 16 + 4 quad + i
       pt[t] = as_bf16x8(bf16x2_pack(p[0], p[1]), bf16x2_pack(p[2], p[3]), bf16x2_pack(p[4], p[5]),
                         bf16x2_pack(p[6], p[7]));
+      // the normalizer on the matrix core: a ones matrix times Pᵀ sums each
+      // column's BF16 weights (the ones the P·V product uses) into every row
+      lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u), pt[t], lsum[t], 0, 0, 0);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -522,7 +538,7 @@ struct LongWave {
       fetch(i + 2, d);  // past the end: no valid rows, no traffic
       __syncthreads();
       const int64_t lt0 = lt_of(2 * i);
-      if (lt0 < own_end) process(ring + (i & 1) * kSlotBytes, lt0);
+      if (lt0 < own_end) process(ring + (i & 1) * kSlotBytes, lt0, lt0 + 32 <= full_end);
     };
     u32x4 d0[4], d1[4];
     fetch(0, d0);
@@ -758,6 +774,18 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
       gh_t[t] = colv_t[t] ? ft - qi_t[t] * a.group : 0;
       lw.end_col[t] = colv_t[t] ? kv_len - qo_len + qi_t[t] + 1 : 0;
     }
+    // the smallest causal end of the wave's valid columns: blocks before it
+    // need no mask (the columns past fcols are discarded, so they do not count)
+    int64_t fe = INT64_MAX;
+#pragma unroll
+    for (int t = 0; t < LTT; ++t) fe = colv_t[t] ? min(fe, lw.end_col[t]) : fe;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const int64_t y = ((int64_t)__shfl_xor((int)(fe >> 32), o, 64) << 32) |
+                        (uint32_t)__shfl_xor((int)(uint32_t)fe, o, 64);
+      fe = min(fe, y);
+    }
+    lw.full_end = uni64(fe);
     lw.reset();
   }
   // The current block of up to 64 page indices (one per lane) of this wave.
@@ -848,7 +876,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     // request keeps its sentinels.
     float Lt[LTT];
 #pragma unroll
-    for (int t = 0; t < LTT; ++t) Lt[t] = quad_sum(lw.l_run[t]);
+    for (int t = 0; t < LTT; ++t) Lt[t] = lw.lsum[t][0];
     if (block_or(bad, sm.bad)) return;
 #pragma unroll
     for (int t = 0; t < LTT; ++t) {
