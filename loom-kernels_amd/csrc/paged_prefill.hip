@@ -98,7 +98,7 @@ constexpr int64_t kNoTiles = (int64_t)1 << 50;
 #endif
 constexpr int prefill_depth(int w) { return w >= 16 ? 1 : LOOM_PREFILL_DEPTH; }
 
-template <int W, bool SH, bool LT = false>
+template <int W, bool SH, int LT = 0>
 struct PrefillSmem {
   int64_t wave_tot[W];
   int32_t wave_max[W];
@@ -551,21 +551,23 @@ struct LongWave {
   }
 };
 
-// Query tiles per wave of the long-tile algorithm.
-#ifndef LOOM_PREFILL_LONG_TILES
-#define LOOM_PREFILL_LONG_TILES 2
-#endif
-constexpr int kLongTiles = LOOM_PREFILL_LONG_TILES;
+// Query tiles per wave of the long-tile algorithm: two (128 columns per
+// workgroup) when that still gives at least kLongTwoMinGrid workgroups (two
+// per CU), else one (64 columns).  Measured on GQA4 32/8 prompts: two tiles
+// per wave 624 against 580 TFLOP/s at 8192 rows (2048 workgroups), 497
+// against 477 at 4096, 179 against 161 on 8 x 256 rows (536 workgroups), but
+// 188 against 219 at 1 x 1024 rows (256 against 512 workgroups).
+constexpr int kLongTwoMinGrid = 512;
 
 // SH: the wide-tile algorithm (W = 4, BF16): 16 * W columns per workgroup,
 // one 16-column tile per wave, every wave over the whole page range.
 // LT: the long-tile algorithm (SH's columns and block walk; 32-token blocks,
 // query fragments in registers, BF16 P, Vᵀ staged transposed).
-template <int W, bool RAGGED, bool FP8, bool SH, bool LT = false>
+template <int W, bool RAGGED, bool FP8, bool SH, int LT = 0>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   static_assert(!SH || W == 4, "wide tiles: four waves");
   static_assert(!LT || (SH && !FP8), "long tiles: the wide tiles' columns, BF16 pages");
-  constexpr int TC = LT ? 16 * W * kLongTiles : SH ? 16 * W : 16;  // flattened columns per workgroup
+  constexpr int TC = LT ? 16 * W * LT : SH ? 16 * W : 16;  // flattened columns per workgroup
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   PrefillArgs a = args;
   float v_scale = 1.0f;
@@ -719,7 +721,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   // (fcols <= nnz_qo * Hq fits int32: the plan checks it)
   const int fcols = qo_len * a.group;
   // first column of this wave's tile(s)
-  const int own0 = fbeg + tile0 * TC + (LT ? 16 * kLongTiles * wave : SH ? 16 * wave : 0);
+  const int own0 = fbeg + tile0 * TC + (LT ? 16 * LT * wave : SH ? 16 * wave : 0);
   const int f = own0 + col;
   const bool colv = f < fcols;
   const int qi = colv ? (int)((uint32_t)f / (uint32_t)a.group) : 0;
@@ -761,7 +763,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   w.end_col = colv ? kv_len - qo_len + qi + 1 : 0;
   w.reset();
   // Long tiles: this lane's column of each of the wave's tiles.
-  constexpr int LTT = LT ? kLongTiles : 1;
+  constexpr int LTT = LT ? LT : 1;
   LongWave<LTT> lw{a, lane, col, quad, kvh};
   bool colv_t[LTT];
   int qi_t[LTT], gh_t[LTT];
@@ -971,8 +973,8 @@ constexpr int kPrefillWavesPerEu = 3;
 
 // The long tiles hold two query tiles per wave (about 200 registers): two
 // waves per SIMD.
-template <int W, bool FP8, bool SH = false, bool LT = false>
-__global__ __launch_bounds__(W * 64, LT ? (kLongTiles > 1 ? 2 : 3) : kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
+template <int W, bool FP8, bool SH = false, int LT = 0>
+__global__ __launch_bounds__(W * 64, LT ? (LT > 1 ? 2 : 3) : kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
   prefill_body<W, false, FP8, SH, LT>(a);
 }
 
@@ -993,6 +995,7 @@ struct loom_prefill_provider {
 
 struct loom_paged_prefill_plan {
   loom_paged_prefill_plan_info_t info{};
+  uint32_t tile_cols = 16;  // flattened columns per workgroup
 };
 
 struct loom_ragged_prefill_plan {
@@ -1053,8 +1056,9 @@ loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
   if (t == LOOM_PLAN_PREFILL_TILE_LONG && !long_ok)
     return fail(err, LOOM_PLAN_INVALID_OPTION, "flags", flags);
   if (t) {
-    *tile_cols = t == LOOM_PLAN_PREFILL_TILE_16 ? 16 : t == LOOM_PLAN_PREFILL_TILE_64 ? 64 : 16 * 4 * kLongTiles;
+    *tile_cols = t == LOOM_PLAN_PREFILL_TILE_16 ? 16 : 64;
     *long_tile = t == LOOM_PLAN_PREFILL_TILE_LONG;
+    if (*long_tile && (nnz_qo * (hq / hkv) / 128) * hkv >= kLongTwoMinGrid) *tile_cols = 128;
     return LOOM_OK;
   }
   const uint64_t cols = nnz_qo * (hq / hkv);
@@ -1065,7 +1069,7 @@ loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
   // Long prompts on BF16 pages take the long tiles (see the algorithm's
   // measurements in the plan's documentation).
   *long_tile = *tile_cols == 64 && long_ok && LOOM_PREFILL_LONG_DEFAULT;
-  if (*long_tile) *tile_cols = 16 * 4 * kLongTiles;
+  if (*long_tile && (cols / 128) * hkv >= kLongTwoMinGrid) *tile_cols = 128;
   return LOOM_OK;
 }
 
@@ -1130,6 +1134,7 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   p->info.algorithm = long_tile        ? LOOM_PAGED_PREFILL_LONG_TILE
                       : tile_cols == 64 ? LOOM_PAGED_PREFILL_WIDE_TILE
                                         : LOOM_PAGED_PREFILL_ROW_TILE;
+  p->tile_cols = tile_cols;
 
   p->info.waves = waves;
   p->info.row_tiles = tiles;
@@ -1242,8 +1247,10 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   } else {
     switch (plan->info.waves) {
       case 4:
-        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE)
-          hipLaunchKernelGGL((paged_prefill_kernel<4, false, true, true>), grid, block, 0, stream, a);
+        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
+          hipLaunchKernelGGL((paged_prefill_kernel<4, false, true, 2>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE)
+          hipLaunchKernelGGL((paged_prefill_kernel<4, false, true, 1>), grid, block, 0, stream, a);
         else if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
           hipLaunchKernelGGL((paged_prefill_kernel<4, false, true>), grid, block, 0, stream, a);
         else
