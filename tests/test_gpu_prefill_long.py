@@ -148,3 +148,28 @@ def test_plan_selection_and_rejections(L):
         with pytest.raises(L.PlanError) as e:
             L._call(fn, prov._p, C.byref(spec._c), C.byref(opt), C.byref(out))
         assert e.value.operand == field, (kind, waves, e.value)
+
+
+def test_two_tiles_per_wave_with_a_guarded_request(L, oracle):
+    """Grids large enough for two query tiles per wave (128 columns per
+    workgroup): two 1100-row GQA4 prompts (32/8 heads), the second with an
+    invalid page index.  The first equals the 16-column command within the
+    oracle tolerance; the second keeps every sentinel, as there."""
+    import torch
+    log("long prefill, two tiles per wave, one guarded request")
+    rng = np.random.default_rng(1100)
+    hq, hkv = 32, 8
+    qo_lens, kv_lens = [1100, 1100], [1300, 1100]
+    pool = sum((n + 15) // 16 for n in kv_lens) + 2
+    qo, ip, ix, last = ragged_meta(rng, qo_lens, kv_lens, pool)
+    ix = ix.copy()
+    ix[ip[1] + 40] = pool + 9
+    B, nnz = 2, int(qo[-1])
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q = torch.randn(nnz * hq * 128, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(pool * 16 * hkv * 128, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(pool * 16 * hkv * 128, device="cuda", generator=g).to(torch.bfloat16)
+    res = paged_pair(L, B, nnz, pool, hq, hkv, q, k, v, qo, ip, ix, last, tile="long")
+    log(f"  vs 16-column: {assert_close(oracle, res)}")
+    o = oracle.bf16_to_f32(res[0][0]).reshape(nnz, hq * 128)
+    assert np.all(np.isnan(o[1100:])) and not np.any(np.isnan(o[:1100]))
