@@ -185,6 +185,19 @@ __device__ __forceinline__ float quad_max(float x) {
                                                   false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+// IEEE 754-2019 maximum (a NaN operand gives NaN): unlike fmaxf it needs no
+// quieting of its inputs, and gfx950 takes three operands per instruction.
+__device__ __forceinline__ float fmax_nan(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+__device__ __forceinline__ float quad_max_nan(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmax_nan(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmax_nan(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 __device__ __forceinline__ float quad_sum(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);

@@ -351,9 +351,10 @@ struct PrefillWave {
 //   K as 32 rows of 272 bytes (the A-fragment reads of S = K·Qᵀ are conflict
 //   free), staged by waves 0-1 (four 16-byte loads per lane);
 //   Vᵀ as 8 token groups x 128 dims x 4 tokens (8 bytes: the four tokens of
-//   one dimension), staged by waves 2-3, each lane transposing the 8 dims x 4
-//   tokens it loaded with v_perm, so a lane's A fragment of Oᵀ += Vᵀ·Pᵀ (one
-//   dimension, eight tokens) is two 8-byte reads.
+//   one dimension; layout at LongWave::v_byte), staged by waves 2-3, each
+//   lane transposing the 8 dims x 4 tokens it loaded with v_perm, so a
+//   lane's A fragment of Oᵀ += Vᵀ·Pᵀ (one dimension, eight tokens) is two
+//   8-byte reads.
 // The query fragments stay in registers and every K and V fragment read from
 // LDS feeds all CT tiles.  P enters the MFMA as BF16 (one rounding per
 // weight; the normalizer is summed in FP32), so each 32-token block is 8 S
@@ -372,18 +373,20 @@ struct LongWave {
   u32x4 qf[CT][4];      // B fragments of the query tiles
 
   static constexpr int kKBytes = 32 * 272;
-  static constexpr int kSlotBytes = kKBytes + 8 * 128 * 8;
-  // Vᵀ entry (token group g, dims 2u, 2u + 1) is the 16-byte unit at
-  // v_unit(g, u) * 16 of the Vᵀ region (dim 2u in its first 8 bytes).  With
-  // u = 8a + b the unit index is swizzled as 8a + (b ^ h(a)) within the group,
-  // h(a) = (a ^ (a >> 2)) & 3, and bit 3 flipped for odd groups, so that the
-  // stagers' 16-byte stores (16 lanes: u = 4 d8 + k, d8 = 0..15) and the
-  // 8-byte fragment reads (32 lanes: two groups, u = 8e + 0..7) each touch
-  // distinct banks (with 32 or 64 LDS banks of 4 bytes).
-  __device__ static int v_unit(int g, int u) {
-    const int ah = u >> 3;
-    const int h = (ah ^ (ah >> 2)) & 3;
-    return g * 64 + ((8 * ah + ((u & 7) ^ h)) ^ ((g & 1) << 3));
+  // Vᵀ: token groups 2p and 2p + 1 (tokens 8p .. 8p + 7) share eight rows of
+  // 16 units of 16 bytes, row e (dims 16 e .. 16 e + 15) starting at unit
+  // 17 e + 4 (e >> 2) of the pair's 140; group 2p + s holds units 8 s + c
+  // (c = 0..7: dims 16 e + 2c, 16 e + 2c + 1, four tokens each, dim 16 e + 2c
+  // in the first 8 bytes).  The row starts' residues (0-3, 8-11 mod 16 units)
+  // make the stagers' 16-byte stores (16 lanes: one group, rows 0-7, c = k and
+  // 4 + k) and the 8-byte fragment reads (32 lanes: one pair, one row) free
+  // of bank conflicts with 32 or 64 banks of 4 bytes, and every row offset is
+  // a compile-time constant, so all fragment reads share one lane address.
+  static constexpr int kVPairUnits = 140;
+  static constexpr int kSlotBytes = kKBytes + 4 * kVPairUnits * 16;
+  __device__ static constexpr int v_row(int e) { return 17 * e + 4 * (e >> 2); }
+  __device__ static int v_byte(int g, int e, int c) {
+    return (kVPairUnits * (g >> 1) + v_row(e) + 8 * (g & 1) + c) * 16;
   }
 
   __device__ void reset() {
@@ -436,10 +439,12 @@ struct LongWave {
         }
       }
       // the scale is positive, so the max is taken before scaling
-      float mx = fmaxf(fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])),
-                       fmaxf(fmaxf(sr[4], sr[5]), fmaxf(sr[6], sr[7])));
-      mx = quad_max(mx) * a.scale_log2;
-      const float m_new = fmaxf(m_run[t], mx);
+      // (IEEE maximum: no NaN quieting of the MFMA results, three inputs per
+      // instruction)
+      float mx = fmax_nan(fmax_nan(fmax_nan(sr[0], sr[1]), fmax_nan(sr[2], sr[3])),
+                          fmax_nan(fmax_nan(sr[4], sr[5]), fmax_nan(sr[6], sr[7])));
+      mx = quad_max_nan(mx) * a.scale_log2;
+      const float m_new = fmax_nan(m_run[t], mx);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet
       const float al = fast_exp2(m_run[t] - m_use);
       float p[8];
@@ -460,13 +465,14 @@ struct LongWave {
       lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u), pt[t], lsum[t], 0, 0, 0);
     }
+    // dim 16 e + col of groups quad (tokens 4 quad ..) and 4 + quad (16 + 4
+    // quad ..): unit c = col / 2 of row e, half col & 1; group 4 + quad lies
+    // two pairs after group quad
+    const uint8_t *vl = vt + v_byte(quad, 0, col >> 1) + (col & 1) * 8;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      // dim 16 e + col: unit 8e + col / 2 of groups quad and 4 + quad, half col & 1
-      const int u = 8 * e + (col >> 1);
-      const u32x2 lo = *reinterpret_cast<const u32x2 *>(vt + v_unit(quad, u) * 16 + (col & 1) * 8);
-      const u32x2 hi =
-          *reinterpret_cast<const u32x2 *>(vt + v_unit(4 + quad, u) * 16 + (col & 1) * 8);
+      const u32x2 lo = *reinterpret_cast<const u32x2 *>(vl + v_row(e) * 16);
+      const u32x2 hi = *reinterpret_cast<const u32x2 *>(vl + (2 * kVPairUnits + v_row(e)) * 16);
       const bf16x8 va = as_bf16x8(lo[0], lo[1], hi[0], hi[1]);
 #pragma unroll
       for (int t = 0; t < CT; ++t)
@@ -521,15 +527,16 @@ struct LongWave {
         for (int j = 0; j < 4; ++j)
           *reinterpret_cast<u32x4 *>(slot + (8 * j + (t >> 4)) * 272 + (t & 15) * 16) = d[j];
       } else {
-        uint8_t *vt = slot + kKBytes;
         const int g = t >> 4, d8 = t & 15;
+        // dims 8 d8 .. 8 d8 + 7: row d8 / 2, units 4 (d8 & 1) .. + 3
+        uint8_t *vs = slot + kKBytes + v_byte(g, d8 >> 1, 4 * (d8 & 1));
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           // dims 8 d8 + 2k (low halves) and + 2k + 1 (high halves) of tokens
           // 4g .. 4g + 3: one unit
           const u32x4 w = {pack_lo16(d[0][k], d[1][k]), pack_lo16(d[2][k], d[3][k]),
                            pack_hi16(d[0][k], d[1][k]), pack_hi16(d[2][k], d[3][k])};
-          *reinterpret_cast<u32x4 *>(vt + v_unit(g, 4 * d8 + k) * 16) = w;
+          *reinterpret_cast<u32x4 *>(vs + k * 16) = w;
         }
       }
     };
