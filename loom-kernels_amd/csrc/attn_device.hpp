@@ -66,6 +66,46 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rows_rsrc(const uint16_t 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
 }
 
+// 16 bytes per lane from a buffer straight into LDS: lane i's bytes land at
+// lds + 16 i (the LDS address is the same for every lane; offsets outside the
+// buffer's range read as zeros).  Completion is counted by vmcnt and is NOT
+// tracked by the compiler: the caller waits (wait_vmcnt) before the barrier
+// that publishes the data.  (Issued as inline assembly so that the compiler
+// does not wait for these loads before every later LDS access or barrier: it
+// cannot tell the ring slot being filled from the one being read.)
+// M0 (the LDS base of the load) is written here and declared clobbered; the
+// kernels that use this keep nothing else in M0 (they use no LDS-DMA
+// builtins or indexed register moves), so the compiler's note that it does
+// not preserve reserved registers around the statement does not apply.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void *lds, int byte_offset) {
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(byte_offset),
+               "s"(m0), "s"(r)
+               : "m0", "memory");
+}
+#pragma clang diagnostic pop
+
+// Transposing 8-byte LDS read (ds_read_b64_tr_b16): within each 16 lanes,
+// lane i receives element i % 4 of the four 16-bit elements addressed by
+// lane 4k + i / 4, for k = 0..3.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void *lds) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(lds));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// Waits until at most N vector memory loads of this wave are outstanding
+// (lgkm and export counters not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((0xF << 8) | (0x7 << 4) | N);
+}
+
 // 8-byte raw buffer load (FP8 rows: 8 elements per lane).
 template <bool NT>
 __device__ __forceinline__ u32x2 load8_rows(__amdgpu_buffer_rsrc_t r, int byte_offset) {

@@ -107,11 +107,13 @@ struct PrefillSmem {
   // the located request's qo_indptr pair, page (or kv) indptr pair, tail, and
   // the first flattened column it owns
   int32_t meta[6];
-  u32x4 qfrag[(SH && !LT) ? W : 1][4][64];  // MFMA B fragments of 16 query columns (per wave: SH)
+  // MFMA B fragments of 16 query columns (per wave: SH; long tiles keep them
+  // in registers)
+  u32x4 qfrag[LT ? 0 : SH ? W : 1][4][64];
   float m[W][16];      // per-wave running max (log2 domain) per column
   float l[W][16];      // per-wave normalizer per column
   uint32_t bad[W];     // per-wave invalid-page-index flags
-  f32x4 red[(SH || LT) ? 1 : (W / 2 > 0 ? W / 2 : 1)][4][64];  // tree-sum staging (row tiles only)
+  f32x4 red[(SH || LT) ? 0 : (W / 2 > 0 ? W / 2 : 1)][4][64];  // tree-sum staging (row tiles only)
 };
 
 // One page of K (A-fragment layout) and V (row layout) for one wave.
@@ -347,20 +349,22 @@ struct PrefillWave {
 // ---- long tiles (LOOM_PAGED_PREFILL_LONG_TILE, BF16 pages) --------------------
 // A workgroup of four waves owns 16 * CT * 4 flattened columns; each wave owns
 // CT tiles of 16 and walks the whole causal range in 32-token blocks (two
-// 16-row blocks).  Per block, in a two-slot LDS ring:
-//   K as 32 rows of 272 bytes (the A-fragment reads of S = K·Qᵀ are conflict
-//   free), staged by waves 0-1 (four 16-byte loads per lane);
-//   Vᵀ as 8 token groups x 128 dims x 4 tokens (8 bytes: the four tokens of
-//   one dimension; layout at LongWave::v_byte), staged by waves 2-3, each
-//   lane transposing the 8 dims x 4 tokens it loaded with v_perm, so a
-//   lane's A fragment of Oᵀ += Vᵀ·Pᵀ (one dimension, eight tokens) is two
-//   8-byte reads.
-// The query fragments stay in registers and every K and V fragment read from
-// LDS feeds all CT tiles.  P enters the MFMA as BF16 (one rounding per
-// weight; the normalizer is summed in FP32), so each 32-token block is 8 S
-// and 8 P·V MFMAs of 16x16x32 per tile, against 12 per 16 tokens with the
-// wide tiles' high/residual split of P.  acc[t][e][i] = O[column col of tile
-// t][dim 16 e + 4 quad + i].
+// 16-row blocks).  Each block is loaded straight into a three-slot LDS ring
+// (buffer loads to LDS: no VGPRs, LDS stores or transposes), in 1 KB regions
+// of 16 rows x 32 dims:
+//   K region (h, c): unit (row r, 16-byte chunk j) at 16 j + r, so a lane's A
+//   fragment of S = K·Qᵀ (row col, dims 32c + 8 quad ..) is one conflict-free
+//   16-byte read;
+//   V region (h, c): unit (r, j) at 32 (j >> 1) + 2 r + (j & 1), read with
+//   the transposing ds_read_b64_tr_b16 into the A fragment of Oᵀ += Vᵀ·Pᵀ
+//   (one dimension, eight tokens: two reads).
+// Every fragment read is one lane address plus a compile-time offset.  The
+// query fragments stay in registers and every K and V fragment read from LDS
+// feeds all CT tiles.  P enters the MFMA as BF16 (one rounding per weight;
+// the normalizer is summed in FP32), so each 32-token block is 8 S and 8 P·V
+// MFMAs of 16x16x32 per tile, against 12 per 16 tokens with the wide tiles'
+// high/residual split of P.  acc[t][e][i] = O[column col of tile t][dim
+// 16 e + 4 quad + i].
 template <int CT>
 struct LongWave {
   const PrefillArgs &a;
@@ -371,23 +375,9 @@ struct LongWave {
   f32x4 lsum[CT];       // running normalizer of each column (every element)
   f32x4 acc[CT][8];
   u32x4 qf[CT][4];      // B fragments of the query tiles
+  int rpos = 0;         // ring slot of the next block staged
 
-  static constexpr int kKBytes = 32 * 272;
-  // Vᵀ: token groups 2p and 2p + 1 (tokens 8p .. 8p + 7) share eight rows of
-  // 16 units of 16 bytes, row e (dims 16 e .. 16 e + 15) starting at unit
-  // 17 e + 4 (e >> 2) of the pair's 140; group 2p + s holds units 8 s + c
-  // (c = 0..7: dims 16 e + 2c, 16 e + 2c + 1, four tokens each, dim 16 e + 2c
-  // in the first 8 bytes).  The row starts' residues (0-3, 8-11 mod 16 units)
-  // make the stagers' 16-byte stores (16 lanes: one group, rows 0-7, c = k and
-  // 4 + k) and the 8-byte fragment reads (32 lanes: one pair, one row) free
-  // of bank conflicts with 32 or 64 banks of 4 bytes, and every row offset is
-  // a compile-time constant, so all fragment reads share one lane address.
-  static constexpr int kVPairUnits = 140;
-  static constexpr int kSlotBytes = kKBytes + 4 * kVPairUnits * 16;
-  __device__ static constexpr int v_row(int e) { return 17 * e + 4 * (e >> 2); }
-  __device__ static int v_byte(int g, int e, int c) {
-    return (kVPairUnits * (g >> 1) + v_row(e) + 8 * (g & 1) + c) * 16;
-  }
+  static constexpr int kSlotBytes = 16384;  // K regions (4h + c), then V regions
 
   __device__ void reset() {
 #pragma unroll
@@ -399,26 +389,33 @@ struct LongWave {
     }
   }
 
-  // `full`: every token of the block lies inside the causal range of every
-  // valid column of the wave (no masking needed).
-  __device__ void process(const uint8_t *slot, int64_t lt0, bool full) {
-    const uint8_t *kt = slot;
-    const uint8_t *vt = slot + kKBytes;
+  // S = K·Qᵀ of the block in `slot` for every tile: s0 tokens 0-15, s1 16-31.
+  struct Scores {
     f32x4 s0[CT], s1[CT];
-#pragma unroll
-    for (int t = 0; t < CT; ++t) s0[t] = s1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  __device__ void scores(const uint8_t *slot, Scores &sc) const {
+    // K region (h, c): dims 32c .. 32c + 31 of 16-row block h
+    const uint8_t *kt = slot + (16 * quad + col) * 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kt + col * 272 + (4 * c + quad) * 16);
-      const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kt + (16 + col) * 272 + (4 * c + quad) * 16);
+      const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kt + c * 1024);
+      const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kt + (4 + c) * 1024);
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < CT; ++t) {
-        s0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k0), as_bf16x8(qf[t][c]), s0[t], 0,
-                                                        0, 0);
-        s1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k1), as_bf16x8(qf[t][c]), s1[t], 0,
-                                                        0, 0);
+        sc.s0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k0), as_bf16x8(qf[t][c]),
+                                                           c ? sc.s0[t] : z, 0, 0, 0);
+        sc.s1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k1), as_bf16x8(qf[t][c]),
+                                                           c ? sc.s1[t] : z, 0, 0, 0);
       }
     }
+  }
+
+  // The online softmax and O += P·V of the block in `slot` from its scores.
+  // `full`: every token of the block lies inside the causal range of every
+  // valid column of the wave (no masking needed).
+  __device__ void apply(const uint8_t *slot, const Scores &sc, int64_t lt0, bool full) {
+    const f32x4 *s0 = sc.s0, *s1 = sc.s1;
     bf16x8 pt[CT];
 #pragma unroll
     for (int t = 0; t < CT; ++t) {
@@ -465,14 +462,16 @@ struct LongWave {
       lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u), pt[t], lsum[t], 0, 0, 0);
     }
-    // dim 16 e + col of groups quad (tokens 4 quad ..) and 4 + quad (16 + 4
-    // quad ..): unit c = col / 2 of row e, half col & 1; group 4 + quad lies
-    // two pairs after group quad
-    const uint8_t *vl = vt + v_byte(quad, 0, col >> 1) + (col & 1) * 8;
+    // V region (h, e / 2) of 16-row block h: lane 4k + m of a quad addresses
+    // dims 16 e + 4m .. + 3 of token row 4 quad + k, and the transposing read
+    // gives lane col the four tokens 4 quad .. 4 quad + 3 (16 + 4 quad .. for
+    // block 1) of dim 16 e + col, as the Pᵀ fragment orders them
+    const uint8_t *vl =
+        slot + 8192 + (8 * quad + 2 * (col >> 2) + ((col & 3) >> 1)) * 16 + (col & 1) * 8;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const u32x2 lo = *reinterpret_cast<const u32x2 *>(vl + v_row(e) * 16);
-      const u32x2 hi = *reinterpret_cast<const u32x2 *>(vl + (2 * kVPairUnits + v_row(e)) * 16);
+      const u32x2 lo = lds_read_tr16(vl + (e >> 1) * 1024 + 512 * (e & 1));
+      const u32x2 hi = lds_read_tr16(vl + (4 + (e >> 1)) * 1024 + 512 * (e & 1));
       const bf16x8 va = as_bf16x8(lo[0], lo[1], hi[0], hi[1]);
 #pragma unroll
       for (int t = 0; t < CT; ++t)
@@ -482,79 +481,59 @@ struct LongWave {
 
   // 16-row blocks 0..n16-1 of the current page-index window as 32-token
   // blocks (the second half of the last one is empty when n16 is odd: no
-  // rows, no traffic).  Every wave stages its share of each block two blocks
-  // ahead; one barrier per block.  A slot is rewritten two blocks later, after
-  // every wave has passed the barrier that follows its reads; windows hold 64
-  // 16-row blocks (an even number of 32-token blocks), so a window's first
-  // block never reuses the slot its predecessor's last block is read from.
-  // `own_end`: causal end of the wave's last column; blocks at or past it are
-  // staged but not computed.
+  // rows).  Each block is 16 buffer loads of 1 KB straight into LDS (64 lanes
+  // x 16 bytes, written in lane order); wave w loads K and V regions (h =
+  // w / 2, c = 2 (w & 1), c + 1) of 16-row block h.  Rows past a page's
+  // valid rows read as zeros (buffer bounds).  Three ring slots, used in turn
+  // across windows (`rpos`): after barrier i, block i + 2 goes into the slot
+  // block i - 1 used (every wave has finished it); before barrier i, each
+  // wave waits for its own loads of block i.  A new window's first two
+  // blocks go into the two slots after the previous window's last block.
   template <class PageTok, class RowsOf, class LtOf>
   __device__ void stream(int n16, PageTok page_tok, RowsOf rows_of, LtOf lt_of, uint8_t *ring,
                          int wave, int64_t own_end) {
-    const int t = threadIdx.x & 127;
-    const bool stage_v = wave >= 2;
     const int row_bytes = a.row_elems * 2;
     const int nb = (n16 + 1) >> 1;
-    // K stagers: chunk j of lane t is row 8 (j & 1) + (t >> 4) of 16-row block
-    // 2i + (j >> 1), bytes (t & 15) * 16 .. +16.  V stagers: token group g =
-    // t >> 4 (tokens 4g .. 4g + 3 of the 32), dims 8 (t & 15) .. +8.
-    auto fetch = [&](int i, u32x4 (&d)[4]) {
-      if (!stage_v) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int b16 = 2 * i + h;
-          const __amdgpu_buffer_rsrc_t r = page_rows_rsrc(
-              a.k + page_tok(b16) + (int64_t)kvh * a.head_elems, rows_of(b16), a.row_elems);
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
-            d[2 * h + jj] = load16_rows<false>(r, (8 * jj + (t >> 4)) * row_bytes + (t & 15) * 16);
-        }
-      } else {
-        const int g = t >> 4;
-        const int b16 = 2 * i + (wave - 2);  // wave 2: tokens 0-15, wave 3: 16-31
-        const __amdgpu_buffer_rsrc_t r = page_rows_rsrc(
-            a.v + page_tok(b16) + (int64_t)kvh * a.head_elems, rows_of(b16), a.row_elems);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          d[j] = load16_rows<false>(r, (4 * (g & 3) + j) * row_bytes + (t & 15) * 16);
-      }
+    const int h = wave >> 1, c0 = 2 * (wave & 1);
+    // K: LDS unit l = (row l & 15, chunk l >> 4); V: (row (l >> 1) & 15,
+    // chunk 2 (l >> 5) + (l & 1)); region c0 + 1 is 64 bytes further per row
+    const int koff = (lane & 15) * row_bytes + (4 * c0 + (lane >> 4)) * 16;
+    const int voff = ((lane >> 1) & 15) * row_bytes + (4 * c0 + 2 * (lane >> 5) + (lane & 1)) * 16;
+    const uint16_t *kb = a.k + (int64_t)kvh * a.head_elems;
+    const uint16_t *vb = a.v + (int64_t)kvh * a.head_elems;
+    auto slot_at = [&](int r) { return ring + r * kSlotBytes; };
+    auto next_slot = [](int r) { return r == 2 ? 0 : r + 1; };
+    auto issue = [&](int i, uint8_t *slot) {
+      const int b16 = 2 * i + h;
+      const int rows = rows_of(b16);
+      const int64_t tok = page_tok(b16);
+      const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(kb + tok, rows, a.row_elems);
+      const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(vb + tok, rows, a.row_elems);
+      uint8_t *kr = slot + (4 * h + c0) * 1024;
+      lds_load16(rk, kr, koff);
+      lds_load16(rk, kr + 1024, koff + 64);
+      lds_load16(rv, kr + 8192, voff);
+      lds_load16(rv, kr + 9216, voff + 64);
     };
-    auto store = [&](int i, const u32x4 (&d)[4]) {
-      uint8_t *slot = ring + (i & 1) * kSlotBytes;
-      if (!stage_v) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<u32x4 *>(slot + (8 * j + (t >> 4)) * 272 + (t & 15) * 16) = d[j];
-      } else {
-        const int g = t >> 4, d8 = t & 15;
-        // dims 8 d8 .. 8 d8 + 7: row d8 / 2, units 4 (d8 & 1) .. + 3
-        uint8_t *vs = slot + kKBytes + v_byte(g, d8 >> 1, 4 * (d8 & 1));
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          // dims 8 d8 + 2k (low halves) and + 2k + 1 (high halves) of tokens
-          // 4g .. 4g + 3: one unit
-          const u32x4 w = {pack_lo16(d[0][k], d[1][k]), pack_lo16(d[2][k], d[3][k]),
-                           pack_hi16(d[0][k], d[1][k]), pack_hi16(d[2][k], d[3][k])};
-          *reinterpret_cast<u32x4 *>(vs + k * 16) = w;
-        }
-      }
-    };
-    auto step = [&](int i, u32x4 (&d)[4]) {
-      store(i, d);
-      fetch(i + 2, d);  // past the end: no valid rows, no traffic
+    int cur = rpos;
+    issue(0, slot_at(cur));
+    if (nb > 1) issue(1, slot_at(next_slot(cur)));
+    for (int i = 0; i < nb; ++i) {
+      if (i + 1 < nb)
+        wait_vmcnt<4>();
+      else
+        wait_vmcnt<0>();
       __syncthreads();
+      if (i + 2 < nb) issue(i + 2, slot_at(next_slot(next_slot(cur))));
       const int64_t lt0 = lt_of(2 * i);
-      if (lt0 < own_end) process(ring + (i & 1) * kSlotBytes, lt0, lt0 + 32 <= full_end);
-    };
-    u32x4 d0[4], d1[4];
-    fetch(0, d0);
-    fetch(1, d1);
-    for (int i = 0; i < nb; i += 2) {
-      step(i, d0);
-      if (i + 1 >= nb) break;
-      step(i + 1, d1);
+      if (lt0 < own_end) {
+        Scores sc;
+        scores(slot_at(cur), sc);
+        apply(slot_at(cur), sc, lt0, lt0 + 32 <= full_end);
+      }
+      cur = next_slot(cur);
     }
+    rpos = cur;
   }
 };
 
@@ -869,7 +848,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
               ? kv_len - qo_len + (int)((uint32_t)min(last_own, fcols - 1) / (uint32_t)a.group) + 1
               : 0;
       if constexpr (LT) {
-        __shared__ __align__(16) uint8_t lring[2 * LongWave<LTT>::kSlotBytes];
+        __shared__ __align__(16) uint8_t lring[3 * decltype(lw)::kSlotBytes];
         lw.stream(n, page_tok, rows_of, lt_of, lring, wave, uni64(own_end));
       } else {
         __shared__ u32x4 ring[2][2][16][17];
