@@ -349,7 +349,7 @@ struct PrefillWave {
 // ---- long tiles (LOOM_PAGED_PREFILL_LONG_TILE, BF16 pages) --------------------
 // A workgroup of four waves owns 16 * CT * 4 flattened columns; each wave owns
 // CT tiles of 16 and walks the whole causal range in 32-token blocks (two
-// 16-row blocks).  Each block is loaded straight into a three-slot LDS ring
+// 16-row blocks).  Each block is loaded straight into a two-slot LDS ring
 // (buffer loads to LDS: no VGPRs, LDS stores or transposes), in 1 KB regions
 // of 16 rows x 32 dims:
 //   K region (h, c): unit (row r, 16-byte chunk j) at 16 j + r, so a lane's A
@@ -484,11 +484,13 @@ struct LongWave {
   // rows).  Each block is 16 buffer loads of 1 KB straight into LDS (64 lanes
   // x 16 bytes, written in lane order); wave w loads K and V regions (h =
   // w / 2, c = 2 (w & 1), c + 1) of 16-row block h.  Rows past a page's
-  // valid rows read as zeros (buffer bounds).  Three ring slots, used in turn
-  // across windows (`rpos`): after barrier i, block i + 2 goes into the slot
-  // block i - 1 used (every wave has finished it); before barrier i, each
-  // wave waits for its own loads of block i.  A new window's first two
-  // blocks go into the two slots after the previous window's last block.
+  // valid rows read as zeros (buffer bounds).  Two ring slots, used in turn
+  // across windows (`rpos`): after barrier i, block i + 1 goes into the slot
+  // block i - 1 used (every wave has finished it), one block step ahead of
+  // its use; before barrier i, each wave waits for its own loads of block i.
+  // A new window's first block goes into the slot after the previous
+  // window's last block.  (Loading two blocks ahead through a third slot
+  // measured the same at 4-8K rows and 25% slower on a 1024-row prompt.)
   template <class PageTok, class RowsOf, class LtOf>
   __device__ void stream(int n16, PageTok page_tok, RowsOf rows_of, LtOf lt_of, uint8_t *ring,
                          int wave, int64_t own_end) {
@@ -502,7 +504,7 @@ struct LongWave {
     const uint16_t *kb = a.k + (int64_t)kvh * a.head_elems;
     const uint16_t *vb = a.v + (int64_t)kvh * a.head_elems;
     auto slot_at = [&](int r) { return ring + r * kSlotBytes; };
-    auto next_slot = [](int r) { return r == 2 ? 0 : r + 1; };
+    auto next_slot = [](int r) { return r ^ 1; };
     auto issue = [&](int i, uint8_t *slot) {
       const int b16 = 2 * i + h;
       const int rows = rows_of(b16);
@@ -517,14 +519,10 @@ struct LongWave {
     };
     int cur = rpos;
     issue(0, slot_at(cur));
-    if (nb > 1) issue(1, slot_at(next_slot(cur)));
     for (int i = 0; i < nb; ++i) {
-      if (i + 1 < nb)
-        wait_vmcnt<4>();
-      else
-        wait_vmcnt<0>();
+      wait_vmcnt<0>();
       __syncthreads();
-      if (i + 2 < nb) issue(i + 2, slot_at(next_slot(next_slot(cur))));
+      if (i + 1 < nb) issue(i + 1, slot_at(next_slot(cur)));
       const int64_t lt0 = lt_of(2 * i);
       if (lt0 < own_end) {
         Scores sc;
@@ -539,10 +537,11 @@ struct LongWave {
 
 // Query tiles per wave of the long-tile algorithm: two (128 columns per
 // workgroup) when that still gives at least kLongTwoMinGrid workgroups (two
-// per CU), else one (64 columns).  Measured on GQA4 32/8 prompts: two tiles
-// per wave 624 against 580 TFLOP/s at 8192 rows (2048 workgroups), 497
-// against 477 at 4096, 179 against 161 on 8 x 256 rows (536 workgroups), but
-// 188 against 219 at 1 x 1024 rows (256 against 512 workgroups).
+// per CU), else one (64 columns).  Measured on GQA4 32/8 prompts, two tiles
+// per wave at three waves per SIMD against one tile at four: 980 against 747
+// TFLOP/s at 8192 rows, 804-841 against 627 at 4096, 778 against 623 on 4 x
+// 2048 rows, 185-191 against 185 on 8 x 256; on 1 x 1024 rows (256 against
+// 512 workgroups) the two measured the same.
 constexpr int kLongTwoMinGrid = 512;
 
 // SH: the wide-tile algorithm (W = 4, BF16): 16 * W columns per workgroup,
@@ -848,7 +847,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
               ? kv_len - qo_len + (int)((uint32_t)min(last_own, fcols - 1) / (uint32_t)a.group) + 1
               : 0;
       if constexpr (LT) {
-        __shared__ __align__(16) uint8_t lring[3 * decltype(lw)::kSlotBytes];
+        __shared__ __align__(16) uint8_t lring[2 * decltype(lw)::kSlotBytes];
         lw.stream(n, page_tok, rows_of, lt_of, lring, wave, uni64(own_end));
       } else {
         __shared__ u32x4 ring[2][2][16][17];
@@ -957,7 +956,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
 // those gaps (the four-wave BF16 kernel would otherwise settle at two).
 constexpr int kPrefillWavesPerEu = 3;
 
-// Long tiles: three waves per SIMD (three workgroups of 49.8 KB LDS per CU).
+// Long tiles: three waves per SIMD (three workgroups of 33.4 KB LDS per CU).
 // With two query tiles per wave that is 168 registers: a few values live
 // across the whole walk go to scratch, outside the block loop.  Measured
 // against two waves per SIMD (176 registers, no scratch): 975 against 869
