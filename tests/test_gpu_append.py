@@ -496,16 +496,18 @@ def _many_requests_case(oracle, rng, B, T, hq, hkv):
     return pool, indptr, indices, last, bi, pos, q, k, v
 
 
-@pytest.mark.parametrize("B,T", [(3000, 300), (64, 8192)], ids=["batch3000_table_in_memory",
-                                                               "tokens8192_grid_over_residency"])
+@pytest.mark.parametrize("B,T", [(3000, 300), (64, 8192), (64, 2048)],
+                         ids=["batch3000_table_in_memory", "tokens8192_grid_over_residency",
+                              "tokens2048"])
 @pytest.mark.parametrize("brk", ["valid", "duplicate_far"])
 def test_chunked_path_large_batch_and_max_tokens(L, oracle, B, T, brk):
     """The chunk-validated path where the validation workgroups read the
-    request table from memory (B > 2048 requests), and at the contract's
-    largest command (T = 8192 tokens: 8192 + V workgroups, more than the
-    device holds at once, so later token workgroups start only after earlier
-    ones finish); valid commands against the oracle, a duplicate pair in the
-    first and last chunk leaving every output untouched."""
+    request table from memory (B > 2048 requests), at the contract's largest
+    command (T = 8192 tokens: 8192 + V workgroups, more than the device holds
+    at once, so later token workgroups start only after earlier ones finish),
+    and at 2048 tokens (eight token validation chunks); valid commands
+    against the oracle, a duplicate pair in the first and last token leaving
+    every output untouched."""
     log(f"append chunked B={B} T={T} break={brk}")
     rng = np.random.default_rng(B * 7 + T)
     hq, hkv = 4, 2
