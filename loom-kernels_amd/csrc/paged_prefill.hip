@@ -365,13 +365,17 @@ struct PrefillWave {
 // MFMAs of 16x16x32 per tile, against 12 per 16 tokens with the wide tiles'
 // high/residual split of P.  acc[t][e][i] = O[column col of tile t][dim
 // 16 e + 4 quad + i].
+// Lazy rescale threshold of the long tiles (log2 units).
+constexpr float kLazyRescaleLog2 = 8.0f;
+
 template <int CT>
 struct LongWave {
   const PrefillArgs &a;
   int lane, col, quad, kvh;
   int64_t end_col[CT];  // causal end (exclusive) of the lane's column of each tile
   int64_t full_end;     // smallest causal end of the wave's valid columns
-  float m_run[CT];      // running max (log2 domain, scaled) of each column
+  float m_run[CT];      // reference max (log2 domain, scaled) of each column: at most
+                        // kLazyRescaleLog2 below the running max
   f32x4 lsum[CT];       // running normalizer of each column (every element)
   f32x4 acc[CT][8];
   u32x4 qf[CT][4];      // B fragments of the query tiles
@@ -441,18 +445,23 @@ struct LongWave {
       float mx = fmax_nan(fmax_nan(fmax_nan(sr[0], sr[1]), fmax_nan(sr[2], sr[3])),
                           fmax_nan(fmax_nan(sr[4], sr[5]), fmax_nan(sr[6], sr[7])));
       mx = quad_max_nan(mx) * a.scale_log2;
-      const float m_new = fmax_nan(m_run[t], mx);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet
-      const float al = fast_exp2(m_run[t] - m_use);
+      // Lazy rescale: the column's reference max moves only when a score
+      // exceeds it by more than 2^8 (weights stay <= 256, exact in range for
+      // BF16 and FP32), so after the first blocks O and the normalizer are
+      // almost never rescaled.  LSE = reference max + log2(normalizer).
+      const bool grow = mx > m_run[t] + kLazyRescaleLog2;
+      const float m_ref = grow ? mx : m_run[t];
+      const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // nothing visible yet
       float p[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(sr[i], a.scale_log2, -m_use));
-      m_run[t] = m_new;
-      if (__builtin_amdgcn_ballot_w64(al != 1.0f)) {
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float al = fast_exp2(m_run[t] - m_use);  // 1 where the max stays
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[t][e] *= al;
         lsum[t] *= al;
       }
+      m_run[t] = m_ref;
       // Pᵀ as the B fragment (lane: column, k = 8 quad + [0, 8)): k = 8 quad +
       // i is token 4 quad + i, k = 8 quad + 4 + i token 16 + 4 quad + i
       pt[t] = as_bf16x8(bf16x2_pack(p[0], p[1]), bf16x2_pack(p[2], p[3]), bf16x2_pack(p[4], p[5]),
