@@ -134,6 +134,8 @@ enum {
   LOOM_ENQ_MISALIGNED_BUFFER = 92,
   LOOM_ENQ_PAGE_INDICES_TOO_LONG = 93, /* more pages than the plan's workspace covers */
   LOOM_ENQ_STATIC_SCRATCH_TOO_SMALL = 94, /* plan workspace beyond the static scratch */
+  LOOM_ENQ_STATIC_SCRATCH_BUSY = 96, /* an allocation-free command of another stream
+                                        still holds this device's static scratch */
   LOOM_ENQ_WORKSPACE_NOT_RESERVED = 95, /* the queue's workspace would have to grow while
                                            its stream is being captured */
 
@@ -524,8 +526,13 @@ loom_status_t loom_paged_decode_enqueue_bf16(const loom_paged_decode_plan_t *pla
  * device).  Allocates nothing.  Plans whose workspace_bytes exceed the array
  * are rejected with LOOM_ENQ_STATIC_SCRATCH_TOO_SMALL (BASELINE-sized plans
  * need at most ~11 MiB).  Every call on a device shares its one array: calls
- * whose commands overlap in time on one device (two streams, two queues)
- * race; calls ordered on one stream do not. */
+ * ordered on one stream never conflict.  An eager call on another stream than
+ * the device's previous allocation-free command, while that command has not
+ * finished, is rejected with LOOM_ENQ_STATIC_SCRATCH_BUSY (nothing is
+ * enqueued; the caller orders the streams or waits, then retries).  Calls
+ * under stream capture are not checked (the captured work runs later): the
+ * caller keeps replays of such graphs ordered with every other
+ * allocation-free command on the device, or they race. */
 #define LOOM_PAGED_DECODE_STATIC_SCRATCH_BYTES (32u << 20)
 loom_status_t loom_paged_decode_enqueue_bf16_no_alloc(
     const loom_paged_decode_plan_t *plan, loom_command_scope_t *scope,

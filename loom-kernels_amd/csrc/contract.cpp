@@ -250,6 +250,12 @@ void format_message(loom_error_t *e) {
                "enqueue holds %lld",
                op, (long long)f[1], (long long)f[0]);
       break;
+    case LOOM_ENQ_STATIC_SCRATCH_BUSY:
+      snprintf(m, n,
+               "the static scratch of device %lld is held by an allocation-free command of "
+               "another stream that has not finished (order the streams, or wait, and retry)",
+               (long long)f[0]);
+      break;
     case LOOM_ENQ_WORKSPACE_NOT_RESERVED:
       snprintf(m, n,
                "the command queue's %s holds %lld bytes, the command needs %lld, and the queue's "

@@ -1482,6 +1482,12 @@ enum class DecodeWorkspace {
 // current).  Host code uses these addresses, never the array's name.
 constexpr int kMaxDevices = 64;
 uint8_t *g_scratch_ptr[kMaxDevices] = {};
+// Completion of the device's last eager allocation-free command (an event
+// created with the scratch address, recorded after each such command) and
+// the stream it ran on: a later call on another stream checks the event.
+hipEvent_t g_scratch_done[kMaxDevices] = {};
+hipStream_t g_scratch_stream[kMaxDevices] = {};
+bool g_scratch_used[kMaxDevices] = {};
 std::mutex g_scratch_mu;
 
 }  // namespace
@@ -1490,7 +1496,9 @@ std::mutex g_scratch_mu;
 // header and states of one command.  Every command on a device shares that
 // device's copy and keeps the last command's contents (the partial kernel
 // rewrites the header and every state it reads, so nothing needs clearing);
-// commands that overlap in time on one device race.
+// commands that overlap in time on one device race (an eager call on another
+// stream while the previous command runs is rejected; captured calls are not
+// checked).
 static __device__ __align__(256) uint8_t scratch[LOOM_PAGED_DECODE_STATIC_SCRATCH_BYTES];
 
 namespace {
@@ -1504,11 +1512,14 @@ loom_status_t bind_static_scratch(int device, loom_error_t *err) {
   hipGetDevice(&prev);
   hipError_t e = hipSetDevice(device);
   void *ptr = nullptr;
+  hipEvent_t done = nullptr;
   if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
   hipSetDevice(prev);
   if (e != hipSuccess || !ptr)
     return fail(err, LOOM_CMD_DRIVER, "static scratch", 0, 0, 0, 0, 0.0, e);
   g_scratch_ptr[device] = (uint8_t *)ptr;
+  g_scratch_done[device] = done;
   return LOOM_OK;
 }
 
@@ -1699,9 +1710,28 @@ loom_status_t loom_paged_decode_enqueue_bf16_no_alloc(
     const loom_paged_decode_plan_t *plan, loom_command_scope_t *scope,
     const loom_bf16_paged_batch_decode_args_t *args, loom_error_t *err) {
   if (!plan || !scope || !args) return fail(err, LOOM_NULL_ARGUMENT, "plan");
+  if (!scope->queue) return fail(err, LOOM_NULL_ARGUMENT, "scope");
   loom_handle_t hs[10];
   ref_handles(args, hs);
-  return paged_decode_enqueue_impl(plan, scope, hs, DecodeWorkspace::kStatic, err);
+  const int dev = scope->queue->device;
+  hipStream_t stream = scope->queue->stream;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(err, LOOM_PLAN_UNSUPPORTED_DEVICE, "static scratch", dev);
+  // Held from the check through the launch and the record, so calls from
+  // several host threads are checked in the order they launch.
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const bool eager = hipStreamIsCapturing(stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone;
+  if (eager && g_scratch_used[dev] && g_scratch_stream[dev] != stream &&
+      hipEventQuery(g_scratch_done[dev]) == hipErrorNotReady)
+    return fail(err, LOOM_ENQ_STATIC_SCRATCH_BUSY, "static scratch", dev);
+  const loom_status_t rc = paged_decode_enqueue_impl(plan, scope, hs, DecodeWorkspace::kStatic, err);
+  if (rc == LOOM_OK && eager && g_scratch_done[dev] &&
+      hipEventRecord(g_scratch_done[dev], stream) == hipSuccess) {
+    g_scratch_stream[dev] = stream;
+    g_scratch_used[dev] = true;
+  }
+  return rc;
 }
 
 

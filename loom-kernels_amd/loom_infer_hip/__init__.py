@@ -118,7 +118,7 @@ PLAN_VARIANTS = {70: "StateCountOutOfRange", 71: "StateCountOverflow",
                  74: "UnsupportedDevice", 75: "InvalidOption"}
 ENQUEUE_VARIANTS = {90: "LengthMismatch", 91: "PageIndicesTooShort", 92: "MisalignedBuffer",
                     93: "PageIndicesTooLong", 94: "StaticScratchTooSmall",
-                    95: "WorkspaceNotReserved"}
+                    95: "WorkspaceNotReserved", 96: "StaticScratchBusy"}
 GRAPH_VARIANTS = {110: "DefaultStreamUnsupported", 111: "EmptyCapture",
                   112: "CaptureInvalidated", 113: "NullExecutableHandle",
                   114: "ExecutionPoisoned", 115: "ReplayInFlight", 116: "LaunchCountExhausted",

@@ -96,3 +96,65 @@ def test_no_alloc_rejects_plans_beyond_the_scratch(L):
     comp = scope.finish()
     assert comp.submitted() == 0
     comp.wait()
+
+
+def test_no_alloc_from_another_stream_while_busy_is_rejected(L, oracle):
+    """An eager allocation-free call on a second stream while the device's
+    previous one (queued behind a bounded spin kernel on the first stream)
+    has not finished is rejected with StaticScratchBusy and enqueues
+    nothing; once the first completes, the same call runs and matches the
+    caller-workspace entry point bit for bit."""
+    import torch
+    rng = np.random.default_rng(78)
+    hq, hkv = 32, 8
+    lens = [3000, 40, 8000, 17]
+    B = len(lens)
+    pool = sum((x + 15) // 16 for x in lens) + 7
+    ip, ix, ln = ragged_table(rng, lens, pool)
+    q = seeded_normal_bf16(oracle, rng, B * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    r = DecodeRunner(L, B, pool, hq, hkv)
+    want_o, want_l = r.run(q, k, v, ip, ix, ln)
+    ins = [to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), to_dev_i32(ip), to_dev_i32(ix),
+           to_dev_i32(ln)]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    q1, q2 = L.CommandQueue(s1, 1), L.CommandQueue(s2, 1)
+    outs = [(nan_bf16(r.spec.output_numel),
+             torch.full((r.spec.lse_numel,), float("nan"), dtype=torch.float32, device="cuda"))
+            for _ in range(3)]
+    torch.cuda.synchronize()
+
+    def enqueue(queue, i):
+        out, lse = outs[i]
+        b = queue.bindings(8)
+        h = [b.bind_read(x) for x in ins]
+        ho, hl = b.bind_read_write(out), b.bind_read_write(lse)
+        scope = queue.begin(b)
+        err = None
+        try:
+            r.plan.enqueue_into_no_alloc(scope, L.Bf16PagedBatchDecodeArgs(*h, ho.write(), hl.write()))
+        except L.EnqueueError as e:
+            err = e
+        return scope.finish(), ho, hl, err
+
+    log("stream 1: spin kernel, then an allocation-free decode behind it")
+    with torch.cuda.stream(s1):
+        torch.cuda._sleep(50_000_000)  # bounded spin (tens of ms)
+    c1, ho1, hl1, e1 = enqueue(q1, 0)
+    assert e1 is None and c1.submitted() == 1
+    log("stream 2 while stream 1's command is pending: rejected")
+    c2, _, _, e2 = enqueue(q2, 1)
+    assert e2 is not None and e2.variant == "StaticScratchBusy", e2
+    assert c2.submitted() == 0
+    c2.wait()
+    b1 = c1.wait()
+    assert np.array_equal(bf16_host(b1.take_read_write(ho1)), want_o)
+    log("stream 2 after stream 1 finished: runs")
+    c3, ho3, hl3, e3 = enqueue(q2, 2)
+    assert e3 is None and c3.submitted() == 1
+    b3 = c3.wait()
+    assert np.array_equal(bf16_host(b3.take_read_write(ho3)), want_o)
+    assert np.array_equal(b3.take_read_write(hl3).cpu().numpy(), want_l)
+    torch.cuda.synchronize()
