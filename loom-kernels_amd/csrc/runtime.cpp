@@ -241,7 +241,7 @@ loom_status_t loom_command_queue_new(void *hip_stream, uint64_t max_commands,
   hipGetDevice(&prev);
   hipSetDevice(device);
   hipEvent_t ev = nullptr;
-  e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  e = hipEventCreateWithFlags(&ev, loom::kCompletionEventFlags);
   hipSetDevice(prev);
   if (e != hipSuccess) return fail(err, LOOM_CMD_DRIVER, "event", 0, 0, 0, 0, 0.0, e);
   auto *q = new loom_command_queue;
@@ -886,7 +886,7 @@ loom_status_t loom_captured_graph_instantiate(loom_captured_graph_t *c, loom_gra
   hipGetDevice(&prev);
   hipSetDevice(c->queue->device);
   hipEvent_t ev = nullptr;
-  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  hipError_t e = hipEventCreateWithFlags(&ev, loom::kCompletionEventFlags);
   hipGraphExec_t exec = nullptr;
   if (e == hipSuccess) e = hipGraphInstantiate(&exec, c->graph, nullptr, nullptr, 0);
   hipSetDevice(prev);
