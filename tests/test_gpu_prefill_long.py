@@ -137,6 +137,14 @@ def test_plan_selection_and_rejections(L):
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
         1, 4096, 256, 32, 8, kv_dtype="fp8_e4m3")).algorithm == "wide_tile"
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 4, 8, 8, 8)).algorithm == "row_tile"
+    # the long tiles from a 64-column grid of 256 workgroups (GQA4 32/8: 512
+    # rows); FP8 pages need 512 for the wide tiles
+    assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 512, 32, 32, 8)).algorithm == \
+        "long_tile"
+    assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 256, 16, 32, 8)).algorithm == \
+        "row_tile"
+    assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
+        1, 512, 32, 32, 8, kv_dtype="fp8_e4m3")).algorithm == "row_tile"
     cases = [(L.Bf16PagedPrefillSpec(1, 64, 8, 32, 8, kv_dtype="fp8_e4m3"), 4, "flags", "paged"),
              (L.Bf16PagedPrefillSpec(1, 64, 8, 32, 8), 8, "waves", "paged"),
              (L.Bf16RaggedPrefillSpec(1, 64, 64, 32, 8), 4, "flags", "ragged")]
