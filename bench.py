@@ -980,6 +980,23 @@ def long_prefill_shapes(L, stream, samples=5, shapes=None):
                          for _ in range(samples))[samples // 2]
             rec.update(wide_eager_us=round(wus, 2),
                        wide_TFLOPs=round(flops / (wus * 1e-6) / 1e12, 1))
+            # the same prompt on FP8 E4M3 pages (codes of |x| <= 3, scales 0.3 / 0.7)
+            fspec = L.Bf16PagedPrefillSpec(B, nnz, pool, hq, hkv, kv_dtype="fp8_e4m3")
+            fplan = L.PrefillProvider.load(0).plan_bf16_paged(fspec)
+            k8, v8 = (torch.randint(0, 0x44, (pool * 16 * hkv * 128,), device=dev,
+                                    dtype=torch.uint8, generator=g) for _ in range(2))
+            sc = torch.tensor([0.3, 0.7], dtype=torch.float32, device=dev)
+
+            def bind8(b):
+                return L.Bf16PagedPrefillArgs(
+                    b.bind_read(t[0]), b.bind_read(k8), b.bind_read(v8), b.bind_read(qo),
+                    b.bind_read(ip), b.bind_read(ix), b.bind_read(ln),
+                    b.bind_read_write(o).write(), b.bind_read_write(lse).write(),
+                    b.bind_read(sc))
+            fus = sorted(_timed_enqueues(L, stream, 10, bind8, fplan.enqueue_into, 5, 2)
+                         for _ in range(samples))[samples // 2]
+            rec.update(fp8_algorithm=fplan.algorithm, fp8_eager_us=round(fus, 2),
+                       fp8_TFLOPs=round(flops / (fus * 1e-6) / 1e12, 1))
         out[f"gqa4_b{B}_q{n}_kv{n}"] = rec
     return out
 

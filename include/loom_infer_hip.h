@@ -702,11 +702,11 @@ typedef enum loom_paged_prefill_algorithm {
    * quarter of the L2 bytes per column that ROW_TILE reads.  No cross-wave
    * merge.  No workspace. */
   LOOM_PAGED_PREFILL_WIDE_TILE = 2,
-  /* Long prompts on BF16 pages (paged prefill only): WIDE_TILE's columns and
-   * page walk with 32-token blocks, the query fragments in registers, the
-   * softmax weights P rounded once to BF16 for the P·V product (the
-   * normalizer is summed in FP32; within the attention tolerance of the f32
-   * reference) and V staged transposed in LDS.  No workspace. */
+  /* Long prompts on BF16 or FP8 pages (paged prefill only): WIDE_TILE's
+   * columns and page walk with 32-token blocks loaded straight into LDS, the
+   * query fragments in registers and the softmax weights P rounded once to
+   * BF16 for the P·V product (the normalizer is summed in FP32; within the
+   * attention tolerance of the f32 reference).  No workspace. */
   LOOM_PAGED_PREFILL_LONG_TILE = 3
 } loom_paged_prefill_algorithm_t;
 
@@ -720,7 +720,7 @@ typedef struct loom_paged_prefill_plan_options {
   uint32_t waves; /* waves per workgroup: 0 (the default, four), 4, 8 or 16 */
   uint32_t flags; /* LOOM_PLAN_PAGE_INDICES_CAPACITY (paged only) and at most one of
                      LOOM_PLAN_PREFILL_TILE_16 / _64 / _LONG (the last two: four waves;
-                     _LONG: paged prefill on BF16 pages only) */
+                     _LONG: paged prefill only) */
 } loom_paged_prefill_plan_options_t;
 
 typedef struct loom_paged_prefill_plan_info {

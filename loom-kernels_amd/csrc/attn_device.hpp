@@ -98,6 +98,16 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void *lds) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// Transposing 8-byte LDS read of bytes (ds_read_b64_tr_b8): within each 16
+// lanes, lane i receives as byte k (k = 0..7) byte i % 8 of the 8 bytes lane
+// 2k + i / 8 addresses.
+__device__ __forceinline__ u32x2 lds_read_tr8(const void *lds) {
+  typedef int s32x2 __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) s32x2 lds_s32x2;
+  const s32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2 *)(lds));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // Waits until at most N vector memory loads of this wave are outstanding
 // (lgkm and export counters not waited on).
 template <int N>

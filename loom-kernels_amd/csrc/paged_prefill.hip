@@ -368,7 +368,7 @@ struct PrefillWave {
 // Lazy rescale threshold of the long tiles (log2 units).
 constexpr float kLazyRescaleLog2 = 8.0f;
 
-template <int CT>
+template <int CT, bool FP8>
 struct LongWave {
   const PrefillArgs &a;
   int lane, col, quad, kvh;
@@ -381,7 +381,10 @@ struct LongWave {
   u32x4 qf[CT][4];      // B fragments of the query tiles
   int rpos = 0;         // ring slot of the next block staged
 
-  static constexpr int kSlotBytes = 16384;  // K regions (4h + c), then V regions
+  // K regions (4h + c), then V regions; on FP8 E4M3 pages regions of 16 rows
+  // x 64 dims (one byte each), K (2h + c) then V
+  static constexpr int kSlotBytes = FP8 ? 8192 : 16384;
+  static constexpr int kVBase = kSlotBytes / 2;
 
   __device__ void reset() {
 #pragma unroll
@@ -398,12 +401,24 @@ struct LongWave {
     f32x4 s0[CT], s1[CT];
   };
   __device__ void scores(const uint8_t *slot, Scores &sc) const {
-    // K region (h, c): dims 32c .. 32c + 31 of 16-row block h
-    const uint8_t *kt = slot + (16 * quad + col) * 16;
+    // BF16: K region (h, c) holds dims 32c .. 32c + 31 of 16-row block h.
+    // FP8: K region (h, cc) dims 64cc .. 64cc + 63, unit (row r, 16-byte chunk
+    // j) at 16 j + r; the lane's 8 dims 32c + 8 quad .. are half quad & 1 of
+    // unit 2 (c & 1) + (quad >> 1) of region (h, c >> 1), widened to BF16
+    // (exactly) after the read.
+    const uint8_t *kt = FP8 ? slot + 256 * (quad >> 1) + 16 * col + 8 * (quad & 1)
+                            : slot + (16 * quad + col) * 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kt + c * 1024);
-      const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kt + (4 + c) * 1024);
+      u32x4 k0, k1;
+      if constexpr (FP8) {
+        const int o = (c >> 1) * 1024 + 512 * (c & 1);
+        k0 = fp8x8_to_bf16x8(*reinterpret_cast<const u32x2 *>(kt + o));
+        k1 = fp8x8_to_bf16x8(*reinterpret_cast<const u32x2 *>(kt + 2048 + o));
+      } else {
+        k0 = *reinterpret_cast<const u32x4 *>(kt + c * 1024);
+        k1 = *reinterpret_cast<const u32x4 *>(kt + (4 + c) * 1024);
+      }
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < CT; ++t) {
@@ -475,13 +490,29 @@ struct LongWave {
     // dims 16 e + 4m .. + 3 of token row 4 quad + k, and the transposing read
     // gives lane col the four tokens 4 quad .. 4 quad + 3 (16 + 4 quad .. for
     // block 1) of dim 16 e + col, as the Pᵀ fragment orders them
+    //
+    // FP8: V region (h, cc) holds dims 64cc .. 64cc + 63 of block h, unit (row
+    // r, chunk j) at 16 j + ((r + 8h) & 15); lane c of a quad addresses dims
+    // 16 e + 8 (c & 1) .. + 7 of token row 4 quad + ((c >> 1) & 3) of block
+    // c >> 3, and the transposing byte read (ds_read_b64_tr_b8: lane i
+    // receives byte i % 8 of the 8 bytes lane 2k + i / 8 addresses, k =
+    // 0..7) gives lane col the eight tokens of dim 16 e + col in Pᵀ order.
+    const int hv = col >> 3, rv = (4 * quad + ((col >> 1) & 3) + 8 * hv) & 15;
     const uint8_t *vl =
-        slot + 8192 + (8 * quad + 2 * (col >> 2) + ((col & 3) >> 1)) * 16 + (col & 1) * 8;
+        FP8 ? slot + kVBase + 2048 * hv + 16 * rv + 8 * (col & 1)
+            : slot + kVBase + (8 * quad + 2 * (col >> 2) + ((col & 3) >> 1)) * 16 + (col & 1) * 8;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const u32x2 lo = lds_read_tr16(vl + (e >> 1) * 1024 + 512 * (e & 1));
-      const u32x2 hi = lds_read_tr16(vl + (4 + (e >> 1)) * 1024 + 512 * (e & 1));
-      const bf16x8 va = as_bf16x8(lo[0], lo[1], hi[0], hi[1]);
+      bf16x8 va;
+      if constexpr (FP8) {
+        const u32x2 b = lds_read_tr8(vl + (e >> 2) * 1024 + 256 * (e & 3));
+        const u32x4 w = fp8x8_to_bf16x8(b);
+        va = as_bf16x8(w[0], w[1], w[2], w[3]);
+      } else {
+        const u32x2 lo = lds_read_tr16(vl + (e >> 1) * 1024 + 512 * (e & 1));
+        const u32x2 hi = lds_read_tr16(vl + (4 + (e >> 1)) * 1024 + 512 * (e & 1));
+        va = as_bf16x8(lo[0], lo[1], hi[0], hi[1]);
+      }
 #pragma unroll
       for (int t = 0; t < CT; ++t)
         acc[t][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pt[t], acc[t][e], 0, 0, 0);
@@ -503,33 +534,45 @@ struct LongWave {
   template <class PageTok, class RowsOf, class LtOf>
   __device__ void stream(int n16, PageTok page_tok, RowsOf rows_of, LtOf lt_of, uint8_t *ring,
                          int wave, int64_t own_end) {
-    const int row_bytes = a.row_elems * 2;
+    const int row_bytes = a.row_elems * (FP8 ? 1 : 2);
     const int nb = (n16 + 1) >> 1;
-    const int h = wave >> 1, c0 = 2 * (wave & 1);
-    // K: LDS unit l = (row l & 15, chunk l >> 4); V: (row (l >> 1) & 15,
-    // chunk 2 (l >> 5) + (l & 1)); region c0 + 1 is 64 bytes further per row
-    const int koff = (lane & 15) * row_bytes + (4 * c0 + (lane >> 4)) * 16;
-    const int voff = ((lane >> 1) & 15) * row_bytes + (4 * c0 + 2 * (lane >> 5) + (lane & 1)) * 16;
-    const uint16_t *kb = a.k + (int64_t)kvh * a.head_elems;
-    const uint16_t *vb = a.v + (int64_t)kvh * a.head_elems;
+    const int h = wave >> 1, c0 = FP8 ? (wave & 1) : 2 * (wave & 1);
+    // BF16 K: LDS unit l = (row l & 15, chunk l >> 4); V: (row (l >> 1) & 15,
+    // chunk 2 (l >> 5) + (l & 1)); region c0 + 1 is 64 bytes further per row.
+    // FP8 (one region of K and one of V per wave): K unit l = (row l & 15,
+    // chunk l >> 4); V unit l = (row ((l & 15) + 8h) & 15, chunk l >> 4).
+    const int koff = FP8 ? (lane & 15) * row_bytes + 64 * c0 + (lane >> 4) * 16
+                         : (lane & 15) * row_bytes + (4 * c0 + (lane >> 4)) * 16;
+    const int voff = FP8 ? (((lane & 15) + 8 * h) & 15) * row_bytes + 64 * c0 + (lane >> 4) * 16
+                         : ((lane >> 1) & 15) * row_bytes + (4 * c0 + 2 * (lane >> 5) + (lane & 1)) * 16;
+    const uint8_t *kb = reinterpret_cast<const uint8_t *>(a.k) + (int64_t)kvh * a.head_elems * (FP8 ? 1 : 2);
+    const uint8_t *vb = reinterpret_cast<const uint8_t *>(a.v) + (int64_t)kvh * a.head_elems * (FP8 ? 1 : 2);
     auto slot_at = [&](int r) { return ring + r * kSlotBytes; };
     auto next_slot = [](int r) { return r ^ 1; };
     auto issue = [&](int i, uint8_t *slot) {
       const int b16 = 2 * i + h;
       const int rows = rows_of(b16);
-      const int64_t tok = page_tok(b16);
-      const __amdgpu_buffer_rsrc_t rk = page_rows_rsrc(kb + tok, rows, a.row_elems);
-      const __amdgpu_buffer_rsrc_t rv = page_rows_rsrc(vb + tok, rows, a.row_elems);
-      uint8_t *kr = slot + (4 * h + c0) * 1024;
-      lds_load16(rk, kr, koff);
-      lds_load16(rk, kr + 1024, koff + 64);
-      lds_load16(rv, kr + 8192, voff);
-      lds_load16(rv, kr + 9216, voff + 64);
+      const int64_t tok = page_tok(b16) * (FP8 ? 1 : 2);  // bytes
+      const int bytes = rows > 0 ? ((rows - 1) * a.row_elems + 128) * (FP8 ? 1 : 2) : 0;
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(kb + tok), 0, bytes, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(vb + tok), 0, bytes, 0x00020000);
+      if constexpr (FP8) {
+        lds_load16(rk, slot + (2 * h + c0) * 1024, koff);
+        lds_load16(rv, slot + kVBase + (2 * h + c0) * 1024, voff);
+      } else {
+        uint8_t *kr = slot + (4 * h + c0) * 1024;
+        lds_load16(rk, kr, koff);
+        lds_load16(rk, kr + 1024, koff + 64);
+        lds_load16(rv, kr + 8192, voff);
+        lds_load16(rv, kr + 9216, voff + 64);
+      }
     };
     int cur = rpos;
     issue(0, slot_at(cur));
     for (int i = 0; i < nb; ++i) {
-      wait_vmcnt<0>();
+      wait_vmcnt<0>();  // this wave's loads of block i
       __syncthreads();
       if (i + 1 < nb) issue(i + 1, slot_at(next_slot(cur)));
       const int64_t lt0 = lt_of(2 * i);
@@ -560,7 +603,7 @@ constexpr int kLongTwoMinGrid = 512;
 template <int W, bool RAGGED, bool FP8, bool SH, int LT = 0>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   static_assert(!SH || W == 4, "wide tiles: four waves");
-  static_assert(!LT || (SH && !FP8), "long tiles: the wide tiles' columns, BF16 pages");
+  static_assert(!LT || SH, "long tiles: the wide tiles' columns");
   constexpr int TC = LT ? 16 * W * LT : SH ? 16 * W : 16;  // flattened columns per workgroup
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   PrefillArgs a = args;
@@ -758,7 +801,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   w.reset();
   // Long tiles: this lane's column of each of the wave's tiles.
   constexpr int LTT = LT ? LT : 1;
-  LongWave<LTT> lw{a, lane, col, quad, kvh};
+  LongWave<LTT, FP8> lw{a, lane, col, quad, kvh};
   bool colv_t[LTT];
   int qi_t[LTT], gh_t[LTT];
   if constexpr (LT) {
@@ -884,8 +927,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         *reinterpret_cast<u32x2 *>(orow + 16 * e) =
-            u32x2{bf16x2_pack(lw.acc[t][e][0] * inv, lw.acc[t][e][1] * inv),
-                  bf16x2_pack(lw.acc[t][e][2] * inv, lw.acc[t][e][3] * inv)};
+            u32x2{bf16x2_pack(lw.acc[t][e][0] * inv * v_scale, lw.acc[t][e][1] * inv * v_scale),
+                  bf16x2_pack(lw.acc[t][e][2] * inv * v_scale, lw.acc[t][e][3] * inv * v_scale)};
       if (quad == 0) a.lse[row_head] = lw.m_run[t] + __log2f(Lt[t]);
     }
     return;
@@ -1049,7 +1092,8 @@ loom_status_t prefill_grid(uint64_t batch, uint64_t nnz_qo, uint64_t hq, uint64_
 #endif
 loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
                                 uint64_t nnz_qo, uint64_t hq, uint64_t hkv, bool long_ok,
-                                uint32_t *tile_cols, bool *long_tile, loom_error_t *err) {
+                                bool long_default, uint32_t *tile_cols, bool *long_tile,
+                                loom_error_t *err) {
   const uint32_t t = flags & (LOOM_PLAN_PREFILL_TILE_16 | LOOM_PLAN_PREFILL_TILE_64 |
                               LOOM_PLAN_PREFILL_TILE_LONG);
   *long_tile = false;
@@ -1070,7 +1114,7 @@ loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
   // Long prompts on BF16 pages take the long tiles, from a smaller grid than
   // the wide tiles need (see the algorithm's measurements in the plan's
   // documentation).
-  *long_tile = long_requests && long_ok && LOOM_PREFILL_LONG_DEFAULT &&
+  *long_tile = long_requests && long_ok && long_default && LOOM_PREFILL_LONG_DEFAULT &&
                grid64 >= LOOM_PREFILL_LONG_MIN_GRID;
   if (*long_tile) {
     *tile_cols = (cols / 128) * hkv >= kLongTwoMinGrid ? 128 : 64;
@@ -1128,9 +1172,8 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   uint32_t tile_cols = 16;
   bool long_tile = false;
   loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->batch_size, spec->nnz_qo,
-                                       spec->num_query_heads, spec->num_kv_heads,
-                                       spec->kv_dtype == LOOM_KV_DTYPE_BF16, &tile_cols,
-                                       &long_tile, err);
+                                       spec->num_query_heads, spec->num_kv_heads, true, true,
+                                       &tile_cols, &long_tile, err);
   if (rc) return rc;
   uint64_t tiles = 0, grid = 0;
   rc = prefill_grid(spec->batch_size, spec->nnz_qo, spec->num_query_heads, spec->num_kv_heads,
@@ -1241,7 +1284,11 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   if (fp8) {
     switch (plan->info.waves) {
       case 4:
-        if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
+        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
+          hipLaunchKernelGGL((paged_prefill_kernel<4, true, true, 2>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE)
+          hipLaunchKernelGGL((paged_prefill_kernel<4, true, true, 1>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
           hipLaunchKernelGGL((paged_prefill_kernel<4, true, true>), grid, block, 0, stream, a);
         else
           hipLaunchKernelGGL((paged_prefill_kernel<4, true>), grid, block, 0, stream, a);
@@ -1288,7 +1335,7 @@ loom_status_t loom_prefill_provider_plan_bf16_ragged(
   uint32_t tile_cols = 16;
   bool long_tile = false;
   loom_status_t rc = prefill_tile_cols(opt.flags, waves, spec->batch_size, spec->nnz_qo,
-                                       spec->num_query_heads, spec->num_kv_heads, false,
+                                       spec->num_query_heads, spec->num_kv_heads, false, false,
                                        &tile_cols, &long_tile, err);
   if (rc) return rc;
   uint64_t tiles = 0, grid = 0;

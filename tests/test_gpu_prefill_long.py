@@ -127,26 +127,25 @@ def test_long_guards_equal_narrow(L, oracle, guard):
 
 
 def test_plan_selection_and_rejections(L):
-    """BF16 long prompts default to the long tiles; FP8 pages keep the wide
-    tiles and reject the long-tile flag; ragged prefill rejects it; it needs
-    four waves."""
+    """Long prompts default to the long tiles (BF16 and FP8 pages); ragged
+    prefill rejects the long-tile flag; it needs four waves."""
     import ctypes as C
     prov = L.PrefillProvider.load(0)
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 4096, 256, 32, 8)).algorithm == \
         "long_tile"
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
-        1, 4096, 256, 32, 8, kv_dtype="fp8_e4m3")).algorithm == "wide_tile"
+        1, 4096, 256, 32, 8, kv_dtype="fp8_e4m3")).algorithm == "long_tile"
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 4, 8, 8, 8)).algorithm == "row_tile"
     # the long tiles from a 64-column grid of 256 workgroups (GQA4 32/8: 512
-    # rows); FP8 pages need 512 for the wide tiles
-    assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 512, 32, 32, 8)).algorithm == \
-        "long_tile"
-    assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(1, 256, 16, 32, 8)).algorithm == \
-        "row_tile"
+    # rows), on either page type
+    for dt in ("bf16", "fp8_e4m3"):
+        assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
+            1, 512, 32, 32, 8, kv_dtype=dt)).algorithm == "long_tile"
+        assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
+            1, 256, 16, 32, 8, kv_dtype=dt)).algorithm == "row_tile"
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
-        1, 512, 32, 32, 8, kv_dtype="fp8_e4m3")).algorithm == "row_tile"
-    cases = [(L.Bf16PagedPrefillSpec(1, 64, 8, 32, 8, kv_dtype="fp8_e4m3"), 4, "flags", "paged"),
-             (L.Bf16PagedPrefillSpec(1, 64, 8, 32, 8), 8, "waves", "paged"),
+        1, 64, 8, 32, 8, kv_dtype="fp8_e4m3"), tile_cols="long").algorithm == "long_tile"
+    cases = [(L.Bf16PagedPrefillSpec(1, 64, 8, 32, 8), 8, "waves", "paged"),
              (L.Bf16RaggedPrefillSpec(1, 64, 64, 32, 8), 4, "flags", "ragged")]
     for spec, waves, field, kind in cases:
         fn = (L.lib().loom_prefill_provider_plan_bf16_paged_options if kind == "paged"
@@ -178,6 +177,69 @@ def test_two_tiles_per_wave_with_a_guarded_request(L, oracle):
     k = torch.randn(pool * 16 * hkv * 128, device="cuda", generator=g).to(torch.bfloat16)
     v = torch.randn(pool * 16 * hkv * 128, device="cuda", generator=g).to(torch.bfloat16)
     res = paged_pair(L, B, nnz, pool, hq, hkv, q, k, v, qo, ip, ix, last, tile="long")
+    log(f"  vs 16-column: {assert_close(oracle, res)}")
+    o = oracle.bf16_to_f32(res[0][0]).reshape(nnz, hq * 128)
+    assert np.all(np.isnan(o[1100:])) and not np.any(np.isnan(o[:1100]))
+
+
+FP8_CASES = [  # (name, hq, hkv, qo_lens, kv_lens, spec keywords)
+    ("ragged_mix", 16, 4, [70, 5, 130], [400, 90, 130], {}),
+    ("odd_blocks", 32, 8, [17, 33, 1, 50], [17, 49, 31, 1100], {}),
+    ("hnd", 16, 4, [70, 5, 130], [400, 90, 130], {"kv_layout": "HND"}),
+    ("page32", 16, 4, [70, 5, 130], [400, 90, 130], {"kv_page_size": 32}),
+    ("page64", 8, 1, [64, 3], [1200, 40], {"kv_page_size": 64}),
+]
+
+
+@pytest.mark.parametrize("case", FP8_CASES, ids=lambda c: c[0])
+def test_fp8_pages_on_long_tiles(L, oracle, case):
+    """FP8 E4M3 pages on the long tiles (regions of 64 one-byte dims loaded
+    straight into LDS, K widened to BF16 after its fragment reads, V through
+    the transposing byte read), with K and V scales: the same sentinels and,
+    elsewhere, the 16-column FP8 command's result within the oracle
+    tolerance (codes up to 0x44, |x| <= 3)."""
+    import torch
+    from test_gpu_fp8 import random_fp8
+    name, hq, hkv, qo_lens, kv_lens, kw = case
+    log(f"long prefill fp8 {name}")
+    rng = np.random.default_rng(len(name) + 880)
+    P = kw.get("kv_page_size", 16)
+    pages = [(x + P - 1) // P for x in kv_lens]
+    pool = sum(pages) + 2
+    ip = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    ix = rng.permutation(pool)[: ip[-1]].astype(np.int32)
+    last = np.array([x - (p - 1) * P for x, p in zip(kv_lens, pages)], np.int32)
+    qo = np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32)
+    B, nnz = len(qo_lens), int(qo[-1])
+    q = seeded_normal_bf16(oracle, rng, nnz * hq * 128)
+    n_kv = pool * P * hkv * 128
+    k = torch.from_numpy(random_fp8(rng, n_kv, max_code=0x44)).to("cuda")
+    v = torch.from_numpy(random_fp8(rng, n_kv, max_code=0x44)).to("cuda")
+    res = paged_pair(L, B, nnz, pool, hq, hkv, q, k, v, qo, ip, ix, last,
+                     spec_kw={"kv_dtype": "fp8_e4m3", **kw}, scales=[0.3, 0.7], tile="long")
+    assert not np.any(np.isnan(oracle.bf16_to_f32(res[0][0])))
+    log(f"  vs 16-column: {assert_close(oracle, res)}")
+
+
+def test_fp8_two_tiles_per_wave_with_a_guarded_request(L, oracle):
+    """The FP8 long tiles at two query tiles per wave: two 1100-row GQA4
+    prompts, the second with an invalid page index."""
+    import torch
+    from test_gpu_fp8 import random_fp8
+    log("long prefill fp8, two tiles per wave, one guarded request")
+    rng = np.random.default_rng(1101)
+    hq, hkv = 32, 8
+    qo_lens, kv_lens = [1100, 1100], [1300, 1100]
+    pool = sum((n + 15) // 16 for n in kv_lens) + 2
+    qo, ip, ix, last = ragged_meta(rng, qo_lens, kv_lens, pool)
+    ix = ix.copy()
+    ix[ip[1] + 40] = pool + 9
+    B, nnz = 2, int(qo[-1])
+    q = seeded_normal_bf16(oracle, rng, nnz * hq * 128)
+    k = torch.from_numpy(random_fp8(rng, pool * 16 * hkv * 128, max_code=0x44)).to("cuda")
+    v = torch.from_numpy(random_fp8(rng, pool * 16 * hkv * 128, max_code=0x44)).to("cuda")
+    res = paged_pair(L, B, nnz, pool, hq, hkv, q, k, v, qo, ip, ix, last,
+                     spec_kw={"kv_dtype": "fp8_e4m3"}, scales=[0.3, 0.7], tile="long")
     log(f"  vs 16-column: {assert_close(oracle, res)}")
     o = oracle.bf16_to_f32(res[0][0]).reshape(nnz, hq * 128)
     assert np.all(np.isnan(o[1100:])) and not np.any(np.isnan(o[:1100]))

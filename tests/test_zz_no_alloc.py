@@ -4,6 +4,7 @@ split-KV workspace is the library's static per-device scratch.  Checked
 against the caller-workspace entry point (loom_paged_decode_enqueue) bit for
 bit on two calls in a row, the second with a smaller input, so the second
 runs over the first call's scratch contents."""
+import gc
 import sys
 
 import numpy as np
@@ -139,13 +140,21 @@ def test_no_alloc_from_another_stream_while_busy_is_rejected(L, oracle):
             err = e
         return scope.finish(), ho, hl, err
 
-    log("stream 1: spin kernel, then an allocation-free decode behind it")
-    with torch.cuda.stream(s1):
-        torch.cuda._sleep(50_000_000)  # bounded spin (tens of ms)
-    c1, ho1, hl1, e1 = enqueue(q1, 0)
-    assert e1 is None and c1.submitted() == 1
-    log("stream 2 while stream 1's command is pending: rejected")
-    c2, _, _, e2 = enqueue(q2, 1)
+    # Nothing may synchronize the device while stream 1 is held: freeing a
+    # command queue does (hipFree of its workspaces), so earlier tests'
+    # garbage is collected first and the collector is off until the check.
+    gc.collect()
+    gc.disable()
+    try:
+        log("stream 1: spin kernel, then an allocation-free decode behind it")
+        with torch.cuda.stream(s1):
+            torch.cuda._sleep(50_000_000)  # bounded spin (tens of ms)
+        c1, ho1, hl1, e1 = enqueue(q1, 0)
+        assert e1 is None and c1.submitted() == 1
+        log("stream 2 while stream 1's command is pending: rejected")
+        c2, _, _, e2 = enqueue(q2, 1)
+    finally:
+        gc.enable()
     assert e2 is not None and e2.variant == "StaticScratchBusy", e2
     assert c2.submitted() == 0
     c2.wait()
