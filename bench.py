@@ -590,7 +590,7 @@ def capi_eager(B, pool, hq, hkv, indptr, indices, last, samples=30):
 
 
 def reference_shapes(L, stream, samples=30):
-    """The reference's own published shapes (its H20 records, BASELINE.md):
+    """The reference's own published shapes (its H20 records):
     tiny decode and append fixtures, whose time is launch latency.  Eager = the
     mean of 100 back-to-back calls between two events, median over `samples`
     batches (benchmarks/matched.rs:141-173); graph = one replay plus its
