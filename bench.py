@@ -186,12 +186,13 @@ class DecodeCase:
                                           h[7].write(), h[8].write())
 
 
-def _timed_enqueues(L, stream, n_bind, bind, enqueue, steps, warmup):
+def _timed_enqueues(L, stream, n_bind, bind, enqueue, steps, warmup, commands_per_call=1):
     """hipEvent pair around `steps` back-to-back enqueues on one stream, per call
     (the reference's eager_stream_batch_cuda_event, benchmarks/matched.rs:141-173).
-    The events are recorded on the stream the kernels are launched on."""
+    The events are recorded on the stream the kernels are launched on.
+    `commands_per_call`: commands one enqueue submits (the queue's capacity)."""
     import torch
-    q = L.CommandQueue(stream, steps + warmup + 1)
+    q = L.CommandQueue(stream, (steps + warmup) * commands_per_call + 1)
     b = q.bindings(n_bind)
     args = bind(b)
     with torch.cuda.stream(stream):
@@ -740,6 +741,64 @@ def reference_shapes(L, stream, samples=30):
     return out
 
 
+# The reference's contiguous single-decode eager records (H20, median of 100
+# samples; docs/results/h20-flashinfer-v0.6.16.post1-parallel-merge-eager-
+# performance-20260805.json `results`): (case, kv_len, Hq, Hkv, its algorithm
+# and partitions, its median µs).
+SINGLE_DECODE_REFERENCE = (
+    ("bf16_mha_l1_qh8_kvh8", 1, 8, 8, 0, 2.599),
+    ("bf16_mqa_l33_qh8_kvh1", 33, 8, 1, 12, 6.432),
+    ("bf16_gqa_l127_qh16_kvh4", 127, 16, 4, 16, 8.342),
+    ("bf16_gqa_l4096_qh32_kvh4", 4096, 32, 4, 64, 35.877),
+)
+
+
+def single_decode_shapes(L, stream, samples=30):
+    """Contiguous single decode (single_decode/mod.rs, decode.rs:1016-1450) at
+    the shapes of the reference's single-decode eager records: the direct
+    plan, and split-K with the reference's partition count where it used
+    split-K (two kernels, as there).  Eager = the mean of 100 back-to-back
+    calls between two events, median over `samples` batches; synthetic
+    values."""
+    import torch
+    dev = "cuda"
+    out = {}
+    prov = L.DecodeProvider.load(0)
+    for case, kv_len, hq, hkv, parts, ref_us in SINGLE_DECODE_REFERENCE:
+        spec = L.Bf16SingleDecodeSpec(kv_len, hq, hkv)
+        g = torch.Generator(device=dev).manual_seed(kv_len * 31 + hq)
+        q, k, v = (torch.randn(n, device=dev, generator=g).to(torch.bfloat16)
+                   for n in (spec.query_numel, spec.kv_numel, spec.kv_numel))
+        o = torch.empty(spec.output_numel, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(spec.lse_numel, dtype=torch.float32, device=dev)
+        rec = {"h20_loom_eager_us": ref_us}
+        plan = prov.plan_bf16(spec)
+
+        def bind(b):
+            return L.Bf16SingleDecodeArgs(b.bind_read(q), b.bind_read(k), b.bind_read(v),
+                                          b.bind_read_write(o).write(),
+                                          b.bind_read_write(lse).write())
+        us = sorted(_timed_enqueues(L, stream, 5, bind, plan.enqueue_into, 100, 10 if i == 0 else 2)
+                    for i in range(samples))[samples // 2]
+        rec["direct_eager_us"] = round(us, 3)
+        if parts:
+            sk = L.Bf16SingleDecodeSplitKSpec(spec, parts)
+            kplan = prov.plan_bf16_split_k(sk)
+            ws = torch.empty(sk.workspace_numel, dtype=torch.float32, device=dev)
+
+            def bind_k(b):
+                return L.Bf16SingleDecodeSplitKArgs(
+                    b.bind_read(q), b.bind_read(k), b.bind_read(v), b.bind_read_write(ws),
+                    b.bind_read_write(o).write(), b.bind_read_write(lse).write())
+            us = sorted(_timed_enqueues(L, stream, 6, bind_k, kplan.enqueue_into, 100,
+                                        10 if i == 0 else 2, commands_per_call=2)
+                        for i in range(samples))[samples // 2]
+            rec["split_k_partitions"] = parts
+            rec["split_k_eager_us"] = round(us, 3)
+        out[case] = rec
+    return out
+
+
 def replay_floor(L, stream, n=200):
     """Where a graph replay's time goes (run under rocprofv3 --runtime-trace
     --kernel-trace for the per-call breakdown): the reference's T=6
@@ -1275,6 +1334,8 @@ def main():
         log("[bench] reference published shapes")
         detail["reference_shapes"] = reference_shapes(L, stream)
         log(f"[bench] {detail['reference_shapes']}")
+        detail["single_decode"] = single_decode_shapes(L, stream)
+        log(f"[bench] {detail['single_decode']}")
     if not a.quick and (not a.only or a.only == "prefill"):
         log("[bench] paged prefill at the reference's shapes")
         detail["paged_prefill"] = prefill_shapes(L, stream)
