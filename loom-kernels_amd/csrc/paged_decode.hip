@@ -1193,45 +1193,78 @@ __global__ __launch_bounds__(kThreads, waves_per_eu<GT>()) void single_decode_sp
 
 // Split-K merge (single_decode/mod.rs:332-381): one workgroup of 128 lanes
 // (one per output column) per query head.
-__global__ __launch_bounds__(128) void single_decode_split_k_merge_kernel(
+// One workgroup of four waves per query head: wave w takes partitions w, w +
+// 4, ..., each lane two of the 128 dims; the first kMergeBatch partitions of
+// every wave are loaded before the heads' maximum is reduced, so up to 64
+// partitions take one memory round trip.  The waves' sums are combined in
+// LDS in wave order (deterministic).  Empty partitions (max -inf, normalizer
+// 0) weigh nothing.
+constexpr int kMergeWaves = 4, kMergeBatch = 16;
+__global__ __launch_bounds__(kMergeWaves * 64) void single_decode_split_k_merge_kernel(
     DecodeArgs a, int partitions, const float *__restrict__ ws) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qh = blockIdx.x;
   const float *row = ws + (int64_t)qh * partitions * loom::kStateWidth;
+  float ms[kMergeBatch], ls[kMergeBatch];
+  f32x2 xs[kMergeBatch];
+  auto load_batch = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const int p = base + u * kMergeWaves;
+      if (p < partitions) {
+        const float *ss = row + (int64_t)p * loom::kStateWidth;
+        ms[u] = ss[0];
+        ls[u] = ss[1];
+        xs[u] = *reinterpret_cast<const f32x2 *>(ss + 2 + 2 * lane);
+      } else {
+        ms[u] = -INFINITY;
+        ls[u] = 0.f;
+        xs[u] = f32x2{0.f, 0.f};
+      }
+    }
+  };
+  load_batch(wave);
   float mloc = -INFINITY;
-  for (int p = tid; p < partitions; p += 128) mloc = fmaxf(mloc, row[(int64_t)p * loom::kStateWidth]);
+  for (int p = tid; p < partitions; p += kMergeWaves * 64)
+    mloc = fmaxf(mloc, row[(int64_t)p * loom::kStateWidth]);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
-  __shared__ float s_m[2];
+  __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
+  __shared__ f32x2 s_o[kMergeWaves][64];
   if (lane == 0) s_m[wave] = mloc;
   __syncthreads();
-  const float M = fmaxf(s_m[0], s_m[1]);
-  float l = 0.f, o = 0.f;
-  int p = 0;
-  for (; p + 8 <= partitions; p += 8) {
-    float ms[8], ls[8], xs[8];
+  float M = s_m[0];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float *ss = row + (int64_t)(p + u) * loom::kStateWidth;
-      ms[u] = ss[0];
-      ls[u] = ss[1];
-      xs[u] = ss[2 + tid];
-    }
+  for (int w = 1; w < kMergeWaves; ++w) M = fmaxf(M, s_m[w]);
+  float l = 0.f;
+  f32x2 o = {0.f, 0.f};
+  for (int base = wave;; base += kMergeWaves * kMergeBatch) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float f = fast_exp2(ms[u] - M);
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const float f = ms[u] == -INFINITY ? 0.f : fast_exp2(ms[u] - M);
       l = fmaf(ls[u], f, l);
-      o = fmaf(xs[u], f, o);
+      o[0] = fmaf(xs[u][0], f, o[0]);
+      o[1] = fmaf(xs[u][1], f, o[1]);
     }
+    if (base + kMergeWaves * kMergeBatch >= partitions) break;
+    load_batch(base + kMergeWaves * kMergeBatch);
   }
-  for (; p < partitions; ++p) {
-    const float *ss = row + (int64_t)p * loom::kStateWidth;
-    const float f = fast_exp2(ss[0] - M);
-    l = fmaf(ss[1], f, l);
-    o = fmaf(ss[2 + tid], f, o);
+  if (lane == 0) s_l[wave] = l;
+  s_o[wave][lane] = o;
+  __syncthreads();
+  if (wave == 0) {
+    float lt = s_l[0];
+    f32x2 ot = s_o[0][lane];
+#pragma unroll
+    for (int w = 1; w < kMergeWaves; ++w) {
+      lt += s_l[w];
+      ot[0] += s_o[w][lane][0];
+      ot[1] += s_o[w][lane][1];
+    }
+    *reinterpret_cast<uint32_t *>(a.out + (int64_t)qh * 128 + 2 * lane) =
+        bf16x2_pack(ot[0] / lt, ot[1] / lt);
+    if (lane == 0) a.lse[qh] = M + __log2f(lt);
   }
-  a.out[(int64_t)qh * 128 + tid] = f32_to_bf16(o / l);
-  if (tid == 0) a.lse[qh] = M + __log2f(l);
 }
 
 }  // namespace
@@ -1883,7 +1916,7 @@ loom_status_t loom_single_decode_split_k_enqueue(const loom_single_decode_split_
   rc = loom::record_launch(scope, hipGetLastError(), err);
   if (rc) return rc;
   hipLaunchKernelGGL(single_decode_split_k_merge_kernel, dim3((unsigned)s.num_query_heads),
-                     dim3(128), 0, stream, a, P, (const float *)ws);
+                     dim3(kMergeWaves * 64), 0, stream, a, P, (const float *)ws);
   return loom::record_launch(scope, hipGetLastError(), err);
 }
 
