@@ -1017,13 +1017,14 @@ __global__ __launch_bounds__(128) void paged_decode_direct_merge_kernel(DecodeAr
 }
 
 // Merges the states of one (request, query head) whose pages span several
-// teams into O and log2-LSE: 128 lanes, one per output column, one pass with
-// a running max over blocks of 16 teams (one load round trip per block).  The
-// header written by the partial kernel gives the request's virtual page
-// range; a poisoned state (invalid page index) leaves the request's sentinels.
-__global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
+// teams into O and log2-LSE: one wave, 2 output columns per lane, one pass
+// with a running max over blocks of 16 teams (one load round trip per
+// block). The header written by the partial kernel gives the request's
+// virtual page range; a poisoned state (invalid page index) leaves the
+// request's sentinels.
+__global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int kBlock = 16;
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x;
   const int r = blockIdx.x / a.hq;
   const int qh = blockIdx.x % a.hq;
   const int64_t total = a.header[0];
@@ -1033,22 +1034,24 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
   const int64_t t0 = team_of(total, pre, teams), t1 = team_of(total, pend - 1, teams);
   if (t0 == t1) return;
   const bool all_nonempty = total >= teams;
-  float M = -INFINITY, l = 0.f, o = 0.f;
+  float M = -INFINITY, l = 0.f;
+  f32x2 o = {0.f, 0.f};
   bool poisoned = false;
   for (int64_t t = t0; t <= t1; t += kBlock) {
-    float ms[kBlock], ls[kBlock], xs[kBlock];
+    float ms[kBlock], ls[kBlock];
+    f32x2 xs[kBlock];
 #pragma unroll
     for (int u = 0; u < kBlock; ++u) {
       ms[u] = -INFINITY;
       ls[u] = 0.f;
-      xs[u] = 0.f;
+      xs[u] = f32x2{0.f, 0.f};
       const int64_t tu = t + u;
       if (tu <= t1 && (all_nonempty || team_start(total, tu, teams) <
                                            team_start(total, tu + 1, teams))) {
         const float *ss = a.states + ((tu + r) * a.hq + qh) * (int64_t)kStateStride;
         ms[u] = ss[0];
         ls[u] = ss[1];
-        xs[u] = ss[4 + tid];
+        xs[u] = *reinterpret_cast<const f32x2 *>(ss + 4 + 2 * lane);
       }
     }
     float mb = M;
@@ -1057,22 +1060,31 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
       mb = fmaxf(mb, ms[u]);
       poisoned |= ls[u] < 0.0f;
     }
+    // A block of empty teams (possible when there are fewer pages than
+    // teams) leaves the state as it is.
+    if (mb == -INFINITY) continue;
     const float sc = fast_exp2(M - mb);
     l *= sc;
-    o *= sc;
+    o[0] *= sc;
+    o[1] *= sc;
 #pragma unroll
     for (int u = 0; u < kBlock; ++u) {
       const float f = fast_exp2(ms[u] - mb);
       l = fmaf(ls[u], f, l);
-      o = fmaf(xs[u], f, o);
+      o[0] = fmaf(xs[u][0], f, o[0]);
+      o[1] = fmaf(xs[u][1], f, o[1]);
     }
     M = mb;
   }
   if (poisoned) return;
-  float ov = o / l;
-  if (a.kv_scales) ov *= a.kv_scales[1];  // FP8 pages: V's scale
-  a.out[((int64_t)r * a.hq + qh) * 128 + tid] = f32_to_bf16(ov);
-  if (tid == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(l);
+  float v0 = o[0] / l, v1 = o[1] / l;
+  if (a.kv_scales) {  // FP8 pages: V's scale
+    v0 *= a.kv_scales[1];
+    v1 *= a.kv_scales[1];
+  }
+  *reinterpret_cast<uint32_t *>(a.out + ((int64_t)r * a.hq + qh) * 128 + 2 * lane) =
+      bf16x2_pack(v0, v1);
+  if (lane == 0) a.lse[(int64_t)r * a.hq + qh] = M + __log2f(l);
 }
 
 // ---- contiguous single decode -------------------------------------------------
@@ -1698,7 +1710,7 @@ loom_status_t paged_decode_enqueue_impl(const loom_paged_decode_plan_t *plan,
   if (e == hipSuccess) {
     // One command: the partial kernel, then the merge of split requests.
     hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)(s.batch_size * s.num_query_heads)),
-                       dim3(128), 0, stream, a);
+                       dim3(64), 0, stream, a);
     e = hipGetLastError();
   }
   return loom::record_launch(scope, e, err);
