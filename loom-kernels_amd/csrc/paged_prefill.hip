@@ -457,26 +457,34 @@ struct LongWave {
       // the scale is positive, so the max is taken before scaling
       // (IEEE maximum: no NaN quieting of the MFMA results, three inputs per
       // instruction)
-      float mx = fmax_nan(fmax_nan(fmax_nan(sr[0], sr[1]), fmax_nan(sr[2], sr[3])),
-                          fmax_nan(fmax_nan(sr[4], sr[5]), fmax_nan(sr[6], sr[7])));
-      mx = quad_max_nan(mx) * a.scale_log2;
+      const float ml = fmax_nan(fmax_nan(fmax_nan(sr[0], sr[1]), sr[2]),
+                                fmax_nan(fmax_nan(fmax_nan(sr[3], sr[4]), sr[5]),
+                                         fmax_nan(sr[6], sr[7])));
       // Lazy rescale: the column's reference max moves only when a score
       // exceeds it by more than 2^8 (weights stay <= 256, exact in range for
       // BF16 and FP32), so after the first blocks O and the normalizer are
       // almost never rescaled.  LSE = reference max + log2(normalizer).
-      const bool grow = mx > m_run[t] + kLazyRescaleLog2;
-      const float m_ref = grow ? mx : m_run[t];
-      const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // nothing visible yet
+      // The column max (across the four row quads) is needed only when some
+      // lane's own max passes the threshold: rounding is monotonic, so no
+      // lane passing means no column passes.
+      if (__builtin_amdgcn_ballot_w64(ml * a.scale_log2 > m_run[t] + kLazyRescaleLog2)) {
+        const float mx = quad_max_nan(ml) * a.scale_log2;
+        const bool grow = mx > m_run[t] + kLazyRescaleLog2;
+        const float m_ref = grow ? mx : m_run[t];
+        // (a column with nothing visible before has O = 0: nothing to rescale)
+        if (__builtin_amdgcn_ballot_w64(grow && m_run[t] != -INFINITY)) {
+          // 1 where the max stays; 0 where nothing was visible
+          const float al = fast_exp2(m_run[t] - (m_ref == -INFINITY ? 0.0f : m_ref));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[t][e] *= al;
+          lsum[t] *= al;
+        }
+        m_run[t] = m_ref;
+      }
+      const float m_use = m_run[t] == -INFINITY ? 0.0f : m_run[t];  // nothing visible yet
       float p[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(sr[i], a.scale_log2, -m_use));
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float al = fast_exp2(m_run[t] - m_use);  // 1 where the max stays
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[t][e] *= al;
-        lsum[t] *= al;
-      }
-      m_run[t] = m_ref;
       // Pᵀ as the B fragment (lane: column, k = 8 quad + [0, 8)): k = 8 quad +
       // i is token 4 quad + i, k = 8 quad + 4 + i token 16 + 4 quad + i
       pt[t] = as_bf16x8(bf16x2_pack(p[0], p[1]), bf16x2_pack(p[2], p[3]), bf16x2_pack(p[4], p[5]),
