@@ -87,6 +87,16 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void *lds, 
                "s"(m0), "s"(r)
                : "m0", "memory");
 }
+// The same with the LDS byte address given directly (wave-uniform), so a
+// caller that keeps one LDS base address needs no generic-to-LDS pointer
+// conversion per load.
+__device__ __forceinline__ void lds_load16_at(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr,
+                                              int byte_offset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(byte_offset),
+               "s"(m0), "s"(r)
+               : "m0", "memory");
+}
 #pragma clang diagnostic pop
 
 // Transposing 8-byte LDS read (ds_read_b64_tr_b16): within each 16 lanes,

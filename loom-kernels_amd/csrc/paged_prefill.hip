@@ -539,8 +539,8 @@ struct LongWave {
   // A new window's first block goes into the slot after the previous
   // window's last block.  (Loading two blocks ahead through a third slot
   // measured the same at 4-8K rows and 25% slower on a 1024-row prompt.)
-  template <class PageTok, class RowsOf, class LtOf>
-  __device__ void stream(int n16, PageTok page_tok, RowsOf rows_of, LtOf lt_of, uint8_t *ring,
+  template <class PageOff, class RowsOf, class LtOf>
+  __device__ void stream(int n16, PageOff page_off, RowsOf rows_of, LtOf lt_of, uint8_t *ring,
                          int wave, int64_t own_end) {
     const int row_bytes = a.row_elems * (FP8 ? 1 : 2);
     const int nb = (n16 + 1) >> 1;
@@ -557,32 +557,36 @@ struct LongWave {
     const uint8_t *vb = reinterpret_cast<const uint8_t *>(a.v) + (int64_t)kvh * a.head_elems * (FP8 ? 1 : 2);
     auto slot_at = [&](int r) { return ring + r * kSlotBytes; };
     auto next_slot = [](int r) { return r ^ 1; };
-    auto issue = [&](int i, uint8_t *slot) {
+    // LDS byte address of the ring (one generic-to-LDS conversion)
+    const uint32_t ring_lds =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
+    auto issue = [&](int i, int slot) {
       const int b16 = 2 * i + h;
       const int rows = rows_of(b16);
-      const int64_t tok = page_tok(b16) * (FP8 ? 1 : 2);  // bytes
+      const uint64_t off = page_off(b16);  // bytes
       const int bytes = rows > 0 ? ((rows - 1) * a.row_elems + 128) * (FP8 ? 1 : 2) : 0;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t *>(kb + tok), 0, bytes, 0x00020000);
+          const_cast<uint8_t *>(kb + off), 0, bytes, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint8_t *>(vb + tok), 0, bytes, 0x00020000);
+          const_cast<uint8_t *>(vb + off), 0, bytes, 0x00020000);
+      const uint32_t sl = ring_lds + (uint32_t)(slot * kSlotBytes);
       if constexpr (FP8) {
-        lds_load16(rk, slot + (2 * h + c0) * 1024, koff);
-        lds_load16(rv, slot + kVBase + (2 * h + c0) * 1024, voff);
+        lds_load16_at(rk, sl + (2 * h + c0) * 1024, koff);
+        lds_load16_at(rv, sl + kVBase + (2 * h + c0) * 1024, voff);
       } else {
-        uint8_t *kr = slot + (4 * h + c0) * 1024;
-        lds_load16(rk, kr, koff);
-        lds_load16(rk, kr + 1024, koff + 64);
-        lds_load16(rv, kr + 8192, voff);
-        lds_load16(rv, kr + 9216, voff + 64);
+        const uint32_t kr = sl + (4 * h + c0) * 1024;
+        lds_load16_at(rk, kr, koff);
+        lds_load16_at(rk, kr + 1024, koff + 64);
+        lds_load16_at(rv, kr + 8192, voff);
+        lds_load16_at(rv, kr + 9216, voff + 64);
       }
     };
     int cur = rpos;
-    issue(0, slot_at(cur));
+    issue(0, cur);
     for (int i = 0; i < nb; ++i) {
       wait_vmcnt<0>();  // this wave's loads of block i
       __syncthreads();
-      if (i + 1 < nb) issue(i + 1, slot_at(next_slot(cur)));
+      if (i + 1 < nb) issue(i + 1, next_slot(cur));
       const int64_t lt0 = lt_of(2 * i);
       if (lt0 < own_end) {
         Scores sc;
@@ -851,6 +855,18 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     return uni(blk(s0 + i) == req_pages - 1 ? (int)tl : 16);
   };
   auto lt_of = [&](int i) { return (int64_t)blk(s0 + i) * 16; };
+  // Long tiles: byte offset of 16-row block i of the window in K or V (kv-head
+  // 0), with 32-bit factors: a page's bytes (page_rows x Hkv x 128 elements)
+  // are far below 2^32, and an index failing the guard has no valid rows, so
+  // its loads read nothing whatever the offset.
+  const uint32_t page_bytes = (uint32_t)(a.page_rows * a.hkv * 128 * (FP8 ? 1 : 2));
+  const uint32_t block_bytes = (uint32_t)(16 * a.row_elems * (FP8 ? 1 : 2));
+  auto page_off = [&](int i) -> uint64_t {
+    const int j = uni(min(i, n - 1));
+    const uint32_t pg = (uint32_t)__builtin_amdgcn_readlane(idx, j);
+    const uint32_t sub = (uint32_t)(blk(s0 + j) & ((1 << a.blocks_lg) - 1));
+    return (uint64_t)pg * page_bytes + sub * block_bytes;
+  };
   // The query tile's loads and the first blocks' loads go out together,
   // before the barrier that publishes the tile.  They follow the first index
   // block, so no wait for it holds back the page loads.  Lanes past the tile's
@@ -908,7 +924,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
               : 0;
       if constexpr (LT) {
         __shared__ __align__(16) uint8_t lring[2 * decltype(lw)::kSlotBytes];
-        lw.stream(n, page_tok, rows_of, lt_of, lring, wave, uni64(own_end));
+        lw.stream(n, page_off, rows_of, lt_of, lring, wave, uni64(own_end));
       } else {
         __shared__ u32x4 ring[2][2][16][17];
         w.template stream_shared<FP8>(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
