@@ -140,7 +140,7 @@ def algorithmic_decode_bytes(lens, B, hq, hkv):
 class DecodeCase:
     """Device-resident synthetic workload for one decode config."""
 
-    def __init__(self, L, name, B, hq, hkv, pool, lens, seed, teams=0):
+    def __init__(self, L, name, B, hq, hkv, pool, lens, seed, teams=0, arena=None):
         import numpy as np
         import torch
         self.name, self.B, self.hq, self.hkv, self.pool = name, B, hq, hkv, pool
@@ -156,8 +156,11 @@ class DecodeCase:
         g.manual_seed(seed)
         self.q = torch.randn(B * hq * 128, generator=g, device=dev).to(torch.bfloat16)
         n = pool * 16 * hkv * 128
-        self.k = torch.empty(n, dtype=torch.bfloat16, device=dev)
-        self.v = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        if arena is not None:  # the config's K/V pools, allocated once (see kv_arenas)
+            self.k, self.v = arena[:n], arena[n:2 * n]
+        else:
+            self.k = torch.empty(n, dtype=torch.bfloat16, device=dev)
+            self.v = torch.empty(n, dtype=torch.bfloat16, device=dev)
         step = 1 << 28
         for buf in (self.k, self.v):
             for s in range(0, n, step):
@@ -261,13 +264,14 @@ def draw_lens(name, seed):
     return [1024]
 
 
-def seed_stats(L, stream, name, B, hq, hkv, pool, seeds, samples, per_sample, warmup):
+def seed_stats(L, stream, name, B, hq, hkv, pool, seeds, samples, per_sample, warmup,
+               arena=None):
     """Per-call µs over seeds 0..n-1 (each seed its own lengths, page table and
     inputs): median / p10 / p90 over every sample, and each seed's median."""
     import torch
     us_all, gbs_all, per_seed = [], [], []
     for sd in seeds:
-        case = DecodeCase(L, name, B, hq, hkv, pool, draw_lens(name, sd), seed=sd)
+        case = DecodeCase(L, name, B, hq, hkv, pool, draw_lens(name, sd), seed=sd, arena=arena)
         xs = _sampled_enqueues(L, stream, 9, case.bind, case.plan.enqueue_into, samples,
                                per_sample, warmup)
         us_all += xs
@@ -1090,6 +1094,22 @@ def cpu_append_baseline(app, min_s=3.0):
                                       f"{t_total:.1f} s, single thread"}
 
 
+def kv_arenas(cases, seeds=True):
+    """One K/V allocation per decode config, made before any measurement and
+    kept to the end, as a serving engine reserves its cache once; every case
+    of the config (the measured one and the seed statistics') views it.  The
+    per-call time of the long-context config depends on where its 1.08 GB
+    pool lands: on one box the same command took 163.5-164.2 µs on some
+    allocations and 172-173 µs on others, stable on each, and up to 188 µs
+    when the pool was allocated after the other configs' allocate/free churn.
+    Two arenas per config: the measured case's (kept, e.g. for the CPU
+    baseline) and one the seed statistics' cases take in turn."""
+    import torch
+    return {n: tuple(torch.empty(2 * pool * 16 * hkv * 128, dtype=torch.bfloat16, device="cuda")
+                     for _ in range(2 if seeds else 1))
+            for n, (B, hq, hkv, pool, lens) in cases.items()}
+
+
 def make_cases(L, quick=False):
     import numpy as np
     rng = np.random.default_rng(2026)
@@ -1146,11 +1166,12 @@ def main():
     stream = torch.cuda.Stream()  # default priority
     detail = {}
     head = None
-    for name, (B, hq, hkv, pool, lens) in make_cases(L, a.quick).items():
-        if a.only and not name.startswith(a.only):
-            continue
+    cases = {n: c for n, c in make_cases(L, a.quick).items()
+             if not a.only or n.startswith(a.only)}
+    arenas = kv_arenas(cases, seeds=not a.no_stats)
+    for name, (B, hq, hkv, pool, lens) in cases.items():
         log(f"[bench] setting up {name}")
-        case = DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name))
+        case = DecodeCase(L, name, B, hq, hkv, pool, lens, seed=len(name), arena=arenas[name][0])
         us = time_eager(L, case, stream, a.steps, a.warmup)
         g_samples = []
         g_us = time_graph(L, case, samples_out=g_samples)
@@ -1265,7 +1286,8 @@ def main():
             del app
         if not a.no_stats:
             detail[name]["seed_stats"] = seed_stats(L, stream, name, B, hq, hkv, pool,
-                                                    range(5), 10, 10, a.warmup)
+                                                    range(5), 10, 10, a.warmup,
+                                                    arena=arenas[name][1])
         log(f"[bench] {name}: {detail[name]}")
         if name.startswith("c3"):
             head = case
