@@ -649,10 +649,8 @@ __global__ void grid_probe_kernel(int *p, int v) {
 // argument values; 0 when the node does not read back as expected (the
 // executable then replays with hipGraphLaunch only).  Probed once per process
 // by capturing (never running) a launch of known shape and arguments.
-int node_grid_semantics() {
-  static int probed = -1;
-  if (probed >= 0) return probed;
-  probed = 0;
+int probe_node_grid_semantics() {
+  int probed = 0;
   hipStream_t s = nullptr;
   if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return probed;
   int *const marker = reinterpret_cast<int *>(uintptr_t{0x7a5e1000});  // never dereferenced
@@ -678,6 +676,12 @@ int node_grid_semantics() {
   }
   (void)hipGetLastError();
   hipStreamDestroy(s);
+  return probed;
+}
+// Probed once per process (a function-local static: initialised once even
+// when several threads instantiate graphs at the same time).
+int node_grid_semantics() {
+  static const int probed = probe_node_grid_semantics();
   return probed;
 }
 
