@@ -368,7 +368,7 @@ struct PrefillWave {
 // Lazy rescale threshold of the long tiles (log2 units).
 constexpr float kLazyRescaleLog2 = 8.0f;
 
-template <int CT, bool FP8>
+template <int CT, bool FP8, int G = 1>
 struct LongWave {
   const PrefillArgs &a;
   int lane, col, quad, kvh;
@@ -539,9 +539,12 @@ struct LongWave {
   // A new window's first block goes into the slot after the previous
   // window's last block.  (Loading two blocks ahead through a third slot
   // measured the same at 4-8K rows and 25% slower on a 1024-row prompt.)
+  // G wave groups (the wave's group `grp`, its wave within the group `wave`)
+  // split the blocks: group g takes blocks g, g + G, ..., through a ring of
+  // its own, in lockstep with the others (one workgroup barrier per step).
   template <class PageOff, class RowsOf, class LtOf>
   __device__ void stream(int n16, PageOff page_off, RowsOf rows_of, LtOf lt_of, uint8_t *ring,
-                         int wave, int64_t own_end) {
+                         int wave, int grp, int64_t own_end) {
     const int row_bytes = a.row_elems * (FP8 ? 1 : 2);
     const int nb = (n16 + 1) >> 1;
     const int h = wave >> 1, c0 = FP8 ? (wave & 1) : 2 * (wave & 1);
@@ -555,11 +558,12 @@ struct LongWave {
                          : ((lane >> 1) & 15) * row_bytes + (4 * c0 + 2 * (lane >> 5) + (lane & 1)) * 16;
     const uint8_t *kb = reinterpret_cast<const uint8_t *>(a.k) + (int64_t)kvh * a.head_elems * (FP8 ? 1 : 2);
     const uint8_t *vb = reinterpret_cast<const uint8_t *>(a.v) + (int64_t)kvh * a.head_elems * (FP8 ? 1 : 2);
-    auto slot_at = [&](int r) { return ring + r * kSlotBytes; };
+    auto slot_at = [&](int r) { return ring + (grp * 2 + r) * kSlotBytes; };
     auto next_slot = [](int r) { return r ^ 1; };
-    // LDS byte address of the ring (one generic-to-LDS conversion)
+    // LDS byte address of this group's ring (one generic-to-LDS conversion)
     const uint32_t ring_lds =
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring +
+        (uint32_t)(grp * 2 * kSlotBytes);
     auto issue = [&](int i, int slot) {
       const int b16 = 2 * i + h;
       const int rows = rows_of(b16);
@@ -582,13 +586,15 @@ struct LongWave {
       }
     };
     int cur = rpos;
-    issue(0, cur);
-    for (int i = 0; i < nb; ++i) {
+    if (grp < nb) issue(grp, cur);
+    const int steps = (nb + G - 1) / G;
+    for (int j = 0; j < steps; ++j) {
+      const int i = G * j + grp;
       wait_vmcnt<0>();  // this wave's loads of block i
       __syncthreads();
-      if (i + 1 < nb) issue(i + 1, next_slot(cur));
+      if (i + G < nb) issue(i + G, next_slot(cur));
       const int64_t lt0 = lt_of(2 * i);
-      if (lt0 < own_end) {
+      if (i < nb && lt0 < own_end) {
         Scores sc;
         scores(slot_at(cur), sc);
         apply(slot_at(cur), sc, lt0, lt0 + 32 <= full_end);
@@ -614,9 +620,13 @@ constexpr int kLongTwoMinGrid = 512;
 // query fragments in registers, BF16 P, Vᵀ staged transposed).
 template <int W, bool RAGGED, bool FP8, bool SH, int LT = 0>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
-  static_assert(!SH || W == 4, "wide tiles: four waves");
+  static_assert(!SH || W == 4 || (LT == 1 && W == 8),
+                "wide tiles: four waves; long tiles: four, or two groups of four with one tile");
   static_assert(!LT || SH, "long tiles: the wide tiles' columns");
-  constexpr int TC = LT ? 16 * W * LT : SH ? 16 * W : 16;  // flattened columns per workgroup
+  // Long tiles: four waves own the query tiles; G groups of them split the
+  // K/V blocks and merge at the end.
+  constexpr int G = LT ? W / 4 : 1;
+  constexpr int TC = LT ? 16 * 4 * LT : SH ? 16 * W : 16;  // flattened columns per workgroup
   // FP8 pages: K's scale folds into the score scale, V's into the output.
   PrefillArgs a = args;
   float v_scale = 1.0f;
@@ -625,6 +635,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
     v_scale = a.kv_scales[1];
   }
   __shared__ PrefillSmem<W, SH, LT> sm;
+  // long tiles: two K/V block slots per wave group (two groups: at least the
+  // merge staging of four waves' column states, 34 floats per lane and tile)
+  constexpr int kRingBytes = LT ? 2 * G * (FP8 ? 8192 : 16384) : 16;
+  constexpr int kMergeBytes = G == 2 ? LT * 34 * 4 * 64 * 4 : 0;
+  __shared__ __align__(16) uint8_t lring[kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, quad = lane >> 4;
@@ -770,7 +785,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   // (fcols <= nnz_qo * Hq fits int32: the plan checks it)
   const int fcols = qo_len * a.group;
   // first column of this wave's tile(s)
-  const int own0 = fbeg + tile0 * TC + (LT ? 16 * LT * wave : SH ? 16 * wave : 0);
+  const int wq = LT ? (wave & 3) : wave;  // long tiles: the wave's tiles within its group
+  const int grp = LT ? (wave >> 2) : 0;
+  const int own0 = fbeg + tile0 * TC + (LT ? 16 * LT * wq : SH ? 16 * wave : 0);
   const int f = own0 + col;
   const bool colv = f < fcols;
   const int qi = colv ? (int)((uint32_t)f / (uint32_t)a.group) : 0;
@@ -813,7 +830,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   w.reset();
   // Long tiles: this lane's column of each of the wave's tiles.
   constexpr int LTT = LT ? LT : 1;
-  LongWave<LTT, FP8> lw{a, lane, col, quad, kvh};
+  LongWave<LTT, FP8, G> lw{a, lane, col, quad, kvh};
   bool colv_t[LTT];
   int qi_t[LTT], gh_t[LTT];
   if constexpr (LT) {
@@ -923,8 +940,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
               ? kv_len - qo_len + (int)((uint32_t)min(last_own, fcols - 1) / (uint32_t)a.group) + 1
               : 0;
       if constexpr (LT) {
-        __shared__ __align__(16) uint8_t lring[2 * decltype(lw)::kSlotBytes];
-        lw.stream(n, page_off, rows_of, lt_of, lring, wave, uni64(own_end));
+        lw.stream(n, page_off, rows_of, lt_of, lring, wq, grp, uni64(own_end));
       } else {
         __shared__ u32x4 ring[2][2][16][17];
         w.template stream_shared<FP8>(n, page_tok, rows_of, lt_of, ring, wave, uni64(own_end));
@@ -941,6 +957,42 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
 #pragma unroll
     for (int t = 0; t < LTT; ++t) Lt[t] = lw.lsum[t][0];
     if (block_or(bad, sm.bad)) return;
+    if constexpr (G == 2) {
+      // Group 1 hands its column states to group 0 through the ring's LDS
+      // (every wave is past its last ring read: block_or's barrier), and
+      // group 0 merges them with its own, as the split-K merge does.
+      static_assert(LTT * 34 * 4 * 64 * 4 <= sizeof(lring), "merge staging fits the ring");
+      float *xs = reinterpret_cast<float *>(lring) + wq * (LTT * 34 * 64) + lane;
+      if (grp == 1) {
+#pragma unroll
+        for (int t = 0; t < LTT; ++t) {
+          float *x = xs + t * 34 * 64;
+          x[0] = lw.m_run[t];
+          x[64] = Lt[t];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[(2 + 4 * e + i) * 64] = lw.acc[t][e][i];
+        }
+      }
+      __syncthreads();
+      if (grp == 1) return;
+#pragma unroll
+      for (int t = 0; t < LTT; ++t) {
+        const float *x = xs + t * 34 * 64;
+        const float m1 = x[0], l1 = x[64], m0 = lw.m_run[t];
+        const float M = fmaxf(m0, m1);
+        const float f0 = m0 == -INFINITY ? 0.0f : fast_exp2(m0 - M);
+        const float f1 = m1 == -INFINITY ? 0.0f : fast_exp2(m1 - M);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            lw.acc[t][e][i] = lw.acc[t][e][i] * f0 + x[(2 + 4 * e + i) * 64] * f1;
+        Lt[t] = Lt[t] * f0 + l1 * f1;
+        lw.m_run[t] = M;
+      }
+    }
 #pragma unroll
     for (int t = 0; t < LTT; ++t) {
       if (!colv_t[t]) continue;
@@ -1038,7 +1090,7 @@ constexpr int kPrefillWavesPerEu = 3;
 // against two waves per SIMD (176 registers, no scratch): 975 against 869
 // TFLOP/s at 8192 rows, 822 against 695 at 4096.
 template <int W, bool FP8, bool SH = false, int LT = 0>
-__global__ __launch_bounds__(W * 64, LT ? 3 : kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(W * 64, LT ? (W == 8 ? 4 : 3) : kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
   prefill_body<W, false, FP8, SH, LT>(a);
 }
 
@@ -1060,6 +1112,7 @@ struct loom_prefill_provider {
 struct loom_paged_prefill_plan {
   loom_paged_prefill_plan_info_t info{};
   uint32_t tile_cols = 16;  // flattened columns per workgroup
+  uint32_t long_groups = 1;  // long tiles: wave groups splitting the K/V blocks
 };
 
 struct loom_ragged_prefill_plan {
@@ -1113,6 +1166,9 @@ loom_status_t prefill_grid(uint64_t batch, uint64_t nnz_qo, uint64_t hq, uint64_
 // workgroups), 11.0 against 9.8 us at 1 x 256 (128).
 #ifndef LOOM_PREFILL_LONG_MIN_GRID
 #define LOOM_PREFILL_LONG_MIN_GRID 256
+#endif
+#ifndef LOOM_PREFILL_LONG_GROUPS
+#define LOOM_PREFILL_LONG_GROUPS 2
 #endif
 loom_status_t prefill_tile_cols(uint32_t flags, uint32_t waves, uint64_t batch,
                                 uint64_t nnz_qo, uint64_t hq, uint64_t hkv, bool long_ok,
@@ -1209,10 +1265,22 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
                       : tile_cols == 64 ? LOOM_PAGED_PREFILL_WIDE_TILE
                                         : LOOM_PAGED_PREFILL_ROW_TILE;
   p->tile_cols = tile_cols;
+  // Long tiles of one query tile per wave (grids too small for two): two
+  // groups of four waves split each tile's K/V blocks, halving the longest
+  // tiles' serial block walk, when the grid fits one round of two such
+  // workgroups per CU or the requests are long enough (1024 rows on average)
+  // that the heaviest tiles dominate.  Measured (GQA4 32/8, BF16 / FP8 pages,
+  // two groups against one): 1 x 512 rows -6% / -15%, 1 x 1024 -2% / -16%,
+  // 1 x 1536 -10% / +2%, and 2 x 512 rows (520 workgroups, a second round)
+  // +6% / -4%.
+  const bool grouped = long_tile && tile_cols == 64 &&
+                       (grid <= 2 * (uint64_t)provider->dev.cus ||
+                        spec->nnz_qo >= 1024 * spec->batch_size);
+  p->long_groups = grouped ? LOOM_PREFILL_LONG_GROUPS : 1;
 
   p->info.waves = waves;
   p->info.row_tiles = tiles;
-  p->info.block_threads = p->info.waves * 64;
+  p->info.block_threads = p->info.waves * 64 * p->long_groups;
   p->info.grid_blocks = grid;
   p->info.flags = opt.flags;
   *out = p;
@@ -1310,6 +1378,8 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
       case 4:
         if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
           hipLaunchKernelGGL((paged_prefill_kernel<4, true, true, 2>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->long_groups == 2)
+          hipLaunchKernelGGL((paged_prefill_kernel<8, true, true, 1>), grid, block, 0, stream, a);
         else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE)
           hipLaunchKernelGGL((paged_prefill_kernel<4, true, true, 1>), grid, block, 0, stream, a);
         else if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)
@@ -1327,6 +1397,8 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
       case 4:
         if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
           hipLaunchKernelGGL((paged_prefill_kernel<4, false, true, 2>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->long_groups == 2)
+          hipLaunchKernelGGL((paged_prefill_kernel<8, false, true, 1>), grid, block, 0, stream, a);
         else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE)
           hipLaunchKernelGGL((paged_prefill_kernel<4, false, true, 1>), grid, block, 0, stream, a);
         else if (plan->info.algorithm == LOOM_PAGED_PREFILL_WIDE_TILE)

@@ -145,6 +145,15 @@ def test_plan_selection_and_rejections(L):
             1, 256, 16, 32, 8, kv_dtype=dt)).algorithm == "row_tile"
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
         1, 64, 8, 32, 8, kv_dtype="fp8_e4m3"), tile_cols="long").algorithm == "long_tile"
+    # one query tile per wave: two groups of four waves split the K/V blocks
+    # when the grid fits one round of two workgroups per CU or the requests
+    # average 1024 rows or more; four waves otherwise
+    for dt in ("bf16", "fp8_e4m3"):
+        for (B, n), threads in (((1, 512), 512), ((1, 1024), 512), ((1, 1536), 512),
+                                ((2, 512), 256), ((1, 4096), 256)):
+            p = prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(B, B * n, B * n // 16, 32, 8,
+                                                            kv_dtype=dt))
+            assert p.algorithm == "long_tile" and p.info.block_threads == threads, (dt, B, n)
     cases = [(L.Bf16PagedPrefillSpec(1, 64, 8, 32, 8), 8, "waves", "paged"),
              (L.Bf16RaggedPrefillSpec(1, 64, 64, 32, 8), 4, "flags", "ragged")]
     for spec, waves, field, kind in cases:
