@@ -706,7 +706,11 @@ typedef enum loom_paged_prefill_algorithm {
    * columns and page walk with 32-token blocks loaded straight into LDS, the
    * query fragments in registers and the softmax weights P rounded once to
    * BF16 for the P·V product (the normalizer is summed in FP32; within the
-   * attention tolerance of the f32 reference).  No workspace. */
+   * attention tolerance of the f32 reference).  One or two 16-column query
+   * tiles per wave (64 or 128 columns per workgroup); plans with one tile per
+   * wave and a small grid (or requests averaging 1024 rows or more) run two
+   * groups of four waves that split the K/V blocks and merge in LDS
+   * (block_threads 512).  No workspace. */
   LOOM_PAGED_PREFILL_LONG_TILE = 3
 } loom_paged_prefill_algorithm_t;
 
@@ -729,8 +733,9 @@ typedef struct loom_paged_prefill_plan_info {
   uint32_t waves;
   uint64_t row_tiles;  /* upper bound of tiles over any valid qo_indptr:
                           min(C, floor((C + (t - 1) * batch) / t)), C = nnz_qo * group,
-                          t = 16 (ROW_TILE) or 64 (WIDE_TILE) columns per tile */
-  uint32_t block_threads;
+                          t = 16 (ROW_TILE), 64 (WIDE_TILE) or 64 / 128 (LONG_TILE)
+                          columns per tile */
+  uint32_t block_threads; /* waves * 64; 512 for LONG_TILE plans with two wave groups */
   uint64_t grid_blocks; /* row_tiles * Hkv */
   uint32_t flags;
 } loom_paged_prefill_plan_info_t;
