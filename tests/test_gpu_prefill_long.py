@@ -252,3 +252,29 @@ def test_fp8_two_tiles_per_wave_with_a_guarded_request(L, oracle):
     log(f"  vs 16-column: {assert_close(oracle, res)}")
     o = oracle.bf16_to_f32(res[0][0]).reshape(nnz, hq * 128)
     assert np.all(np.isnan(o[1100:])) and not np.any(np.isnan(o[:1100]))
+
+
+@pytest.mark.parametrize("n", [1024, 1536])
+def test_two_wave_groups_at_prompt_scale(L, oracle, n):
+    """One-tile long-tile plans of these prompts run two groups of four waves
+    that split each tile's K/V blocks and merge in LDS (1024 rows: a grid of
+    one round, one page-index window; 1536: two windows); the same command
+    on the 16-column algorithm agrees within the attention tolerance."""
+    log(f"long prefill two wave groups, 1 x {n} rows")
+    import torch
+    rng = np.random.default_rng(n)
+    hq, hkv = 32, 8
+    pages = (n + 15) // 16
+    pool = pages + 5
+    qo = np.array([0, n], np.int32)
+    ip = np.array([0, pages], np.int32)
+    ix = rng.permutation(pool)[:pages].astype(np.int32)
+    last = np.array([n - (pages - 1) * 16], np.int32)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    q, k, v = (torch.randn(x, device="cuda", generator=g).to(torch.bfloat16)
+               for x in (n * hq * 128, pool * 16 * hkv * 128, pool * 16 * hkv * 128))
+    plan = L.PrefillProvider.load(0).plan_bf16_paged(L.Bf16PagedPrefillSpec(1, n, pool, hq, hkv))
+    assert plan.algorithm == "long_tile" and plan.info.block_threads == 512
+    res = paged_pair(L, 1, n, pool, hq, hkv, q, k, v, qo, ip, ix, last, tile="long")
+    assert not np.any(np.isnan(oracle.bf16_to_f32(res[0][0])))
+    log(f"  vs 16-column: {assert_close(oracle, res)}")
