@@ -284,9 +284,12 @@ __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int ti
     int64_t pg = 0;
     if (slot_of(a, r_given, p_given, pages, &rr, &p, &pg, &off, ip, ln)) {
       const uint32_t key = (uint32_t)(pg * a.page_rows + off);
-      // Open addressing at load <= 1/2: every probe sequence ends at an
-      // empty entry or at the same key (a duplicate slot).
-      const uint32_t mask = (uint32_t)hash_slots(a.tokens) - 1u;
+      // Open addressing over the whole table (load T / kTableSlots <= 1/2):
+      // every probe sequence ends at an empty entry or at the same key (a
+      // duplicate slot).  The validation workgroup's verdict waits for its
+      // slowest thread, and every further probe is another agent-scope round
+      // trip, so the table is used at its lowest load.
+      const uint32_t mask = (uint32_t)kTableSlots - 1u;
       uint32_t h = (key * 0x9E3779B1u) >> 16 & mask;
       while (true) {
         uint32_t expected = 0u;
