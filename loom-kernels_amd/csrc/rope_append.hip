@@ -190,11 +190,11 @@ __device__ __forceinline__ bool table_bounds_bad(const AppendArgs &a, int32_t ip
 // `ip` / `ln`: the request table (page_indptr, last_page_len), in global
 // memory or an LDS copy.
 // `r` / `p_given`: the token's request and (explicit form) position.
-__device__ __forceinline__ bool slot_of(const AppendArgs &a, int r, int p_given, int64_t pages,
-                                        int *req, int *pos, int64_t *page, int *off,
-                                        const int32_t *ip, const int32_t *ln) {
-  if (r < 0 || r >= a.batch) return false;
-  const int32_t st = ip[r], en = ip[r + 1], tl = ln[r];
+// The slot from the request's table words (st, en) = page_indptr[r, r + 1]
+// and tl = last_page_len[r].
+__device__ __forceinline__ bool slot_from(const AppendArgs &a, int r, int p_given, int64_t pages,
+                                          int32_t st, int32_t en, int32_t tl, int *req, int *pos,
+                                          int64_t *page, int *off) {
   if (st < 0 || en <= st || (int64_t)en > pages || tl < 1 || tl > a.page_rows) return false;
   const int kv_len = (en - st - 1) * a.page_rows + tl;
   const int p = a.batch_indices ? p_given : kv_len - 1;
@@ -207,6 +207,12 @@ __device__ __forceinline__ bool slot_of(const AppendArgs &a, int r, int p_given,
   *off = p % a.page_rows;
   return true;
 }
+__device__ __forceinline__ bool slot_of(const AppendArgs &a, int r, int p_given, int64_t pages,
+                                        int *req, int *pos, int64_t *page, int *off,
+                                        const int32_t *ip, const int32_t *ln) {
+  if (r < 0 || r >= a.batch) return false;
+  return slot_from(a, r, p_given, pages, ip[r], ip[r + 1], ln[r], req, pos, page, off);
+}
 __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t pages, int *req,
                                            int *pos, int64_t *page, int *off,
                                            const int32_t *ip, const int32_t *ln) {
@@ -214,6 +220,23 @@ __device__ __forceinline__ bool token_slot(const AppendArgs &a, int t, int64_t p
   const int r = a.batch_indices ? a.batch_indices[t] : t;
   const int p_given = a.batch_indices ? a.positions[t] : 0;
   return slot_of(a, r, p_given, pages, req, pos, page, off, ip, ln);
+}
+// Token t's slot for an apply workgroup (every thread the same).  A request
+// table of fewer than 64 requests comes whole, in the token words' round
+// trip (each wave its own copy, in registers), so the walk is two round
+// trips instead of three.
+__device__ __forceinline__ bool token_slot_apply(const AppendArgs &a, int t, int tid, int64_t pages,
+                                                 int *req, int *pos, int64_t *page, int *off) {
+  if (a.batch >= 64) return token_slot(a, t, pages, req, pos, page, off, a.indptr, a.last);
+  const int lane = tid & 63;
+  const int32_t ipv = lane <= a.batch ? a.indptr[lane] : 0;
+  const int32_t lnv = lane < a.batch ? a.last[lane] : 0;
+  const int rg = a.batch_indices ? a.batch_indices[t] : t;
+  const int pgv = a.batch_indices ? a.positions[t] : 0;
+  const bool in = rg >= 0 && rg < a.batch;
+  const int rs = in ? rg : 0;
+  const int32_t st = __shfl(ipv, rs, 64), en = __shfl(ipv, rs + 1, 64), tl = __shfl(lnv, rs, 64);
+  return in && slot_from(a, rg, pgv, pages, st, en, tl, req, pos, page, off);
 }
 
 // Validation of chunk b, all-or-nothing.  Chunks [0, index_blocks) check the
@@ -579,7 +602,7 @@ void append_validated_kernel(AppendArgs a) {
   int r = 0, pos = 0, off = 0;
   int64_t page = 0;
   const int64_t pages = table_pages(a, a.indptr[a.batch]);
-  if (!token_slot(a, t, pages, &r, &pos, &page, &off, a.indptr, a.last)) pos = 0, page = 0;
+  if (!token_slot_apply(a, t, tid, pages, &r, &pos, &page, &off)) pos = 0, page = 0;
   // Row loads after the walk: the validation's dependent loads run while the
   // memory system is not yet flooded with the command's row traffic, and the
   // rows still arrive before the verdicts.
@@ -649,7 +672,7 @@ void append_apply_kernel(AppendArgs a) {
   int r = 0, pos = 0, off = 0;
   int64_t page = 0;
   const int64_t pages = table_pages(a, a.indptr[a.batch]);
-  if (!token_slot(a, t, pages, &r, &pos, &page, &off, a.indptr, a.last)) pos = 0, page = 0;
+  if (!token_slot_apply(a, t, tid, pages, &r, &pos, &page, &off)) pos = 0, page = 0;
   const RowSlices first = load_first_slices(a, t, tid);
   token_sincos(a, pos, tid, s_sin, s_cos);
   // empty this workgroup's share of the table the validation kernel filled
