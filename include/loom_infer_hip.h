@@ -707,10 +707,10 @@ typedef enum loom_paged_prefill_algorithm {
    * query fragments in registers and the softmax weights P rounded once to
    * BF16 for the P·V product (the normalizer is summed in FP32; within the
    * attention tolerance of the f32 reference).  One or two 16-column query
-   * tiles per wave (64 or 128 columns per workgroup); plans with one tile per
-   * wave and a small grid (or requests averaging 1024 rows or more) run two
-   * groups of four waves that split the K/V blocks and merge in LDS
-   * (block_threads 512).  No workspace. */
+   * tiles per wave (64 or 128 columns per workgroup); plans whose grid fits
+   * one round of two workgroups per CU (and, with one tile per wave, requests
+   * averaging 1024 rows or more) run two groups of four waves that split the
+   * K/V blocks and merge in LDS (block_threads 512).  No workspace. */
   LOOM_PAGED_PREFILL_LONG_TILE = 3
 } loom_paged_prefill_algorithm_t;
 

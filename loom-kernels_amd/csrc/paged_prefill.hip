@@ -620,7 +620,7 @@ constexpr int kLongTwoMinGrid = 512;
 // query fragments in registers, BF16 P, Vᵀ staged transposed).
 template <int W, bool RAGGED, bool FP8, bool SH, int LT = 0>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
-  static_assert(!SH || W == 4 || (LT == 1 && W == 8),
+  static_assert(!SH || W == 4 || (LT >= 1 && W == 8),
                 "wide tiles: four waves; long tiles: four, or two groups of four with one tile");
   static_assert(!LT || SH, "long tiles: the wide tiles' columns");
   // Long tiles: four waves own the query tiles; G groups of them split the
@@ -1090,7 +1090,7 @@ constexpr int kPrefillWavesPerEu = 3;
 // against two waves per SIMD (176 registers, no scratch): 975 against 869
 // TFLOP/s at 8192 rows, 822 against 695 at 4096.
 template <int W, bool FP8, bool SH = false, int LT = 0>
-__global__ __launch_bounds__(W * 64, LT ? (W == 8 ? 4 : 3) : kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(W * 64, LT ? (W == 8 ? (LT == 1 ? 4 : 2) : 3) : kPrefillWavesPerEu) void paged_prefill_kernel(PrefillArgs a) {
   prefill_body<W, false, FP8, SH, LT>(a);
 }
 
@@ -1272,10 +1272,14 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   // that the heaviest tiles dominate.  Measured (GQA4 32/8, BF16 / FP8 pages,
   // two groups against one): 1 x 512 rows -6% / -15%, 1 x 1024 -2% / -16%,
   // 1 x 1536 -10% / +2%, and 2 x 512 rows (520 workgroups, a second round)
-  // +6% / -4%.
-  const bool grouped = long_tile && tile_cols == 64 &&
-                       (grid <= 2 * (uint64_t)provider->dev.cus ||
-                        spec->nnz_qo >= 1024 * spec->batch_size);
+  // +6% / -4%.  Long tiles of two query tiles per wave split into two groups
+  // only when the grid fits that one round: 1 x 2048 rows -11% / -13%, but
+  // 1 x 3072 +16%, 1 x 4096 +27%, 1 x 8192 +25% and 4 x 2048 +36% (the
+  // 8-wave, 2-tile workgroup holds two waves per SIMD and 70 KB of LDS).
+  const bool one_round = grid <= 2 * (uint64_t)provider->dev.cus;
+  const bool grouped = long_tile &&
+                       ((tile_cols == 64 && (one_round || spec->nnz_qo >= 1024 * spec->batch_size)) ||
+                        (tile_cols == 128 && one_round));
   p->long_groups = grouped ? LOOM_PREFILL_LONG_GROUPS : 1;
 
   p->info.waves = waves;
@@ -1376,7 +1380,9 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   if (fp8) {
     switch (plan->info.waves) {
       case 4:
-        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
+        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128 && plan->long_groups == 2)
+          hipLaunchKernelGGL((paged_prefill_kernel<8, true, true, 2>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
           hipLaunchKernelGGL((paged_prefill_kernel<4, true, true, 2>), grid, block, 0, stream, a);
         else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->long_groups == 2)
           hipLaunchKernelGGL((paged_prefill_kernel<8, true, true, 1>), grid, block, 0, stream, a);
@@ -1395,7 +1401,9 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   } else {
     switch (plan->info.waves) {
       case 4:
-        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
+        if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128 && plan->long_groups == 2)
+          hipLaunchKernelGGL((paged_prefill_kernel<8, false, true, 2>), grid, block, 0, stream, a);
+        else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->tile_cols == 128)
           hipLaunchKernelGGL((paged_prefill_kernel<4, false, true, 2>), grid, block, 0, stream, a);
         else if (plan->info.algorithm == LOOM_PAGED_PREFILL_LONG_TILE && plan->long_groups == 2)
           hipLaunchKernelGGL((paged_prefill_kernel<8, false, true, 1>), grid, block, 0, stream, a);

@@ -145,12 +145,14 @@ def test_plan_selection_and_rejections(L):
             1, 256, 16, 32, 8, kv_dtype=dt)).algorithm == "row_tile"
     assert prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(
         1, 64, 8, 32, 8, kv_dtype="fp8_e4m3"), tile_cols="long").algorithm == "long_tile"
-    # one query tile per wave: two groups of four waves split the K/V blocks
-    # when the grid fits one round of two workgroups per CU or the requests
-    # average 1024 rows or more; four waves otherwise
+    # two groups of four waves split the K/V blocks when the grid fits one
+    # round of two workgroups per CU (1 x 512, 1 x 1024: one tile per wave;
+    # 1 x 2048: two) or, with one tile per wave, the requests average 1024
+    # rows or more (1 x 1536); four waves otherwise
     for dt in ("bf16", "fp8_e4m3"):
         for (B, n), threads in (((1, 512), 512), ((1, 1024), 512), ((1, 1536), 512),
-                                ((2, 512), 256), ((1, 4096), 256)):
+                                ((2, 512), 256), ((1, 2048), 512), ((1, 3072), 256),
+                                ((1, 4096), 256)):
             p = prov.plan_bf16_paged(L.Bf16PagedPrefillSpec(B, B * n, B * n // 16, 32, 8,
                                                             kv_dtype=dt))
             assert p.algorithm == "long_tile" and p.info.block_threads == threads, (dt, B, n)
@@ -254,12 +256,13 @@ def test_fp8_two_tiles_per_wave_with_a_guarded_request(L, oracle):
     assert np.all(np.isnan(o[1100:])) and not np.any(np.isnan(o[:1100]))
 
 
-@pytest.mark.parametrize("n", [1024, 1536])
+@pytest.mark.parametrize("n", [1024, 1536, 2048])
 def test_two_wave_groups_at_prompt_scale(L, oracle, n):
-    """One-tile long-tile plans of these prompts run two groups of four waves
-    that split each tile's K/V blocks and merge in LDS (1024 rows: a grid of
-    one round, one page-index window; 1536: two windows); the same command
-    on the 16-column algorithm agrees within the attention tolerance."""
+    """Long-tile plans of these prompts run two groups of four waves that
+    split each tile's K/V blocks and merge in LDS (1024 rows: one tile per
+    wave, a grid of one round, one page-index window; 1536: two windows;
+    2048: two tiles per wave, a grid of one round); the same command on the
+    16-column algorithm agrees within the attention tolerance."""
     log(f"long prefill two wave groups, 1 x {n} rows")
     import torch
     rng = np.random.default_rng(n)
