@@ -239,19 +239,64 @@ __device__ __forceinline__ bool token_slot_apply(const AppendArgs &a, int t, int
   return in && slot_from(a, rg, pgv, pages, st, en, tl, req, pos, page, off);
 }
 
+// Stores 1 into the queue's device status word `word` (system scope: the
+// words live in host memory and are read when the command is settled).
+__device__ __forceinline__ void report_status(const AppendArgs &a, int word) {
+  __hip_atomic_store(&a.status[word], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The workspace's epoch and broken word, read together at the start of a
+// command.
+struct WsEpoch {
+  uint64_t epoch;
+  uint32_t broken;
+};
+__device__ __forceinline__ WsEpoch read_epoch(const AppendArgs &a) {
+  WsEpoch e;
+  e.epoch = __hip_atomic_load(reinterpret_cast<uint64_t *>(a.ws + kWsEpoch), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+  e.broken = __hip_atomic_load(a.ws + kWsBroken, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return e;
+}
+
+// The words of read_epoch as of this point of the program: an empty asm that
+// takes them in vector registers keeps everything computed from them (their
+// moves to scalar registers, the tag, the table choice) after it, so the
+// load's round trip overlaps whatever was issued before this point.
+__device__ __forceinline__ WsEpoch settle(WsEpoch e) {
+  asm volatile("" : "+v"(e.epoch), "+v"(e.broken));
+  return e;
+}
+
+// A workgroup of the one-launch append refuses on a broken workspace (nothing
+// inserted, nothing written) and otherwise tags its start word: it has read
+// the epoch.  Returns whether it refused.
+__device__ __forceinline__ bool refused_or_started(const AppendArgs &a, uint64_t *started,
+                                                   const WsEpoch &ep, int tid) {
+  if (tid == 0) {
+    if (ep.broken)
+      report_status(a, loom::kStatusAppendRefused);
+    else
+      __hip_atomic_store(&started[blockIdx.x], ep.epoch + 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return ep.broken != 0u;
+}
+
 // Validation of chunk b, all-or-nothing.  Chunks [0, index_blocks) check the
 // page indices [b*chunk, (b+1)*chunk) (rope/mod.rs:143-150), chunk 0 also
 // the table bounds; chunk index_blocks + j checks requests [j*256, (j+1)*256)
 // (paged_decode/mod.rs:164-205) and tokens [j*256, (j+1)*256)
 // (paged_append/mod.rs:262-309), one token per thread, and inserts every
-// valid slot key into the hash set `table` (agent-scope compare-and-swap, so
-// two tokens with one slot meet whichever XCDs they run on; the second finds
-// the first).  The two kinds run in different workgroups so that neither
-// waits for the other's loads.  Returns nonzero if the chunk is invalid.
+// valid slot key into the hash set, table ep.epoch & 1 of `tables`
+// (agent-scope compare-and-swap, so two tokens with one slot meet whichever
+// XCDs they run on; the second finds the first).  The two kinds run in different workgroups so that neither
+// waits for the other's loads.  Returns nonzero if the chunk is invalid; on
+// a broken workspace it inserts nothing and fails every token.
 // `s_ip` / `s_last` hold kValidateLdsBatch + 1 / kValidateLdsBatch words of
 // LDS; `s_or` one word per wave for the verdict.
 __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int tid, int32_t *s_ip,
-                                              int32_t *s_last, uint32_t *table,
+                                              int32_t *s_last, uint32_t *tables, WsEpoch ep,
                                               uint32_t (&s_or)[kValidateThreads / 64]) {
   int bad = 0;
   const int32_t ipB = a.indptr[a.batch];
@@ -302,10 +347,12 @@ __device__ __forceinline__ int validate_chunk(const AppendArgs &a, int b, int ti
     bad |= (en <= st || tl < 1 || tl > a.page_rows) ? 1 : 0;
   }
   __syncthreads();  // the LDS request table
+  ep = settle(ep);
+  uint32_t *const table = ep.broken ? nullptr : tables + (ep.epoch & 1u) * kTableSlots;
   if (has_token) {
     int rr = 0, p = 0, off = 0;
     int64_t pg = 0;
-    if (slot_of(a, r_given, p_given, pages, &rr, &p, &pg, &off, ip, ln)) {
+    if (table && slot_of(a, r_given, p_given, pages, &rr, &p, &pg, &off, ip, ln)) {
       const uint32_t key = (uint32_t)(pg * a.page_rows + off);
       // Open addressing over the whole table (load T / kTableSlots <= 1/2):
       // every probe sequence ends at an empty entry or at the same key (a
@@ -473,26 +520,6 @@ __device__ __forceinline__ void apply_token(const AppendArgs &a, int t, int64_t 
   }
 }
 
-// Stores 1 into the queue's device status word `word` (system scope: the
-// words live in host memory and are read when the command is settled).
-__device__ __forceinline__ void report_status(const AppendArgs &a, int word) {
-  __hip_atomic_store(&a.status[word], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// The workspace's epoch and broken word, read together at the start of a
-// command.
-struct WsEpoch {
-  uint64_t epoch;
-  uint32_t broken;
-};
-__device__ __forceinline__ WsEpoch read_epoch(const AppendArgs &a) {
-  WsEpoch e;
-  e.epoch = __hip_atomic_load(reinterpret_cast<uint64_t *>(a.ws + kWsEpoch), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-  e.broken = __hip_atomic_load(a.ws + kWsBroken, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return e;
-}
-
 // One launch per command.  Workgroups 0..V-1 each validate one chunk of the
 // command (validate_chunk) and publish the chunk's verdict, tagged with the
 // command's epoch, to every signal copy, then empty their share of the hash
@@ -536,20 +563,19 @@ void append_validated_kernel(AppendArgs a) {
   __shared__ int s_bad;
   const int tid = threadIdx.x;
   const WsLayout w = ws_layout(a.ws);
-  const WsEpoch ep = read_epoch(a);
-  const uint64_t epoch = ep.epoch;
-  const uint64_t tag = epoch + 1u;
-  if (ep.broken) {
-    if (tid == 0) report_status(a, loom::kStatusAppendRefused);
-    return;
-  }
-  if (tid == 0)
-    __hip_atomic_store(&w.started[blockIdx.x], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // The epoch and broken words are first needed at the slot-key inserts (a
+  // validation workgroup) or the verdict polls (a token workgroup): their
+  // round trip overlaps the metadata and row loads issued before those.
+  const WsEpoch ep0 = read_epoch(a);
 
   if ((int)blockIdx.x < a.validate_blocks) {
     // validation workgroup b
     const int b = blockIdx.x;
-    const int bad = validate_chunk(a, b, tid, s_ip, s_last, w.tables + (epoch & 1u) * kTableSlots, s_or);
+    const int bad = validate_chunk(a, b, tid, s_ip, s_last, w.tables, ep0, s_or);
+    const WsEpoch ep = settle(ep0);
+    const uint64_t epoch = ep.epoch;
+    const uint64_t tag = epoch + 1u;
+    if (refused_or_started(a, w.started, ep, tid)) return;
     if (tid < kSignalCopies)
       __hip_atomic_store(&w.signals[tid * kMaxValidateBlocks + b], tag * 2u + (bad ? 0u : 1u),
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -603,6 +629,11 @@ void append_validated_kernel(AppendArgs a) {
   int64_t page = 0;
   const int64_t pages = table_pages(a, a.indptr[a.batch]);
   if (!token_slot_apply(a, t, tid, pages, &r, &pos, &page, &off)) pos = 0, page = 0;
+  // The walk has waited for loads issued after the epoch's: the start tag
+  // costs no extra round trip here, and goes out before the row loads.
+  const WsEpoch ep = settle(ep0);
+  const uint64_t tag = ep.epoch + 1u;
+  if (refused_or_started(a, w.started, ep, tid)) return;
   // Row loads after the walk: the validation's dependent loads run while the
   // memory system is not yet flooded with the command's row traffic, and the
   // rows still arrive before the verdicts.
@@ -650,8 +681,7 @@ __global__ __launch_bounds__(kValidateThreads) void append_validate_kernel(Appen
   if (ep.broken) {
     if (b == 0 && tid == 0) report_status(a, loom::kStatusAppendRefused);
   } else {
-    bad = validate_chunk(a, b, tid, s_ip, s_last, ws_layout(a.ws).tables + (ep.epoch & 1u) * kTableSlots,
-                         s_or);
+    bad = validate_chunk(a, b, tid, s_ip, s_last, ws_layout(a.ws).tables, ep, s_or);
   }
   if (tid == 0)
     __hip_atomic_store(a.ws + kWsVerdicts + b, bad ? 0u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
