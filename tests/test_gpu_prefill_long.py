@@ -256,6 +256,35 @@ def test_fp8_two_tiles_per_wave_with_a_guarded_request(L, oracle):
     assert np.all(np.isnan(o[1100:])) and not np.any(np.isnan(o[:1100]))
 
 
+def test_fp8_two_groups_of_two_tiles_at_prompt_scale(L, oracle):
+    """FP8 pages at two query tiles per wave and two wave groups (a 2048-row
+    GQA4 prompt: 512 workgroups, one round of two per CU), with K and V
+    scales: the 16-column FP8 command agrees within the oracle tolerance."""
+    import torch
+    from test_gpu_fp8 import random_fp8
+    n = 2048
+    log(f"long prefill fp8, two wave groups of two tiles, 1 x {n} rows")
+    rng = np.random.default_rng(2048 + 8)
+    hq, hkv = 32, 8
+    pages = n // 16
+    pool = pages + 3
+    qo = np.array([0, n], np.int32)
+    ip = np.array([0, pages], np.int32)
+    ix = rng.permutation(pool)[:pages].astype(np.int32)
+    last = np.array([16], np.int32)
+    plan = L.PrefillProvider.load(0).plan_bf16_paged(
+        L.Bf16PagedPrefillSpec(1, n, pool, hq, hkv, kv_dtype="fp8_e4m3"))
+    assert plan.algorithm == "long_tile" and plan.info.block_threads == 512
+    assert plan.info.row_tiles == n * 4 // 128, plan.info.row_tiles
+    q = seeded_normal_bf16(oracle, rng, n * hq * 128)
+    k = torch.from_numpy(random_fp8(rng, pool * 16 * hkv * 128, max_code=0x44)).to("cuda")
+    v = torch.from_numpy(random_fp8(rng, pool * 16 * hkv * 128, max_code=0x44)).to("cuda")
+    res = paged_pair(L, 1, n, pool, hq, hkv, q, k, v, qo, ip, ix, last,
+                     spec_kw={"kv_dtype": "fp8_e4m3"}, scales=[0.3, 0.7], tile="long")
+    assert not np.any(np.isnan(oracle.bf16_to_f32(res[0][0])))
+    log(f"  vs 16-column: {assert_close(oracle, res)}")
+
+
 @pytest.mark.parametrize("n", [1024, 1536, 2048])
 def test_two_wave_groups_at_prompt_scale(L, oracle, n):
     """Long-tile plans of these prompts run two groups of four waves that
@@ -278,6 +307,7 @@ def test_two_wave_groups_at_prompt_scale(L, oracle, n):
                for x in (n * hq * 128, pool * 16 * hkv * 128, pool * 16 * hkv * 128))
     plan = L.PrefillProvider.load(0).plan_bf16_paged(L.Bf16PagedPrefillSpec(1, n, pool, hq, hkv))
     assert plan.algorithm == "long_tile" and plan.info.block_threads == 512
+    assert plan.info.row_tiles == n * 4 // (128 if n == 2048 else 64), plan.info.row_tiles
     res = paged_pair(L, 1, n, pool, hq, hkv, q, k, v, qo, ip, ix, last, tile="long")
     assert not np.any(np.isnan(oracle.bf16_to_f32(res[0][0])))
     log(f"  vs 16-column: {assert_close(oracle, res)}")
