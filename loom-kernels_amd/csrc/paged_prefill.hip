@@ -80,6 +80,10 @@ struct PrefillArgs {
   // starting at token row p * page_rows + 16 * j.
   int32_t page_rows;
   int32_t blocks_lg;
+  // Tiles per dispatch layer (one workgroup on each CU that the kv-heads of
+  // one workgroup's XCD share: CUs / Hkv) for the serpentine tile order; 0:
+  // plain heaviest-first order.
+  int32_t tile_layer;
   // FP8 E4M3 pages: device [k_scale, v_scale] (K = fp8 * k_scale, V = fp8 *
   // v_scale); null for BF16 pages.
   const float *kv_scales;
@@ -650,7 +654,18 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &args) {
   // find no tile, come first and exit at once).  Workgroup b runs on XCD
   // b % 8; with the kv-head fastest, each XCD keeps to a fixed set of
   // kv-heads, whose K/V its L2 shares across tiles.
-  const int64_t tile = (int64_t)(gridDim.x / a.hkv) - 1 - blockIdx.x / a.hkv;
+  const int64_t n_tiles = (int64_t)(gridDim.x / a.hkv), m = blockIdx.x / a.hkv;
+  int64_t rank = m;
+  if (a.tile_layer > 0) {
+    // Serpentine: every other layer of tile_layer workgroups (one per CU of
+    // the XCDs this kv-head runs on) takes its tiles in reverse, so a CU's
+    // successive workgroups pair heavy tiles with light ones instead of
+    // stacking the heaviest of every layer.
+    const int64_t L = a.tile_layer, layer = m / L, c = m - layer * L;
+    const int64_t width = min(L, n_tiles - layer * L);
+    rank = layer * L + ((layer & 1) ? width - 1 - c : c);
+  }
+  const int64_t tile = n_tiles - 1 - rank;
 
   // Metadata in as few dependent round trips as possible: the global guard
   // words and every request's qo range, page (kv) range and tail are loaded
@@ -1113,6 +1128,7 @@ struct loom_paged_prefill_plan {
   loom_paged_prefill_plan_info_t info{};
   uint32_t tile_cols = 16;  // flattened columns per workgroup
   uint32_t long_groups = 1;  // long tiles: wave groups splitting the K/V blocks
+  uint32_t tile_layer = 0;   // serpentine tile order layer (PrefillArgs::tile_layer)
 };
 
 struct loom_ragged_prefill_plan {
@@ -1272,15 +1288,28 @@ loom_status_t loom_prefill_provider_plan_bf16_paged_options(
   // that the heaviest tiles dominate.  Measured (GQA4 32/8, BF16 / FP8 pages,
   // two groups against one): 1 x 512 rows -6% / -15%, 1 x 1024 -2% / -16%,
   // 1 x 1536 -10% / +2%, and 2 x 512 rows (520 workgroups, a second round)
-  // +6% / -4%.  Long tiles of two query tiles per wave split into two groups
-  // only when the grid fits that one round: 1 x 2048 rows -11% / -13%, but
+  // +6% / -4%.  Long tiles of two query tiles per wave (one such 8-wave
+  // workgroup per CU) split into two groups only on grids of at most two
+  // workgroups per CU: 1 x 2048 rows -11% / -13%, but
   // 1 x 3072 +16%, 1 x 4096 +27%, 1 x 8192 +25% and 4 x 2048 +36% (the
   // 8-wave, 2-tile workgroup holds two waves per SIMD and 70 KB of LDS).
-  const bool one_round = grid <= 2 * (uint64_t)provider->dev.cus;
+  const bool two_per_cu = grid <= 2 * (uint64_t)provider->dev.cus;
   const bool grouped = long_tile &&
-                       ((tile_cols == 64 && (one_round || spec->nnz_qo >= 1024 * spec->batch_size)) ||
-                        (tile_cols == 128 && one_round));
+                       ((tile_cols == 64 && (two_per_cu || spec->nnz_qo >= 1024 * spec->batch_size)) ||
+                        (tile_cols == 128 && two_per_cu));
   p->long_groups = grouped ? LOOM_PREFILL_LONG_GROUPS : 1;
+  // Serpentine tile order when the whole grid is resident at once (long
+  // tiles: three 4-wave workgroups per CU; two 8-wave ones of one tile per
+  // wave; one of two tiles per wave).  A second round is dispatched as CUs
+  // free up, where heaviest-first order balances better.  Measured (GQA4
+  // 32/8, BF16, same box): 1 x 1024 rows 28.6 -> 25.3 us, 2 x 512 18.5 ->
+  // 17.2, 1 x 3072 100.5 -> 98.0, 8 x 256 20.1 -> 19.8; on grids of more
+  // than one round 1 x 2048 (two tiles, two groups) 58 -> 70, 1 x 4096 141 ->
+  // 147, 4 x 2048 153 -> 163.
+  const uint64_t cus = provider->dev.cus, hkv_n = spec->num_kv_heads;
+  const uint64_t resident = p->long_groups == 2 ? (tile_cols == 128 ? 1 : 2) : 3;
+  p->tile_layer = long_tile && hkv_n > 0 && cus >= hkv_n && grid <= cus * resident
+                      ? (uint32_t)(cus / hkv_n) : 0;
 
   p->info.waves = waves;
   p->info.row_tiles = tiles;
@@ -1375,6 +1404,7 @@ loom_status_t loom_paged_prefill_enqueue(const loom_paged_prefill_plan_t *plan,
   a.row_elems = hnd ? 128 : a.hkv * 128;
   a.page_rows = (int32_t)page_rows;
   a.blocks_lg = page_rows == 64 ? 2 : page_rows == 32 ? 1 : 0;
+  a.tile_layer = (int32_t)plan->tile_layer;
   hipStream_t stream = scope->queue->stream;
   const dim3 grid((unsigned)plan->info.grid_blocks), block(plan->info.block_threads);
   if (fp8) {
