@@ -213,6 +213,18 @@ __device__ __forceinline__ int64_t shfl_up64(int64_t x, int o) {
   return ((int64_t)hi << 32) | (uint32_t)lo;
 }
 
+// Sum / max of an int over the wave (butterfly: every lane gets the result).
+__device__ __forceinline__ int wave_sum_i32(int x) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+__device__ __forceinline__ int wave_max_i32(int x) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) x = max(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
 __device__ __forceinline__ int64_t wave_incl_scan64(int64_t x, int lane) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {

@@ -162,3 +162,36 @@ def test_paged_prefill_random_shapes_long_tiles(L, oracle, seed):
     assert r.plan.algorithm == "long_tile"
     out, lse = r.run(q, k, v, qo, indptr, indices, last)
     log(f"  block_threads {r.plan.info.block_threads} {compare_decode(oracle, out, lse, *ref)}")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_paged_prefill_random_batches_long_tiles(L, oracle, seed):
+    """The long-tile algorithm forced on random batches of 3-12 ragged
+    requests, whose tiles the kernel takes interleaved by their distance from
+    their request's end (rank k: the k-th heaviest tile of every request);
+    every tile is computed once: the result equals the oracle's."""
+    from gpu_util import PrefillRunner
+    rng = np.random.default_rng(5000 + seed)
+    hkv = int(rng.choice([1, 2, 4]))
+    hq = hkv * int(rng.choice([1, 2, 4]))
+    B = int(rng.integers(3, 13))
+    kv_lens = rng.integers(1, 600, size=B)
+    qo_lens = np.array([int(rng.integers(1, min(k, 120) + 1)) for k in kv_lens])
+    pages = (kv_lens + 15) // 16
+    pool = int(pages.sum()) + int(rng.integers(0, 6))
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    indices = rng.permutation(pool)[: indptr[-1]].astype(np.int32)
+    last = (kv_lens - (pages - 1) * 16).astype(np.int32)
+    qo = np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32)
+    nnz = int(qo[-1])
+    log(f"long prefill batch sweep {seed}: B={B} hq={hq} hkv={hkv} qo={qo_lens.tolist()} "
+        f"kv={kv_lens.tolist()}")
+    q = seeded_normal_bf16(oracle, rng, nnz * hq * 128)
+    k = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    v = seeded_normal_bf16(oracle, rng, pool * 16 * hkv * 128)
+    ref = oracle.prefill(oracle.prefill_spec(B, nnz, pool, hq, hkv), q, k, v, qo, indptr,
+                         indices, last)
+    r = PrefillRunner(L, B, nnz, pool, hq, hkv, tile_cols="long")
+    assert r.plan.algorithm == "long_tile"
+    out, lse = r.run(q, k, v, qo, indptr, indices, last)
+    log(f"  block_threads {r.plan.info.block_threads} {compare_decode(oracle, out, lse, *ref)}")
